@@ -1,0 +1,369 @@
+/*
+ * teeny_hip.h — C ABI of the MI355X (gfx950) teeny-kernels operator library.
+ *
+ * This header is the whole boundary between a host executor and the HIP
+ * kernels.  It replaces two pieces of the reference:
+ *
+ *   1. the CUDA driver crate's device/buffer/stream/module/launch surface
+ *      (drivers/teeny-cuda/src/device/mod.rs:212-490,
+ *       drivers/teeny-cuda/src/device/buffer.rs:37-62), and
+ *   2. the per-kernel C-ABI entry points that the #[kernel] macro generates as
+ *      "{name}_entry_point" (macros/teeny-macros/src/macros/kernel.rs:781-803)
+ *      for the hot-path operators in kernels/teeny-kernels/src/nn/ and the
+ *      host-side int8 quantizer in utilities/teeny-quant/src/quant/affine.rs.
+ *
+ * Conventions (all functions):
+ *   - Every function returns a teeny_status; 0 is success.  On failure the
+ *     thread-local message behind teeny_hip_last_error() says what was wrong.
+ *   - Operator entry points keep the reference kernel's argument order and
+ *     meaning.  Compile-time generics of the reference (KH, KW, HEAD_DIM, ...)
+ *     become trailing arguments, followed by a dtype (and layout where the op
+ *     has one) and a stream.  Element counts and dimensions are int64_t where
+ *     the reference used i32, so tensors beyond 2^31 elements are addressable.
+ *   - Operators never allocate and never synchronize: work is enqueued on the
+ *     given stream (NULL = the device's null stream).  Setting the
+ *     environment variable TEENY_HIP_SYNC=1 makes every operator synchronize
+ *     the stream after its launch, reproducing the reference executor's
+ *     synchronize-after-every-launch behaviour
+ *     (drivers/teeny-cuda/src/device/mod.rs:366-388).
+ *   - Argument validation (null pointers, shapes, dtypes, alignment) happens
+ *     on the host before any HIP call, so a rejected call has no effect on
+ *     the device.
+ *   - The caller owns every buffer (reference: LoadedModel owns params and
+ *     intermediates, drivers/teeny-cuda/src/model/mod.rs:680-691).
+ *   - Handles are plain HIP handles (hipStream_t, hipEvent_t, hipModule_t,
+ *     hipFunction_t) passed as void*, so callers that already hold HIP
+ *     objects can pass them directly.
+ */
+#ifndef TEENY_HIP_H
+#define TEENY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── status codes ─────────────────────────────────────────────────────────
+ * Reference: anyhow::Result with Error::CudaError{code,message}
+ * (drivers/teeny-cuda/src/errors.rs) for device failures, lowering errors for
+ * unsupported dtypes (kernels/teeny-kernels/src/graph/mod.rs:164,194,208) and
+ * teeny-quant's Error::{ShapeMismatch,InvalidAxis,InvalidGroupSize}
+ * (utilities/teeny-quant/src/quant/affine.rs:62-87). */
+typedef int32_t teeny_status;
+#define TEENY_OK 0
+#define TEENY_ERR_INVALID_ARGUMENT 1
+#define TEENY_ERR_NULL_POINTER 2
+#define TEENY_ERR_UNSUPPORTED_DTYPE 3
+#define TEENY_ERR_SHAPE_MISMATCH 4
+#define TEENY_ERR_MISALIGNED 5
+#define TEENY_ERR_INVALID_AXIS 6
+#define TEENY_ERR_INVALID_GROUP_SIZE 7
+#define TEENY_ERR_NO_DEVICE 8
+#define TEENY_ERR_HIP 9
+#define TEENY_ERR_NOT_FOUND 10
+#define TEENY_ERR_UNSUPPORTED 11
+
+/* Element types.  TEENY_F32 is the reference's D = f32; TEENY_BF16 stores
+ * IEEE bfloat16 (round-to-nearest-even on store, fp32 arithmetic inside every
+ * kernel); TEENY_I8 is the int8 output of teeny-quant. */
+typedef enum teeny_dtype {
+  TEENY_F32 = 0,
+  TEENY_BF16 = 1,
+  TEENY_I8 = 2
+} teeny_dtype;
+
+/* Activation layouts for conv2d.  NCHW is the reference's only layout
+ * (kernels/teeny-kernels/src/nn/conv/conv2d.rs:28-42): x [B,C_IN,H,W],
+ * w [C_OUT,C_IN/G,KH,KW], y [B,C_OUT,OH,OW].  NHWC is this library's
+ * MFMA layout: x [B,H,W,C_IN], w [C_OUT,KH,KW,C_IN/G], y [B,OH,OW,C_OUT]. */
+typedef enum teeny_layout {
+  TEENY_NCHW = 0,
+  TEENY_NHWC = 1
+} teeny_layout;
+
+/* Elementwise epilogues that conv/norm entry points can fuse. */
+typedef enum teeny_activation {
+  TEENY_ACT_NONE = 0,
+  TEENY_ACT_RELU = 1,
+  TEENY_ACT_GELU_TANH = 2,
+  TEENY_ACT_SILU = 3
+} teeny_activation;
+
+typedef void *teeny_stream;   /* hipStream_t */
+typedef void *teeny_event;    /* hipEvent_t */
+typedef void *teeny_module;   /* hipModule_t */
+typedef void *teeny_function; /* hipFunction_t */
+
+/* Message for the last failure on the calling thread ("" if none). */
+const char *teeny_hip_last_error(void);
+/* Static name of a status code. */
+const char *teeny_status_string(teeny_status status);
+/* Library version string. */
+const char *teeny_hip_version(void);
+
+/* ── device ───────────────────────────────────────────────────────────────
+ * Reference: CudaDevice::try_new (cuDeviceGet, cuCtxCreate_v4),
+ * drivers/teeny-cuda/src/device/mod.rs:225-262; teeny-runtime open(),
+ * runtime/teeny-runtime/src/lib.rs:250-259. */
+typedef struct teeny_device_info {
+  char name[256];
+  char arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int32_t clock_khz;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width;
+  int32_t l2_cache_bytes;
+  int64_t total_global_mem;
+  int64_t shared_mem_per_block;
+} teeny_device_info;
+
+teeny_status teeny_hip_init(void);
+teeny_status teeny_hip_device_count(int32_t *count);
+/* Makes `ordinal` the calling thread's current device. */
+teeny_status teeny_hip_device_open(int32_t ordinal);
+teeny_status teeny_hip_device_info(int32_t ordinal, teeny_device_info *info);
+teeny_status teeny_hip_device_synchronize(void);
+teeny_status teeny_hip_device_close(int32_t ordinal);
+
+/* ── device buffers ───────────────────────────────────────────────────────
+ * Reference: device.buffer::<T>(n), to_device, to_host
+ * (drivers/teeny-cuda/src/device/buffer.rs:37-62). */
+teeny_status teeny_hip_malloc(void **ptr, size_t bytes);
+teeny_status teeny_hip_free(void *ptr);
+teeny_status teeny_hip_memcpy_h2d(void *dst, const void *src, size_t bytes, teeny_stream stream);
+teeny_status teeny_hip_memcpy_d2h(void *dst, const void *src, size_t bytes, teeny_stream stream);
+teeny_status teeny_hip_memcpy_d2d(void *dst, const void *src, size_t bytes, teeny_stream stream);
+teeny_status teeny_hip_memset(void *dst, int32_t value, size_t bytes, teeny_stream stream);
+
+/* ── streams and events ───────────────────────────────────────────────────
+ * Reference: synchronous launches on the null stream plus CUDA-event timing in
+ * CudaGraphModel::run_timed (drivers/teeny-cuda/src/model/mod.rs:1729-1797).
+ * Streams are always created at the default priority. */
+teeny_status teeny_hip_stream_create(teeny_stream *stream);
+teeny_status teeny_hip_stream_destroy(teeny_stream stream);
+teeny_status teeny_hip_stream_sync(teeny_stream stream);
+teeny_status teeny_hip_event_create(teeny_event *event);
+teeny_status teeny_hip_event_destroy(teeny_event event);
+teeny_status teeny_hip_event_record(teeny_event event, teeny_stream stream);
+teeny_status teeny_hip_event_sync(teeny_event event);
+teeny_status teeny_hip_event_elapsed_ms(float *ms, teeny_event start, teeny_event stop);
+
+/* ── code objects and raw launch ──────────────────────────────────────────
+ * Reference: CudaProgram::try_from_ptx (cuModuleLoadDataEx) and
+ * CudaDevice::launch_with_packer (cuLaunchKernel with a void** argument
+ * array), drivers/teeny-cuda/src/device/program.rs:327-390 and
+ * drivers/teeny-cuda/src/device/mod.rs:430-490.  Here the image is a gfx950
+ * code object (.hsaco); no trailing Triton scratch pointers are appended. */
+teeny_status teeny_hip_module_load(teeny_module *module, const char *path);
+teeny_status teeny_hip_module_load_data(teeny_module *module, const void *image);
+teeny_status teeny_hip_module_get_function(teeny_function *function, teeny_module module,
+                                           const char *name);
+teeny_status teeny_hip_module_unload(teeny_module module);
+teeny_status teeny_hip_launch(teeny_function function, const uint32_t grid[3],
+                              const uint32_t block[3], uint32_t shared_mem_bytes,
+                              teeny_stream stream, void **args);
+
+/* ── elementwise activations ──────────────────────────────────────────────
+ * y[i] = f(x[i]) for i < n_elements; x and y may alias (in-place).
+ *   relu:  max(x, 0)                      nn/activation/relu.rs:27-64
+ *   gelu:  x / (1 + exp(-2c(x + 0.044715 x^3))), c = sqrt(2/pi)
+ *                                         nn/activation/gelu.rs:31-78
+ *   silu:  x * 1/(1 + exp(-x))            nn/activation/sigmoid.rs:119-158
+ * Reference arguments: (x_ptr, y_ptr, n_elements).  dtype: F32 or BF16. */
+teeny_status teeny_relu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream);
+teeny_status teeny_gelu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream);
+teeny_status teeny_silu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream);
+
+/* ── normalisation ────────────────────────────────────────────────────────
+ * LayerNorm over the last dimension of a row-major [M, N] tensor:
+ *   y = (x - mean) * rsqrt(var + eps) * weight + bias   (biased variance)
+ * Reference: layer_norm_forward_inference(x, y, weight, bias, M, N, eps),
+ * kernels/teeny-kernels/src/nn/norm/layernorm.rs:42-157, RuntimeOp :486-561.
+ * x, y, weight, bias share `dtype` (F32 or BF16); statistics are fp32. */
+teeny_status teeny_layer_norm_forward_inference(const void *x, void *y, const void *weight,
+                                                const void *bias, int64_t M, int64_t N,
+                                                float eps, teeny_dtype dtype,
+                                                teeny_stream stream);
+
+/* RMSNorm: rrms[m] = rsqrt(mean(x[m,:]^2) + eps), y = x * rrms * weight.
+ * Reference: rms_norm_forward(x, y, weight, rrms, M, N, eps),
+ * kernels/teeny-kernels/src/nn/norm/rmsnorm.rs:39-119.  rrms is always fp32
+ * (for dtype F32 this is the reference's D); it may be NULL to skip it. */
+teeny_status teeny_rms_norm_forward(const void *x, void *y, const void *weight, float *rrms,
+                                    int64_t M, int64_t N, float eps, teeny_dtype dtype,
+                                    teeny_stream stream);
+
+/* Fused norm + activation: one pass computing act(norm(x)).  No reference
+ * counterpart as a single kernel: it is the composition of the two kernels
+ * above with the activation kernels (the Anduin pointwise-fusion idea,
+ * kernels/teeny-kernels/src/graph/optimizer/anduin.rs:27-60, applied to a
+ * norm epilogue).  is_rms = 0: LayerNorm (bias used), 1: RMSNorm (bias
+ * ignored, may be NULL). */
+teeny_status teeny_norm_act_forward(const void *x, void *y, const void *weight, const void *bias,
+                                    int64_t M, int64_t N, float eps, int32_t is_rms,
+                                    teeny_activation act, teeny_dtype dtype, teeny_stream stream);
+
+/* ── conv2d ───────────────────────────────────────────────────────────────
+ * y[b,co,oh,ow] = sum_{ci in group(co), kh, kw} x[b,ci,oh*SH-PH+kh, ow*SW-PW+kw]
+ *                 * w[co, ci - g*C_IN/G, kh, kw]  (+ bias[co])
+ * with zero padding.  Reference: conv2d_forward / conv2d_bias_forward
+ * (x, w, [bias,] y, B, C_IN, C_OUT, H, W, OH, OW) with const generics
+ * KH, KW, STRIDE_H, STRIDE_W, PAD_H, PAD_W, G,
+ * kernels/teeny-kernels/src/nn/conv/conv2d.rs:43-156 and :642-764.
+ * BLOCK_OW is a reference tiling choice and has no counterpart here.
+ * `act` fuses an activation after the bias (TEENY_ACT_NONE = reference).
+ * Layout NCHW: any dtype (F32, BF16).  Layout NHWC: BF16 runs the MFMA
+ * implicit-GEMM kernels (weights [C_OUT,KH,KW,C_IN/G]); F32 also accepted. */
+typedef struct teeny_conv2d_params {
+  int32_t KH, KW;
+  int32_t stride_h, stride_w;
+  int32_t pad_h, pad_w;
+  int32_t groups;
+  int32_t act; /* teeny_activation */
+} teeny_conv2d_params;
+
+teeny_status teeny_conv2d_forward(const void *x, const void *w, void *y, int64_t B, int64_t C_IN,
+                                  int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                  const teeny_conv2d_params *params, teeny_dtype dtype,
+                                  teeny_layout layout, teeny_stream stream);
+teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void *bias, void *y,
+                                       int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H,
+                                       int64_t W, int64_t OH, int64_t OW,
+                                       const teeny_conv2d_params *params, teeny_dtype dtype,
+                                       teeny_layout layout, teeny_stream stream);
+
+/* ── attention ────────────────────────────────────────────────────────────
+ * O = softmax(Q K^T * softmax_scale) V per (batch*head), L = logsumexp of the
+ * scaled scores (natural log).  Layout [BH, n_ctx, head_dim] row-major.
+ * Reference: flash_attention2_forward(q, k, v, o, l, n_ctx_q, n_ctx_k,
+ * softmax_scale, neg_inf) with const HEAD_DIM and grid (n_ctx_q, BH, 1),
+ * kernels/teeny-kernels/src/nn/attention/flash_attn2.rs:52-158.  Here BH and
+ * head_dim are arguments, neg_inf is internal, and `causal` != 0 masks key j
+ * from query i when j > i (top-left aligned, as torch's is_causal).
+ * l is fp32 for every dtype and may be NULL.  dtype F32: head_dim a power of
+ * two <= 256.  dtype BF16: MFMA flash kernel, head_dim 64 or 128. */
+teeny_status teeny_flash_attention2_forward(const void *q, const void *k, const void *v, void *o,
+                                            float *l, int64_t n_ctx_q, int64_t n_ctx_k,
+                                            float softmax_scale, int64_t BH, int64_t head_dim,
+                                            int32_t causal, teeny_dtype dtype,
+                                            teeny_stream stream);
+
+/* ── int8 affine quantization (teeny-quant) ───────────────────────────────
+ * Reference: quantize_affine(tensor, data, shape, granularity, symmetric,
+ * bits) and dequantize_affine, utilities/teeny-quant/src/quant/affine.rs
+ * :55-161, groups from assign_groups (quant/groups.rs:78-100).
+ *   q = clamp(round_half_away(x / scale) + zero_point, qmin, qmax)
+ *   symmetric:  scale = amax == 0 ? 1 : amax / qmax, zero_point = 0
+ *   asymmetric: scale = hi == lo ? 1 : (hi - lo) / (qmax - qmin),
+ *               zero_point = clamp(round_half_away(qmin - lo / scale))
+ * with lo = min(min(x), 0), hi = max(max(x), 0) per group, qmax = 2^(bits-1)-1,
+ * qmin = -qmax (symmetric) or -qmax-1.  Bit-exact with the reference. */
+typedef enum teeny_granularity {
+  TEENY_PER_TENSOR = 0,
+  TEENY_PER_CHANNEL = 1, /* one group per index along `axis` */
+  TEENY_GROUP = 2        /* group_size-runs along `axis`, other axes independent */
+} teeny_granularity;
+
+/* Number of groups for a shape/granularity (reference assign_groups). */
+teeny_status teeny_quant_num_groups(const int64_t *shape, int32_t ndim,
+                                    teeny_granularity granularity, int32_t axis,
+                                    int64_t group_size, int64_t *num_groups);
+
+/* data: fp32 [prod(shape)] on device.  Outputs on device: qvalues int8
+ * [prod(shape)], scales fp32 [num_groups], zero_points int32 [num_groups]
+ * (all three required; scales and zero_points also serve as the min/max
+ * reduction space), groups uint32 [prod(shape)] optional (NULL = skip).
+ * bits in [2, 8]. */
+teeny_status teeny_quantize_affine(const float *data, const int64_t *shape, int32_t ndim,
+                                   teeny_granularity granularity, int32_t axis,
+                                   int64_t group_size, int32_t symmetric, int32_t bits,
+                                   int8_t *qvalues, float *scales, int32_t *zero_points,
+                                   uint32_t *groups, teeny_stream stream);
+
+/* out[i] = (q[i] - zero_point[g(i)]) * scale[g(i)] in fp32; zero_points may
+ * be NULL for symmetric tensors. */
+teeny_status teeny_dequantize_affine(const int8_t *qvalues, const float *scales,
+                                     const int32_t *zero_points, const int64_t *shape,
+                                     int32_t ndim, teeny_granularity granularity, int32_t axis,
+                                     int64_t group_size, float *out, teeny_stream stream);
+
+/* ── linear / W8A16 ───────────────────────────────────────────────────────
+ * y[m,n] = sum_k x[m,k] * w[n,k] (+ b[n]).  Reference: linear_forward(x, w,
+ * b, y, M, N, K, stride_xm, stride_xk, stride_wn, stride_wk, stride_ym,
+ * stride_yn), kernels/teeny-kernels/src/nn/mlp/linear.rs:20-116; b may be
+ * NULL (USE_BIAS = false).  dtype F32 or BF16 (x, w, b, y share it). */
+teeny_status teeny_linear_forward(const void *x, const void *w, const void *b, void *y,
+                                  int64_t M, int64_t N, int64_t K, int64_t stride_xm,
+                                  int64_t stride_xk, int64_t stride_wn, int64_t stride_wk,
+                                  int64_t stride_ym, int64_t stride_yn, teeny_dtype dtype,
+                                  teeny_stream stream);
+
+/* W8A16 linear: y[m,n] = scale[n] * sum_k x[m,k] * q[n,k] (+ bias[n]).
+ * x bf16 [M,K] row-major, q int8 [N,K] row-major (teeny-quant per-channel
+ * axis-0 symmetric output), scale fp32 [N], bias fp32 [N] or NULL, y bf16
+ * [M,N].  Equals linear_forward on dequantize_affine's weights
+ * (utilities/teeny-quant/src/quant/affine.rs:151-161): int8 is exact in bf16,
+ * so the dequant is q -> bf16 in registers and the scale is applied to the
+ * fp32 accumulator.  act: fused epilogue activation. */
+teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, const float *scale,
+                                        const float *bias, void *y, int64_t M, int64_t N,
+                                        int64_t K, teeny_activation act, teeny_stream stream);
+
+/* W8A16 conv2d, NHWC bf16 activations, int8 weights [C_OUT,KH,KW,C_IN/G]
+ * with per-output-channel fp32 scale, fp32 bias or NULL, bf16 output:
+ * conv2d_bias_forward (conv2d.rs:642-764) on dequantize_affine's weights. */
+teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, const float *scale,
+                                        const float *bias, void *y, int64_t B, int64_t C_IN,
+                                        int64_t C_OUT, int64_t H, int64_t W, int64_t OH,
+                                        int64_t OW, const teeny_conv2d_params *params,
+                                        teeny_stream stream);
+
+/* ── reference-shaped dispatch ────────────────────────────────────────────
+ * Runs an operator from exactly the argument list that the reference's
+ * RuntimeOp::pack_args visits (core/teeny-core/src/model/mod.rs:78-331,
+ * ArgVisitor core/teeny-core/src/device/program.rs:22-46), the kernel's
+ * const generics in declaration order, and the launch grid from
+ * RuntimeOp::grid.  This lets an executor written against the reference
+ * contract (LoadedModel::forward, drivers/teeny-cuda/src/model/mod.rs:524-700)
+ * call this library in place of cuLaunchKernel.  Entry point names are the
+ * reference's "{name}_entry_point" symbols, e.g.
+ * "conv2d_bias_forward_entry_point". */
+typedef enum teeny_arg_kind {
+  TEENY_ARG_PTR = 0,
+  TEENY_ARG_I32 = 1,
+  TEENY_ARG_I64 = 2,
+  TEENY_ARG_F32 = 3,
+  TEENY_ARG_F64 = 4,
+  TEENY_ARG_U32 = 5,
+  TEENY_ARG_BOOL = 6
+} teeny_arg_kind;
+
+typedef struct teeny_arg {
+  int32_t kind; /* teeny_arg_kind */
+  int32_t pad_;
+  union {
+    void *ptr;
+    int32_t i32;
+    int64_t i64;
+    float f32;
+    double f64;
+    uint32_t u32;
+    int32_t b;
+  } v;
+} teeny_arg;
+
+teeny_status teeny_dispatch(const char *entry_point, const int64_t *const_generics,
+                            int32_t n_const_generics, const teeny_arg *args, int32_t n_args,
+                            const uint32_t grid[3], teeny_dtype dtype, teeny_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEENY_HIP_H */

@@ -1,0 +1,253 @@
+"""CPU oracle for the teeny-kernels hot path — TEST INFRASTRUCTURE ONLY.
+
+ctypes wrappers over oracle/_build/libteeny_oracle.so, the plain-C
+restatement of the reference kernels (oracle/teeny_oracle.c, each function
+citing the reference file:line it follows).  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+package, and only as the checker or the timed CPU baseline; the product
+(teenygrad_amd) never calls it.
+
+Arrays are numpy fp32 (int8/int32/uint32 for quantization).  For bf16
+workloads callers pass the bf16-rounded inputs as fp32: the oracle computes
+in fp32 on the same values the GPU reads.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import POINTER, c_float, c_int, c_int64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libteeny_oracle.so")
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    P = c_void_p
+    I = c_int64
+    sigs = {
+        "oracle_set_threads": [c_int],
+        "oracle_threads": [],
+        "oracle_relu_forward": [P, P, I, I, I, I],
+        "oracle_gelu_forward": [P, P, I, I, I, I],
+        "oracle_silu_forward": [P, P, I, I, I, I],
+        "oracle_layer_norm_forward_inference": [P, P, P, P, I, I, c_float, I, I, I],
+        "oracle_rms_norm_forward": [P, P, P, P, I, I, c_float, I, I, I],
+        "oracle_conv2d_forward": [P, P, P, P] + [I] * 15 + [I, I],
+        "oracle_flash_attention2_forward": [P, P, P, P, P, I, I, I, I, c_float, c_int, I, I],
+        "oracle_flash_attention2_rows": [P, P, P, P, P, I, I, I, I, c_float, c_int, P, I],
+        "oracle_linear_forward": [P, P, P, P] + [I] * 9 + [I, I],
+        "oracle_quant_num_groups": [P, c_int, c_int, c_int, I, POINTER(c_int64)],
+        "oracle_quantize_affine": [P, I, P, c_int, c_int, c_int, I, c_int, c_int, P, P, P, P],
+        "oracle_dequantize_affine": [P, P, P, P, c_int, c_int, c_int, I, P],
+    }
+    for name, args in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = c_int
+    return lib
+
+
+lib = _load()
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"oracle {what} failed with status {status}")
+        self.status = status
+
+
+def _chk(rc: int, what: str) -> None:
+    if rc != 0:
+        raise OracleError(rc, what)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def set_threads(n: int) -> None:
+    lib.oracle_set_threads(int(n))
+
+
+def threads() -> int:
+    return lib.oracle_threads()
+
+
+# ── activations (relu.rs:27-64, gelu.rs:31-78, sigmoid.rs:119-158) ────────
+
+
+def _act(fn, x, block_size, pid_begin, pid_end):
+    x = _f32(x)
+    y = np.zeros_like(x)
+    _chk(fn(_p(x), _p(y), x.size, block_size, pid_begin, pid_end), fn.__name__)
+    return y
+
+
+def relu(x, block_size=1024, pid_begin=0, pid_end=-1):
+    return _act(lib.oracle_relu_forward, x, block_size, pid_begin, pid_end)
+
+
+def gelu(x, block_size=1024, pid_begin=0, pid_end=-1):
+    return _act(lib.oracle_gelu_forward, x, block_size, pid_begin, pid_end)
+
+
+def silu(x, block_size=1024, pid_begin=0, pid_end=-1):
+    return _act(lib.oracle_silu_forward, x, block_size, pid_begin, pid_end)
+
+
+# ── norms (layernorm.rs:42-157, rmsnorm.rs:39-119) ──────────────────────────
+
+
+def layer_norm(x, weight, bias, eps=1e-5, block_n=1024, pid_begin=0, pid_end=-1):
+    x = _f32(x)
+    w, b = _f32(weight), _f32(bias)
+    n = x.shape[-1]
+    m = x.size // n
+    y = np.zeros_like(x)
+    _chk(lib.oracle_layer_norm_forward_inference(_p(x), _p(y), _p(w), _p(b), m, n, eps, block_n,
+                                                 pid_begin, pid_end), "layer_norm")
+    return y
+
+
+def rms_norm(x, weight, eps=1e-8, block_n=1024, pid_begin=0, pid_end=-1):
+    x = _f32(x)
+    w = _f32(weight)
+    n = x.shape[-1]
+    m = x.size // n
+    y = np.zeros_like(x)
+    rrms = np.zeros(m, dtype=np.float32)
+    _chk(lib.oracle_rms_norm_forward(_p(x), _p(y), _p(w), _p(rrms), m, n, eps, block_n, pid_begin,
+                                     pid_end), "rms_norm")
+    return y, rrms
+
+
+# ── conv2d (conv2d.rs:43-156, :642-764) ─────────────────────────────────────
+
+
+def conv2d_nchw(x, w, bias=None, stride=(1, 1), padding=(0, 0), groups=1, block_ow=16,
+                pid_begin=0, pid_end=-1):
+    """x [B,Cin,H,W], w [Cout,Cin/G,KH,KW] -> y [B,Cout,OH,OW] (fp32)."""
+    x, w = _f32(x), _f32(w)
+    bias = None if bias is None else _f32(bias)
+    sh, sw = (stride, stride) if isinstance(stride, int) else stride
+    ph, pw = (padding, padding) if isinstance(padding, int) else padding
+    B, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    y = np.zeros((B, Cout, OH, OW), dtype=np.float32)
+    _chk(lib.oracle_conv2d_forward(_p(x), _p(w), _p(bias), _p(y), B, Cin, Cout, H, W, OH, OW, KH, KW,
+                                   sh, sw, ph, pw, groups, block_ow, pid_begin, pid_end), "conv2d")
+    return y
+
+
+def conv2d_nhwc(x, w, bias=None, stride=(1, 1), padding=(0, 0), groups=1):
+    """x [B,H,W,Cin], w [Cout,KH,KW,Cin/G] -> y [B,OH,OW,Cout], via the NCHW restatement."""
+    y = conv2d_nchw(np.transpose(x, (0, 3, 1, 2)), np.transpose(w, (0, 3, 1, 2)), bias, stride,
+                    padding, groups)
+    return np.ascontiguousarray(np.transpose(y, (0, 2, 3, 1)))
+
+
+# ── attention (flash_attn2.rs:52-158) ───────────────────────────────────────
+
+
+def flash_attention(q, k, v, softmax_scale=None, causal=False, pid_begin=0, pid_end=-1):
+    """q [BH,Nq,D], k/v [BH,Nk,D] -> (o [BH,Nq,D], l [BH,Nq])."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, nq, D = q.shape
+    nk = k.shape[1]
+    scale = 1.0 / np.sqrt(D) if softmax_scale is None else softmax_scale
+    o = np.zeros_like(q)
+    l = np.zeros((BH, nq), dtype=np.float32)
+    _chk(lib.oracle_flash_attention2_forward(_p(q), _p(k), _p(v), _p(o), _p(l), BH, nq, nk, D,
+                                             scale, int(causal), pid_begin, pid_end), "flash_attention")
+    return o, l
+
+
+def flash_attention_rows(q, k, v, rows, softmax_scale=None, causal=False):
+    """Only program ids `rows` (= bh * Nq + q_row); returns (o_rows [n,D], l_rows [n])."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, nq, D = q.shape
+    nk = k.shape[1]
+    scale = 1.0 / np.sqrt(D) if softmax_scale is None else softmax_scale
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    o = np.zeros_like(q)
+    l = np.zeros((BH, nq), dtype=np.float32)
+    _chk(lib.oracle_flash_attention2_rows(_p(q), _p(k), _p(v), _p(o), _p(l), BH, nq, nk, D, scale,
+                                          int(causal), _p(rows), rows.size), "flash_attention_rows")
+    return o.reshape(-1, D)[rows], l.reshape(-1)[rows]
+
+
+# ── linear (linear.rs:20-116) ───────────────────────────────────────────────
+
+
+def linear(x, w, b=None, pid_begin=0, pid_end=-1):
+    x, w = _f32(x), _f32(w)
+    b = None if b is None else _f32(b)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.zeros((M, N), dtype=np.float32)
+    _chk(lib.oracle_linear_forward(_p(x), _p(w), _p(b), _p(y), M, N, K, K, 1, K, 1, N, 1, pid_begin,
+                                   pid_end), "linear")
+    return y
+
+
+# ── teeny-quant (affine.rs:47-161, groups.rs:20-100) ───────────────────────
+
+GRAN = {"tensor": 0, "channel": 1, "group": 2}
+
+
+def quant_num_groups(shape, granularity="channel", axis=0, group_size=1) -> int:
+    sh = np.ascontiguousarray(shape, dtype=np.int64)
+    out = c_int64()
+    _chk(lib.oracle_quant_num_groups(_p(sh), len(shape), GRAN[granularity], axis, group_size,
+                                     ctypes.byref(out)), "quant_num_groups")
+    return out.value
+
+
+def quantize_affine(data, shape, granularity="channel", axis=0, group_size=1, symmetric=True,
+                    bits=8):
+    """Returns (qvalues int8, scales f32, zero_points i32, groups u32)."""
+    data = _f32(data).reshape(-1)
+    sh = np.ascontiguousarray(shape, dtype=np.int64)
+    ng = quant_num_groups(shape, granularity, axis, group_size)
+    n = int(np.prod(shape)) if len(shape) else 1
+    q = np.zeros(max(n, data.size), dtype=np.int8)
+    scales = np.zeros(max(ng, 1), dtype=np.float32)
+    zps = np.zeros(max(ng, 1), dtype=np.int32)
+    groups = np.zeros(max(n, 1), dtype=np.uint32)
+    _chk(lib.oracle_quantize_affine(_p(data), data.size, _p(sh), len(shape), GRAN[granularity],
+                                    axis, group_size, int(bool(symmetric)), bits, _p(q),
+                                    _p(scales), _p(zps), _p(groups)), "quantize_affine")
+    return q[:n], scales[:ng], zps[:ng], groups[:n]
+
+
+def dequantize_affine(q, scales, zero_points, shape, granularity="channel", axis=0, group_size=1):
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    scales = _f32(scales)
+    zps = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.int32)
+    sh = np.ascontiguousarray(shape, dtype=np.int64)
+    out = np.zeros(int(np.prod(shape)) if len(shape) else 1, dtype=np.float32)
+    _chk(lib.oracle_dequantize_affine(_p(q), _p(scales), _p(zps), _p(sh), len(shape),
+                                      GRAN[granularity], axis, group_size, _p(out)),
+         "dequantize_affine")
+    return out.reshape(shape)
+
+
+def w8a16_linear(x, q, scales, bias=None):
+    """linear_forward on dequantize_affine's weights (per-channel axis 0)."""
+    w = dequantize_affine(q, scales, None, q.shape, "channel", 0)
+    return linear(x, w, bias)

@@ -1,0 +1,570 @@
+/*
+ * teeny_oracle.c — CPU restatement of the reference's teeny-kernels hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * library: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  No product code path calls it.
+ *
+ * Each function restates one reference kernel in plain C, fp32, following
+ * that kernel's program-id decomposition and per-program loop, so that its
+ * arithmetic (operation order, accumulation type, masking) is the
+ * reference's.  Programs are spread over host threads the way the
+ * reference's CPU launcher spreads them (drivers/teeny-riscv/src/native.rs
+ * :305-374): threads = TEENY_CPU_THREADS or all online cores; program ids
+ * are taken from an atomic counter in chunks of max(total / (threads*8), 1).
+ *
+ * Every function takes a program range [pid_begin, pid_end) so that a caller
+ * can run a prefix (CPU-baseline sampling) or the full grid (pid_end < 0).
+ * Status codes match include/teeny_hip.h.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#define OK 0
+#define ERR_INVALID_ARGUMENT 1
+#define ERR_SHAPE_MISMATCH 4
+#define ERR_INVALID_AXIS 6
+#define ERR_INVALID_GROUP_SIZE 7
+
+/* ── threaded launcher (native.rs:305-374) ─────────────────────────────── */
+
+typedef void (*program_fn)(const void *ctx, int64_t pid);
+
+typedef struct {
+  program_fn fn;
+  const void *ctx;
+  int64_t begin, end, chunk;
+  atomic_llong next;
+} launch_t;
+
+static int g_threads_override = 0;
+
+int oracle_set_threads(int n) {
+  g_threads_override = n > 0 ? n : 0;
+  return OK;
+}
+
+int oracle_threads(void) {
+  if (g_threads_override > 0) return g_threads_override;
+  const char *v = getenv("TEENY_CPU_THREADS");
+  if (v != NULL && atoi(v) > 0) return atoi(v);
+  long n = sysconf(_SC_NPROCESSORS_ONLN);
+  return n > 0 ? (int)n : 1;
+}
+
+static void *worker(void *arg) {
+  launch_t *L = (launch_t *)arg;
+  for (;;) {
+    int64_t start = atomic_fetch_add(&L->next, L->chunk);
+    if (start >= L->end) break;
+    int64_t stop = start + L->chunk < L->end ? start + L->chunk : L->end;
+    for (int64_t pid = start; pid < stop; ++pid) L->fn(L->ctx, pid);
+  }
+  return NULL;
+}
+
+static void launch(program_fn fn, const void *ctx, int64_t total, int64_t begin, int64_t end) {
+  if (end < 0 || end > total) end = total;
+  if (begin < 0) begin = 0;
+  if (begin >= end) return;
+  int64_t n = end - begin;
+  int64_t threads = oracle_threads();
+  if (threads > n) threads = n;
+  if (threads < 1) threads = 1;
+  launch_t L;
+  L.fn = fn;
+  L.ctx = ctx;
+  L.begin = begin;
+  L.end = end;
+  L.chunk = n / (threads * 8) > 1 ? n / (threads * 8) : 1;
+  atomic_init(&L.next, begin);
+  if (threads == 1) {
+    worker(&L);
+    return;
+  }
+  pthread_t *tids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+  for (int64_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, worker, &L);
+  for (int64_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+  free(tids);
+}
+
+/* ── activations ─────────────────────────────────────────────────────────
+ * relu.rs:27-64, gelu.rs:31-78, sigmoid.rs:119-158: program pid covers
+ * offsets [pid*BLOCK_SIZE, pid*BLOCK_SIZE + BLOCK_SIZE) masked by n. */
+
+typedef struct {
+  const float *x;
+  float *y;
+  int64_t n;
+  int64_t block;
+  int kind;
+} act_ctx;
+
+static float gelu_ref(float x) {
+  /* gelu.rs:53-64: one = 1, neg2c = -2*0.7978845608028654, coeff = 0.044715
+   * inner = x + coeff*x*x*x ; y = x / (one + exp(neg2c * inner)) */
+  const float one = 1.0f;
+  const float neg2c = (float)(-2.0 * 0.7978845608028654);
+  const float coeff = 0.044715f;
+  float inner = x + coeff * x * x * x;
+  return x / (one + expf(neg2c * inner));
+}
+
+static float silu_ref(float x) {
+  /* sigmoid.rs:144-148: s = one / (one + exp(neg1 * x)); y = x * s */
+  const float one = 1.0f, neg1 = -1.0f;
+  float s = one / (one + expf(neg1 * x));
+  return x * s;
+}
+
+static float relu_ref(float x) {
+  /* relu.rs:52-53: maximum(x, zeros_like(x)); NaN propagates. */
+  return x < 0.0f ? 0.0f : x;
+}
+
+static void act_program(const void *c, int64_t pid) {
+  const act_ctx *a = (const act_ctx *)c;
+  int64_t start = pid * a->block;
+  for (int64_t i = start; i < start + a->block && i < a->n; ++i) {
+    float v = a->x[i];
+    a->y[i] = a->kind == 0 ? relu_ref(v) : a->kind == 1 ? gelu_ref(v) : silu_ref(v);
+  }
+}
+
+static int act_run(const float *x, float *y, int64_t n, int64_t block, int kind, int64_t pb,
+                   int64_t pe) {
+  if (n < 0 || block <= 0) return ERR_SHAPE_MISMATCH;
+  act_ctx a = {x, y, n, block, kind};
+  launch(act_program, &a, (n + block - 1) / block, pb, pe);
+  return OK;
+}
+
+int oracle_relu_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
+                        int64_t pe) {
+  return act_run(x, y, n, block_size, 0, pb, pe);
+}
+int oracle_gelu_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
+                        int64_t pe) {
+  return act_run(x, y, n, block_size, 1, pb, pe);
+}
+int oracle_silu_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
+                        int64_t pe) {
+  return act_run(x, y, n, block_size, 2, pb, pe);
+}
+
+/* ── LayerNorm / RMSNorm ─────────────────────────────────────────────────
+ * layernorm.rs:42-157 and rmsnorm.rs:39-119: program = row; the row is
+ * visited in BLOCK_N tiles; each tile is reduced (T::sum) and the tile sums
+ * are accumulated in D = f32. */
+
+typedef struct {
+  const float *x;
+  float *y;
+  const float *w;
+  const float *b;
+  float *rrms;
+  int64_t N;
+  float eps;
+  int64_t block;
+} norm_ctx;
+
+static float tile_sum(const float *v, int64_t n) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) s += v[i];
+  return s;
+}
+
+static void layernorm_program(const void *c, int64_t row) {
+  const norm_ctx *a = (const norm_ctx *)c;
+  const float *x = a->x + row * a->N;
+  float *y = a->y + row * a->N;
+  const int64_t N = a->N, B = a->block;
+  float *tile = (float *)malloc(sizeof(float) * (size_t)B);
+  /* pass 1: mean (layernorm.rs:61-79) */
+  float sum = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    sum = sum + tile_sum(x + s, m);
+  }
+  const float n_inv = 1.0f / (float)N;
+  const float mean = sum * n_inv;
+  /* pass 2: variance of (x - mean), masked (layernorm.rs:81-100) */
+  float var_sum = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    for (int64_t i = 0; i < m; ++i) {
+      float d = x[s + i] - mean;
+      tile[i] = d * d;
+    }
+    var_sum = var_sum + tile_sum(tile, m);
+  }
+  const float rstd = 1.0f / sqrtf(var_sum * n_inv + a->eps);
+  /* pass 3: y = (x - mean) * rstd * gamma + beta (layernorm.rs:102-156) */
+  for (int64_t i = 0; i < N; ++i) y[i] = (x[i] - mean) * rstd * a->w[i] + a->b[i];
+  free(tile);
+}
+
+static void rmsnorm_program(const void *c, int64_t row) {
+  const norm_ctx *a = (const norm_ctx *)c;
+  const float *x = a->x + row * a->N;
+  float *y = a->y + row * a->N;
+  const int64_t N = a->N, B = a->block;
+  float *tile = (float *)malloc(sizeof(float) * (size_t)B);
+  const float n_inv = 1.0f / (float)N;
+  /* pass 1: sum of squares (rmsnorm.rs:58-79) */
+  float sq_sum = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    for (int64_t i = 0; i < m; ++i) tile[i] = x[s + i] * x[s + i];
+    sq_sum = sq_sum + tile_sum(tile, m);
+  }
+  const float rrms = 1.0f / sqrtf(sq_sum * n_inv + a->eps);
+  if (a->rrms != NULL) a->rrms[row] = rrms; /* rmsnorm.rs:83 */
+  /* pass 2: y = x * rrms * gamma (rmsnorm.rs:85-118) */
+  for (int64_t i = 0; i < N; ++i) y[i] = x[i] * rrms * a->w[i];
+  free(tile);
+}
+
+int oracle_layer_norm_forward_inference(const float *x, float *y, const float *w, const float *b,
+                                        int64_t M, int64_t N, float eps, int64_t block_n,
+                                        int64_t pb, int64_t pe) {
+  if (M < 0 || N <= 0 || block_n <= 0) return ERR_SHAPE_MISMATCH;
+  norm_ctx a = {x, y, w, b, NULL, N, eps, block_n};
+  launch(layernorm_program, &a, M, pb, pe);
+  return OK;
+}
+
+int oracle_rms_norm_forward(const float *x, float *y, const float *w, float *rrms, int64_t M,
+                            int64_t N, float eps, int64_t block_n, int64_t pb, int64_t pe) {
+  if (M < 0 || N <= 0 || block_n <= 0) return ERR_SHAPE_MISMATCH;
+  norm_ctx a = {x, y, w, NULL, rrms, N, eps, block_n};
+  launch(rmsnorm_program, &a, M, pb, pe);
+  return OK;
+}
+
+/* ── conv2d ──────────────────────────────────────────────────────────────
+ * conv2d.rs:43-156 (conv2d_forward) and :642-764 (conv2d_bias_forward):
+ * pid = ((b*C_OUT + c_out)*OH + oh)*num_ow_tiles + ow_tile; each program
+ * accumulates a BLOCK_OW strip over the flat (c_in_local, kh, kw) loop with
+ * zero padding by masking, then adds bias[c_out] (bias variant). */
+
+typedef struct {
+  const float *x, *w, *bias;
+  float *y;
+  int64_t B, Cin, Cout, H, W, OH, OW;
+  int64_t KH, KW, SH, SW, PH, PW, G, block_ow;
+} conv_ctx;
+
+static void conv_program(const void *c, int64_t pid) {
+  const conv_ctx *a = (const conv_ctx *)c;
+  const int64_t tiles = (a->OW + a->block_ow - 1) / a->block_ow;
+  const int64_t ow_tile = pid % tiles;
+  const int64_t bco = pid / tiles;
+  const int64_t oh = bco % a->OH;
+  const int64_t bc = bco / a->OH;
+  const int64_t c_out = bc % a->Cout;
+  const int64_t b = bc / a->Cout;
+  const int64_t ow_start = ow_tile * a->block_ow;
+  const int64_t cin_g = a->Cin / a->G;
+  const int64_t g_idx = c_out / (a->Cout / a->G);
+  const int64_t c_in_start = g_idx * cin_g;
+  float acc[512];
+  const int64_t BO = a->block_ow;
+  for (int64_t t = 0; t < BO; ++t) acc[t] = 0.0f;
+  const int64_t loop = cin_g * a->KH * a->KW;
+  for (int64_t idx = 0; idx < loop; ++idx) {
+    const int64_t kw = idx % a->KW;
+    const int64_t kh_cin = idx / a->KW;
+    const int64_t kh = kh_cin % a->KH;
+    const int64_t cl = kh_cin / a->KH;
+    const int64_t ci = c_in_start + cl;
+    const int64_t ih = oh * a->SH + kh - a->PH;
+    const float wv = a->w[((c_out * cin_g + cl) * a->KH + kh) * a->KW + kw];
+    for (int64_t t = 0; t < BO; ++t) {
+      const int64_t ow = ow_start + t;
+      const int64_t iw = ow * a->SW + kw - a->PW;
+      const int in_b = ow < a->OW && ih >= 0 && ih < a->H && iw >= 0 && iw < a->W;
+      const float xv = in_b ? a->x[((b * a->Cin + ci) * a->H + ih) * a->W + iw] : 0.0f;
+      acc[t] = acc[t] + xv * wv;
+    }
+  }
+  float bias = a->bias != NULL ? a->bias[c_out] : 0.0f;
+  for (int64_t t = 0; t < BO; ++t) {
+    const int64_t ow = ow_start + t;
+    if (ow < a->OW) {
+      float v = a->bias != NULL ? acc[t] + bias : acc[t];
+      a->y[((b * a->Cout + c_out) * a->OH + oh) * a->OW + ow] = v;
+    }
+  }
+}
+
+int oracle_conv2d_forward(const float *x, const float *w, const float *bias, float *y, int64_t B,
+                          int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                          int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                          int64_t G, int64_t block_ow, int64_t pb, int64_t pe) {
+  if (G <= 0 || Cin % G != 0 || Cout % G != 0) return ERR_SHAPE_MISMATCH;
+  if (block_ow <= 0 || block_ow > 512 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0)
+    return ERR_INVALID_ARGUMENT;
+  if (OH != (H + 2 * PH - KH) / SH + 1 || OW != (W + 2 * PW - KW) / SW + 1)
+    return ERR_SHAPE_MISMATCH;
+  conv_ctx a = {x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow};
+  const int64_t tiles = (OW + block_ow - 1) / block_ow;
+  launch(conv_program, &a, B * Cout * OH * tiles, pb, pe);
+  return OK;
+}
+
+/* ── flash attention 2 forward ───────────────────────────────────────────
+ * flash_attn2.rs:52-158: program (pid_m, pid_bh); q row in registers;
+ * sequential loop over key rows with the online-softmax recurrence
+ *   qk = sum(q*k) * scale; m_new = max(m, qk); a = exp(m - m_new);
+ *   p = exp(qk - m_new); l = a*l + p; acc = a*acc + p*v; m = m_new
+ * then o = acc / l and L = m + log(l).  Causal (an extension: the reference
+ * kernel is non-causal) stops the key loop at k_row = pid_m (top-left
+ * aligned).  Program id = pid_bh * n_ctx_q + pid_m. */
+
+typedef struct {
+  const float *q, *k, *v;
+  float *o, *l;
+  int64_t nq, nk, D;
+  float scale;
+  int causal;
+  const int64_t *rows; /* optional explicit program list */
+} fa_ctx;
+
+static void fa_program_id(const fa_ctx *a, int64_t id) {
+  const int64_t pid_bh = id / a->nq, pid_m = id % a->nq;
+  const int64_t D = a->D;
+  const float *q = a->q + (pid_bh * a->nq + pid_m) * D;
+  const float *kb = a->k + pid_bh * a->nk * D;
+  const float *vb = a->v + pid_bh * a->nk * D;
+  float acc[1024];
+  float m_i = -INFINITY, l_i = 0.0f;
+  for (int64_t d = 0; d < D; ++d) acc[d] = 0.0f;
+  int64_t kend = a->nk;
+  if (a->causal && pid_m + 1 < kend) kend = pid_m + 1;
+  for (int64_t kr = 0; kr < kend; ++kr) {
+    const float *k = kb + kr * D, *v = vb + kr * D;
+    float dot = 0.0f;
+    for (int64_t d = 0; d < D; ++d) dot += q[d] * k[d];
+    const float qk = dot * a->scale;
+    const float m_new = m_i > qk ? m_i : qk;
+    const float ed = expf(m_i - m_new);
+    const float p = expf(qk - m_new);
+    l_i = ed * l_i + p;
+    for (int64_t d = 0; d < D; ++d) acc[d] = ed * acc[d] + p * v[d];
+    m_i = m_new;
+  }
+  float *o = a->o + (pid_bh * a->nq + pid_m) * D;
+  for (int64_t d = 0; d < D; ++d) o[d] = acc[d] / l_i;
+  if (a->l != NULL) a->l[pid_bh * a->nq + pid_m] = m_i + logf(l_i);
+}
+
+static void fa_program(const void *c, int64_t id) {
+  const fa_ctx *a = (const fa_ctx *)c;
+  fa_program_id(a, a->rows != NULL ? a->rows[id] : id);
+}
+
+int oracle_flash_attention2_forward(const float *q, const float *k, const float *v, float *o,
+                                    float *l, int64_t BH, int64_t nq, int64_t nk, int64_t D,
+                                    float scale, int causal, int64_t pb, int64_t pe) {
+  if (D <= 0 || D > 1024 || nq < 0 || nk <= 0 || BH < 0) return ERR_SHAPE_MISMATCH;
+  fa_ctx a = {q, k, v, o, l, nq, nk, D, scale, causal, NULL};
+  launch(fa_program, &a, BH * nq, pb, pe);
+  return OK;
+}
+
+/* Runs only the listed program ids (pid_bh * nq + pid_m); o and l are
+ * written at those rows only.  Used to check full-size outputs on a sample. */
+int oracle_flash_attention2_rows(const float *q, const float *k, const float *v, float *o,
+                                 float *l, int64_t BH, int64_t nq, int64_t nk, int64_t D,
+                                 float scale, int causal, const int64_t *rows, int64_t n_rows) {
+  if (D <= 0 || D > 1024 || nq < 0 || nk <= 0 || BH < 0) return ERR_SHAPE_MISMATCH;
+  for (int64_t i = 0; i < n_rows; ++i)
+    if (rows[i] < 0 || rows[i] >= BH * nq) return ERR_SHAPE_MISMATCH;
+  fa_ctx a = {q, k, v, o, l, nq, nk, D, scale, causal, rows};
+  launch(fa_program, &a, n_rows, 0, -1);
+  return OK;
+}
+
+/* ── linear ──────────────────────────────────────────────────────────────
+ * linear.rs:20-116: y[m,n] = sum_k x[m,k] * w[n,k] (+ b[n]) with fp32
+ * accumulation in k order.  Program = output row m. */
+
+typedef struct {
+  const float *x, *w, *b;
+  float *y;
+  int64_t N, K, sxm, sxk, swn, swk, sym, syn;
+} lin_ctx;
+
+static void linear_program(const void *c, int64_t m) {
+  const lin_ctx *a = (const lin_ctx *)c;
+  for (int64_t n = 0; n < a->N; ++n) {
+    float acc = 0.0f;
+    for (int64_t k = 0; k < a->K; ++k)
+      acc += a->x[m * a->sxm + k * a->sxk] * a->w[n * a->swn + k * a->swk];
+    if (a->b != NULL) acc = acc + a->b[n];
+    a->y[m * a->sym + n * a->syn] = acc;
+  }
+}
+
+int oracle_linear_forward(const float *x, const float *w, const float *b, float *y, int64_t M,
+                          int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swn,
+                          int64_t swk, int64_t sym, int64_t syn, int64_t pb, int64_t pe) {
+  if (M < 0 || N < 0 || K < 0) return ERR_SHAPE_MISMATCH;
+  lin_ctx a = {x, w, b, y, N, K, sxm, sxk, swn, swk, sym, syn};
+  launch(linear_program, &a, M, pb, pe);
+  return OK;
+}
+
+/* ── teeny-quant affine quantization ─────────────────────────────────────
+ * utilities/teeny-quant/src/quant/affine.rs:47-161 and groups.rs:20-100.
+ * Rust semantics restated: f32::round rounds half away from zero; `as i32`
+ * saturates and maps NaN to 0; min/max of f32 via `<`/`>` comparisons. */
+
+enum { PER_TENSOR = 0, PER_CHANNEL = 1, GROUP = 2 };
+
+static int32_t rust_f32_as_i32(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483648.0f) return INT32_MAX;
+  if (v <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)v;
+}
+
+static float rust_round(float v) { return roundf(v); /* C roundf: half away from zero */ }
+
+static void row_major_strides(const int64_t *shape, int ndim, int64_t *strides) {
+  if (ndim == 0) return;
+  strides[ndim - 1] = 1;
+  for (int i = ndim - 2; i >= 0; --i) strides[i] = strides[i + 1] * shape[i + 1];
+}
+
+/* groups.rs:78-100 (assign_groups) restated per element. */
+static int64_t group_of(int64_t flat, const int64_t *shape, const int64_t *strides, int ndim,
+                        int gran, int axis, int64_t group_size) {
+  if (gran == PER_TENSOR) return 0;
+  int64_t idx_axis = (flat / strides[axis]) % shape[axis];
+  if (gran == PER_CHANNEL) return idx_axis;
+  /* group_wise_id (groups.rs:51-63): outer id over the other axes, last axis fastest. */
+  int64_t outer = 0, mult = 1;
+  for (int d = ndim - 1; d >= 0; --d) {
+    if (d == axis) continue;
+    int64_t idx_d = (flat / strides[d]) % shape[d];
+    outer += idx_d * mult;
+    mult *= shape[d];
+  }
+  int64_t along = (shape[axis] + group_size - 1) / group_size;
+  return outer * along + idx_axis / group_size;
+}
+
+int oracle_quant_num_groups(const int64_t *shape, int ndim, int gran, int axis,
+                            int64_t group_size, int64_t *ngroups) {
+  if (gran == PER_TENSOR) {
+    *ngroups = 1;
+    return OK;
+  }
+  if (axis < 0 || axis >= ndim) return ERR_INVALID_AXIS;
+  if (gran == PER_CHANNEL) {
+    *ngroups = shape[axis];
+    return OK;
+  }
+  if (group_size == 0) return ERR_INVALID_GROUP_SIZE;
+  int64_t outer = 1;
+  for (int d = 0; d < ndim; ++d)
+    if (d != axis) outer *= shape[d];
+  *ngroups = outer * ((shape[axis] + group_size - 1) / group_size);
+  return OK;
+}
+
+int oracle_quantize_affine(const float *data, int64_t n_data, const int64_t *shape, int ndim,
+                           int gran, int axis, int64_t group_size, int symmetric, int bits,
+                           int8_t *qvalues, float *scales, int32_t *zero_points,
+                           uint32_t *groups) {
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) n *= shape[d];
+  if (n_data != n) return ERR_SHAPE_MISMATCH; /* affine.rs:63-70 */
+  if (gran != PER_TENSOR) {
+    if (axis < 0 || axis >= ndim) return ERR_INVALID_AXIS;                /* :73-80 */
+    if (gran == GROUP && group_size == 0) return ERR_INVALID_GROUP_SIZE; /* :81-83 */
+  }
+  if (bits < 2 || bits > 8) return ERR_INVALID_ARGUMENT;
+  const int32_t qmax = (1 << (bits - 1)) - 1;           /* qrange, :47-51 */
+  const int32_t qmin = symmetric ? -qmax : -qmax - 1;
+  int64_t ngroups = 0;
+  int rc = oracle_quant_num_groups(shape, ndim, gran, axis, gran == PER_CHANNEL ? 1 : group_size,
+                                   &ngroups);
+  if (rc != OK) return rc;
+  int64_t strides[16];
+  if (ndim > 16) return ERR_INVALID_ARGUMENT;
+  row_major_strides(shape, ndim, strides);
+  float *vmin = (float *)malloc(sizeof(float) * (size_t)(ngroups > 0 ? ngroups : 1));
+  float *vmax = (float *)malloc(sizeof(float) * (size_t)(ngroups > 0 ? ngroups : 1));
+  for (int64_t g = 0; g < ngroups; ++g) {
+    vmin[g] = INFINITY;
+    vmax[g] = -INFINITY;
+  }
+  /* pass 1: per-group min/max (:90-101) */
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t g = group_of(i, shape, strides, ndim, gran, axis, group_size);
+    if (groups != NULL) groups[i] = (uint32_t)g;
+    float x = data[i];
+    if (x < vmin[g]) vmin[g] = x;
+    if (x > vmax[g]) vmax[g] = x;
+  }
+  /* params (:103-132) */
+  for (int64_t g = 0; g < ngroups; ++g) {
+    float lo, hi;
+    if (isfinite(vmin[g])) {
+      lo = fminf(vmin[g], 0.0f);
+      hi = fmaxf(vmax[g], 0.0f);
+    } else {
+      lo = 0.0f;
+      hi = 0.0f;
+    }
+    if (symmetric) {
+      float amax = fmaxf(fabsf(lo), fabsf(hi));
+      scales[g] = amax == 0.0f ? 1.0f : amax / (float)qmax;
+      zero_points[g] = 0;
+    } else {
+      float scale = hi == lo ? 1.0f : (hi - lo) / (float)(qmax - qmin);
+      int32_t zp = rust_f32_as_i32(rust_round((float)qmin - lo / scale));
+      scales[g] = scale;
+      zero_points[g] = zp < qmin ? qmin : zp > qmax ? qmax : zp;
+    }
+  }
+  /* pass 2: q = clamp(round(x / scale) as i32 + zp, qmin, qmax) (:134-142) */
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t g = group_of(i, shape, strides, ndim, gran, axis, group_size);
+    int64_t q = (int64_t)rust_f32_as_i32(rust_round(data[i] / scales[g])) + zero_points[g];
+    /* i32 add in Rust: wrapping is impossible here because |zp| <= 128 and
+     * the saturated value is at most i32::MAX; widen to keep C defined. */
+    if (q > INT32_MAX) q = INT32_MAX; /* unreachable for finite scales */
+    qvalues[i] = (int8_t)(q < qmin ? qmin : q > qmax ? qmax : q);
+  }
+  free(vmin);
+  free(vmax);
+  return OK;
+}
+
+/* dequantize_affine (affine.rs:151-161): (v as i32 - zp) as f32 * scale. */
+int oracle_dequantize_affine(const int8_t *q, const float *scales, const int32_t *zero_points,
+                             const int64_t *shape, int ndim, int gran, int axis,
+                             int64_t group_size, float *out) {
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) n *= shape[d];
+  if (gran != PER_TENSOR && (axis < 0 || axis >= ndim)) return ERR_INVALID_AXIS;
+  if (gran == GROUP && group_size == 0) return ERR_INVALID_GROUP_SIZE;
+  int64_t strides[16];
+  if (ndim > 16) return ERR_INVALID_ARGUMENT;
+  row_major_strides(shape, ndim, strides);
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t g = group_of(i, shape, strides, ndim, gran, axis, group_size);
+    int32_t zp = zero_points != NULL ? zero_points[g] : 0;
+    out[i] = (float)((int32_t)q[i] - zp) * scales[g];
+  }
+  return OK;
+}

@@ -1,0 +1,127 @@
+// Elementwise activations: relu / gelu-tanh / silu, fp32 and bf16.
+//
+// Reference kernels (one BLOCK_SIZE-element tile per program id, masked tail):
+//   relu_forward  kernels/teeny-kernels/src/nn/activation/relu.rs:27-64
+//   gelu_forward  kernels/teeny-kernels/src/nn/activation/gelu.rs:31-78
+//   silu_forward  kernels/teeny-kernels/src/nn/activation/sigmoid.rs:119-158
+//
+// MI355X design: the op moves 2 bytes in and 2 out per bf16 element with a
+// handful of VALU ops, so it is bound by HBM.  Each thread moves UNROLL
+// 16-byte vectors with all loads issued before any math (bytes in flight per
+// wave = UNROLL * 1 KiB), lanes of a wave touch consecutive 16-byte chunks so
+// every load instruction is one fully coalesced 1 KiB request, and the grid
+// has one workgroup per UNROLL*4 KiB so that a [16384, 4096] bf16 tensor
+// spreads 8192 workgroups over the 256 CUs.  Unaligned pointers or a ragged
+// tail take a scalar kernel.
+#include "common.hpp"
+
+namespace teeny {
+
+constexpr int kActThreads = 256;
+constexpr int kActUnroll = 4;
+
+template <typename T, int ACT>
+__device__ __forceinline__ T act_one(T v) {
+  constexpr bool fast = !std::is_same<T, float>::value;
+  return from_f32<T>(apply_act<ACT, fast>(to_f32(v)));
+}
+
+// x and y may alias: every element is read and written by the same thread.
+template <typename T, int ACT>
+__global__ __launch_bounds__(kActThreads) void act_vec_kernel(const T *x, T *y, int64_t n_vec) {
+  constexpr int VEC = 16 / sizeof(T);
+  typedef u32x4 raw_t;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kActThreads * kActUnroll) + threadIdx.x;
+  raw_t r[kActUnroll];
+#pragma unroll
+  for (int u = 0; u < kActUnroll; ++u) {
+    int64_t v = base + u * kActThreads;
+    if (v < n_vec) r[u] = reinterpret_cast<const raw_t *>(x)[v];
+  }
+#pragma unroll
+  for (int u = 0; u < kActUnroll; ++u) {
+    int64_t v = base + u * kActThreads;
+    if (v < n_vec) {
+      T e[VEC];
+      __builtin_memcpy(e, &r[u], 16);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) e[i] = act_one<T, ACT>(e[i]);
+      __builtin_memcpy(&r[u], e, 16);
+      reinterpret_cast<raw_t *>(y)[v] = r[u];
+    }
+  }
+}
+
+template <typename T, int ACT>
+__global__ __launch_bounds__(kActThreads) void act_scalar_kernel(const T *x, T *y, int64_t begin,
+                                                                 int64_t n) {
+  int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kActThreads + threadIdx.x;
+  if (i < n) y[i] = act_one<T, ACT>(x[i]);
+}
+
+template <typename T, int ACT>
+static teeny_status launch_act(const void *xv, void *yv, int64_t n, hipStream_t s,
+                               const char *name) {
+  const T *x = static_cast<const T *>(xv);
+  T *y = static_cast<T *>(yv);
+  constexpr int VEC = 16 / sizeof(T);
+  int64_t done = 0;
+  if (aligned(x, 16) && aligned(y, 16)) {
+    int64_t n_vec = n / VEC;
+    if (n_vec > 0) {
+      int64_t blocks = cdiv(n_vec, kActThreads * kActUnroll);
+      TEENY_REQUIRE(blocks <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, "tensor too large");
+      hipLaunchKernelGGL((act_vec_kernel<T, ACT>), dim3(blocks), dim3(kActThreads), 0, s, x, y,
+                         n_vec);
+      teeny_status st = after_launch(name, s);
+      if (st != TEENY_OK) return st;
+    }
+    done = n_vec * VEC;
+  }
+  if (done < n) {
+    int64_t blocks = cdiv(n - done, kActThreads);
+    TEENY_REQUIRE(blocks <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, "tensor too large");
+    hipLaunchKernelGGL((act_scalar_kernel<T, ACT>), dim3(blocks), dim3(kActThreads), 0, s, x, y,
+                       done, n);
+    return after_launch(name, s);
+  }
+  return TEENY_OK;
+}
+
+template <int ACT>
+static teeny_status act_entry(const void *x, void *y, int64_t n, teeny_dtype dtype,
+                              teeny_stream stream, const char *name) {
+  TEENY_REQUIRE(n >= 0, TEENY_ERR_SHAPE_MISMATCH, std::string(name) + ": n_elements < 0");
+  if (n == 0) return TEENY_OK;
+  TEENY_REQUIRE(x != nullptr && y != nullptr, TEENY_ERR_NULL_POINTER, std::string(name) + ": x/y");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TEENY_F32: return launch_act<float, ACT>(x, y, n, s, name);
+    case TEENY_BF16: return launch_act<bf16, ACT>(x, y, n, s, name);
+    default:
+      return fail(TEENY_ERR_UNSUPPORTED_DTYPE, std::string(name) + ": dtype must be F32 or BF16");
+  }
+}
+
+}  // namespace teeny
+
+using namespace teeny;
+
+extern "C" {
+
+teeny_status teeny_relu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream) {
+  return act_entry<TEENY_ACT_RELU>(x, y, n_elements, dtype, stream, "relu_forward");
+}
+
+teeny_status teeny_gelu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream) {
+  return act_entry<TEENY_ACT_GELU_TANH>(x, y, n_elements, dtype, stream, "gelu_forward");
+}
+
+teeny_status teeny_silu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
+                                teeny_stream stream) {
+  return act_entry<TEENY_ACT_SILU>(x, y, n_elements, dtype, stream, "silu_forward");
+}
+
+}  // extern "C"

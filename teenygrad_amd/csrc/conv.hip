@@ -1,0 +1,294 @@
+// conv2d forward (+ bias, + fused activation), and the W8A16 int8-weight conv.
+//
+// Reference: conv2d_forward / conv2d_bias_forward,
+// kernels/teeny-kernels/src/nn/conv/conv2d.rs:43-156 and :642-764 — NCHW,
+// weight [C_OUT, C_IN/G, KH, KW], zero padding by masked loads (:108-127),
+// accumulation over the flat (c_in_local, kh, kw) loop (:97-146), bias added
+// after the loop (:740-753).
+//
+// Two kernel families:
+//
+// conv_direct: any dtype, NCHW or NHWC (strided addressing), any groups.
+//   One thread per output pixel and COB output channels of one group;
+//   weights are read with workgroup-uniform addresses (scalar loads,
+//   broadcast), the accumulation order is the reference's (c_in_local,
+//   kh, kw).  This is the fp32 NCHW path (the reference's own config) and the
+//   fallback for shapes the MFMA path does not take.
+//
+// implicit GEMM (gemm_core.hpp): NHWC bf16 with groups == 1.  M = B*OH*OW
+//   output pixels, N = C_OUT, K = KH*KW*C_IN; weights [C_OUT, KH, KW, C_IN]
+//   are a plain K-contiguous [N, K] matrix and the activation tile is
+//   gathered from NHWC in 16-byte chunks (C_IN % 8 == 0) or element-wise
+//   (e.g. the 3-channel stem).  1x1 stride-1 unpadded convs are plain GEMMs.
+//   int8 weights (W8A16) are converted to bf16 while staging into LDS and
+//   the per-channel scale is applied to the fp32 accumulator.
+#include "gemm_core.hpp"
+
+namespace teeny {
+
+struct ConvGeo {
+  int B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G;
+  int64_t xs[4];  // strides of x in (b, c, h, w)
+  int64_t ys[4];  // strides of y in (b, c, h, w)
+  int64_t ws[4];  // strides of w in (co, ci_local, kh, kw)
+};
+
+template <typename WT> __device__ __forceinline__ float wload(const WT *w, int64_t i) {
+  return to_f32(w[i]);
+}
+template <> __device__ __forceinline__ float wload<int8_t>(const int8_t *w, int64_t i) {
+  return static_cast<float>(w[i]);
+}
+
+template <typename T, typename WT, int COB, int ACT>
+__global__ __launch_bounds__(64) void conv_direct(const T *__restrict__ x, const WT *__restrict__ w,
+                                                  const float *__restrict__ wscale,
+                                                  const T *__restrict__ bias_t,
+                                                  const float *__restrict__ bias_f,
+                                                  T *__restrict__ y, ConvGeo q) {
+  constexpr bool fast = !std::is_same<T, float>::value;
+  const int64_t pix = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t npix = static_cast<int64_t>(q.B) * q.OH * q.OW;
+  const int co0 = blockIdx.y * COB;
+  const int cin_g = q.Cin / q.G;
+  const int g_idx = co0 / (q.Cout / q.G);
+  const int ci0 = g_idx * cin_g;
+  const bool valid = pix < npix;
+  const int64_t pp = valid ? pix : 0;
+  const int ow = static_cast<int>(pp % q.OW);
+  const int oh = static_cast<int>((pp / q.OW) % q.OH);
+  const int b = static_cast<int>(pp / (static_cast<int64_t>(q.OW) * q.OH));
+  const T *xb = x + b * q.xs[0];
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = 0.0f;
+  for (int cl = 0; cl < cin_g; ++cl) {
+    const T *xc = xb + static_cast<int64_t>(ci0 + cl) * q.xs[1];
+    for (int kh = 0; kh < q.KH; ++kh) {
+      const int ih = oh * q.SH + kh - q.PH;
+      const bool hok = ih >= 0 && ih < q.H;
+      for (int kw = 0; kw < q.KW; ++kw) {
+        const int iw = ow * q.SW + kw - q.PW;
+        const float xv = (valid && hok && iw >= 0 && iw < q.W)
+                             ? to_f32(xc[ih * q.xs[2] + iw * q.xs[3]])
+                             : 0.0f;
+        const int64_t wo = cl * q.ws[1] + kh * q.ws[2] + kw * q.ws[3];
+#pragma unroll
+        for (int j = 0; j < COB; ++j) {
+          float wv = wload(w, (co0 + j) * q.ws[0] + wo);
+          if (wscale != nullptr) wv = wv * wscale[co0 + j];  // dequantize_affine: q * scale
+          acc[j] = acc[j] + xv * wv;
+        }
+      }
+    }
+  }
+  if (!valid) return;
+#pragma unroll
+  for (int j = 0; j < COB; ++j) {
+    const int co = co0 + j;
+    float r = acc[j];
+    if (bias_t != nullptr) r = r + to_f32(bias_t[co]);
+    if (bias_f != nullptr) r = r + bias_f[co];
+    y[b * q.ys[0] + co * q.ys[1] + oh * q.ys[2] + ow * q.ys[3]] = from_f32<T>(apply_act<ACT, fast>(r));
+  }
+}
+
+template <typename T, typename WT, int ACT>
+static void launch_direct_act(const T *x, const WT *w, const float *wscale, const T *bias_t,
+                              const float *bias_f, T *y, const ConvGeo &q, hipStream_t s) {
+  const int64_t npix = static_cast<int64_t>(q.B) * q.OH * q.OW;
+  const int cout_g = q.Cout / q.G;
+  const dim3 blk(64);
+  if (cout_g % 8 == 0) {
+    hipLaunchKernelGGL((conv_direct<T, WT, 8, ACT>), dim3(cdiv(npix, 64), q.Cout / 8), blk, 0, s,
+                       x, w, wscale, bias_t, bias_f, y, q);
+  } else if (cout_g % 4 == 0) {
+    hipLaunchKernelGGL((conv_direct<T, WT, 4, ACT>), dim3(cdiv(npix, 64), q.Cout / 4), blk, 0, s,
+                       x, w, wscale, bias_t, bias_f, y, q);
+  } else {
+    hipLaunchKernelGGL((conv_direct<T, WT, 1, ACT>), dim3(cdiv(npix, 64), q.Cout), blk, 0, s, x,
+                       w, wscale, bias_t, bias_f, y, q);
+  }
+}
+
+template <typename T, typename WT>
+static void launch_direct(const T *x, const WT *w, const float *wscale, const T *bias_t,
+                          const float *bias_f, T *y, const ConvGeo &q, int act, hipStream_t s) {
+  switch (act) {
+    case TEENY_ACT_RELU: launch_direct_act<T, WT, TEENY_ACT_RELU>(x, w, wscale, bias_t, bias_f, y, q, s); break;
+    case TEENY_ACT_GELU_TANH: launch_direct_act<T, WT, TEENY_ACT_GELU_TANH>(x, w, wscale, bias_t, bias_f, y, q, s); break;
+    case TEENY_ACT_SILU: launch_direct_act<T, WT, TEENY_ACT_SILU>(x, w, wscale, bias_t, bias_f, y, q, s); break;
+    default: launch_direct_act<T, WT, TEENY_ACT_NONE>(x, w, wscale, bias_t, bias_f, y, q, s); break;
+  }
+}
+
+// Validates geometry (conv2d.rs:28-42 shape rules) and fills strides for the layout.
+static teeny_status make_geo(int64_t B, int64_t Cin, int64_t Cout, int64_t H, int64_t W,
+                             int64_t OH, int64_t OW, const teeny_conv2d_params *prm,
+                             teeny_layout layout, ConvGeo *q, const char *name) {
+  const std::string n(name);
+  TEENY_REQUIRE(prm != nullptr, TEENY_ERR_NULL_POINTER, n + ": params");
+  TEENY_REQUIRE(B >= 0 && Cin > 0 && Cout > 0 && H > 0 && W > 0 && OH >= 0 && OW >= 0,
+                TEENY_ERR_SHAPE_MISMATCH, n + ": non-positive dimension");
+  TEENY_REQUIRE(prm->KH > 0 && prm->KW > 0 && prm->stride_h > 0 && prm->stride_w > 0 &&
+                    prm->pad_h >= 0 && prm->pad_w >= 0 && prm->groups > 0,
+                TEENY_ERR_INVALID_ARGUMENT, n + ": kernel/stride/pad/groups out of range");
+  TEENY_REQUIRE(Cin % prm->groups == 0 && Cout % prm->groups == 0, TEENY_ERR_SHAPE_MISMATCH,
+                n + ": channels not divisible by groups");
+  TEENY_REQUIRE(OH == (H + 2 * prm->pad_h - prm->KH) / prm->stride_h + 1 &&
+                    OW == (W + 2 * prm->pad_w - prm->KW) / prm->stride_w + 1 &&
+                    H + 2 * prm->pad_h >= prm->KH && W + 2 * prm->pad_w >= prm->KW,
+                TEENY_ERR_SHAPE_MISMATCH,
+                n + ": OH/OW do not match (H + 2*pad - K) / stride + 1");
+  TEENY_REQUIRE(layout == TEENY_NCHW || layout == TEENY_NHWC, TEENY_ERR_INVALID_ARGUMENT,
+                n + ": unknown layout");
+  TEENY_REQUIRE(prm->act >= TEENY_ACT_NONE && prm->act <= TEENY_ACT_SILU,
+                TEENY_ERR_INVALID_ARGUMENT, n + ": unknown activation");
+  TEENY_REQUIRE(B * H * W * Cin < (1ll << 40) && B * OH * OW * Cout < (1ll << 40) &&
+                    B * OH * OW <= 0x7fffffff && Cout <= 0x7fffffff,
+                TEENY_ERR_SHAPE_MISMATCH, n + ": tensor too large");
+  q->B = static_cast<int>(B);
+  q->Cin = static_cast<int>(Cin);
+  q->Cout = static_cast<int>(Cout);
+  q->H = static_cast<int>(H);
+  q->W = static_cast<int>(W);
+  q->OH = static_cast<int>(OH);
+  q->OW = static_cast<int>(OW);
+  q->KH = prm->KH;
+  q->KW = prm->KW;
+  q->SH = prm->stride_h;
+  q->SW = prm->stride_w;
+  q->PH = prm->pad_h;
+  q->PW = prm->pad_w;
+  q->G = prm->groups;
+  const int64_t cg = Cin / prm->groups;
+  if (layout == TEENY_NCHW) {
+    q->xs[0] = Cin * H * W; q->xs[1] = H * W; q->xs[2] = W; q->xs[3] = 1;
+    q->ys[0] = Cout * OH * OW; q->ys[1] = OH * OW; q->ys[2] = OW; q->ys[3] = 1;
+    q->ws[0] = cg * prm->KH * prm->KW; q->ws[1] = prm->KH * prm->KW; q->ws[2] = prm->KW; q->ws[3] = 1;
+  } else {
+    q->xs[0] = H * W * Cin; q->xs[1] = 1; q->xs[2] = W * Cin; q->xs[3] = Cin;
+    q->ys[0] = OH * OW * Cout; q->ys[1] = 1; q->ys[2] = OW * Cout; q->ys[3] = Cout;
+    q->ws[0] = prm->KH * prm->KW * cg; q->ws[1] = 1; q->ws[2] = prm->KW * cg; q->ws[3] = cg;
+  }
+  return TEENY_OK;
+}
+
+static GemmParams conv_gemm_params(const void *x, const void *w, const float *scale,
+                                   const float *bias, const bf16 *bias_bf16, void *y,
+                                   const ConvGeo &q) {
+  GemmParams p{};
+  p.A = static_cast<const bf16 *>(x);
+  p.lda = q.Cin;
+  p.B = w;
+  p.ldb = static_cast<int64_t>(q.KH) * q.KW * q.Cin;
+  p.C = static_cast<bf16 *>(y);
+  p.ldc = q.Cout;
+  p.scale = scale;
+  p.bias = bias;
+  p.bias_bf16 = bias_bf16;
+  p.M = q.B * q.OH * q.OW;
+  p.N = q.Cout;
+  p.K = q.KH * q.KW * q.Cin;
+  p.H = q.H; p.W = q.W; p.Cin = q.Cin; p.OH = q.OH; p.OW = q.OW;
+  p.KH = q.KH; p.KW = q.KW; p.SH = q.SH; p.SW = q.SW; p.PH = q.PH; p.PW = q.PW;
+  return p;
+}
+
+// bf16 NHWC, groups == 1 -> MFMA implicit GEMM.  Returns false if not taken.
+template <bool INT8B>
+static bool try_conv_mfma(const void *x, const void *w, const float *scale, const float *bias,
+                          const bf16 *bias_bf16, void *y, const ConvGeo &q, int act,
+                          hipStream_t s) {
+  if (q.G != 1 || q.B == 0) return false;
+  if (!aligned(x, 16) || !aligned(w, 16)) return false;
+  GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
+  const bool one_by_one = q.KH == 1 && q.KW == 1 && q.SH == 1 && q.SW == 1 && q.PH == 0 && q.PW == 0;
+  if (INT8B) {
+    // 16-byte int8 chunks: C_IN must be a multiple of 16.
+    if (q.Cin % 16 != 0) return false;
+    return one_by_one ? launch_gemm_mfma<true, kAPlain>(p, act, s)
+                      : launch_gemm_mfma<true, kAConvVec>(p, act, s);
+  }
+  if (q.Cin % 8 == 0) {
+    return one_by_one ? launch_gemm_mfma<false, kAPlain>(p, act, s)
+                      : launch_gemm_mfma<false, kAConvVec>(p, act, s);
+  }
+  return launch_gemm_mfma<false, kAConvScalar>(p, act, s);
+}
+
+static teeny_status conv_entry(const void *x, const void *w, const void *bias, void *y, int64_t B,
+                               int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH,
+                               int64_t OW, const teeny_conv2d_params *prm, teeny_dtype dtype,
+                               teeny_layout layout, teeny_stream stream, const char *name) {
+  ConvGeo q;
+  teeny_status st = make_geo(B, Cin, Cout, H, W, OH, OW, prm, layout, &q, name);
+  if (st != TEENY_OK) return st;
+  if (B == 0) return TEENY_OK;
+  TEENY_REQUIRE(x != nullptr && w != nullptr && y != nullptr, TEENY_ERR_NULL_POINTER,
+                std::string(name) + ": x/w/y");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TEENY_F32) {
+    launch_direct<float, float>(static_cast<const float *>(x), static_cast<const float *>(w),
+                                nullptr, static_cast<const float *>(bias), nullptr,
+                                static_cast<float *>(y), q, prm->act, s);
+    return after_launch(name, s);
+  }
+  if (dtype == TEENY_BF16) {
+    if (!(layout == TEENY_NHWC &&
+          try_conv_mfma<false>(x, w, nullptr, nullptr, static_cast<const bf16 *>(bias), y, q,
+                               prm->act, s))) {
+      launch_direct<bf16, bf16>(static_cast<const bf16 *>(x), static_cast<const bf16 *>(w),
+                                nullptr, static_cast<const bf16 *>(bias), nullptr,
+                                static_cast<bf16 *>(y), q, prm->act, s);
+    }
+    return after_launch(name, s);
+  }
+  return fail(TEENY_ERR_UNSUPPORTED_DTYPE, std::string(name) + ": dtype must be F32 or BF16");
+}
+
+}  // namespace teeny
+
+using namespace teeny;
+
+extern "C" {
+
+teeny_status teeny_conv2d_forward(const void *x, const void *w, void *y, int64_t B, int64_t C_IN,
+                                  int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                  const teeny_conv2d_params *params, teeny_dtype dtype,
+                                  teeny_layout layout, teeny_stream stream) {
+  return conv_entry(x, w, nullptr, y, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
+                    "conv2d_forward");
+}
+
+teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void *bias, void *y,
+                                       int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H,
+                                       int64_t W, int64_t OH, int64_t OW,
+                                       const teeny_conv2d_params *params, teeny_dtype dtype,
+                                       teeny_layout layout, teeny_stream stream) {
+  TEENY_REQUIRE(bias != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_bias_forward: bias");
+  return conv_entry(x, w, bias, y, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
+                    "conv2d_bias_forward");
+}
+
+teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, const float *scale,
+                                        const float *bias, void *y, int64_t B, int64_t C_IN,
+                                        int64_t C_OUT, int64_t H, int64_t W, int64_t OH,
+                                        int64_t OW, const teeny_conv2d_params *params,
+                                        teeny_stream stream) {
+  const char *name = "w8a16_conv2d_forward";
+  ConvGeo q;
+  teeny_status st = make_geo(B, C_IN, C_OUT, H, W, OH, OW, params, TEENY_NHWC, &q, name);
+  if (st != TEENY_OK) return st;
+  if (B == 0) return TEENY_OK;
+  TEENY_REQUIRE(x != nullptr && qweight != nullptr && scale != nullptr && y != nullptr,
+                TEENY_ERR_NULL_POINTER, "w8a16_conv2d_forward: x/qweight/scale/y");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!try_conv_mfma<true>(x, qweight, scale, bias, nullptr, y, q, params->act, s)) {
+    launch_direct<bf16, int8_t>(static_cast<const bf16 *>(x), qweight, scale, nullptr, bias,
+                                static_cast<bf16 *>(y), q, params->act, s);
+  }
+  return after_launch(name, s);
+}
+
+}  // extern "C"

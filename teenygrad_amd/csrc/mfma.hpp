@@ -1,0 +1,45 @@
+// gfx950 MFMA fragment conventions used by the attention, GEMM and conv kernels.
+//
+// v_mfma_f32_32x32x16_bf16 (one wave64):  D[32x32] += A[32x16] * B[16x32]
+//   A: lane l holds A[l % 32][8 * (l / 32) + j], j = 0..7   (bf16x8)
+//   B: lane l holds B[8 * (l / 32) + j][l % 32], j = 0..7   (bf16x8)
+//   D: lane l holds D[8 * (v / 4) + 4 * (l / 32) + (v % 4)][l % 32], v = 0..15
+// Only the D layout matters for correctness of a kernel that builds A and B
+// with the same k assignment: the k order inside one instruction is a
+// permutation shared by A and B and cancels in the sum.
+#pragma once
+
+#include "common.hpp"
+
+namespace teeny {
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row of the D fragment held in register v by lane group g = lane / 32.
+__device__ __forceinline__ constexpr int mfma32_row(int v, int g) {
+  return 8 * (v >> 2) + 4 * g + (v & 3);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// Concatenates two 4-element bf16 vectors (two 8-byte LDS reads) into one operand.
+__device__ __forceinline__ bf16x8 cat8(bf16x4 lo, bf16x4 hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Packs two bf16 bit patterns (low halves of a and b) into one 32-bit word.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+
+}  // namespace teeny

@@ -1,0 +1,276 @@
+// LayerNorm (inference) and RMSNorm over the last dimension of [M, N].
+//
+// Reference kernels (one program per row, BLOCK_N-wide tiles):
+//   layer_norm_forward_inference  kernels/teeny-kernels/src/nn/norm/layernorm.rs:42-157
+//     three passes over the row: mean (:61-77), variance of (x - mean) (:79-100),
+//     normalise + affine (:102-156).
+//   rms_norm_forward              kernels/teeny-kernels/src/nn/norm/rmsnorm.rs:39-119
+//     two passes: sum of squares (:58-79) and rrms store (:80-83), normalise (:85-118).
+//
+// MI355X design: one wave64 owns one row.  For N <= 64 * VEC * 16 the whole
+// row is held in registers (VEC = 8 bf16 or 4 fp32 per 16-byte load), so x
+// is read from HBM exactly once and y written once: the 4-tensor-pass
+// reference becomes the 2-pass minimum with the same two-pass mean/variance
+// arithmetic done on registers.  Reductions are wave shuffles (no LDS, no
+// barriers).  Lane l of the wave loads columns [(j*64 + l)*VEC, +VEC) for
+// j < VPL, so each load instruction is one contiguous 1 KiB request.
+// gamma/beta are loaded once per wave and reused for every row the wave
+// handles (rows are strided over the grid).  Longer rows, unaligned
+// pointers or N % VEC != 0 take a multi-pass kernel with the reference's
+// pass structure.
+#include "common.hpp"
+
+namespace teeny {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormWaves = kNormThreads / 64;
+constexpr int kNormMaxBlocks = 256 * 8;
+
+template <typename T, int VPL, bool RMS, int ACT>
+__global__ __launch_bounds__(kNormThreads) void norm_reg_kernel(
+    const T *__restrict__ x, T *__restrict__ y, const T *__restrict__ gamma,
+    const T *__restrict__ beta, float *__restrict__ rrms, int64_t M, int32_t N, float eps,
+    float inv_n) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr bool fast = !std::is_same<T, float>::value;
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kNormWaves;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+
+  float g[VPL][VEC], b[VPL][VEC];
+  bool valid[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int col = (j * 64 + lane) * VEC;
+    valid[j] = col < N;
+    if (valid[j]) {
+      u32x4 rg = *reinterpret_cast<const u32x4 *>(gamma + col);
+      T eg[VEC];
+      __builtin_memcpy(eg, &rg, 16);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) g[j][i] = to_f32(eg[i]);
+      if constexpr (!RMS) {
+        u32x4 rb = *reinterpret_cast<const u32x4 *>(beta + col);
+        T eb[VEC];
+        __builtin_memcpy(eb, &rb, 16);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) b[j][i] = to_f32(eb[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) g[j][i] = b[j][i] = 0.0f;
+    }
+  }
+
+  for (; row < M; row += nwaves) {
+    const T *xr = x + row * N;
+    T *yr = y + row * N;
+    u32x4 raw[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int col = (j * 64 + lane) * VEC;
+      if (valid[j]) raw[j] = *reinterpret_cast<const u32x4 *>(xr + col);
+    }
+    float v[VPL][VEC];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      T e[VEC];
+      __builtin_memcpy(e, &raw[j], 16);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[j][i] = valid[j] ? to_f32(e[i]) : 0.0f;
+    }
+
+    float mean = 0.0f, rstd;
+    if constexpr (RMS) {
+      float q = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) q += v[j][i] * v[j][i];
+      q = wave_sum(q);
+      rstd = rsqrtf(q * inv_n + eps);
+      if (rrms != nullptr && lane == 0) rrms[row] = rstd;
+    } else {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) s += v[j][i];
+      s = wave_sum(s);
+      mean = s * inv_n;
+      float q = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        if (valid[j]) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            float d = v[j][i] - mean;
+            q += d * d;
+          }
+        }
+      }
+      q = wave_sum(q);
+      rstd = rsqrtf(q * inv_n + eps);
+    }
+
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (!valid[j]) continue;
+      const int col = (j * 64 + lane) * VEC;
+      T e[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float o = RMS ? v[j][i] * rstd * g[j][i] : (v[j][i] - mean) * rstd * g[j][i] + b[j][i];
+        e[i] = from_f32<T>(apply_act<ACT, fast>(o));
+      }
+      u32x4 r;
+      __builtin_memcpy(&r, e, 16);
+      *reinterpret_cast<u32x4 *>(yr + col) = r;
+    }
+  }
+}
+
+// Any N, any alignment: the reference's multi-pass structure, one wave per row.
+template <typename T, bool RMS, int ACT>
+__global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
+    const T *__restrict__ x, T *__restrict__ y, const T *__restrict__ gamma,
+    const T *__restrict__ beta, float *__restrict__ rrms, int64_t M, int64_t N, float eps,
+    float inv_n) {
+  constexpr bool fast = !std::is_same<T, float>::value;
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kNormWaves;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + (threadIdx.x >> 6); row < M;
+       row += nwaves) {
+    const T *xr = x + row * N;
+    T *yr = y + row * N;
+    float mean = 0.0f, rstd;
+    if constexpr (RMS) {
+      float q = 0.0f;
+      for (int64_t c = lane; c < N; c += 64) {
+        float v = to_f32(xr[c]);
+        q += v * v;
+      }
+      q = wave_sum(q);
+      rstd = rsqrtf(q * inv_n + eps);
+      if (rrms != nullptr && lane == 0) rrms[row] = rstd;
+    } else {
+      float s = 0.0f;
+      for (int64_t c = lane; c < N; c += 64) s += to_f32(xr[c]);
+      s = wave_sum(s);
+      mean = s * inv_n;
+      float q = 0.0f;
+      for (int64_t c = lane; c < N; c += 64) {
+        float d = to_f32(xr[c]) - mean;
+        q += d * d;
+      }
+      q = wave_sum(q);
+      rstd = rsqrtf(q * inv_n + eps);
+    }
+    for (int64_t c = lane; c < N; c += 64) {
+      float v = to_f32(xr[c]);
+      float o = RMS ? v * rstd * to_f32(gamma[c])
+                    : (v - mean) * rstd * to_f32(gamma[c]) + to_f32(beta[c]);
+      yr[c] = from_f32<T>(apply_act<ACT, fast>(o));
+    }
+  }
+}
+
+template <typename T, int VPL, bool RMS, int ACT>
+static void launch_reg(const void *x, void *y, const void *g, const void *b, float *rrms, int64_t M,
+                       int64_t N, float eps, float inv_n, int blocks, hipStream_t s) {
+  hipLaunchKernelGGL((norm_reg_kernel<T, VPL, RMS, ACT>), dim3(blocks), dim3(kNormThreads), 0, s,
+                     static_cast<const T *>(x), static_cast<T *>(y), static_cast<const T *>(g),
+                     static_cast<const T *>(b), rrms, M, static_cast<int32_t>(N), eps, inv_n);
+}
+
+template <typename T, bool RMS, int ACT>
+static teeny_status launch_norm(const void *x, void *y, const void *g, const void *b, float *rrms,
+                                int64_t M, int64_t N, float eps, hipStream_t s, const char *name) {
+  constexpr int VEC = 16 / sizeof(T);
+  const float inv_n = 1.0f / static_cast<float>(N);
+  const int blocks = static_cast<int>(std::min<int64_t>(cdiv(M, kNormWaves), kNormMaxBlocks));
+  const bool vec_ok = (N % VEC == 0) && aligned(x, 16) && aligned(y, 16) && aligned(g, 16) &&
+                      (RMS || aligned(b, 16));
+  const int64_t vpl = cdiv(N, 64 * VEC);
+  if (vec_ok && vpl <= 16) {
+    if (vpl <= 1) launch_reg<T, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+    else if (vpl <= 2) launch_reg<T, 2, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+    else if (vpl <= 4) launch_reg<T, 4, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+    else if (vpl <= 8) launch_reg<T, 8, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+    else launch_reg<T, 16, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+  } else {
+    hipLaunchKernelGGL((norm_multipass_kernel<T, RMS, ACT>), dim3(blocks), dim3(kNormThreads), 0,
+                       s, static_cast<const T *>(x), static_cast<T *>(y),
+                       static_cast<const T *>(g), static_cast<const T *>(b), rrms, M, N, eps,
+                       inv_n);
+  }
+  return after_launch(name, s);
+}
+
+template <typename T, bool RMS>
+static teeny_status dispatch_act(const void *x, void *y, const void *g, const void *b, float *rrms,
+                                 int64_t M, int64_t N, float eps, int act, hipStream_t s,
+                                 const char *name) {
+  switch (act) {
+    case TEENY_ACT_NONE: return launch_norm<T, RMS, TEENY_ACT_NONE>(x, y, g, b, rrms, M, N, eps, s, name);
+    case TEENY_ACT_RELU: return launch_norm<T, RMS, TEENY_ACT_RELU>(x, y, g, b, rrms, M, N, eps, s, name);
+    case TEENY_ACT_GELU_TANH: return launch_norm<T, RMS, TEENY_ACT_GELU_TANH>(x, y, g, b, rrms, M, N, eps, s, name);
+    case TEENY_ACT_SILU: return launch_norm<T, RMS, TEENY_ACT_SILU>(x, y, g, b, rrms, M, N, eps, s, name);
+    default: return fail(TEENY_ERR_INVALID_ARGUMENT, std::string(name) + ": unknown activation");
+  }
+}
+
+static teeny_status norm_entry(const void *x, void *y, const void *g, const void *b, float *rrms,
+                               int64_t M, int64_t N, float eps, bool rms, int act,
+                               teeny_dtype dtype, teeny_stream stream, const char *name) {
+  const std::string n(name);
+  TEENY_REQUIRE(M >= 0 && N >= 0, TEENY_ERR_SHAPE_MISMATCH, n + ": negative M or N");
+  if (M == 0) return TEENY_OK;
+  TEENY_REQUIRE(N > 0, TEENY_ERR_SHAPE_MISMATCH, n + ": N must be positive");
+  TEENY_REQUIRE(N <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, n + ": N exceeds 2^31-1");
+  TEENY_REQUIRE(x != nullptr && y != nullptr && g != nullptr, TEENY_ERR_NULL_POINTER,
+                n + ": x/y/weight");
+  TEENY_REQUIRE(rms || b != nullptr, TEENY_ERR_NULL_POINTER, n + ": bias");
+  TEENY_REQUIRE(act >= TEENY_ACT_NONE && act <= TEENY_ACT_SILU, TEENY_ERR_INVALID_ARGUMENT,
+                n + ": unknown activation");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TEENY_F32) {
+    return rms ? dispatch_act<float, true>(x, y, g, b, rrms, M, N, eps, act, s, name)
+               : dispatch_act<float, false>(x, y, g, b, rrms, M, N, eps, act, s, name);
+  }
+  if (dtype == TEENY_BF16) {
+    return rms ? dispatch_act<bf16, true>(x, y, g, b, rrms, M, N, eps, act, s, name)
+               : dispatch_act<bf16, false>(x, y, g, b, rrms, M, N, eps, act, s, name);
+  }
+  return fail(TEENY_ERR_UNSUPPORTED_DTYPE, n + ": dtype must be F32 or BF16");
+}
+
+}  // namespace teeny
+
+using namespace teeny;
+
+extern "C" {
+
+teeny_status teeny_layer_norm_forward_inference(const void *x, void *y, const void *weight,
+                                                const void *bias, int64_t M, int64_t N,
+                                                float eps, teeny_dtype dtype,
+                                                teeny_stream stream) {
+  return norm_entry(x, y, weight, bias, nullptr, M, N, eps, false, TEENY_ACT_NONE, dtype, stream,
+                    "layer_norm_forward_inference");
+}
+
+teeny_status teeny_rms_norm_forward(const void *x, void *y, const void *weight, float *rrms,
+                                    int64_t M, int64_t N, float eps, teeny_dtype dtype,
+                                    teeny_stream stream) {
+  return norm_entry(x, y, weight, nullptr, rrms, M, N, eps, true, TEENY_ACT_NONE, dtype, stream,
+                    "rms_norm_forward");
+}
+
+teeny_status teeny_norm_act_forward(const void *x, void *y, const void *weight, const void *bias,
+                                    int64_t M, int64_t N, float eps, int32_t is_rms,
+                                    teeny_activation act, teeny_dtype dtype, teeny_stream stream) {
+  return norm_entry(x, y, weight, bias, nullptr, M, N, eps, is_rms != 0, act, dtype, stream,
+                    "norm_act_forward");
+}
+
+}  // extern "C"

@@ -1,0 +1,655 @@
+"""Host-side mirror of teeny-kernels' operator contract, dispatching to HIP.
+
+Two layers:
+
+* ``RuntimeOp`` subclasses reproduce the reference's per-kernel RuntimeOp
+  impls — ``param_shapes``, ``param_names``, ``pack_args`` (argument kinds and
+  order exactly as the reference visits them), ``grid`` and the
+  ``"{name}_entry_point"`` symbol — and ``launch`` hands the packed list to
+  ``teeny_dispatch`` in place of cuLaunchKernel.  Reference:
+  core/teeny-core/src/model/mod.rs:78-331 (RuntimeOp),
+  core/teeny-core/src/device/program.rs:22-46 (ArgVisitor), the impls cited
+  on each class, and the executor loop that calls them,
+  drivers/teeny-cuda/src/model/mod.rs:524-700.
+
+* Functions (``relu``, ``layer_norm``, ``conv2d``, ``flash_attention`` ...)
+  call the typed entry points of include/teeny_hip.h directly on
+  ``Buffer`` objects, with this library's extensions (bf16, NHWC, causal,
+  fused activations, W8A16).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+from .dtypes import DType, bf16, f32, from_any, i8
+from .runtime import Buffer, Stream, _h
+
+# ── ArgVisitor (core/teeny-core/src/device/program.rs:22-46) ────────────────
+
+
+class ArgVisitor:
+    def visit_ptr(self, ptr): raise NotImplementedError
+    def visit_bool(self, v: bool): raise NotImplementedError
+    def visit_i32(self, v: int): raise NotImplementedError
+    def visit_i64(self, v: int): raise NotImplementedError
+    def visit_u32(self, v: int): raise NotImplementedError
+    def visit_f32(self, v: float): raise NotImplementedError
+    def visit_f64(self, v: float): raise NotImplementedError
+
+
+def _addr(p) -> Optional[int]:
+    if p is None:
+        return None
+    if isinstance(p, Buffer):
+        return p.ptr
+    return int(p)
+
+
+class RecordingVisitor(ArgVisitor):
+    """Records (kind, value) pairs; used to compare packing with the reference."""
+
+    def __init__(self):
+        self.args: List[Tuple[str, object]] = []
+
+    def visit_ptr(self, ptr): self.args.append(("ptr", _addr(ptr)))
+    def visit_bool(self, v): self.args.append(("bool", bool(v)))
+    def visit_i32(self, v): self.args.append(("i32", int(v)))
+    def visit_i64(self, v): self.args.append(("i64", int(v)))
+    def visit_u32(self, v): self.args.append(("u32", int(v)))
+    def visit_f32(self, v): self.args.append(("f32", float(v)))
+    def visit_f64(self, v): self.args.append(("f64", float(v)))
+
+
+class DispatchPacker(ArgVisitor):
+    """Builds the teeny_arg array that teeny_dispatch consumes."""
+
+    def __init__(self):
+        self.args: List[_lib.TeenyArg] = []
+
+    def _push(self, kind, field, value):
+        a = _lib.TeenyArg()
+        a.kind = kind
+        setattr(a.v, field, value)
+        self.args.append(a)
+
+    def visit_ptr(self, ptr): self._push(_lib.ARG_PTR, "ptr", _addr(ptr))
+    def visit_bool(self, v): self._push(_lib.ARG_BOOL, "b", int(bool(v)))
+    def visit_i32(self, v): self._push(_lib.ARG_I32, "i32", int(v))
+    def visit_i64(self, v): self._push(_lib.ARG_I64, "i64", int(v))
+    def visit_u32(self, v): self._push(_lib.ARG_U32, "u32", int(v))
+    def visit_f32(self, v): self._push(_lib.ARG_F32, "f32", float(v))
+    def visit_f64(self, v): self._push(_lib.ARG_F64, "f64", float(v))
+
+    def array(self):
+        arr = (_lib.TeenyArg * max(1, len(self.args)))(*self.args)
+        return arr, len(self.args)
+
+
+# ── RuntimeOp (core/teeny-core/src/model/mod.rs:78-331) ─────────────────────
+
+
+def _prod(s: Sequence[int]) -> int:
+    return int(np.prod(s)) if len(s) else 1
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+class RuntimeOp:
+    name: str = ""
+
+    def const_generics(self) -> Tuple[int, ...]:
+        return ()
+
+    def entry_point_name(self) -> str:  # Kernel::entry_point_name, program.rs:212-216
+        return f"{self.name}_entry_point"
+
+    def n_activation_inputs(self) -> int:
+        return 1
+
+    def param_shapes(self, input_shapes, output_shape) -> List[List[int]]:
+        return []
+
+    def param_names(self) -> Tuple[str, ...]:
+        return ()
+
+    def forward_output_row_elems(self, output_shape) -> int:
+        return int(output_shape[-1]) if len(output_shape) else 1
+
+    def forward_output_row_stride(self, output_shape) -> int:
+        return self.forward_output_row_elems(output_shape)
+
+    def compute_concrete_output_shape(self, input_shapes, resolved):
+        return list(resolved)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        raise NotImplementedError
+
+    def grid(self, output_shape) -> Tuple[int, int, int]:
+        raise NotImplementedError
+
+    def check_buffers(self, inputs, params, output, output_shape) -> None:
+        """Buffers given as Buffer objects must hold the shapes the op will touch
+        (input shapes, param_shapes, output shape); raw addresses are trusted."""
+        shapes = [list(s) for _, s in inputs]
+        expect = self.param_shapes(shapes, list(output_shape))
+        pairs = [(b, s, "input") for b, s in inputs] + [(output, output_shape, "output")]
+        pairs += [(b, s, f"param {n}") for b, s, n in zip(params, expect, self.param_names())]
+        for buf, shape, what in pairs:
+            if isinstance(buf, Buffer):
+                _need(buf.numel >= _prod(shape),
+                      f"{self.name}: {what} buffer holds {buf.numel} elements, needs {_prod(shape)}")
+
+    def launch(self, inputs, params, output, output_shape, dtype, stream: Optional[Stream] = None):
+        """Executor step: pack_args + grid, then run through teeny_dispatch."""
+        self.check_buffers(inputs, params, output, output_shape)
+        packer = DispatchPacker()
+        self.pack_args(inputs, params, output, output_shape,
+                       self.forward_output_row_stride(output_shape), packer)
+        args, n = packer.array()
+        cg = self.const_generics()
+        cg_arr = (ctypes.c_int64 * max(1, len(cg)))(*cg)
+        grid = (ctypes.c_uint32 * 3)(*self.grid(output_shape))
+        check(lib.teeny_dispatch(self.entry_point_name().encode(), cg_arr, len(cg), args, n, grid,
+                                 from_any(dtype).code, _h(stream)))
+
+
+class _Elementwise(RuntimeOp):
+    """relu.rs:119-180, gelu.rs:258-317, sigmoid.rs:389-448."""
+
+    def __init__(self, block_size: int = 1024):
+        self.block_size = int(block_size)
+
+    def const_generics(self):
+        return (self.block_size,)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        n = _prod(output_shape)
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(output)
+        visitor.visit_i32(n)
+
+    def grid(self, output_shape):
+        n = _prod(output_shape)
+        return (-(-n // self.block_size), 1, 1)
+
+
+class ReluForward(_Elementwise):
+    name = "relu_forward"
+
+
+class GeluForward(_Elementwise):
+    name = "gelu_forward"
+
+
+class SiluForward(_Elementwise):
+    name = "silu_forward"
+
+
+class LayerNormForwardInferenceRuntimeOp(RuntimeOp):
+    """layernorm.rs:486-561; BLOCK_N = 1024 and eps as the lowering passes them
+    (kernels/teeny-kernels/src/graph/mod.rs:1184-1227)."""
+
+    name = "layer_norm_forward_inference"
+
+    def __init__(self, block_n: int = 1024, eps: float = 1e-5):
+        self.block_n = int(block_n)
+        self.eps = float(eps)
+
+    def const_generics(self):
+        return (self.block_n,)
+
+    def param_shapes(self, input_shapes, output_shape):
+        n = int(input_shapes[0][-1])
+        return [[n], [n]]
+
+    def param_names(self):
+        return ("weight", "bias")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        shape = inputs[0][1]
+        n = int(shape[-1])
+        m = _prod(shape) // n
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(output)
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_i32(m)
+        visitor.visit_i32(n)
+        visitor.visit_f32(self.eps)
+
+    def grid(self, output_shape):
+        n = int(output_shape[-1])
+        return (_prod(output_shape) // n, 1, 1)
+
+
+class RmsNormForwardRuntimeOp(RuntimeOp):
+    """A working RuntimeOp for rms_norm_forward (rmsnorm.rs:39-119); the
+    reference's graph RuntimeOp for RMSNorm is a panicking stub
+    (kernels/teeny-kernels/src/graph/mod.rs:454).  Params: weight [N] and the
+    rrms output [M] (fp32), in the kernel's argument order."""
+
+    name = "rms_norm_forward"
+
+    def __init__(self, block_n: int = 1024, eps: float = 1e-8):
+        self.block_n = int(block_n)
+        self.eps = float(eps)
+
+    def const_generics(self):
+        return (self.block_n,)
+
+    def param_shapes(self, input_shapes, output_shape):
+        n = int(input_shapes[0][-1])
+        m = _prod(input_shapes[0]) // n
+        return [[n], [m]]
+
+    def param_names(self):
+        return ("weight", "rrms")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        shape = inputs[0][1]
+        n = int(shape[-1])
+        m = _prod(shape) // n
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(output)
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_i32(m)
+        visitor.visit_i32(n)
+        visitor.visit_f32(self.eps)
+
+    def grid(self, output_shape):
+        n = int(output_shape[-1])
+        return (_prod(output_shape) // n, 1, 1)
+
+
+class Conv2dForward(RuntimeOp):
+    """conv2d.rs:523-618: const generics KH, KW, STRIDE_H, STRIDE_W, PAD_H,
+    PAD_W, G, BLOCK_OW; args (x, w, y, B, C_IN, C_OUT, H, W, OH, OW)."""
+
+    name = "conv2d_forward"
+    has_bias = False
+
+    def __init__(self, kh, kw, stride_h=1, stride_w=1, pad_h=0, pad_w=0, groups=1, block_ow=16):
+        self.kh, self.kw = int(kh), int(kw)
+        self.sh, self.sw = int(stride_h), int(stride_w)
+        self.ph, self.pw = int(pad_h), int(pad_w)
+        self.g = int(groups)
+        self.block_ow = int(block_ow)
+
+    def const_generics(self):
+        return (self.kh, self.kw, self.sh, self.sw, self.ph, self.pw, self.g, self.block_ow)
+
+    def output_hw(self, h, w):
+        return ((h + 2 * self.ph - self.kh) // self.sh + 1, (w + 2 * self.pw - self.kw) // self.sw + 1)
+
+    def param_shapes(self, input_shapes, output_shape):
+        c_in, c_out = int(input_shapes[0][1]), int(output_shape[1])
+        shapes = [[c_out, c_in // self.g, self.kh, self.kw]]
+        if self.has_bias:
+            shapes.append([c_out])
+        return shapes
+
+    def param_names(self):
+        return ("weight", "bias") if self.has_bias else ("weight",)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        ish = inputs[0][1]
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        if self.has_bias:
+            visitor.visit_ptr(params[1])
+        visitor.visit_ptr(output)
+        visitor.visit_i32(ish[0])
+        visitor.visit_i32(ish[1])
+        visitor.visit_i32(output_shape[1])
+        visitor.visit_i32(ish[2])
+        visitor.visit_i32(ish[3])
+        visitor.visit_i32(output_shape[2])
+        visitor.visit_i32(output_shape[3])
+
+    def grid(self, output_shape):
+        tiles = -(-int(output_shape[3]) // self.block_ow)
+        return (int(output_shape[0]) * int(output_shape[1]) * int(output_shape[2]) * tiles, 1, 1)
+
+
+class Conv2dBiasForward(Conv2dForward):
+    """conv2d.rs:766-820: the conv2d_forward contract plus bias after w."""
+
+    name = "conv2d_bias_forward"
+    has_bias = True
+
+
+class FlashAttention2Forward(RuntimeOp):
+    """flash_attn2.rs:52-158.  The reference has no RuntimeOp for it (its
+    tests launch it directly, tests/test_flash_attn2.rs:96-180); this mirrors
+    that launch: args (q, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale,
+    neg_inf), const HEAD_DIM, grid (N_CTX_Q, BH, 1).  Inputs are q, k, v of
+    shape [BH, N, HEAD_DIM]; params[0] is the l (logsumexp) buffer."""
+
+    name = "flash_attention2_forward"
+
+    def __init__(self, head_dim: int, softmax_scale: Optional[float] = None):
+        self.head_dim = int(head_dim)
+        self.softmax_scale = float(softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(head_dim))
+
+    def const_generics(self):
+        return (self.head_dim,)
+
+    def n_activation_inputs(self):
+        return 3
+
+    def param_shapes(self, input_shapes, output_shape):
+        return [[int(output_shape[0]), int(output_shape[1])]]
+
+    def param_names(self):
+        return ("l",)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(inputs[1][0])
+        visitor.visit_ptr(inputs[2][0])
+        visitor.visit_ptr(output)
+        visitor.visit_ptr(params[0])
+        visitor.visit_i32(inputs[0][1][1])
+        visitor.visit_i32(inputs[1][1][1])
+        visitor.visit_f32(self.softmax_scale)
+        visitor.visit_f32(float("-inf"))
+
+    def grid(self, output_shape):
+        return (int(output_shape[1]), int(output_shape[0]), 1)
+
+
+class LinearForward(RuntimeOp):
+    """linear.rs:250-320: const generics USE_BIAS, BLOCK_M, BLOCK_N, BLOCK_K,
+    GROUP_M; args (x, w, b, y, M, N, K, stride_xm, stride_xk, stride_wn,
+    stride_wk, stride_ym, stride_yn); b is null without bias."""
+
+    name = "linear_forward"
+
+    def __init__(self, use_bias=True, block_m=64, block_n=64, block_k=32, group_m=8):
+        self.use_bias = bool(use_bias)
+        self.block_m, self.block_n, self.block_k, self.group_m = block_m, block_n, block_k, group_m
+
+    def const_generics(self):
+        return (int(self.use_bias), self.block_m, self.block_n, self.block_k, self.group_m)
+
+    def param_shapes(self, input_shapes, output_shape):
+        k, n = int(input_shapes[0][1]), int(output_shape[1])
+        return [[n, k], [n]] if self.use_bias else [[n, k]]
+
+    def param_names(self):
+        return ("weight", "bias") if self.use_bias else ("weight",)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        m, n = int(output_shape[0]), int(output_shape[1])
+        k = int(inputs[0][1][1])
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1] if self.use_bias else None)
+        visitor.visit_ptr(output)
+        for v in (m, n, k, k, 1, k, 1, output_row_stride, 1):
+            visitor.visit_i32(v)
+
+    def grid(self, output_shape):
+        pm = -(-int(output_shape[0]) // self.block_m)
+        pn = -(-int(output_shape[1]) // self.block_n)
+        return (pm * pn, 1, 1)
+
+
+# ── direct entry points on Buffers ──────────────────────────────────────────
+
+
+def _out(like: Buffer, out: Optional[Buffer], shape=None, dtype=None) -> Buffer:
+    """The output buffer: `out` if given (its size and dtype must match), else a new one."""
+    shape = tuple(shape if shape is not None else like.shape)
+    dtype = from_any(dtype or like.dtype)
+    if out is not None:
+        _need(out.numel == _prod(shape), f"output holds {out.numel} elements, op writes {_prod(shape)}")
+        _need(out.dtype == dtype, f"output dtype {out.dtype.name}, op writes {dtype.name}")
+        return out
+    return Buffer(dtype, shape)
+
+
+# Shape rules of each entry point, as pure functions of buffer shapes (so the
+# rules are testable without a device).  Every wrapper below checks its
+# buffers with these before calling the C ABI, which cannot see allocation
+# sizes through raw pointers.
+
+def linear_dims(x_shape, w_shape, b_shape=None) -> Tuple[int, int, int]:
+    _need(len(x_shape) == 2 and len(w_shape) == 2, "linear: x and w must be 2-D")
+    m, k = x_shape
+    n, kw = w_shape
+    _need(k == kw, f"linear: x has K={k}, w has K={kw}")
+    _need(b_shape is None or _prod(b_shape) == n, f"linear: bias must have {n} elements")
+    return int(m), int(n), int(k)
+
+
+def w8a16_dims(x_shape, q_shape, scale_shape, bias_shape=None) -> Tuple[int, int, int]:
+    m, n, k = linear_dims(x_shape, q_shape, bias_shape)
+    _need(_prod(scale_shape) == n, f"w8a16: scale must have N={n} elements, has {_prod(scale_shape)}")
+    return m, n, k
+
+
+def conv2d_dims(x_shape, w_shape, stride, padding, groups, layout, b_shape=None):
+    """-> (B, Cin, Cout, H, W, OH, OW, KH, KW, sh, sw, ph, pw) with the reference's shape rules."""
+    sh, sw = (stride, stride) if isinstance(stride, int) else stride
+    ph, pw = (padding, padding) if isinstance(padding, int) else padding
+    _need(len(x_shape) == 4 and len(w_shape) == 4, "conv2d: x and w must be 4-D")
+    if layout == "nhwc":
+        b, h, wd, cin = x_shape
+        cout, kh, kw, cg = w_shape
+    else:
+        b, cin, h, wd = x_shape
+        cout, cg, kh, kw = w_shape
+    _need(groups > 0 and cin % groups == 0 and cout % groups == 0,
+          f"conv2d: groups={groups} must divide C_IN={cin} and C_OUT={cout}")
+    _need(cg == cin // groups, f"conv2d: weight has {cg} input channels per group, expected {cin // groups}")
+    _need(b_shape is None or _prod(b_shape) == cout, f"conv2d: bias must have {cout} elements")
+    _need(h + 2 * ph >= kh and wd + 2 * pw >= kw, "conv2d: kernel larger than padded input")
+    oh, ow = (h + 2 * ph - kh) // sh + 1, (wd + 2 * pw - kw) // sw + 1
+    return b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw
+
+
+def attention_dims(q_shape, k_shape, v_shape, lse_shape=None):
+    _need(len(q_shape) == 3 and len(k_shape) == 3 and len(v_shape) == 3,
+          "attention: q, k, v must be [BH, N, D]")
+    bh, nq, d = q_shape
+    _need(tuple(k_shape) == tuple(v_shape), "attention: k and v shapes differ")
+    _need(k_shape[0] == bh and k_shape[2] == d, "attention: k/v must share BH and D with q")
+    _need(lse_shape is None or _prod(lse_shape) == bh * nq, f"attention: lse must have {bh * nq} elements")
+    return int(bh), int(nq), int(k_shape[1]), int(d)
+
+
+def norm_dims(x_shape, weight_shape, bias_shape=None, rrms_shape=None):
+    n = int(x_shape[-1])
+    m = _prod(x_shape) // n
+    _need(_prod(weight_shape) == n, f"norm: weight must have N={n} elements")
+    _need(bias_shape is None or _prod(bias_shape) == n, f"norm: bias must have N={n} elements")
+    _need(rrms_shape is None or _prod(rrms_shape) == m, f"norm: rrms must have M={m} elements")
+    return m, n
+
+
+def relu(x: Buffer, y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    y = _out(x, y)
+    check(lib.teeny_relu_forward(x.ptr, y.ptr, x.numel, x.dtype.code, _h(stream)))
+    return y
+
+
+def gelu(x: Buffer, y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    y = _out(x, y)
+    check(lib.teeny_gelu_forward(x.ptr, y.ptr, x.numel, x.dtype.code, _h(stream)))
+    return y
+
+
+def silu(x: Buffer, y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    y = _out(x, y)
+    check(lib.teeny_silu_forward(x.ptr, y.ptr, x.numel, x.dtype.code, _h(stream)))
+    return y
+
+
+def layer_norm(x: Buffer, weight: Buffer, bias: Buffer, eps: float = 1e-5,
+               y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    m, n = norm_dims(x.shape, weight.shape, bias.shape)
+    _need(weight.dtype == x.dtype and bias.dtype == x.dtype, "layer_norm: weight/bias dtype must match x")
+    y = _out(x, y)
+    check(lib.teeny_layer_norm_forward_inference(x.ptr, y.ptr, weight.ptr, bias.ptr, m, n, eps,
+                                                 x.dtype.code, _h(stream)))
+    return y
+
+
+def rms_norm(x: Buffer, weight: Buffer, eps: float = 1e-8, y: Optional[Buffer] = None,
+             rrms: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    m, n = norm_dims(x.shape, weight.shape, None, rrms.shape if rrms is not None else None)
+    _need(weight.dtype == x.dtype, "rms_norm: weight dtype must match x")
+    _need(rrms is None or rrms.dtype == f32, "rms_norm: rrms is fp32")
+    y = _out(x, y)
+    check(lib.teeny_rms_norm_forward(x.ptr, y.ptr, weight.ptr, rrms.ptr if rrms is not None else None,
+                                     m, n, eps, x.dtype.code, _h(stream)))
+    return y
+
+
+ACTS = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "relu": _lib.ACT_RELU,
+        "gelu": _lib.ACT_GELU_TANH, "gelu_tanh": _lib.ACT_GELU_TANH, "silu": _lib.ACT_SILU}
+
+
+def norm_act(x: Buffer, weight: Buffer, bias: Optional[Buffer], eps: float, rms: bool, act: str,
+             y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    m, n = norm_dims(x.shape, weight.shape, bias.shape if bias is not None else None)
+    _need(rms or bias is not None, "norm_act: LayerNorm needs a bias")
+    y = _out(x, y)
+    check(lib.teeny_norm_act_forward(x.ptr, y.ptr, weight.ptr, bias.ptr if bias is not None else None,
+                                     m, n, eps, int(rms), ACTS[act], x.dtype.code, _h(stream)))
+    return y
+
+
+def conv2d(x: Buffer, w: Buffer, bias: Optional[Buffer] = None, stride=(1, 1), padding=(0, 0),
+           groups: int = 1, act: Optional[str] = None, layout: str = "nchw",
+           y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """x NCHW [B,C,H,W] or NHWC [B,H,W,C]; w [Cout,Cin/G,KH,KW] (NCHW) or
+    [Cout,KH,KW,Cin/G] (NHWC)."""
+    nhwc = layout.lower() == "nhwc"
+    b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw = conv2d_dims(
+        x.shape, w.shape, stride, padding, groups, "nhwc" if nhwc else "nchw",
+        bias.shape if bias is not None else None)
+    _need(w.dtype == x.dtype and (bias is None or bias.dtype == x.dtype),
+          "conv2d: w/bias dtype must match x")
+    yshape = (b, oh, ow, cout) if nhwc else (b, cout, oh, ow)
+    y = _out(x, y, yshape)
+    prm = _lib.Conv2dParams(kh, kw, sh, sw, ph, pw, groups, ACTS[act])
+    lay = _lib.NHWC if nhwc else _lib.NCHW
+    if bias is None:
+        check(lib.teeny_conv2d_forward(x.ptr, w.ptr, y.ptr, b, cin, cout, h, wd, oh, ow,
+                                       ctypes.byref(prm), x.dtype.code, lay, _h(stream)))
+    else:
+        check(lib.teeny_conv2d_bias_forward(x.ptr, w.ptr, bias.ptr, y.ptr, b, cin, cout, h, wd, oh,
+                                            ow, ctypes.byref(prm), x.dtype.code, lay, _h(stream)))
+    return y
+
+
+def flash_attention(q: Buffer, k: Buffer, v: Buffer, softmax_scale: Optional[float] = None,
+                    causal: bool = False, o: Optional[Buffer] = None, lse: Optional[Buffer] = None,
+                    stream: Optional[Stream] = None) -> Buffer:
+    """q [BH, Nq, D], k/v [BH, Nk, D] -> o [BH, Nq, D]; lse (fp32 [BH, Nq]) optional."""
+    bh, nq, nk, d = attention_dims(q.shape, k.shape, v.shape, lse.shape if lse is not None else None)
+    _need(k.dtype == q.dtype and v.dtype == q.dtype, "attention: q/k/v dtypes differ")
+    _need(lse is None or lse.dtype == f32, "attention: lse is fp32")
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    o = _out(q, o)
+    check(lib.teeny_flash_attention2_forward(q.ptr, k.ptr, v.ptr, o.ptr,
+                                             lse.ptr if lse is not None else None, nq, nk, scale,
+                                             bh, d, int(bool(causal)), q.dtype.code, _h(stream)))
+    return o
+
+
+GRANULARITY = {"tensor": _lib.PER_TENSOR, "channel": _lib.PER_CHANNEL, "group": _lib.GROUP}
+
+
+def quant_num_groups(shape, granularity="channel", axis=0, group_size=1) -> int:
+    sh = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+    out = ctypes.c_int64()
+    check(lib.teeny_quant_num_groups(sh, len(shape), GRANULARITY[granularity], axis, group_size,
+                                     ctypes.byref(out)))
+    return out.value
+
+
+def quantize_affine(data: Buffer, shape, granularity="channel", axis=0, group_size=1,
+                    symmetric=True, bits=8, want_groups=False, stream: Optional[Stream] = None):
+    """teeny-quant quantize_affine on the GPU (affine.rs:55-148).  Returns
+    (qvalues int8, scales f32, zero_points i32, groups u32 or None)."""
+    ng = quant_num_groups(shape, granularity, axis, group_size)
+    n = _prod(shape)
+    _need(data.dtype == f32 and data.numel == n, f"quantize_affine: data must be fp32 with {n} elements")
+    q = Buffer(i8, tuple(shape))
+    scales = Buffer(f32, (max(ng, 1),))
+    zps = Buffer("i32", (max(ng, 1),))
+    groups = Buffer("u32", (n,)) if want_groups else None
+    sh = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+    check(lib.teeny_quantize_affine(data.ptr, sh, len(shape), GRANULARITY[granularity], axis,
+                                    group_size, int(bool(symmetric)), bits, q.ptr, scales.ptr,
+                                    zps.ptr, groups.ptr if groups is not None else None, _h(stream)))
+    return q, scales, zps, groups
+
+
+def dequantize_affine(q: Buffer, scales: Buffer, zero_points: Optional[Buffer], shape,
+                      granularity="channel", axis=0, group_size=1, out: Optional[Buffer] = None,
+                      stream: Optional[Stream] = None) -> Buffer:
+    ng = quant_num_groups(shape, granularity, axis, group_size)
+    _need(q.numel == _prod(shape) and q.dtype == i8, "dequantize_affine: q must be int8 of the shape")
+    _need(scales.numel >= ng and (zero_points is None or zero_points.numel >= ng),
+          f"dequantize_affine: scales/zero_points need {ng} entries")
+    out = _out(q, out, tuple(shape), f32)
+    sh = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+    check(lib.teeny_dequantize_affine(q.ptr, scales.ptr,
+                                      zero_points.ptr if zero_points is not None else None, sh,
+                                      len(shape), GRANULARITY[granularity], axis, group_size,
+                                      out.ptr, _h(stream)))
+    return out
+
+
+def linear(x: Buffer, w: Buffer, b: Optional[Buffer] = None, y: Optional[Buffer] = None,
+           stream: Optional[Stream] = None) -> Buffer:
+    m, n, k = linear_dims(x.shape, w.shape, b.shape if b is not None else None)
+    _need(w.dtype == x.dtype and (b is None or b.dtype == x.dtype), "linear: w/b dtype must match x")
+    y = _out(x, y, (m, n))
+    check(lib.teeny_linear_forward(x.ptr, w.ptr, b.ptr if b is not None else None, y.ptr, m, n, k,
+                                   k, 1, k, 1, n, 1, x.dtype.code, _h(stream)))
+    return y
+
+
+def w8a16_linear(x: Buffer, qweight: Buffer, scale: Buffer, bias: Optional[Buffer] = None,
+                 act: Optional[str] = None, y: Optional[Buffer] = None,
+                 stream: Optional[Stream] = None) -> Buffer:
+    m, n, k = w8a16_dims(x.shape, qweight.shape, scale.shape, bias.shape if bias is not None else None)
+    _need(x.dtype == bf16 and qweight.dtype == i8 and scale.dtype == f32 and
+          (bias is None or bias.dtype == f32), "w8a16_linear: x bf16, qweight int8, scale/bias fp32")
+    y = _out(x, y, (m, n), bf16)
+    check(lib.teeny_w8a16_linear_forward(x.ptr, qweight.ptr, scale.ptr,
+                                         bias.ptr if bias is not None else None, y.ptr, m, n, k,
+                                         ACTS[act], _h(stream)))
+    return y
+
+
+def w8a16_conv2d(x: Buffer, qweight: Buffer, scale: Buffer, bias: Optional[Buffer] = None,
+                 stride=(1, 1), padding=(0, 0), groups: int = 1, act: Optional[str] = None,
+                 y: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """x NHWC bf16 [B,H,W,Cin], qweight int8 [Cout,KH,KW,Cin/G], scale f32 [Cout]."""
+    b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw = conv2d_dims(
+        x.shape, qweight.shape, stride, padding, groups, "nhwc", bias.shape if bias is not None else None)
+    _need(_prod(scale.shape) == cout, f"w8a16_conv2d: scale must have {cout} elements")
+    _need(x.dtype == bf16 and qweight.dtype == i8 and scale.dtype == f32 and
+          (bias is None or bias.dtype == f32), "w8a16_conv2d: x bf16, qweight int8, scale/bias fp32")
+    y = _out(x, y, (b, oh, ow, cout), bf16)
+    prm = _lib.Conv2dParams(kh, kw, sh, sw, ph, pw, groups, ACTS[act])
+    check(lib.teeny_w8a16_conv2d_forward(x.ptr, qweight.ptr, scale.ptr,
+                                         bias.ptr if bias is not None else None, y.ptr, b, cin,
+                                         cout, h, wd, oh, ow, ctypes.byref(prm), _h(stream)))
+    return y

@@ -1,0 +1,185 @@
+"""The C ABI without a GPU: exports, and the error paths of every entry point.
+
+Every argument check of include/teeny_hip.h happens on the host before any
+HIP call, so these run in a container without a device.  Pointers passed
+here are never dereferenced (the calls are rejected first).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import teenygrad_amd as tg
+from teenygrad_amd import _lib
+from teenygrad_amd._lib import lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "teeny_hip.h")
+FAKE = 0x100000  # 16-byte aligned, never dereferenced
+FAKE_ODD = 0x100002
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:teeny_status|const char \*)\s*(teeny_\w+)\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = header_functions()
+    assert len(names) >= 40
+    so = ctypes.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(so, n), f"{n} declared in teeny_hip.h but not exported"
+        assert n in _lib.EXPORTED, f"{n} not bound in teenygrad_amd/_lib.py"
+    assert set(_lib.EXPORTED) == set(names)
+
+
+def test_status_strings_and_version():
+    assert lib.teeny_status_string(0) == b"ok"
+    assert lib.teeny_status_string(_lib.ERR_NULL_POINTER) == b"null pointer"
+    assert b"gfx950" in lib.teeny_hip_version()
+
+
+def expect(status, code):
+    assert status == code, f"status {status} ({tg._lib.last_error()}), wanted {code}"
+    assert tg._lib.last_error() != ""
+
+
+@pytest.mark.parametrize("fn", ["teeny_relu_forward", "teeny_gelu_forward", "teeny_silu_forward"])
+def test_activation_errors(fn):
+    f = getattr(lib, fn)
+    expect(f(None, FAKE, 10, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(f(FAKE, FAKE, -1, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(f(FAKE, FAKE, 10, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    expect(f(FAKE, FAKE, 10, 99, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    assert f(None, None, 0, _lib.F32, None) == _lib.OK  # empty tensor is a no-op
+
+
+def test_norm_errors():
+    ln = lib.teeny_layer_norm_forward_inference
+    expect(ln(FAKE, FAKE, FAKE, None, 4, 8, 1e-5, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(ln(FAKE, FAKE, FAKE, FAKE, 4, 0, 1e-5, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(ln(FAKE, FAKE, FAKE, FAKE, -4, 8, 1e-5, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(ln(FAKE, FAKE, FAKE, FAKE, 4, 8, 1e-5, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    rms = lib.teeny_rms_norm_forward
+    expect(rms(FAKE, FAKE, None, None, 4, 8, 1e-8, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    na = lib.teeny_norm_act_forward
+    expect(na(FAKE, FAKE, FAKE, FAKE, 4, 8, 1e-5, 0, 17, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    assert ln(None, None, None, None, 0, 8, 1e-5, _lib.F32, None) == _lib.OK
+
+
+def conv_params(kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, g=1, act=0):
+    return ctypes.byref(_lib.Conv2dParams(kh, kw, sh, sw, ph, pw, g, act))
+
+
+def test_conv_errors():
+    c = lib.teeny_conv2d_forward
+    # OH/OW inconsistent with (H + 2p - k)/s + 1
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 7, 8, conv_params(), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_SHAPE_MISMATCH)
+    # groups must divide channels
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 6, 8, 8, 8, 8, conv_params(g=4), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_SHAPE_MISMATCH)
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(sh=0), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, None, _lib.F32, _lib.NCHW, None),
+           _lib.ERR_NULL_POINTER)
+    expect(c(None, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_NULL_POINTER)
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.I8, _lib.NCHW, None),
+           _lib.ERR_UNSUPPORTED_DTYPE)
+    expect(c(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, 5, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_conv2d_bias_forward(FAKE, FAKE, None, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(),
+                                         _lib.F32, _lib.NCHW, None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_w8a16_conv2d_forward(FAKE, FAKE, None, None, FAKE, 1, 16, 16, 8, 8, 8, 8,
+                                          conv_params(), None), _lib.ERR_NULL_POINTER)
+
+
+def test_attention_errors():
+    fa = lib.teeny_flash_attention2_forward
+    expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 0, 0.125, 4, 64, 0, _lib.F32, None),
+           _lib.ERR_SHAPE_MISMATCH)
+    expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 8, 0.125, 4, 96, 0, _lib.BF16, None),
+           _lib.ERR_UNSUPPORTED)
+    expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 8, 0.125, 4, 48, 0, _lib.F32, None),
+           _lib.ERR_UNSUPPORTED)
+    expect(fa(FAKE_ODD, FAKE, FAKE, FAKE, None, 8, 8, 0.125, 4, 128, 0, _lib.BF16, None),
+           _lib.ERR_MISALIGNED)
+    expect(fa(FAKE, None, FAKE, FAKE, None, 8, 8, 0.125, 4, 64, 0, _lib.F32, None),
+           _lib.ERR_NULL_POINTER)
+    expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 8, 0.125, 4, 64, 0, _lib.I8, None),
+           _lib.ERR_UNSUPPORTED_DTYPE)
+
+
+def shape_arr(*s):
+    return (ctypes.c_int64 * len(s))(*s)
+
+
+def test_quant_errors_and_group_count():
+    ng = ctypes.c_int64()
+    assert lib.teeny_quant_num_groups(shape_arr(8, 5, 33), 3, _lib.GROUP, 2, 8, ctypes.byref(ng)) == 0
+    assert ng.value == 8 * 5 * 5
+    assert lib.teeny_quant_num_groups(shape_arr(11008, 4096), 2, _lib.PER_CHANNEL, 0, 1,
+                                      ctypes.byref(ng)) == 0 and ng.value == 11008
+    q = lib.teeny_quantize_affine
+    # affine.rs:72-87: axis out of range -> InvalidAxis, group_size 0 -> InvalidGroupSize
+    expect(q(FAKE, shape_arr(4), 1, _lib.PER_CHANNEL, 3, 1, 1, 8, FAKE, FAKE, FAKE, None, None),
+           _lib.ERR_INVALID_AXIS)
+    expect(q(FAKE, shape_arr(4), 1, _lib.GROUP, 0, 0, 1, 8, FAKE, FAKE, FAKE, None, None),
+           _lib.ERR_INVALID_GROUP_SIZE)
+    expect(q(FAKE, shape_arr(4), 1, _lib.PER_TENSOR, 0, 1, 1, 9, FAKE, FAKE, FAKE, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(q(FAKE, shape_arr(4), 1, _lib.PER_TENSOR, 0, 1, 1, 8, FAKE, None, FAKE, None, None),
+           _lib.ERR_NULL_POINTER)
+    expect(q(FAKE, shape_arr(4), 1, 7, 0, 1, 1, 8, FAKE, FAKE, FAKE, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_dequantize_affine(FAKE, FAKE, None, shape_arr(4, 4), 2, _lib.PER_CHANNEL, 2, 1,
+                                       FAKE, None), _lib.ERR_INVALID_AXIS)
+
+
+def test_linear_errors():
+    li = lib.teeny_linear_forward
+    expect(li(FAKE, FAKE, None, None, 4, 4, 4, 4, 1, 4, 1, 4, 1, _lib.F32, None),
+           _lib.ERR_NULL_POINTER)
+    expect(li(FAKE, FAKE, None, FAKE, 4, 4, 4, 4, 1, 4, 1, 4, 1, _lib.I8, None),
+           _lib.ERR_UNSUPPORTED_DTYPE)
+    w8 = lib.teeny_w8a16_linear_forward
+    expect(w8(FAKE, FAKE, None, None, FAKE, 4, 4, 16, 0, None), _lib.ERR_NULL_POINTER)
+    expect(w8(FAKE, FAKE, FAKE, None, FAKE, -1, 4, 16, 0, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(w8(FAKE, FAKE, FAKE, None, FAKE, 4, 4, 16, 9, None), _lib.ERR_INVALID_ARGUMENT)
+
+
+def packed(*kinds_values):
+    arr = (_lib.TeenyArg * len(kinds_values))()
+    for a, (k, v) in zip(arr, kinds_values):
+        a.kind = k
+        setattr(a.v, {_lib.ARG_PTR: "ptr", _lib.ARG_I32: "i32", _lib.ARG_F32: "f32"}[k], v)
+    return arr
+
+
+def test_dispatch_errors():
+    d = lib.teeny_dispatch
+    cg = (ctypes.c_int64 * 1)(1024)
+    grid = (ctypes.c_uint32 * 3)(1, 1, 1)
+    args = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, 8))
+    expect(d(b"softmax_forward_entry_point", cg, 1, args, 3, grid, _lib.F32, None), _lib.ERR_NOT_FOUND)
+    # wrong kind in position 2 (f32 instead of i32)
+    bad = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_F32, 8.0))
+    expect(d(b"relu_forward_entry_point", cg, 1, bad, 3, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    # missing and trailing arguments
+    expect(d(b"relu_forward_entry_point", cg, 1, args, 2, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    extra = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, 8), (_lib.ARG_I32, 1))
+    expect(d(b"relu_forward_entry_point", cg, 1, extra, 4, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    # const generics count
+    expect(d(b"conv2d_forward_entry_point", cg, 1, args, 3, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    # a rejected op through dispatch keeps the op's own status
+    neg = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, -3))
+    expect(d(b"relu_forward_entry_point", cg, 1, neg, 3, grid, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+
+
+def test_no_device_paths():
+    if tg.device_count() > 0:
+        pytest.skip("a device is visible")
+    expect(lib.teeny_hip_device_open(0), _lib.ERR_NO_DEVICE)

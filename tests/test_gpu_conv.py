@@ -1,0 +1,150 @@
+"""GPU parity: conv2d (fp32 direct, bf16 NHWC MFMA implicit GEMM, W8A16)."""
+import numpy as np
+import pytest
+
+import teenygrad_amd as tg
+from conftest import load_golden
+from gpu_util import check_bf16, check_f32
+from teenygrad_amd import kernels as K
+from teenygrad_amd.dtypes import from_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def rb(a):
+    return from_bf16(to_bf16(a))
+
+
+@pytest.mark.parametrize("case,pad,oh", [("conv2d", 0, 6), ("conv2d_padded", 1, 8)])
+def test_f32_fixture(dev, orc, case, pad, oh):
+    x = load_golden(f"{case}/x.bin").reshape(1, 2, 8, 8)
+    w = load_golden(f"{case}/w.bin").reshape(4, 2, 3, 3)
+    want = load_golden(f"{case}/expected_forward.bin").reshape(1, 4, oh, oh)
+    got = K.conv2d(dev.upload(x), dev.upload(w), padding=pad).to_host()
+    assert np.max(np.abs(got - want)) < 1e-4  # test_conv2d.rs:203
+    check_f32(got, orc.conv2d_nchw(x, w, padding=pad), "conv")
+
+
+def test_f32_conv_bias_relu_config(dev, orc):
+    # conv2d + bias + ReLU, fp32 NCHW, 1 x 64 -> 64, 56 x 56, 3 x 3, s1 p1
+    rng = np.random.default_rng(0x7EE70000)
+    x = rng.standard_normal((1, 64, 56, 56), dtype=np.float32)
+    w = (rng.standard_normal((64, 64, 3, 3), dtype=np.float32) * np.sqrt(2.0 / 576)).astype(np.float32)
+    b = (rng.standard_normal(64, dtype=np.float32) * 0.01).astype(np.float32)
+    got = K.conv2d(dev.upload(x), dev.upload(w), dev.upload(b), padding=1, act="relu").to_host()
+    ref = orc.relu(orc.conv2d_nchw(x, w, b, padding=1))
+    check_f32(got, ref, "conv+bias+relu")
+    # unfused: the reference's two kernels
+    y = K.conv2d(dev.upload(x), dev.upload(w), dev.upload(b), padding=1)
+    check_f32(K.relu(y).to_host(), ref, "conv+bias then relu")
+
+
+CASES = [
+    # B, Cin, Cout, H, W, KH, KW, stride, pad, groups
+    (2, 3, 5, 9, 7, 3, 3, (1, 1), (1, 1), 1),
+    (1, 4, 6, 11, 10, 3, 2, (2, 3), (1, 0), 2),
+    (1, 6, 6, 8, 8, 3, 3, (1, 1), (1, 1), 6),
+    (2, 8, 4, 7, 7, 1, 1, (2, 2), (0, 0), 1),
+    (1, 3, 4, 16, 16, 7, 7, (2, 2), (3, 3), 1),
+    (1, 16, 12, 9, 9, 5, 5, (1, 1), (2, 2), 4),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_f32_cases(dev, orc, case, layout):
+    B, Cin, Cout, H, W, KH, KW, st, pd, G = case
+    rng = np.random.default_rng(Cin * 100 + Cout)
+    x = rng.normal(0, 1, (B, Cin, H, W)).astype(np.float32)
+    w = rng.normal(0, 0.3, (Cout, Cin // G, KH, KW)).astype(np.float32)
+    b = rng.normal(0, 0.1, Cout).astype(np.float32)
+    ref = orc.conv2d_nchw(x, w, b, stride=st, padding=pd, groups=G)
+    if layout == "nchw":
+        got = K.conv2d(dev.upload(x), dev.upload(w), dev.upload(b), st, pd, G).to_host()
+    else:
+        got = K.conv2d(dev.upload(np.ascontiguousarray(x.transpose(0, 2, 3, 1))),
+                       dev.upload(np.ascontiguousarray(w.transpose(0, 2, 3, 1))), dev.upload(b), st,
+                       pd, G, layout="nhwc").to_host().transpose(0, 3, 1, 2)
+    check_f32(got, ref, f"{case} {layout}")
+
+
+BF16_CASES = [
+    # B, Cin, Cout, H, W, KH, KW, stride, pad, act     (path)
+    (2, 64, 64, 14, 14, 3, 3, 1, 1, "relu"),   # 3x3 implicit GEMM, 16-byte gather
+    (2, 64, 256, 14, 14, 1, 1, 1, 0, None),    # 1x1 stride 1: plain GEMM
+    (2, 256, 512, 14, 14, 1, 1, 2, 0, None),   # strided 1x1 downsample
+    (2, 128, 128, 15, 15, 3, 3, 2, 1, "relu"), # strided 3x3
+    (1, 3, 64, 32, 32, 7, 7, 2, 3, "relu"),    # 3-channel stem: element-wise gather
+    (3, 24, 40, 9, 11, 3, 3, 1, 1, None),      # ragged M, N < 64
+    (1, 12, 20, 7, 7, 3, 3, 1, 1, "relu"),     # C_IN % 8 != 0
+    (1, 512, 2048, 7, 7, 1, 1, 1, 0, None),    # deep 1x1 (M = 49)
+    (2, 64, 96, 10, 10, 3, 3, 1, 0, None),     # N = 96: BN=128 tile, half-empty
+]
+
+
+@pytest.mark.parametrize("case", BF16_CASES)
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_bf16_nhwc_mfma(dev, orc, case, with_bias):
+    B, Cin, Cout, H, W, KH, KW, s, p, act = case
+    print(f"[conv bf16] {case} bias={with_bias}", flush=True)
+    rng = np.random.default_rng(Cin * 7 + Cout + H)
+    x = rb(rng.standard_normal((B, H, W, Cin), dtype=np.float32))
+    w = rb((rng.standard_normal((Cout, KH, KW, Cin), dtype=np.float32) * np.sqrt(2.0 / (Cin * KH * KW))).astype(np.float32))
+    b = rb(rng.normal(0, 0.1, Cout).astype(np.float32)) if with_bias else None
+    got = K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                   dev.upload(to_bf16(b), tg.bf16) if with_bias else None, s, p, 1, act,
+                   layout="nhwc").to_host()
+    ref = orc.conv2d_nhwc(x, w, b, stride=s, padding=p)
+    if act == "relu":
+        ref = orc.relu(ref)
+    check_bf16(got, ref, str(case))
+
+
+def test_bf16_nchw_and_grouped_direct(dev, orc):
+    rng = np.random.default_rng(5)
+    x = rb(rng.standard_normal((2, 8, 10, 10), dtype=np.float32))
+    w = rb(rng.normal(0, 0.3, (8, 4, 3, 3)).astype(np.float32))
+    got = K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16), None, 1, 1, 2).to_host()
+    check_bf16(got, orc.conv2d_nchw(x, w, None, padding=1, groups=2), "bf16 nchw grouped")
+    xh = np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    wh = np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    got = K.conv2d(dev.upload(to_bf16(xh), tg.bf16), dev.upload(to_bf16(wh), tg.bf16), None, 1, 1, 2,
+                   layout="nhwc").to_host()
+    check_bf16(got, orc.conv2d_nhwc(xh, wh, None, padding=1, groups=2), "bf16 nhwc grouped")
+
+
+def quantized_conv_weight(orc, rng, cout, kh, kw, cin):
+    wf = rng.normal(0, 0.02, (cout, kh, kw, cin)).astype(np.float32)
+    q, s, z, _ = orc.quantize_affine(wf, wf.shape, "channel", 0)
+    return q.reshape(wf.shape), s
+
+
+@pytest.mark.parametrize("B,Cin,Cout,H,act", [(2, 256, 256, 28, None), (1, 64, 96, 9, "relu"),
+                                              (1, 24, 16, 8, None)])
+def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act):
+    # int8 3x3 conv (the W8A16 conv workload at reduced batch; Cin=24 takes the fallback kernel)
+    rng = np.random.default_rng(Cin + H)
+    x = rb(rng.standard_normal((B, H, H, Cin), dtype=np.float32))
+    q, s = quantized_conv_weight(orc, rng, Cout, 3, 3, Cin)
+    bias = rng.normal(0, 0.1, Cout).astype(np.float32)
+    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s),
+                         dev.upload(bias), 1, 1, act=act).to_host()
+    wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
+    ref = orc.conv2d_nhwc(x, wdeq, bias, stride=1, padding=1)
+    if act == "relu":
+        ref = orc.relu(ref)
+    check_bf16(got, ref, "w8a16 conv")
+
+
+def test_w8a16_conv_config_batch32(dev, orc):
+    # 32 x 256 x 28 x 28, 3x3 p1: first and last image against the oracle
+    B, C, H = 32, 256, 28
+    rng = np.random.default_rng(0x7EE70004)
+    x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
+    q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
+    print("[w8a16 conv config] 32x256x28x28", flush=True)
+    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), None, 1, 1).to_host()
+    wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
+    for b in (0, B - 1):
+        ref = orc.conv2d_nhwc(x[b:b + 1], wdeq, None, stride=1, padding=1)
+        check_bf16(got[b:b + 1], ref, f"image {b}")

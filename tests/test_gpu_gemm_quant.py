@@ -1,0 +1,137 @@
+"""GPU parity: linear (fp32 / bf16), W8A16 GEMM and teeny-quant on the GPU."""
+import numpy as np
+import pytest
+
+import teenygrad_amd as tg
+from conftest import load_golden
+from gpu_util import check_bf16, check_f32
+from quant_cases import KNOWN
+from teenygrad_amd import _lib, kernels as K
+from teenygrad_amd.dtypes import from_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def rb(a):
+    return from_bf16(to_bf16(a))
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_f32_fixture(dev, orc, with_bias):
+    x = load_golden("linear/input.bin").reshape(64, 64)
+    w = load_golden("linear/weight.bin").reshape(48, 64)
+    b = load_golden("linear/bias.bin")
+    want = load_golden(f"linear/expected_{'with' if with_bias else 'no'}_bias.bin").reshape(64, 48)
+    got = K.linear(dev.upload(x), dev.upload(w), dev.upload(b) if with_bias else None).to_host()
+    np.testing.assert_allclose(got, want, rtol=0.02, atol=0.1)  # test_linear.rs:48-54
+    check_f32(got, orc.linear(x, w, b if with_bias else None), "linear f32")
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 300, 136), (64, 48, 64), (33, 17, 70), (256, 512, 1000)])
+def test_linear_bf16(dev, orc, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb((rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float32))
+    b = rb(rng.normal(0, 0.5, n).astype(np.float32))
+    got = K.linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                   dev.upload(to_bf16(b), tg.bf16)).to_host()
+    check_bf16(got, orc.linear(x, w, b), "linear bf16")
+
+
+def test_linear_bf16_strided_generic(dev, orc):
+    # x given as a transposed view (stride_xk = M): the generic kernel path
+    rng = np.random.default_rng(3)
+    m, n, k = 40, 24, 56
+    xt = rb(rng.standard_normal((k, m), dtype=np.float32))  # x = xt^T
+    w = rb((rng.standard_normal((n, k), dtype=np.float32) / 8).astype(np.float32))
+    xb, wb = dev.upload(to_bf16(xt), tg.bf16), dev.upload(to_bf16(w), tg.bf16)
+    y = tg.Buffer(tg.bf16, (m, n))
+    tg.check(_lib.lib.teeny_linear_forward(xb.ptr, wb.ptr, None, y.ptr, m, n, k, 1, m, k, 1, n, 1,
+                                           _lib.BF16, None))
+    check_bf16(y.to_host(), orc.linear(np.ascontiguousarray(xt.T), w), "strided linear")
+
+
+def quantized_weight(orc, rng, n, k):
+    wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    q, s, _, _ = orc.quantize_affine(wf, [n, k], "channel", 0)
+    return q.reshape(n, k), s
+
+
+@pytest.mark.parametrize("m,n,k,act", [(100, 200, 256, None), (256, 384, 512, "silu"),
+                                       (64, 64, 4096, "gelu"), (37, 70, 40, "relu"), (5, 9, 48, None)])
+def test_w8a16_small(dev, orc, m, n, k, act):
+    # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA
+    rng = np.random.default_rng(m * n + k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    q, s = quantized_weight(orc, rng, n, k)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    got = K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s),
+                         dev.upload(bias), act=act).to_host()
+    ref = orc.w8a16_linear(x, q, s, bias)
+    if act is not None:
+        ref = getattr(orc, act)(ref)
+    check_bf16(got, ref, "w8a16")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 11008), (11008, 4096)])
+def test_w8a16_config(dev, orc, k, n):
+    # M = 4096 tokens; weights N(0, 0.02) quantised per output channel on the GPU
+    # (bit-exact with the oracle); output rows 0..31 and M-32..M-1 vs the oracle
+    m = 4096
+    rng = np.random.default_rng(0x7EE70005 + k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    print(f"[w8a16 config] M={m} K={k} N={n}", flush=True)
+    qg, sg, zg, _ = K.quantize_affine(dev.upload(wf), [n, k], "channel", 0)
+    q, s, z, _ = orc.quantize_affine(wf, [n, k], "channel", 0)
+    np.testing.assert_array_equal(qg.to_host().reshape(-1), q)
+    np.testing.assert_array_equal(sg.to_host(), s)
+    y = K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), qg, sg).to_host()
+    assert np.all(np.isfinite(from_bf16(y)))
+    wdeq = orc.dequantize_affine(q, s, None, [n, k], "channel", 0)
+    for lo, hi in ((0, 32), (m - 32, m)):
+        ref = orc.linear(x[lo:hi], wdeq)
+        check_bf16(y[lo:hi], ref, f"rows {lo}..{hi}")
+
+
+# ── teeny-quant on the GPU: bit-exact with the oracle ──────────────────────
+
+
+@pytest.mark.parametrize("case", KNOWN, ids=[c[0] for c in KNOWN])
+def test_quant_known_answers(dev, case):
+    name, data, shape, gran, axis, gs, sym, bits, want_q, want_s, want_z = case
+    q, s, z, g = K.quantize_affine(dev.upload(np.array(data, np.float32)), shape, gran, axis, gs,
+                                   sym, bits, want_groups=True)
+    np.testing.assert_array_equal(q.to_host().reshape(-1), np.array(want_q, np.int8))
+    np.testing.assert_array_equal(s.to_host(), np.array(want_s, np.float32))
+    np.testing.assert_array_equal(z.to_host(), np.array(want_z, np.int32))
+
+
+RANDOM = [((64, 96), "channel", 0, 1, True, 8), ((64, 96), "channel", 1, 1, True, 8),
+          ((64, 96), "tensor", 0, 1, False, 8), ((8, 5, 33), "group", 2, 8, True, 8),
+          ((8, 5, 33), "group", 1, 2, False, 4), ((8, 5, 33), "group", 0, 3, True, 4),
+          ((256, 3, 3, 256), "channel", 0, 1, True, 8), ((3000, 17), "channel", 0, 1, False, 8)]
+
+
+@pytest.mark.parametrize("shape,gran,axis,gs,sym,bits", RANDOM)
+def test_quant_vs_oracle(dev, orc, shape, gran, axis, gs, sym, bits):
+    x = np.random.default_rng(len(shape) + axis).normal(0, 0.02, shape).astype(np.float32)
+    x.reshape(-1)[::5] *= 3.0
+    q, s, z, g = K.quantize_affine(dev.upload(x), shape, gran, axis, gs, sym, bits, want_groups=True)
+    oq, os_, oz, og = orc.quantize_affine(x, shape, gran, axis, gs, sym, bits)
+    np.testing.assert_array_equal(g.to_host(), og)
+    np.testing.assert_array_equal(s.to_host(), os_)
+    np.testing.assert_array_equal(z.to_host(), oz)
+    np.testing.assert_array_equal(q.to_host().reshape(-1), oq)
+    d = K.dequantize_affine(q, s, z, shape, gran, axis, gs).to_host()
+    np.testing.assert_array_equal(d.reshape(-1), orc.dequantize_affine(oq, os_, oz, shape, gran, axis, gs).reshape(-1))
+
+
+def test_quant_empty_groups(dev):
+    # shape [0, 4], per-channel over axis 1: 4 groups, no elements -> scale 1, zp = qmin (asym)
+    ng = K.quant_num_groups([0, 4], "channel", 1)
+    assert ng == 4
+    x = tg.Buffer(tg.f32, (0,))
+    q, s, z, _ = K.quantize_affine(x, [0, 4], "channel", 1, symmetric=False)
+    np.testing.assert_array_equal(s.to_host(), np.ones(4, np.float32))
+    np.testing.assert_array_equal(z.to_host(), np.full(4, -128, np.int32))
