@@ -6,19 +6,22 @@
 //   silu_forward  kernels/teeny-kernels/src/nn/activation/sigmoid.rs:119-158
 //
 // MI355X design: the op moves 2 bytes in and 2 out per bf16 element with a
-// handful of VALU ops, so it is bound by HBM.  Each thread moves UNROLL
-// 16-byte vectors with all loads issued before any math (bytes in flight per
-// wave = UNROLL * 1 KiB), lanes of a wave touch consecutive 16-byte chunks so
-// every load instruction is one fully coalesced 1 KiB request, and the grid
-// has one workgroup per UNROLL*4 KiB so that a [16384, 4096] bf16 tensor
-// spreads 8192 workgroups over the 256 CUs.  Unaligned pointers or a ragged
-// tail take a scalar kernel.
+// handful of VALU ops, so it is bound by HBM.  Each thread moves UNROLL = 2
+// 16-byte vectors with both loads issued before any math; lanes of a wave
+// touch consecutive 16-byte chunks so every load instruction is one fully
+// coalesced 1 KiB request; results leave through non-temporal stores (the
+// output is not re-read by this kernel).  With ~16 VGPRs the kernel runs at
+// 8 waves per SIMD; a [16384, 4096] bf16 tensor is 16384 workgroups.  This
+// shape (2 vectors per thread, non-temporal stores) measured fastest on
+// MI355X among 1/2/4/8 vectors per thread and temporal/non-temporal
+// loads/stores, at the rate of a plain device copy.  Unaligned pointers or a
+// ragged tail take a scalar kernel.
 #include "common.hpp"
 
 namespace teeny {
 
 constexpr int kActThreads = 256;
-constexpr int kActUnroll = 4;
+constexpr int kActUnroll = 2;
 
 template <typename T, int ACT>
 __device__ __forceinline__ T act_one(T v) {
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(kActThreads) void act_vec_kernel(const T *x, T *y, 
 #pragma unroll
       for (int i = 0; i < VEC; ++i) e[i] = act_one<T, ACT>(e[i]);
       __builtin_memcpy(&r[u], e, 16);
-      reinterpret_cast<raw_t *>(y)[v] = r[u];
+      __builtin_nontemporal_store(r[u], reinterpret_cast<raw_t *>(y) + v);
     }
   }
 }

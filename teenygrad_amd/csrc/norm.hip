@@ -7,17 +7,20 @@
 //   rms_norm_forward              kernels/teeny-kernels/src/nn/norm/rmsnorm.rs:39-119
 //     two passes: sum of squares (:58-79) and rrms store (:80-83), normalise (:85-118).
 //
-// MI355X design: one wave64 owns one row.  For N <= 64 * VEC * 16 the whole
-// row is held in registers (VEC = 8 bf16 or 4 fp32 per 16-byte load), so x
-// is read from HBM exactly once and y written once: the 4-tensor-pass
-// reference becomes the 2-pass minimum with the same two-pass mean/variance
-// arithmetic done on registers.  Reductions are wave shuffles (no LDS, no
-// barriers).  Lane l of the wave loads columns [(j*64 + l)*VEC, +VEC) for
-// j < VPL, so each load instruction is one contiguous 1 KiB request.
-// gamma/beta are loaded once per wave and reused for every row the wave
-// handles (rows are strided over the grid).  Longer rows, unaligned
-// pointers or N % VEC != 0 take a multi-pass kernel with the reference's
-// pass structure.
+// MI355X design: a row is held in registers across WPR waves of one
+// workgroup (each lane VPL 16-byte vectors, VEC = 8 bf16 or 4 fp32), so x is
+// read from HBM exactly once and y written once — the reference's four
+// tensor passes become the two-pass minimum, with the same two-pass
+// mean/variance arithmetic done on registers.  Per-row sums are a wave
+// shuffle reduction plus one LDS exchange between the row's waves (one
+// barrier per statistic).  Lane l of wave p of a row loads columns
+// ((p*VPL + j)*64 + l)*VEC, so each load instruction is one contiguous 1 KiB
+// request.  For N = 4096 bf16 this is 4 waves per row and 2 vectors per lane:
+// about 40 VGPRs, 8 waves per SIMD, which keeps enough 16-byte loads in
+// flight to stream at the chip's copy rate; gamma/beta are read after the
+// reduction (L2-resident, 8 KiB).  Outputs use non-temporal stores.  Longer
+// rows, unaligned pointers or N % VEC != 0 take a multi-pass kernel with the
+// reference's pass structure.
 #include "common.hpp"
 
 namespace teeny {
@@ -26,107 +29,103 @@ constexpr int kNormThreads = 256;
 constexpr int kNormWaves = kNormThreads / 64;
 constexpr int kNormMaxBlocks = 256 * 8;
 
-template <typename T, int VPL, bool RMS, int ACT>
-__global__ __launch_bounds__(kNormThreads) void norm_reg_kernel(
+template <typename T, int WPR, int VPL, bool RMS, int ACT>
+__global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     const T *__restrict__ x, T *__restrict__ y, const T *__restrict__ gamma,
     const T *__restrict__ beta, float *__restrict__ rrms, int64_t M, int32_t N, float eps,
     float inv_n) {
   constexpr int VEC = 16 / sizeof(T);
+  constexpr int RPB = kNormWaves / WPR;  // rows per workgroup
   constexpr bool fast = !std::is_same<T, float>::value;
-  const int lane = threadIdx.x & 63;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kNormWaves;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  __shared__ float red[kNormWaves][2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int rsub = w / WPR, part = w % WPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + rsub;
+  const bool row_ok = row < M;
+  const T *xr = x + (row_ok ? row : 0) * N;
+  T *yr = y + (row_ok ? row : 0) * N;
 
-  float g[VPL][VEC], b[VPL][VEC];
+  u32x4 raw[VPL];
   bool valid[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int col = (j * 64 + lane) * VEC;
-    valid[j] = col < N;
-    if (valid[j]) {
-      u32x4 rg = *reinterpret_cast<const u32x4 *>(gamma + col);
-      T eg[VEC];
-      __builtin_memcpy(eg, &rg, 16);
+    const int col = ((part * VPL + j) * 64 + lane) * VEC;
+    valid[j] = row_ok && col < N;
+    raw[j] = valid[j] ? *reinterpret_cast<const u32x4 *>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+  float v[VPL][VEC];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) g[j][i] = to_f32(eg[i]);
-      if constexpr (!RMS) {
-        u32x4 rb = *reinterpret_cast<const u32x4 *>(beta + col);
-        T eb[VEC];
-        __builtin_memcpy(eb, &rb, 16);
+  for (int j = 0; j < VPL; ++j) {
+    T e[VEC];
+    __builtin_memcpy(e, &raw[j], 16);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) b[j][i] = to_f32(eb[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) g[j][i] = b[j][i] = 0.0f;
-    }
+    for (int i = 0; i < VEC; ++i) v[j][i] = to_f32(e[i]);  // invalid vectors hold zeros
   }
 
-  for (; row < M; row += nwaves) {
-    const T *xr = x + row * N;
-    T *yr = y + row * N;
-    u32x4 raw[VPL];
+  // row total of a per-lane partial: wave shuffle, then across the row's waves via LDS
+  auto row_sum = [&](float part_sum, int slot) {
+    part_sum = wave_sum(part_sum);
+    if (WPR == 1) return part_sum;
+    if (lane == 0) red[w][slot] = part_sum;
+    __syncthreads();
+    float t = 0.0f;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int col = (j * 64 + lane) * VEC;
-      if (valid[j]) raw[j] = *reinterpret_cast<const u32x4 *>(xr + col);
-    }
-    float v[VPL][VEC];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      T e[VEC];
-      __builtin_memcpy(e, &raw[j], 16);
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) v[j][i] = valid[j] ? to_f32(e[i]) : 0.0f;
-    }
+    for (int p = 0; p < WPR; ++p) t += red[rsub * WPR + p][slot];
+    return t;
+  };
 
-    float mean = 0.0f, rstd;
-    if constexpr (RMS) {
-      float q = 0.0f;
+  float mean = 0.0f, rstd;
+  if constexpr (RMS) {
+    float q = 0.0f;
 #pragma unroll
-      for (int j = 0; j < VPL; ++j)
+    for (int j = 0; j < VPL; ++j)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) q += v[j][i] * v[j][i];
-      q = wave_sum(q);
-      rstd = rsqrtf(q * inv_n + eps);
-      if (rrms != nullptr && lane == 0) rrms[row] = rstd;
-    } else {
-      float s = 0.0f;
+      for (int i = 0; i < VEC; ++i) q += v[j][i] * v[j][i];
+    q = row_sum(q, 0);
+    rstd = rsqrtf(q * inv_n + eps);
+    if (rrms != nullptr && row_ok && part == 0 && lane == 0) rrms[row] = rstd;
+  } else {
+    float s = 0.0f;
 #pragma unroll
-      for (int j = 0; j < VPL; ++j)
+    for (int j = 0; j < VPL; ++j)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) s += v[j][i];
-      s = wave_sum(s);
-      mean = s * inv_n;
-      float q = 0.0f;
+      for (int i = 0; i < VEC; ++i) s += v[j][i];
+    mean = row_sum(s, 0) * inv_n;
+    float q = 0.0f;
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) {
-        if (valid[j]) {
+    for (int j = 0; j < VPL; ++j) {
+      if (valid[j]) {
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            float d = v[j][i] - mean;
-            q += d * d;
-          }
+        for (int i = 0; i < VEC; ++i) {
+          const float d = v[j][i] - mean;
+          q += d * d;
         }
       }
-      q = wave_sum(q);
-      rstd = rsqrtf(q * inv_n + eps);
     }
+    rstd = rsqrtf(row_sum(q, 1) * inv_n + eps);
+  }
 
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      if (!valid[j]) continue;
-      const int col = (j * 64 + lane) * VEC;
-      T e[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        float o = RMS ? v[j][i] * rstd * g[j][i] : (v[j][i] - mean) * rstd * g[j][i] + b[j][i];
-        e[i] = from_f32<T>(apply_act<ACT, fast>(o));
-      }
-      u32x4 r;
-      __builtin_memcpy(&r, e, 16);
-      *reinterpret_cast<u32x4 *>(yr + col) = r;
+  for (int j = 0; j < VPL; ++j) {
+    if (!valid[j]) continue;
+    const int col = ((part * VPL + j) * 64 + lane) * VEC;
+    T ge[VEC], be[VEC];
+    u32x4 rg = *reinterpret_cast<const u32x4 *>(gamma + col);
+    __builtin_memcpy(ge, &rg, 16);
+    if constexpr (!RMS) {
+      u32x4 rb = *reinterpret_cast<const u32x4 *>(beta + col);
+      __builtin_memcpy(be, &rb, 16);
     }
+    T e[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float o = RMS ? v[j][i] * rstd * to_f32(ge[i])
+                          : (v[j][i] - mean) * rstd * to_f32(ge[i]) + to_f32(be[i]);
+      e[i] = from_f32<T>(apply_act<ACT, fast>(o));
+    }
+    u32x4 r;
+    __builtin_memcpy(&r, e, 16);
+    __builtin_nontemporal_store(r, reinterpret_cast<u32x4 *>(yr + col));
   }
 }
 
@@ -175,12 +174,14 @@ __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
   }
 }
 
-template <typename T, int VPL, bool RMS, int ACT>
-static void launch_reg(const void *x, void *y, const void *g, const void *b, float *rrms, int64_t M,
-                       int64_t N, float eps, float inv_n, int blocks, hipStream_t s) {
-  hipLaunchKernelGGL((norm_reg_kernel<T, VPL, RMS, ACT>), dim3(blocks), dim3(kNormThreads), 0, s,
-                     static_cast<const T *>(x), static_cast<T *>(y), static_cast<const T *>(g),
-                     static_cast<const T *>(b), rrms, M, static_cast<int32_t>(N), eps, inv_n);
+template <typename T, int WPR, int VPL, bool RMS, int ACT>
+static void launch_rows(const void *x, void *y, const void *g, const void *b, float *rrms, int64_t M,
+                        int64_t N, float eps, float inv_n, hipStream_t s) {
+  constexpr int RPB = kNormWaves / WPR;
+  hipLaunchKernelGGL((norm_rows_kernel<T, WPR, VPL, RMS, ACT>), dim3(cdiv(M, RPB)),
+                     dim3(kNormThreads), 0, s, static_cast<const T *>(x), static_cast<T *>(y),
+                     static_cast<const T *>(g), static_cast<const T *>(b), rrms, M,
+                     static_cast<int32_t>(N), eps, inv_n);
 }
 
 template <typename T, bool RMS, int ACT>
@@ -188,17 +189,24 @@ static teeny_status launch_norm(const void *x, void *y, const void *g, const voi
                                 int64_t M, int64_t N, float eps, hipStream_t s, const char *name) {
   constexpr int VEC = 16 / sizeof(T);
   const float inv_n = 1.0f / static_cast<float>(N);
-  const int blocks = static_cast<int>(std::min<int64_t>(cdiv(M, kNormWaves), kNormMaxBlocks));
   const bool vec_ok = (N % VEC == 0) && aligned(x, 16) && aligned(y, 16) && aligned(g, 16) &&
                       (RMS || aligned(b, 16));
-  const int64_t vpl = cdiv(N, 64 * VEC);
-  if (vec_ok && vpl <= 16) {
-    if (vpl <= 1) launch_reg<T, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
-    else if (vpl <= 2) launch_reg<T, 2, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
-    else if (vpl <= 4) launch_reg<T, 4, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
-    else if (vpl <= 8) launch_reg<T, 8, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
-    else launch_reg<T, 16, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, blocks, s);
+  const int64_t nv = N / VEC;  // 16-byte vectors per row
+  TEENY_REQUIRE(cdiv(M, 4) <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, std::string(name) + ": M too large");
+  if (vec_ok && nv <= 64) {
+    launch_rows<T, 1, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+  } else if (vec_ok && nv <= 128) {
+    launch_rows<T, 2, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+  } else if (vec_ok && nv <= 256) {
+    launch_rows<T, 4, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+  } else if (vec_ok && nv <= 512) {
+    launch_rows<T, 4, 2, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+  } else if (vec_ok && nv <= 1024) {
+    launch_rows<T, 4, 4, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+  } else if (vec_ok && nv <= 2048) {
+    launch_rows<T, 4, 8, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
   } else {
+    const int blocks = static_cast<int>(std::min<int64_t>(cdiv(M, kNormWaves), kNormMaxBlocks));
     hipLaunchKernelGGL((norm_multipass_kernel<T, RMS, ACT>), dim3(blocks), dim3(kNormThreads), 0,
                        s, static_cast<const T *>(x), static_cast<T *>(y),
                        static_cast<const T *>(g), static_cast<const T *>(b), rrms, M, N, eps,

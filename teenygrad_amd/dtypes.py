@@ -44,8 +44,10 @@ def from_any(d) -> DType:
 def to_bf16(a) -> np.ndarray:
     """fp32 -> bf16 bit patterns, round to nearest even."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    u = a.view(np.uint32)
+    # uint32 is wide enough: only NaN bit patterns can carry past 2^32, and
+    # NaNs are rewritten below
+    r = ((u + (np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1)))) >> np.uint32(16)).astype(np.uint16)
     nan = np.isnan(a)
     if nan.any():
         r[nan] = ((a.view(np.uint32)[nan] >> 16) | 0x40).astype(np.uint16)

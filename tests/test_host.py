@@ -102,15 +102,16 @@ def test_bf16_rounding_matches_torch():
     assert np.isnan(dtypes.from_bf16(dtypes.to_bf16(np.array([np.nan], np.float32))))[0]
 
 
-def test_synthetic_is_counter_based():
+def test_synthetic_is_seeded():
     a = synthetic.normal(123, (1000,))
-    b = synthetic.normal(123, (1000,))
-    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(a, synthetic.normal(123, (1000,)))
     assert not np.array_equal(a, synthetic.normal(124, (1000,)))
-    big = synthetic.normal(5, (1 << 23) + 17)  # spans chunks
-    assert abs(float(big.mean())) < 2e-3 and abs(float(big.std()) - 1.0) < 2e-3
+    big = synthetic.normal(5, (1 << 23) + 17, mean=1.0, std=0.02)
+    assert big.dtype == np.float32
+    assert abs(float(big.mean()) - 1.0) < 1e-4 and abs(float(big.std()) - 0.02) < 1e-4
     u = synthetic.uniform(9, (100000,), -1, 1)
     assert u.min() >= -1 and u.max() <= 1 and abs(float(u.mean())) < 1e-2
+    assert synthetic.workload_seed(1, 0) != synthetic.workload_seed(1, 1) != synthetic.workload_seed(2, 0)
 
 
 # ── host-side shape rules of the Buffer wrappers (no device needed) ─────────
