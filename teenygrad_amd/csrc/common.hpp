@@ -81,6 +81,16 @@ template <bool FAST> __device__ __forceinline__ float act_silu(float x) {
     return x * s;
   }
 }
+// Runtime-selected activation (workgroup-uniform `act`), for epilogues where
+// one kernel serves every activation.
+__device__ __forceinline__ float apply_act_rt(float x, int act) {
+  switch (act) {
+    case TEENY_ACT_RELU: return act_relu(x);
+    case TEENY_ACT_GELU_TANH: return act_gelu<true>(x);
+    case TEENY_ACT_SILU: return act_silu<true>(x);
+    default: return x;
+  }
+}
 template <int ACT, bool FAST> __device__ __forceinline__ float apply_act(float x) {
   if constexpr (ACT == TEENY_ACT_RELU) return act_relu(x);
   else if constexpr (ACT == TEENY_ACT_GELU_TANH) return act_gelu<FAST>(x);

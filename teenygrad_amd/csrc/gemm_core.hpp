@@ -11,16 +11,24 @@
 // dequant of teeny-quant's dequantize_affine (affine.rs:151-161) costs no
 // HBM traffic and its per-channel scale is applied to the fp32 accumulator.
 //
-// Tiling: BM x BN x 64 per workgroup of 256 threads (4 waves as 2 x 2), each
-// wave a (BM/2) x (BN/2) block of v_mfma_f32_32x32x16_bf16 tiles.  The MFMA
-// computes C^T (weights as the A operand, activations as the B operand) so
-// each lane's accumulator column is one output row m and four consecutive
-// registers are four consecutive n: the epilogue writes 8-byte bf16x4
-// stores.  LDS rows are padded to 72 elements (144 B), which makes the
-// 16-byte fragment reads of 16 consecutive rows hit 16 disjoint bank
-// quads.  Two LDS stages: the next k-tile is fetched into registers before
-// the current one is consumed and written to the other stage afterwards, so
-// one barrier per k-tile suffices.
+// Tiling: BM x BN x 64 per workgroup of 256 threads (4 waves as WAVES_M x
+// WAVES_N), each wave a (BM/WAVES_M) x (BN/WAVES_N) block of
+// v_mfma_f32_32x32x16_bf16 tiles.  Large tiles (256 x 256, 128 x 128 per
+// wave, accumulators in AGPRs, one workgroup per CU) need 0.5 KiB of LDS
+// fragment reads per MFMA; 128 x 128 tiles need 1 KiB, which is the LDS
+// bandwidth limit, so the launcher picks the largest tile that still fills
+// the chip.  The MFMA computes C^T (weights as the A operand, activations as
+// the B operand) so each lane's accumulator column is one output row m and
+// four consecutive registers are four consecutive n: the epilogue writes
+// 8-byte bf16x4 stores.  LDS rows are padded to 72 elements (144 B), which
+// makes the 16-byte fragment reads of 16 consecutive rows hit 16 disjoint
+// bank quads.  Two LDS stages: the next k-tile is fetched into registers
+// before the current one is consumed and written to the other stage
+// afterwards, so one barrier per k-tile suffices; within a k-tile the
+// fragments of step s+1 are read before the MFMAs of step s issue.
+// Workgroups are remapped so that each XCD (8 per chip, workgroups dealt
+// round-robin) receives a contiguous run of tiles, which share B tiles in
+// that XCD's L2.
 #pragma once
 
 #include "mfma.hpp"
@@ -44,46 +52,65 @@ struct GemmParams {
   const float *bias;   // [N] or null (fp32)
   const bf16 *bias_bf16;  // [N] or null
   int M, N, K;
+  int act;  // teeny_activation applied in the epilogue
   // implicit-GEMM conv geometry (NHWC)
   int H, W, Cin, OH, OW, KH, KW, SH, SW, PH, PW;
 };
 
-constexpr int kGemmBK = 64;
-constexpr int kGemmPitch = kGemmBK + 8;  // elements
+// Workgroup id -> tile id such that each of the 8 XCDs (which receive
+// workgroups round-robin) gets one contiguous run of tile ids.
+__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
+  const int q = nwg >> 3, r = nwg & 7;
+  const int xcd = bid & 7, slot = bid >> 3;
+  return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
 
-template <int BM, int BN, bool INT8B, int AMODE, int ACT>
-__global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
-  constexpr int BK = kGemmBK;
-  constexpr int P = kGemmPitch;
+template <int BM, int BN>
+constexpr int gemm_min_waves() {
+  return (BM * BN >= 256 * 128) ? 1 : 2;
+}
+
+// BK: k-tile depth (32 or 64).  PF: global->register prefetch depth in k-tiles (1 or 2).
+template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE, bool KVEC = true>
+__global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_kernel(GemmParams p) {
+  constexpr int P = BK + 8;                      // LDS row pitch (elements)
   constexpr int A_ELEMS = BM * P;
   constexpr int B_ELEMS = BN * P;
   constexpr int STAGE = A_ELEMS + B_ELEMS;
-  constexpr int A_CH = BM / 32;                  // 16-byte A chunks per thread
-  constexpr int B_CH = INT8B ? BN / 64 : BN / 32; // 16-byte B chunks per thread
-  constexpr int WM = BM / 2, WN = BN / 2;        // wave tile
-  constexpr int MB = WM / 32, NB = WN / 32;      // MFMA blocks per wave
+  constexpr int CPR_A = BK / 8;                  // 16-byte chunks per A (and bf16 B) row
+  constexpr int RPP_A = 256 / CPR_A;             // rows per load pass
+  constexpr int A_CH = BM / RPP_A;               // 16-byte A chunks per thread
+  constexpr int CPR_B = INT8B ? BK / 16 : BK / 8;
+  constexpr int RPP_B = 256 / CPR_B;
+  constexpr int B_CH = (BN + RPP_B - 1) / RPP_B;  // threads past row BN-1 hold no B chunk
+  constexpr int WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
+  constexpr int MB = WM / 32, NB = WN / 32;            // MFMA blocks per wave
+  static_assert(MB >= 1 && NB >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
+  static_assert(PF == 1 || PF == 2, "prefetch depth");
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WAVES_N, wn = w % WAVES_N;
 
-  // Tile order: consecutive workgroups walk down M within a BN column so that
-  // the B (weight) tile is shared through L2 by neighbours.
+  // Tile order: consecutive tile ids walk down M within a BN column, so the
+  // run of tiles one XCD receives shares B (weight) tiles through its L2.
   const int tiles_m = (p.M + BM - 1) / BM;
-  const int tm = blockIdx.x % tiles_m;
-  const int tn = blockIdx.x / tiles_m;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tm = tile % tiles_m;
+  const int tn = tile / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
 
   // ── per-thread A row state ────────────────────────────────────────────
-  const int a_col = (tid & 7) * 8;  // k offset of this thread's chunk inside the tile
+  const int a_col = (tid % CPR_A) * 8;  // k offset of this thread's chunk inside the tile
   int a_row[A_CH];
   bool a_ok[A_CH];
   const bf16 *a_base[A_CH];
   int a_ih0[A_CH], a_iw0[A_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
-    a_row[i] = (tid >> 3) + 32 * i;
+    a_row[i] = tid / CPR_A + RPP_A * i;
     const int m = m0 + a_row[i];
     a_ok[i] = m < p.M;
     if constexpr (AMODE == kAPlain) {
@@ -109,15 +136,14 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
     k_kh = r / p.KW;
   }
 
-  u32x4 areg[A_CH];
-  u32x4 breg[B_CH];
-
-  auto load_a = [&](int k0) {
+  auto load_a = [&](int k0, u32x4 (&areg)[A_CH]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int k = k0 + a_col;
       u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if constexpr (AMODE == kAPlain) {
+      if constexpr (AMODE == kAPlain && KVEC) {
+        if (a_ok[i] && k < p.K) v = *reinterpret_cast<const u32x4 *>(a_base[i] + k);
+      } else if constexpr (AMODE == kAPlain) {
         if (a_ok[i] && k + 8 <= p.K) {
           v = *reinterpret_cast<const u32x4 *>(a_base[i] + k);
         } else if (a_ok[i] && k < p.K) {
@@ -131,18 +157,24 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
         if (a_ok[i] && k < p.K && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
           v = *reinterpret_cast<const u32x4 *>(a_base[i] + (static_cast<int64_t>(ih) * p.W + iw) * p.Cin + k_ci);
       } else {
+        // element-wise gather (C_IN % 8 != 0, e.g. the 3-channel stem): the
+        // chunk's first (ci, kw, kh) is decoded once, then stepped
         bf16 e[8];
+        int ci = k % p.Cin;
+        const int r = k / p.Cin;
+        int kw = r % p.KW, kh = r / p.KW;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int kk = k + j;
           e[j] = static_cast<bf16>(0.0f);
-          if (a_ok[i] && kk < p.K) {
-            const int ci = kk % p.Cin;
-            const int r = kk / p.Cin;
-            const int kw = r % p.KW, kh = r / p.KW;
-            const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
-            if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-              e[j] = a_base[i][(static_cast<int64_t>(ih) * p.W + iw) * p.Cin + ci];
+          const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
+          if (a_ok[i] && k + j < p.K && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
+            e[j] = a_base[i][(static_cast<int64_t>(ih) * p.W + iw) * p.Cin + ci];
+          if (++ci == p.Cin) {
+            ci = 0;
+            if (++kw == p.KW) {
+              kw = 0;
+              ++kh;
+            }
           }
         }
         __builtin_memcpy(&v, e, 16);
@@ -162,24 +194,24 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
     }
   };
 
-  auto load_b = [&](int k0) {
+  auto load_b = [&](int k0, u32x4 (&breg)[B_CH]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      const int row = tid / CPR_B + RPP_B * i;
+      const int n = row < BN ? n0 + row : p.N;
       if constexpr (INT8B) {
-        const int row = (tid >> 2) + 64 * i;
-        const int k = k0 + (tid & 3) * 16;
-        const int n = n0 + row;
+        const int k = k0 + (tid % CPR_B) * 16;
         if (n < p.N && k < p.K)
           v = *reinterpret_cast<const u32x4 *>(static_cast<const int8_t *>(p.B) + static_cast<int64_t>(n) * p.ldb + k);
       } else {
-        const int row = (tid >> 3) + 32 * i;
-        const int k = k0 + (tid & 7) * 8;
-        const int n = n0 + row;
+        const int k = k0 + (tid % CPR_B) * 8;
         const bf16 *brow = static_cast<const bf16 *>(p.B) + static_cast<int64_t>(n) * p.ldb;
         // Element-wise when rows are not 16-byte aligned (scalar-gather conv,
         // where ldb = KH*KW*C_IN is arbitrary) or the chunk straddles K.
-        if (AMODE != kAConvScalar && n < p.N && k + 8 <= p.K) {
+        if (KVEC && AMODE != kAConvScalar) {
+          if (n < p.N && k < p.K) v = *reinterpret_cast<const u32x4 *>(brow + k);
+        } else if (AMODE != kAConvScalar && n < p.N && k + 8 <= p.K) {
           v = *reinterpret_cast<const u32x4 *>(brow + k);
         } else if (n < p.N && k < p.K) {
           bf16 e[8];
@@ -192,16 +224,17 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
     }
   };
 
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](int buf, const u32x4 (&areg)[A_CH], const u32x4 (&breg)[B_CH]) __attribute__((always_inline)) {
     bf16 *as = smem + buf * STAGE;
     bf16 *bs = as + A_ELEMS;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) *reinterpret_cast<u32x4 *>(as + a_row[i] * P + a_col) = areg[i];
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
+      const int row = tid / CPR_B + RPP_B * i;
+      if (row >= BN) continue;
       if constexpr (INT8B) {
-        const int row = (tid >> 2) + 64 * i;
-        const int col = (tid & 3) * 16;
+        const int col = (tid % CPR_B) * 16;
         bf16 e[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -214,8 +247,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
         *reinterpret_cast<u32x4 *>(bs + row * P + col) = lo;
         *reinterpret_cast<u32x4 *>(bs + row * P + col + 8) = hi;
       } else {
-        const int row = (tid >> 3) + 32 * i;
-        *reinterpret_cast<u32x4 *>(bs + row * P + (tid & 7) * 8) = breg[i];
+        *reinterpret_cast<u32x4 *>(bs + row * P + (tid % CPR_B) * 8) = breg[i];
       }
     }
   };
@@ -226,100 +258,172 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = zero16();
 
-  const int n_k = (p.K + BK - 1) / BK;
-  load_a(0);
-  load_b(0);
-  store_stage(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < n_k; ++kt) {
-    if (kt + 1 < n_k) {
-      load_a((kt + 1) * BK);
-      load_b((kt + 1) * BK);
-    }
-    const bf16 *as = smem + (kt & 1) * STAGE;
+  // Fragments of k-step s+1 are read before the MFMAs of step s issue; the
+  // two fragment sets are separate variables (no runtime-indexed arrays).
+  auto compute = [&](int stage) __attribute__((always_inline)) {
+    const bf16 *as = smem + stage * STAGE;
     const bf16 *bs = as + A_ELEMS;
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      bf16x8 wf[NB], xf[MB];
+    bf16x8 w0[NB], x0[MB], w1[NB], x1[MB];
+    auto read_frags = [&](int s, bf16x8 (&wf)[NB], bf16x8 (&xf)[MB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
         wf[i] = *reinterpret_cast<const bf16x8 *>(bs + (wn * WN + i * 32 + c) * P + 16 * s + 8 * g);
 #pragma unroll
       for (int j = 0; j < MB; ++j)
         xf[j] = *reinterpret_cast<const bf16x8 *>(as + (wm * WM + j * 32 + c) * P + 16 * s + 8 * g);
+    };
+    auto mma = [&](const bf16x8 (&wf)[NB], const bf16x8 (&xf)[MB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
 #pragma unroll
         for (int j = 0; j < MB; ++j) acc[i][j] = mfma32x32x16(wf[i], xf[j], acc[i][j]);
+    };
+    constexpr int S = BK / 16;
+    static_assert(S % 2 == 0, "BK must be a multiple of 32");
+    read_frags(0, w0, x0);
+#pragma unroll
+    for (int s = 0; s < S; s += 2) {
+      read_frags(s + 1, w1, x1);
+      mma(w0, x0);
+      if (s + 2 < S) read_frags(s + 2, w0, x0);
+      mma(w1, x1);
     }
-    if (kt + 1 < n_k) store_stage((kt + 1) & 1);
+  };
+
+  const int n_k = (p.K + BK - 1) / BK;
+  if constexpr (PF == 1) {
+    // one register set: tile kt+1 is fetched while tile kt is multiplied
+    u32x4 ra[A_CH], rb[B_CH];
+    load_a(0, ra);
+    load_b(0, rb);
+    store_stage(0, ra, rb);
     __syncthreads();
+    for (int kt = 0; kt < n_k; ++kt) {
+      if (kt + 1 < n_k) {
+        load_a((kt + 1) * BK, ra);
+        load_b((kt + 1) * BK, rb);
+      }
+      compute(kt & 1);
+      if (kt + 1 < n_k) store_stage((kt + 1) & 1, ra, rb);
+      __syncthreads();
+    }
+  } else {
+    // two register sets (loop unrolled by two so the sets are named
+    // statically): a tile's loads have two k-tiles of MFMA work to land
+    u32x4 ra0[A_CH], rb0[B_CH], ra1[A_CH], rb1[B_CH];
+    load_a(0, ra0);
+    load_b(0, rb0);
+    if (n_k > 1) {
+      load_a(BK, ra1);
+      load_b(BK, rb1);
+    }
+    store_stage(0, ra0, rb0);
+    __syncthreads();
+    // next_*: the set holding tile kt+1; free_*: the set tile kt+2 is loaded into
+    auto step = [&](int kt, const u32x4 (&next_a)[A_CH], const u32x4 (&next_b)[B_CH],
+                    u32x4 (&free_a)[A_CH], u32x4 (&free_b)[B_CH]) __attribute__((always_inline)) {
+      if (kt + 2 < n_k) {
+        load_a((kt + 2) * BK, free_a);
+        load_b((kt + 2) * BK, free_b);
+      }
+      compute(kt & 1);
+      if (kt + 1 < n_k) store_stage((kt + 1) & 1, next_a, next_b);
+      __syncthreads();
+    };
+    for (int kt = 0; kt < n_k; kt += 2) {
+      step(kt, ra1, rb1, ra0, rb0);
+      if (kt + 1 < n_k) step(kt + 1, ra0, rb0, ra1, rb1);
+    }
   }
 
   // ── epilogue ───────────────────────────────────────────────────────────
-  const bool vec_store = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 7) == 0);
-#pragma unroll
+  // scale / bias / activation on the fp32 accumulators, bf16 tile staged in
+  // LDS (the k-loop's last barrier freed it), then written back as 16-byte
+  // row chunks: fully coalesced, unlike the accumulator layout (4 consecutive
+  // n per lane, rows spread over lanes).  Loops are fully unrolled so every
+  // accumulator index is static and the accumulators stay in registers.
+  constexpr int CP = BN + 8;  // C tile pitch in LDS (elements)
+  static_assert(BM * CP <= 2 * STAGE, "C tile must fit in LDS");
+  bf16 *cs = smem;
+#pragma clang loop unroll(full)
   for (int j = 0; j < MB; ++j) {
-    const int m = m0 + wm * WM + j * 32 + c;
-    if (m >= p.M) continue;
-    bf16 *crow = p.C + static_cast<int64_t>(m) * p.ldc;
-#pragma unroll
+    const int ml = wm * WM + j * 32 + c;
+#pragma clang loop unroll(full)
     for (int i = 0; i < NB; ++i) {
-#pragma unroll
+#pragma clang loop unroll(full)
       for (int v4 = 0; v4 < 4; ++v4) {
-        const int nb = n0 + wn * WN + i * 32 + 8 * v4 + 4 * g;
-        float o[4];
-#pragma unroll
+        const int nl = wn * WN + i * 32 + 8 * v4 + 4 * g;
+        bf16x4 o4;
+#pragma clang loop unroll(full)
         for (int e = 0; e < 4; ++e) {
-          const int n = nb + e;
+          const int n = n0 + nl + e;
           float r = acc[i][j][4 * v4 + e];
           if (n < p.N) {
             if (p.scale != nullptr) r *= p.scale[n];
             if (p.bias != nullptr) r += p.bias[n];
             if (p.bias_bf16 != nullptr) r += static_cast<float>(p.bias_bf16[n]);
           }
-          o[e] = apply_act<ACT, true>(r);
+          o4[e] = static_cast<bf16>(apply_act_rt(r, p.act));
         }
-        if (vec_store && nb + 3 < p.N) {
-          bf16x4 o4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o4[e] = static_cast<bf16>(o[e]);
-          *reinterpret_cast<bf16x4 *>(crow + nb) = o4;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (nb + e < p.N) crow[nb + e] = static_cast<bf16>(o[e]);
-        }
+        *reinterpret_cast<bf16x4 *>(cs + ml * CP + nl) = o4;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR_C = BN / 8;        // 16-byte chunks per C row
+  constexpr int RPP_C = 256 / CPR_C;   // rows per pass
+  const bool vec16 = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+#pragma clang loop unroll(full)
+  for (int r0 = 0; r0 < BM; r0 += RPP_C) {
+    const int ml = r0 + tid / CPR_C, nl = (tid % CPR_C) * 8;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m < p.M && n < p.N) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + nl);
+      bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
+      if (vec16 && n + 8 <= p.N) {
+        *reinterpret_cast<u32x4 *>(dst) = v;
+      } else {
+        bf16 e[8];
+        __builtin_memcpy(e, &v, 16);
+        for (int t = 0; t < 8 && n + t < p.N; ++t) dst[t] = e[t];
       }
     }
   }
 }
 
-// Host launcher: picks the tile shape for the problem and instantiates the kernel.
-template <bool INT8B, int AMODE, int ACT>
-inline void launch_gemm_mfma_act(const GemmParams &p, hipStream_t s) {
-  // BN = 64 tiles for narrow outputs (e.g. the 64-channel convs), else 128.
-  if (p.N <= 64) {
-    constexpr int BM = 128, BN = 64;
-    const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, INT8B, AMODE, ACT>), dim3(grid), dim3(256), 0, s, p);
+// KVEC: K % 8 == 0 and (for the plain A path) 16-byte aligned rows, so no
+// 16-byte chunk straddles K and the element-wise tail paths are compiled out.
+template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
+inline void launch_tile(const GemmParams &p, hipStream_t s) {
+  const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  if (p.K % 8 == 0 && AMODE != kAConvScalar) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, true>), dim3(grid),
+                       dim3(256), 0, s, p);
   } else {
-    constexpr int BM = 128, BN = 128;
-    const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, INT8B, AMODE, ACT>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, false>), dim3(grid),
+                       dim3(256), 0, s, p);
   }
 }
 
+inline int64_t tiles_of(const GemmParams &p, int bm, int bn) {
+  return static_cast<int64_t>((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+}
+
+// Host launcher: 128 x 128 x 64 tiles (two workgroups per CU); narrow
+// outputs (N <= 64, e.g. the 64-channel convs) take 128 x 64 x 32 tiles with
+// a two-tile prefetch.  Measured on MI355X, larger tiles (256 x 128,
+// 256 x 256 with AGPR accumulators and one workgroup per CU) were no faster
+// for these shapes.
 template <bool INT8B, int AMODE>
-inline bool launch_gemm_mfma(const GemmParams &p, int act, hipStream_t s) {
-  switch (act) {
-    case TEENY_ACT_NONE: launch_gemm_mfma_act<INT8B, AMODE, TEENY_ACT_NONE>(p, s); return true;
-    case TEENY_ACT_RELU: launch_gemm_mfma_act<INT8B, AMODE, TEENY_ACT_RELU>(p, s); return true;
-    case TEENY_ACT_GELU_TANH: launch_gemm_mfma_act<INT8B, AMODE, TEENY_ACT_GELU_TANH>(p, s); return true;
-    case TEENY_ACT_SILU: launch_gemm_mfma_act<INT8B, AMODE, TEENY_ACT_SILU>(p, s); return true;
-    default: return false;
+inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s) {
+  if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU) return false;
+  p.act = act;
+  if (p.N <= 64) {
+    launch_tile<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
+  } else {
+    launch_tile<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
   }
+  return true;
 }
 
 }  // namespace teeny
