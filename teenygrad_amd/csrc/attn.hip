@@ -19,12 +19,18 @@
 // rounded to bf16 and fed, in exactly the registers the score MFMA wrote
 // them to, as the B operand of O^T += V^T * P^T; V is written to LDS
 // transposed ([d][key]) so that the matching A operand is two 8-byte LDS
-// reads per MFMA.  Softmax runs in the exp2 domain (scale * log2 e folded
-// into one multiply), fp32 throughout; the output is normalised once at the
-// end.  Causal tiles beyond a wave's last query are skipped per wave and
-// the query-block order is reversed so the heaviest blocks start first;
-// workgroups of one (b, h) share an XCD (blockIdx.x = bh, 8 XCDs
-// round-robin over the linear workgroup id) so K/V hit that XCD's L2.
+// reads per MFMA.  The loop is bound by VALU issue as much as by the matrix
+// cores (32 MFMAs vs 32 quarter-rate exps per lane per tile), so the softmax
+// is pared down: the tile max is taken on raw scores, scale * log2 e and the
+// max subtraction are one FMA ahead of v_exp_f32, the running output is
+// rescaled only when the max grows by more than 2^8 (a wave-uniform branch,
+// normally taken on the first tile only), and probabilities are rounded to
+// bf16 two per v_cvt_pk_bf16_f32.  fp32 throughout; the output is
+// normalised once at the end.  Causal tiles beyond a wave's last query are skipped per wave and
+// the query-block order is reversed so the heaviest blocks start first.
+// The 1-D grid is remapped so that each XCD runs the query blocks of a few
+// (b, h) pairs at a time: they stream the same K/V tiles, which then come
+// from that XCD's L2 rather than once per workgroup from HBM.
 //
 // fa_fwd_f32 (fp32, any power-of-two head_dim <= 256).  The reference's
 // per-query-row structure — grid (N_q, BH), one wave per query row — with
@@ -36,6 +42,9 @@ namespace teeny {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// Largest growth (log2 units) of a tile max over the reference point before
+// the running output is rescaled: probabilities stay <= 2^8.
+constexpr float kRescale = 8.0f;
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q,
@@ -45,20 +54,30 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
                                                       int nq, int nk, float scale_log2, int nqb) {
   constexpr int BM = 128;          // queries per workgroup
   constexpr int BN = 64;           // keys per tile
-  constexpr int KP = D + 8;        // K tile row pitch (elements): conflict-free 16-byte reads
-  constexpr int VP = BN + 4;       // V^T tile row pitch (elements): conflict-free 8-byte reads
-  constexpr int K_ELEMS = BN * KP;
-  constexpr int V_ELEMS = D * VP;
-  constexpr int STAGE = K_ELEMS + V_ELEMS;
-  constexpr int CPR = D / 8;       // 16-byte chunks per row
-  constexpr int RPP = 256 / CPR;   // K rows per load pass
-  constexpr int KPASS = BN / RPP;  // K load passes
+  constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
+  constexpr int RPB = 128 / D;     // rows per 256-byte LDS bank window
+  constexpr int RPI = 256 / CPR;   // rows covered by one load round of the workgroup
+  constexpr int NLD = BN * CPR / 256;  // load rounds per tile
+  constexpr int TILE = BN * D;     // elements of one K or V tile
   constexpr int NS = D / 16;       // k-steps of the score MFMA
   constexpr int ND = D / 32;       // d-blocks of the output
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
+  static_assert(NLD >= 1 && BN * CPR % 256 == 0, "tile must be a whole number of load rounds");
+  // K tiles (t & 1) then V tiles (t & 1), dense rows with XOR-swizzled
+  // 16-byte chunks: chunk j of row r sits at position j ^ fk(r) (K) or
+  // j ^ fv(r) (V).  fk spreads the 16 rows that one ds_read_b128 quarter-wave
+  // touches over all 64 banks; fv does the same for the 4 rows x 64 bytes
+  // that a half-wave of ds_read_b64_tr_b16 touches.
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];
+  bf16 *const kbuf = smem;
+  bf16 *const vbuf = smem + 2 * TILE;
+  auto fk = [](int row) { return (row / RPB) & (CPR - 1); };
+  auto fv = [](int row) { return (4 * (row / RPB)) & (CPR - 1) & ~3; };
 
-  const int bh = blockIdx.x;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.y);
+  // All query blocks of one (b, h) are consecutive logical ids on one XCD,
+  // so they run together and read K/V once from HBM into that XCD's L2.
+  const int tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = tile_id / nqb;
+  const int qb = nqb - 1 - tile_id % nqb;
   const int tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c = lane & 31;
   const int q0 = qb * BM + w * 32;
@@ -68,169 +87,198 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
   const bf16 *Kb = K + static_cast<int64_t>(bh) * nk * D;
   const bf16 *Vb = V + static_cast<int64_t>(bh) * nk * D;
 
+  // A negative softmax scale is applied by negating Q (exact in bf16), so the
+  // score multiplier sc is positive and the running max is a max.  It is at
+  // least FLT_MIN so that a masked -inf score maps to p = 0 even for a zero
+  // scale (where every finite score then gives p = 1 exactly, as it should).
+  const float sc = fmaxf(fabsf(scale_log2), 1.17549435e-38f);
+  const uint32_t qsign = scale_log2 < 0.0f ? 0x80008000u : 0u;
   bf16x8 qf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    if (qi < nq) {
-      qf[s] = *reinterpret_cast<const bf16x8 *>(Qb + static_cast<int64_t>(qi) * D + 16 * s + 8 * g);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[s][j] = static_cast<bf16>(0.0f);
-    }
+    u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+    if (qi < nq) raw = *reinterpret_cast<const u32x4 *>(Qb + static_cast<int64_t>(qi) * D + 16 * s + 8 * g);
+    raw ^= qsign;
+    __builtin_memcpy(&qf[s], &raw, 16);
   }
 
   f32x16 acc[ND];
 #pragma unroll
   for (int d = 0; d < ND; ++d) acc[d] = zero16();
+  // m_run: reference point of the exponentials (log2 domain, already scaled).
+  // It is raised only when a tile's max exceeds it by more than kRescale, so
+  // p = 2^(sc*s - m_run) <= 2^kRescale and O is rescaled on few tiles.
   float m_run = -INFINITY, l_run = 0.0f;
-
   const int kv_end = CAUSAL ? min(nk, qb * BM + BM) : nk;
   const int n_tiles = (kv_end + BN - 1) / BN;
   const int wave_end = CAUSAL ? min(kv_end, q0 + 32) : kv_end;
 
-  u32x4 kreg[KPASS];
-  u32x4 vreg[4];
-  const bool v_loader = tid < 16 * CPR;
-  const int v_kq = tid / CPR, v_dc = tid % CPR;
-
-  auto load_tile = [&](int kt) {
-    const int kbase = kt * BN;
+  // ── global -> LDS: one 16-byte slot per thread per round, straight into
+  // LDS (global_load_lds_dwordx4: lane j of a wave lands at base + 16 j).
+  // Slot t + 256 i of a tile is row t / CPR + RPI i, position t % CPR; the
+  // source chunk is that position XOR the row's swizzle.  Rows past nk are
+  // zero-filled so that P = 0 never meets stale data in the P*V product.
+  const int ld_row = tid / CPR;
+  const int k_off = ld_row * D + ((tid % CPR) ^ fk(ld_row)) * 8;
+  const int v_off = ld_row * D + ((tid % CPR) ^ fv(ld_row)) * 8;
+  auto load_tile = [&](const bf16 *src, bf16 *dst, int kbase, int off) __attribute__((always_inline)) {
+    const bf16 *tile_src = src + static_cast<int64_t>(kbase) * D + off;
+    typedef __attribute__((address_space(3))) void lds_void;
+    if (kbase + BN <= nk) {
 #pragma unroll
-    for (int p = 0; p < KPASS; ++p) {
-      const int row = tid / CPR + RPP * p;
-      const int key = kbase + row;
-      if (key < nk) {
-        kreg[p] = *reinterpret_cast<const u32x4 *>(Kb + static_cast<int64_t>(key) * D + (tid % CPR) * 8);
-      } else {
-        kreg[p] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-    if (v_loader) {
+      for (int i = 0; i < NLD; ++i)
+        __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
+                                         16, 0, 0);
+    } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kbase + 4 * v_kq + r;
-        if (key < nk) {
-          vreg[r] = *reinterpret_cast<const u32x4 *>(Vb + static_cast<int64_t>(key) * D + v_dc * 8);
+      for (int i = 0; i < NLD; ++i) {
+        if (kbase + ld_row + RPI * i < nk) {
+          __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
+                                           16, 0, 0);
         } else {
-          vreg[r] = u32x4{0u, 0u, 0u, 0u};
+          *reinterpret_cast<u32x4 *>(dst + (256 * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
   };
 
-  auto store_tile = [&](int buf) {
-    bf16 *ks = smem + buf * STAGE;
-    bf16 *vs = ks + K_ELEMS;
+  // ── LDS -> operands
+  // K (A operand of S^T = K Q^T): lane (g, c) reads row kb*32 + c, chunk 2st + g.
+  int koff[NS];
 #pragma unroll
-    for (int p = 0; p < KPASS; ++p) {
-      const int row = tid / CPR + RPP * p;
-      *reinterpret_cast<u32x4 *>(ks + row * KP + (tid % CPR) * 8) = kreg[p];
-    }
-    if (v_loader) {
-      // vreg[r] holds V[key 4kq + r][8 dc .. 8 dc + 7]; write V^T[8 dc + i][4 kq .. 4 kq + 3].
+  for (int st = 0; st < NS; ++st) koff[st] = c * D + ((2 * st + g) ^ fk(c)) * 8;
+  // V^T (A operand of O^T += V^T P^T) through ds_read_b64_tr_b16: in each
+  // 16-lane group, lane i receives element i & 3 of the 8-byte pieces
+  // addressed by lanes (i >> 2) + 4 j, j = 0..3.  Lane m of group h points
+  // at key 8 r + 4 g + (m >> 2) (plus kb*32 + 16 tt) and d = 32 dblk +
+  // 16 (h & 1) + 4 (m & 3), so lane l receives d = 32 dblk + l % 32 for the
+  // four keys that its P registers hold.
+  const int hh = lane >> 4, m16 = lane & 15;
+  const int v_row = 4 * g + (m16 >> 2);
+  int voff[ND];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int wi = i >> 1;
-        uint32_t lo, hi;
-        if (i & 1) {
-          lo = pack_hi(vreg[0][wi], vreg[1][wi]);
-          hi = pack_hi(vreg[2][wi], vreg[3][wi]);
-        } else {
-          lo = pack_lo(vreg[0][wi], vreg[1][wi]);
-          hi = pack_lo(vreg[2][wi], vreg[3][wi]);
-        }
-        uint2 pk;
-        pk.x = lo;
-        pk.y = hi;
-        *reinterpret_cast<uint2 *>(vs + (v_dc * 8 + i) * VP + 4 * v_kq) = pk;
+  for (int d = 0; d < ND; ++d)
+    voff[d] = v_row * D + ((4 * d + 2 * (hh & 1) + ((m16 & 3) >> 1)) ^ fv(v_row)) * 8 + (m16 & 1) * 4;
+
+  // S^T for key tile kt (K from LDS as the A operand, Q^T from registers).
+  auto score = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    const bf16 *ks = kbuf + (kt & 1) * TILE;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = zero16();
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + kb * 32 * D + koff[st]);
+        s[kb] = mfma32x32x16(a, qf[st], s[kb]);
       }
     }
   };
 
-  load_tile(0);
-  store_tile(0);
+  // Software pipeline, one barrier per key tile.  Iteration kt starts the
+  // loads of K for tile kt+2 and V for tile kt+1 (each into the buffer whose
+  // last reader finished before the previous barrier), computes the scores
+  // of tile kt+1 on the matrix cores while the softmax of tile kt runs on the
+  // VALU, accumulates P*V of tile kt, and waits for its own loads before the
+  // barrier that publishes them.
+  load_tile(Kb, kbuf, 0, k_off);
+  if (n_tiles > 1) load_tile(Kb, kbuf + TILE, BN, k_off);
+  load_tile(Vb, vbuf, 0, v_off);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  // One pipeline stage.  The loop below is unrolled by two so that the two
+  // score buffers swap roles without register copies.  The scores of tile
+  // kt+1 are computed unconditionally (one straight-line block); past the
+  // last tile they read a stale, in-bounds K buffer and are never used.
+  auto stage = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
+    if (kt + 2 < n_tiles) load_tile(Kb, kbuf + (kt & 1) * TILE, (kt + 2) * BN, k_off);
+    if (kt + 1 < n_tiles) load_tile(Vb, vbuf + ((kt + 1) & 1) * TILE, (kt + 1) * BN, v_off);
 
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    if (kt + 1 < n_tiles) load_tile(kt + 1);
-    const bf16 *ks = smem + (kt & 1) * STAGE;
-    const bf16 *vs = ks + K_ELEMS;
     const int kbase = kt * BN;
-
-    if (kbase < wave_end) {
-      f32x16 sacc[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb] = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + (kb * 32 + c) * KP + 16 * s + 8 * g);
-          sacc[kb] = mfma32x32x16(a, qf[s], sacc[kb]);
-        }
-      }
-
-      float t[2][16];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) t[kb][v] = sacc[kb][v] * scale_log2;
-
-      const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > q0);
-      if (need_mask) {
+    if (kbase < wave_end) {  // causal: later tiles are beyond this wave's last query
+      // Only the last tile and the causal diagonal hold masked keys.  The
+      // empty asm keeps this a (wave-uniform) branch: without it the
+      // compiler turns the block into selects executed on every tile.
+      if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > q0)) {
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int key = kbase + kb * 32 + mfma32_row(v, g);
-            if (key >= nk || (CAUSAL && key > qi)) t[kb][v] = -INFINITY;
+            if (key >= nk || (CAUSAL && key > qi)) s_cur[kb][v] = -INFINITY;
           }
       }
 
+      // max over the raw scores of this tile (keys are split over lane ^ 32)
       float mx = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, t[kb][v]);
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s_cur[kb][v]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float mx_s = mx * sc;  // sc > 0: -inf stays -inf
+      if (__any(mx_s > m_run + kRescale)) {
+        const float m_new = fmaxf(m_run, mx_s);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
+        m_run = m_new;
+      }
+      const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
 
-      float psum = 0.0f;
-      bf16x8 pf[2][2];
+      // One straight-line block: next tile's score MFMAs, this tile's
+      // exponentials, then this tile's P*V MFMAs, so the scheduler can issue
+      // the VALU work in the shadow of the matrix instructions.
+      score(kt + 1, s_nx);
+
+      // p = 2^(sc * s - m_run) (0 for masked keys), rounded to bf16 pairwise
+      // into exactly the registers of the B operand of the P*V product; the
+      // row sum stays in fp32 so that L = m + log(l) keeps fp32 accuracy.
+      u32x4 pw[2][2];
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = __builtin_amdgcn_exp2f(t[kb][v] - m_use);
-          psum += p;
-          pf[kb][v >> 3][v & 7] = static_cast<bf16>(p);
+        for (int v = 0; v < 16; v += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v], sc, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
+          ps[(v >> 1) & 3] += p0 + p1;
+          const bf16x2 pair = cvt_pk_bf16(p0, p1);
+          uint32_t word;
+          __builtin_memcpy(&word, &pair, 4);
+          pw[kb][v >> 3][(v & 7) >> 1] = word;
         }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+      l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
+      const bf16 *vs = vbuf + (kt & 1) * TILE;
 #pragma unroll
       for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
-
-#pragma unroll
-      for (int d = 0; d < ND; ++d) {
-        const bf16 *vrow = vs + (d * 32 + c) * VP;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
-            const int col = kb * 32 + 16 * tt + 4 * g;
-            const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(vrow + col);
-            const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(vrow + col + 8);
-            acc[d] = mfma32x32x16(cat8(lo, hi), pf[kb][tt], acc[d]);
+            const bf16 *vp = vs + (kb * 32 + 16 * tt) * D + voff[d];
+            const bf16x4 lo = ds_read_tr16(vp);
+            const bf16x4 hi = ds_read_tr16(vp + 8 * D);
+            bf16x8 pb;
+            __builtin_memcpy(&pb, &pw[kb][tt], 16);
+            acc[d] = mfma32x32x16(cat8(lo, hi), pb, acc[d]);
           }
-      }
     }
-
-    if (kt + 1 < n_tiles) store_tile((kt + 1) & 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+
+  f32x16 sa[2], sb[2];
+  score(0, sa);
+  __syncthreads();  // K buffer 0 is reloaded (tile 2) at the start of stage 0
+  for (int kt = 0; kt < n_tiles; kt += 2) {
+    stage(kt, sa, sb);
+    if (kt + 1 >= n_tiles) break;
+    stage(kt + 1, sb, sa);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -325,7 +373,7 @@ static void launch_bf16(const void *q, const void *k, const void *v, void *o, fl
                         int nk, float scale, int BH, int causal, hipStream_t s) {
   const int nqb = (nq + 127) / 128;
   const float scale_log2 = scale * kLog2e;
-  const dim3 grid(BH, nqb);
+  const dim3 grid(BH * nqb);
   if (causal) {
     hipLaunchKernelGGL((fa_fwd_bf16<D, true>), grid, dim3(256), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
@@ -355,7 +403,8 @@ extern "C" teeny_status teeny_flash_attention2_forward(const void *q, const void
   if (n_ctx_q == 0 || BH == 0) return TEENY_OK;
   TEENY_REQUIRE(n_ctx_k > 0, TEENY_ERR_SHAPE_MISMATCH,
                 "flash_attention2_forward: n_ctx_k must be positive (softmax over no keys)");
-  TEENY_REQUIRE(n_ctx_q <= 0x7fffffff && n_ctx_k <= 0x7fffffff && BH <= 65535,
+  TEENY_REQUIRE(n_ctx_q <= 0x7fffffff && n_ctx_k <= 0x7fffffff && BH <= 65535 &&
+                    BH * ((n_ctx_q + 127) / 128) <= 0x7fffffff,
                 TEENY_ERR_SHAPE_MISMATCH, "flash_attention2_forward: size out of range");
   TEENY_REQUIRE(q != nullptr && k != nullptr && v != nullptr && o != nullptr,
                 TEENY_ERR_NULL_POINTER, "flash_attention2_forward: q/k/v/o");

@@ -98,6 +98,16 @@ template <int ACT, bool FAST> __device__ __forceinline__ float apply_act(float x
   else return x;
 }
 
+// ── launch geometry ─────────────────────────────────────────────────────────
+// Workgroup id -> logical tile id such that each of the 8 XCDs (which receive
+// workgroups round-robin, each with its own L2) gets one contiguous run of
+// tile ids; neighbouring tiles that share operands then share an L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
+  const int q = nwg >> 3, r = nwg & 7;
+  const int xcd = bid & 7, slot = bid >> 3;
+  return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
 // ── wavefront reductions (wave64) ───────────────────────────────────────────
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -57,14 +57,6 @@ struct GemmParams {
   int H, W, Cin, OH, OW, KH, KW, SH, SW, PH, PW;
 };
 
-// Workgroup id -> tile id such that each of the 8 XCDs (which receive
-// workgroups round-robin) gets one contiguous run of tile ids.
-__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
-  const int q = nwg >> 3, r = nwg & 7;
-  const int xcd = bid & 7, slot = bid >> 3;
-  return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-}
-
 template <int BM, int BN>
 constexpr int gemm_min_waves() {
   return (BM * BN >= 256 * 128) ? 1 : 2;

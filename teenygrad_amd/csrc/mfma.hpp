@@ -34,6 +34,20 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 lo, bf16x4 hi) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Rounds two floats to bf16 (nearest-even) with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ bf16x2 cvt_pk_bf16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_convertvector((f32x2){a, b}, bf16x2);
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
+// element i & 3 of the 8-byte pieces addressed by lanes (i >> 2) + 4 j,
+// j = 0..3 (a 4x4 transpose of 16-bit elements per quarter of the group).
+__device__ __forceinline__ bf16x4 ds_read_tr16(const bf16 *p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p));
+}
+
 // Packs two bf16 bit patterns (low halves of a and b) into one 32-bit word.
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
   return (a & 0xffffu) | (b << 16);

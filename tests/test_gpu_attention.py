@@ -61,7 +61,8 @@ def run_bf16(dev, q, k, v, causal):
 @pytest.mark.parametrize("bh,nq,nk,d,causal", [
     (2, 128, 128, 128, False), (2, 128, 128, 128, True), (3, 200, 200, 128, True),
     (2, 100, 300, 64, False), (1, 257, 129, 128, True), (4, 64, 64, 64, True),
-    (1, 1000, 1000, 128, True), (2, 300, 77, 128, False), (1, 512, 512, 64, False)])
+    (1, 1000, 1000, 128, True), (2, 300, 77, 128, False), (1, 512, 512, 64, False),
+    (1, 33, 17, 128, False), (2, 70, 5, 64, True), (1, 130, 190, 64, True)])
 def test_bf16_vs_oracle(dev, orc, bh, nq, nk, d, causal):
     print(f"[attn bf16] bh={bh} nq={nq} nk={nk} d={d} causal={causal}", flush=True)
     q, k, v = bf16_inputs(np.random.default_rng(nq * 31 + nk), bh, nq, nk, d)
@@ -69,6 +70,22 @@ def test_bf16_vs_oracle(dev, orc, bh, nq, nk, d, causal):
     oo, ol = orc.flash_attention(q, k, v, causal=causal)
     check_bf16(o, oo, "o")
     assert np.max(np.abs(lse - ol)) < 1e-3
+
+
+@pytest.mark.parametrize("scale,causal", [(-0.125, False), (-0.0625, True), (0.0, False), (0.0, True),
+                                          (0.5, True)])
+def test_bf16_scale(dev, orc, scale, causal):
+    # a negative scale is applied by negating Q inside the kernel; a zero scale
+    # gives uniform weights over the unmasked keys
+    bh, nq, nk, d = 2, 150, 150, 128
+    print(f"[attn bf16 scale] scale={scale} causal={causal}", flush=True)
+    q, k, v = bf16_inputs(np.random.default_rng(77), bh, nq, nk, d)
+    lse = tg.Buffer(tg.f32, (bh, nq))
+    o = K.flash_attention(dev.upload(to_bf16(q), tg.bf16), dev.upload(to_bf16(k), tg.bf16),
+                          dev.upload(to_bf16(v), tg.bf16), scale, causal, lse=lse).to_host()
+    oo, ol = orc.flash_attention(q, k, v, softmax_scale=scale, causal=causal)
+    check_bf16(o, oo, "o")
+    assert np.max(np.abs(lse.to_host() - ol)) < 1e-3
 
 
 def sample_rows(bh, nq, n=48, seed=0):
