@@ -45,6 +45,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 // Largest growth (log2 units) of a tile max over the reference point before
 // the running output is rescaled: probabilities stay <= 2^8.
 constexpr float kRescale = 8.0f;
+#ifndef ATTN_LA
+#define ATTN_LA 3
+#endif
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q,
@@ -67,9 +70,13 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
   // j ^ fv(r) (V).  fk spreads the 16 rows that one ds_read_b128 quarter-wave
   // touches over all 64 banks; fv does the same for the 4 rows x 64 bytes
   // that a half-wave of ds_read_b64_tr_b16 touches.
-  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];
-  bf16 *const kbuf = smem;
-  bf16 *const vbuf = smem + 2 * TILE;
+  // Four separate arrays, and every use picks one by a compile-time parity,
+  // so the compiler can tell that a stage's LDS reads never alias the DMA
+  // it has just started into the other buffer (otherwise it waits for that
+  // DMA before the first read).
+  __shared__ __attribute__((aligned(16))) bf16 kbuf0[TILE], kbuf1[TILE], vbuf0[TILE], vbuf1[TILE];
+  auto kbuf = [&](auto par) -> bf16 * { if constexpr (decltype(par)::value) return kbuf1; else return kbuf0; };
+  auto vbuf = [&](auto par) -> bf16 * { if constexpr (decltype(par)::value) return vbuf1; else return vbuf0; };
   auto fk = [](int row) { return (row / RPB) & (CPR - 1); };
   auto fv = [](int row) { return (4 * (row / RPB)) & (CPR - 1) & ~3; };
 
@@ -143,32 +150,32 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
   };
 
   // ── LDS -> operands
-  // K (A operand of S^T = K Q^T): lane (g, c) reads row kb*32 + c, chunk 2st + g.
-  int koff[NS];
-#pragma unroll
-  for (int st = 0; st < NS; ++st) koff[st] = c * D + ((2 * st + g) ^ fk(c)) * 8;
+  // K (A operand of S^T = K Q^T): lane (g, c) reads row kb*32 + c, chunk
+  // 2 st + g, i.e. element offset koff(st) = kofs ^ (st << 4).
   // V^T (A operand of O^T += V^T P^T) through ds_read_b64_tr_b16: in each
   // 16-lane group, lane i receives element i & 3 of the 8-byte pieces
   // addressed by lanes (i >> 2) + 4 j, j = 0..3.  Lane m of group h points
   // at key 8 r + 4 g + (m >> 2) (plus kb*32 + 16 tt) and d = 32 dblk +
   // 16 (h & 1) + 4 (m & 3), so lane l receives d = 32 dblk + l % 32 for the
-  // four keys that its P registers hold.
+  // four keys that its P registers hold; offset voff(dblk) = vofs ^ (dblk << 5).
+  // In both, the step-dependent part is an XOR on offset bits that the row
+  // part does not touch, so each fragment address is one v_xor_b32 from a
+  // single per-lane base (cheaper than holding NS + ND offsets in registers).
+  static_assert(D == 64 || D == 128, "offset XOR layout assumes D of 64 or 128");
   const int hh = lane >> 4, m16 = lane & 15;
   const int v_row = 4 * g + (m16 >> 2);
-  int voff[ND];
-#pragma unroll
-  for (int d = 0; d < ND; ++d)
-    voff[d] = v_row * D + ((4 * d + 2 * (hh & 1) + ((m16 & 3) >> 1)) ^ fv(v_row)) * 8 + (m16 & 1) * 4;
+  int kofs = c * D + ((g ^ fk(c)) << 3);
+  int vofs = v_row * D + ((fv(v_row) | (2 * (hh & 1) + ((m16 & 3) >> 1))) << 3) + (m16 & 1) * 4;
 
   // S^T for key tile kt (K from LDS as the A operand, Q^T from registers).
-  auto score = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
-    const bf16 *ks = kbuf + (kt & 1) * TILE;
+  auto score = [&](auto par, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    const bf16 *ks = kbuf(par);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = zero16();
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + kb * 32 * D + koff[st]);
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + kb * 32 * D + (kofs ^ (st << 4)));
         s[kb] = mfma32x32x16(a, qf[st], s[kb]);
       }
     }
@@ -180,43 +187,61 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
   // of tile kt+1 on the matrix cores while the softmax of tile kt runs on the
   // VALU, accumulates P*V of tile kt, and waits for its own loads before the
   // barrier that publishes them.
-  load_tile(Kb, kbuf, 0, k_off);
-  if (n_tiles > 1) load_tile(Kb, kbuf + TILE, BN, k_off);
-  load_tile(Vb, vbuf, 0, v_off);
+  const std::false_type even{};
+  const std::true_type odd{};
+  load_tile(Kb, kbuf(even), 0, k_off);
+  if (n_tiles > 1) load_tile(Kb, kbuf(odd), BN, k_off);
+  load_tile(Vb, vbuf(even), 0, v_off);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  // One pipeline stage.  The loop below is unrolled by two so that the two
-  // score buffers swap roles without register copies.  The scores of tile
-  // kt+1 are computed unconditionally (one straight-line block); past the
-  // last tile they read a stale, in-bounds K buffer and are never used.
-  auto stage = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
-    if (kt + 2 < n_tiles) load_tile(Kb, kbuf + (kt & 1) * TILE, (kt + 2) * BN, k_off);
-    if (kt + 1 < n_tiles) load_tile(Vb, vbuf + ((kt + 1) & 1) * TILE, (kt + 1) * BN, v_off);
-
+  // Masks tile kt of a wave's scores (keys past nk; causal: keys past the
+  // query) and returns the raw max over the tile for each query lane.
+  auto mask_scores = [&](int kt, f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
     const int kbase = kt * BN;
-    if (kbase < wave_end) {  // causal: later tiles are beyond this wave's last query
-      // Only the last tile and the causal diagonal hold masked keys.  The
-      // empty asm keeps this a (wave-uniform) branch: without it the
-      // compiler turns the block into selects executed on every tile.
-      if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > q0)) {
-        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = kbase + kb * 32 + mfma32_row(v, g);
-            if (key >= nk || (CAUSAL && key > qi)) s_cur[kb][v] = -INFINITY;
-          }
+      for (int v = 0; v < 16; ++v) {
+        const int key = kbase + kb * 32 + mfma32_row(v, g);
+        if (key >= nk || (CAUSAL && key > qi)) sc_t[kb][v] = -INFINITY;
       }
+  };
+  auto tile_max = [&](const f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
+    // pairwise tree (depth 5) rather than a 32-long dependent chain
+    float t[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) t[v] = fmaxf(sc_t[0][v], sc_t[1][v]);
+#pragma unroll
+    for (int n = 8; n > 0; n >>= 1)
+#pragma unroll
+      for (int v = 0; v < n; ++v) t[v] = fmaxf(t[v], t[v + n]);
+    const float mx = t[0];
+    // the keys of a query are split over lanes l and l ^ 32
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  };
+  auto needs_mask = [&](int kt) {
+    return (kt * BN + BN > nk) || (CAUSAL && kt * BN + BN - 1 > q0);
+  };
 
-      // max over the raw scores of this tile (keys are split over lane ^ 32)
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s_cur[kb][v]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mx_s = mx * sc;  // sc > 0: -inf stays -inf
+  // One pipeline stage.  On entry s_cur holds the masked scores of tile kt
+  // and mx_cur their max; the stage leaves the same for tile kt+1 in s_nx and
+  // mx_cur.  The scores of tile kt+1 are computed unconditionally (past the
+  // last tile they read a stale, in-bounds K buffer and are never used).  The
+  // loop below is unrolled by two so that the two score buffers swap roles
+  // without register copies, and each stage body is one straight-line block
+  // in which the VALU work (this tile's exponentials) can issue in the
+  // shadow of the 32 MFMAs; the next tile's max closes the stage.
+  float mx_cur = -INFINITY;
+  // par is the parity of kt (compile time: the loop is unrolled by two).
+  auto stage = [&](auto par, int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
+    constexpr bool P = decltype(par)::value;
+    const std::integral_constant<bool, !P> npar{};
+    if (kt + 2 < n_tiles) load_tile(Kb, kbuf(par), (kt + 2) * BN, k_off);
+    if (kt + 1 < n_tiles) load_tile(Vb, vbuf(npar), (kt + 1) * BN, v_off);
+
+    if (kt * BN < wave_end) {  // causal: later tiles are beyond this wave's last query
+      const float mx_s = mx_cur * sc;  // sc > 0: -inf stays -inf
       if (__any(mx_s > m_run + kRescale)) {
         const float m_new = fmaxf(m_run, mx_s);
         const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
@@ -229,20 +254,44 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
       }
       const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
 
-      // One straight-line block: next tile's score MFMAs, this tile's
-      // exponentials, then this tile's P*V MFMAs, so the scheduler can issue
-      // the VALU work in the shadow of the matrix instructions.
-      score(kt + 1, s_nx);
-
-      // p = 2^(sc * s - m_run) (0 for masked keys), rounded to bf16 pairwise
-      // into exactly the registers of the B operand of the P*V product; the
-      // row sum stays in fp32 so that L = m + log(l) keeps fp32 accuracy.
-      u32x4 pw[2][2];
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; v += 2) {
+      auto body = [&]() __attribute__((always_inline)) {
+        // Hand-pipelined block of 2 NS score MFMAs (next tile) followed by
+        // 4 ND P*V MFMAs (this tile).  Each bundle is one MFMA, the LDS
+        // read(s) for the MFMA kLA bundles later (into a rotating window of
+        // kW fragments) and a slice of the softmax VALU work; a
+        // sched_barrier after each bundle keeps this order, so the reads
+        // stay kLA MFMAs ahead and the window registers are never reused
+        // while a read into them is in flight.
+        constexpr int kLA = ATTN_LA, kW = kLA + 1;
+        constexpr int nS = 2 * NS, nPV = 4 * ND;
+        constexpr int PPB = 16 / nS;  // softmax value pairs per score bundle
+        const bf16 *ks = kbuf(npar);
+        const bf16 *vs = vbuf(par);
+        // opaque per stage: the fragment addresses are re-derived here (one
+        // XOR each) rather than hoisted out of the loop into registers
+        int kofs_s = kofs, vofs_s = vofs;
+        asm volatile("" : "+v"(kofs_s), "+v"(vofs_s));
+        bf16x8 kw[kW];
+        bf16x4 vw[kW][2];
+        // score MFMA i: key block kb = i / NS, k-step st = i % NS
+        auto kread = [&](int i) __attribute__((always_inline)) {
+          kw[i % kW] = *reinterpret_cast<const bf16x8 *>(ks + (i / NS) * 32 * D + (kofs_s ^ ((i % NS) << 4)));
+        };
+        // P*V MFMA j: d-block d = j % ND, then tt, then kb
+        auto vread = [&](int j) __attribute__((always_inline)) {
+          const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
+          const bf16 *vp = vs + (kb * 32 + 16 * tt) * D + (vofs_s ^ (d << 5));
+          vw[j % kW][0] = ds_read_tr16(vp);
+          vw[j % kW][1] = ds_read_tr16(vp + 8 * D);
+        };
+        // p = 2^(sc * s - m_run) (0 for masked keys), rounded to bf16
+        // pairwise into exactly the registers of the B operand of the P*V
+        // product; the row sum stays in fp32 so that L = m + log(l) keeps
+        // fp32 accuracy.
+        u32x4 pw[2][2];
+        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto softmax_pair = [&](int q) __attribute__((always_inline)) {
+          const int kb = q >> 3, v = 2 * (q & 7);
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v], sc, neg_m));
           const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
           ps[(v >> 1) & 3] += p0 + p1;
@@ -250,38 +299,60 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
           uint32_t word;
           __builtin_memcpy(&word, &pair, 4);
           pw[kb][v >> 3][(v & 7) >> 1] = word;
-        }
-      l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        };
 
-      const bf16 *vs = vbuf + (kt & 1) * TILE;
 #pragma unroll
-      for (int d = 0; d < ND; ++d)
+        for (int i = 0; i < kLA; ++i) kread(i);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int i = 0; i < nS; ++i) {
+          const int ahead = i + kLA;
+          if (ahead < nS) kread(ahead);
+          else vread(ahead - nS);
+          const int kb = i / NS, st = i % NS;
+          s_nx[kb] = mfma32x32x16(kw[i % kW], qf[st], st == 0 ? zero16() : s_nx[kb]);
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const bf16 *vp = vs + (kb * 32 + 16 * tt) * D + voff[d];
-            const bf16x4 lo = ds_read_tr16(vp);
-            const bf16x4 hi = ds_read_tr16(vp + 8 * D);
-            bf16x8 pb;
-            __builtin_memcpy(&pb, &pw[kb][tt], 16);
-            acc[d] = mfma32x32x16(cat8(lo, hi), pb, acc[d]);
-          }
+          for (int q = 0; q < PPB; ++q) softmax_pair(i * PPB + q);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+#pragma unroll
+        for (int j = 0; j < nPV; ++j) {
+          if (j + kLA < nPV) vread(j + kLA);
+          const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
+          bf16x8 pb;
+          __builtin_memcpy(&pb, &pw[kb][tt], 16);
+          acc[d] = mfma32x32x16(cat8(vw[j % kW][0], vw[j % kW][1]), pb, acc[d]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // rare (last tile, causal diagonal): a wave-uniform branch after
+        // every MFMA of the stage has issued
+        if (needs_mask(kt + 1)) {
+          asm volatile("" ::: "memory");
+          mask_scores(kt + 1, s_nx);
+        }
+        mx_cur = tile_max(s_nx);
+      };
+      body();
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
 
   f32x16 sa[2], sb[2];
-  score(0, sa);
+  score(even, sa);
+  if (needs_mask(0)) mask_scores(0, sa);
+  mx_cur = tile_max(sa);
   __syncthreads();  // K buffer 0 is reloaded (tile 2) at the start of stage 0
   for (int kt = 0; kt < n_tiles; kt += 2) {
-    stage(kt, sa, sb);
+    stage(even, kt, sa, sb);
     if (kt + 1 >= n_tiles) break;
-    stage(kt + 1, sb, sa);
+    stage(odd, kt + 1, sb, sa);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+  const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
   if (qi < nq) {
     const float inv = 1.0f / l_tot;
     bf16 *orow = O + (static_cast<int64_t>(bh) * nq + qi) * D;
