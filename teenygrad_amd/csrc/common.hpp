@@ -16,6 +16,11 @@ teeny_status fail(teeny_status code, const std::string &msg);
 teeny_status hip_fail(hipError_t err, const char *what);
 // Called after every kernel launch: checks the launch and honours TEENY_HIP_SYNC.
 teeny_status after_launch(const char *what, hipStream_t stream);
+// Compute units of the current device (cached per device ordinal).
+int device_cu_count();
+// Makes the current device's default memory pool keep freed memory (so that
+// per-call hipMallocAsync workspaces are reused, not re-mapped); idempotent.
+bool keep_pool_memory();
 
 #define TEENY_CHECK_HIP(expr)                                                      \
   do {                                                                             \

@@ -4,6 +4,7 @@
 // mod.rs:212-490, buffer.rs:37-62, program.rs:327-390) with direct HIP runtime
 // calls.  Kernels are compiled ahead of time for gfx950, so there is no PTX
 // JIT, no nvrtc and no Triton scratch-pointer convention.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -43,6 +44,38 @@ teeny_status after_launch(const char *what, hipStream_t stream) {
     if (e != hipSuccess) return hip_fail(e, what);
   }
   return TEENY_OK;
+}
+
+bool keep_pool_memory() {
+  // The stream-ordered allocator returns freed memory to the driver at every
+  // synchronize unless the pool keeps it; split-K workspaces are allocated
+  // per call, so keep what was freed (once per device).
+  static std::atomic<int> done[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (done[dev].load(std::memory_order_acquire) == 0) {
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+      uint64_t keep = UINT64_MAX;
+      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
+    (void)hipGetLastError();
+    done[dev].store(1, std::memory_order_release);
+  }
+  return true;
+}
+
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
 }
 
 }  // namespace teeny

@@ -55,6 +55,12 @@ struct GemmParams {
   int act;  // teeny_activation applied in the epilogue
   // implicit-GEMM conv geometry (NHWC)
   int H, W, Cin, OH, OW, KH, KW, SH, SW, PH, PW;
+  // split-K: when ws is set, workgroup (tile, split) multiplies k-tiles
+  // [split * kt_split, (split + 1) * kt_split) and stores its raw fp32
+  // partial tile to ws[split][m][n]; gemm_splitk_finalize sums the splits
+  // and applies the epilogue.
+  float *ws;
+  int kt_split;
 };
 
 template <int BM, int BN>
@@ -89,10 +95,17 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   // Tile order: consecutive tile ids walk down M within a BN column, so the
   // run of tiles one XCD receives shares B (weight) tiles through its L2.
   const int tiles_m = (p.M + BM - 1) / BM;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int n_tiles = tiles_m * ((p.N + BN - 1) / BN);
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = id % n_tiles;
+  const int split = id / n_tiles;  // 0 unless split-K
   const int tm = tile % tiles_m;
   const int tn = tile / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
+  const int n_k_all = (p.K + BK - 1) / BK;
+  const int kt_begin = p.ws != nullptr ? split * p.kt_split : 0;
+  const int kt_end = p.ws != nullptr ? min(n_k_all, kt_begin + p.kt_split) : n_k_all;
+  const int k_first = kt_begin * BK;
 
   // ── per-thread A row state ────────────────────────────────────────────
   const int a_col = (tid % CPR_A) * 8;  // k offset of this thread's chunk inside the tile
@@ -122,8 +135,8 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   // implicit-GEMM k decomposition of this thread's chunk column (vector mode)
   int k_ci = 0, k_kw = 0, k_kh = 0;
   if constexpr (AMODE == kAConvVec) {
-    k_ci = a_col % p.Cin;
-    const int r = a_col / p.Cin;
+    k_ci = (k_first + a_col) % p.Cin;
+    const int r = (k_first + a_col) / p.Cin;
     k_kw = r % p.KW;
     k_kh = r / p.KW;
   }
@@ -282,18 +295,20 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     }
   };
 
-  const int n_k = (p.K + BK - 1) / BK;
+  // k-tiles of this workgroup (all of K unless split-K): kt counts from 0
+  // and k offsets are k_first + kt * BK
+  const int n_k = kt_end - kt_begin;
   if constexpr (PF == 1) {
     // one register set: tile kt+1 is fetched while tile kt is multiplied
     u32x4 ra[A_CH], rb[B_CH];
-    load_a(0, ra);
-    load_b(0, rb);
+    load_a(k_first, ra);
+    load_b(k_first, rb);
     store_stage(0, ra, rb);
     __syncthreads();
     for (int kt = 0; kt < n_k; ++kt) {
       if (kt + 1 < n_k) {
-        load_a((kt + 1) * BK, ra);
-        load_b((kt + 1) * BK, rb);
+        load_a(k_first + (kt + 1) * BK, ra);
+        load_b(k_first + (kt + 1) * BK, rb);
       }
       compute(kt & 1);
       if (kt + 1 < n_k) store_stage((kt + 1) & 1, ra, rb);
@@ -303,11 +318,11 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     // two register sets (loop unrolled by two so the sets are named
     // statically): a tile's loads have two k-tiles of MFMA work to land
     u32x4 ra0[A_CH], rb0[B_CH], ra1[A_CH], rb1[B_CH];
-    load_a(0, ra0);
-    load_b(0, rb0);
+    load_a(k_first, ra0);
+    load_b(k_first, rb0);
     if (n_k > 1) {
-      load_a(BK, ra1);
-      load_b(BK, rb1);
+      load_a(k_first + BK, ra1);
+      load_b(k_first + BK, rb1);
     }
     store_stage(0, ra0, rb0);
     __syncthreads();
@@ -315,8 +330,8 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     auto step = [&](int kt, const u32x4 (&next_a)[A_CH], const u32x4 (&next_b)[B_CH],
                     u32x4 (&free_a)[A_CH], u32x4 (&free_b)[B_CH]) __attribute__((always_inline)) {
       if (kt + 2 < n_k) {
-        load_a((kt + 2) * BK, free_a);
-        load_b((kt + 2) * BK, free_b);
+        load_a(k_first + (kt + 2) * BK, free_a);
+        load_b(k_first + (kt + 2) * BK, free_b);
       }
       compute(kt & 1);
       if (kt + 1 < n_k) store_stage((kt + 1) & 1, next_a, next_b);
@@ -334,6 +349,33 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   // row chunks: fully coalesced, unlike the accumulator layout (4 consecutive
   // n per lane, rows spread over lanes).  Loops are fully unrolled so every
   // accumulator index is static and the accumulators stay in registers.
+  if (p.ws != nullptr) {
+    // split-K partial: raw fp32 accumulators, four consecutive n per lane
+    // (16-byte stores; the four v4 stores of a lane cover 128 contiguous
+    // bytes of the row between the two lane halves)
+    float *wsp = p.ws + static_cast<int64_t>(split) * p.M * p.N;
+#pragma clang loop unroll(full)
+    for (int j = 0; j < MB; ++j) {
+      const int m = m0 + wm * WM + j * 32 + c;
+#pragma clang loop unroll(full)
+      for (int i = 0; i < NB; ++i) {
+#pragma clang loop unroll(full)
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int n = n0 + wn * WN + i * 32 + 8 * v4 + 4 * g;
+          if (m < p.M && n < p.N) {
+            float *dst = wsp + static_cast<int64_t>(m) * p.N + n;
+            if (n + 4 <= p.N && (p.N & 3) == 0) {
+              f32x4 v{acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2], acc[i][j][4 * v4 + 3]};
+              *reinterpret_cast<f32x4 *>(dst) = v;
+            } else {
+              for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = acc[i][j][4 * v4 + e];
+            }
+          }
+        }
+      }
+    }
+    return;
+  }
   constexpr int CP = BN + 8;  // C tile pitch in LDS (elements)
   static_assert(BM * CP <= 2 * STAGE, "C tile must fit in LDS");
   bf16 *cs = smem;
@@ -383,11 +425,64 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   }
 }
 
+// Sums the split-K partials ws[0..S)[m][n] and applies scale / bias /
+// activation; eight consecutive n per thread (16-byte bf16 stores).
+static __global__ __launch_bounds__(256) void gemm_splitk_finalize(GemmParams p, int S) {
+  const int64_t groups_per_row = (p.N + 7) / 8;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= groups_per_row * p.M) return;
+  const int m = static_cast<int>(gid / groups_per_row);
+  const int n0 = static_cast<int>(gid % groups_per_row) * 8;
+  const int64_t plane = static_cast<int64_t>(p.M) * p.N;
+  const float *src = p.ws + static_cast<int64_t>(m) * p.N + n0;
+  float r[8];
+  const bool vec = (p.N & 7) == 0;
+  if (vec) {
+    f32x4 a = *reinterpret_cast<const f32x4 *>(src), b = *reinterpret_cast<const f32x4 *>(src + 4);
+    for (int sp = 1; sp < S; ++sp) {
+      a += *reinterpret_cast<const f32x4 *>(src + sp * plane);
+      b += *reinterpret_cast<const f32x4 *>(src + sp * plane + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = a[e];
+      r[e + 4] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r[e] = 0.0f;
+      if (n0 + e < p.N)
+        for (int sp = 0; sp < S; ++sp) r[e] += src[sp * plane + e];
+    }
+  }
+  bf16 o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int n = n0 + e;
+    float v = r[e];
+    if (n < p.N) {
+      if (p.scale != nullptr) v *= p.scale[n];
+      if (p.bias != nullptr) v += p.bias[n];
+      if (p.bias_bf16 != nullptr) v += static_cast<float>(p.bias_bf16[n]);
+    }
+    o[e] = static_cast<bf16>(apply_act_rt(v, p.act));
+  }
+  bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n0;
+  if (vec && (p.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0) {
+    u32x4 v;
+    __builtin_memcpy(&v, o, 16);
+    *reinterpret_cast<u32x4 *>(dst) = v;
+  } else {
+    for (int e = 0; e < 8 && n0 + e < p.N; ++e) dst[e] = o[e];
+  }
+}
+
 // KVEC: K % 8 == 0 and (for the plain A path) 16-byte aligned rows, so no
 // 16-byte chunk straddles K and the element-wise tail paths are compiled out.
 template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
-inline void launch_tile(const GemmParams &p, hipStream_t s) {
-  const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+inline void launch_tile(const GemmParams &p, hipStream_t s, int splits = 1) {
+  const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * splits;
   if (p.K % 8 == 0 && AMODE != kAConvScalar) {
     hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, true>), dim3(grid),
                        dim3(256), 0, s, p);
@@ -402,20 +497,88 @@ inline int64_t tiles_of(const GemmParams &p, int bm, int bn) {
 }
 
 // Host launcher: 128 x 128 x 64 tiles (two workgroups per CU); narrow
-// outputs (N <= 64, e.g. the 64-channel convs) take 128 x 64 x 32 tiles with
-// a two-tile prefetch.  Measured on MI355X, larger tiles (256 x 128,
+// outputs (N <= 64, e.g. the 64-channel convs) and grids that 128 x 128
+// tiles leave short of the CU count take 128 x 64 x 32 tiles with a
+// two-tile prefetch.  Measured on MI355X, larger tiles (256 x 128,
 // 256 x 256 with AGPR accumulators and one workgroup per CU) were no faster
 // for these shapes.
+// Split-K factor for a BM x BN x BK tiling: deep-K problems whose tiles do
+// not even cover every CU once (the late ResNet stages: M = 3136 or 12544
+// against K = 1152..4608) are split towards two workgroups per CU, keeping
+// at least four k-tiles per split and at most four splits (the fp32
+// partials cost 8 * S * M * N bytes of extra traffic).
+inline int splitk_factor(const GemmParams &p, int bm, int bn, int bk) {
+  const int64_t tiles = tiles_of(p, bm, bn);
+  const int n_k = (p.K + bk - 1) / bk;
+  const int64_t cus = device_cu_count();
+  const int64_t target = 2 * cus;
+  if (tiles >= cus || n_k < 8) return 1;
+  int sp = static_cast<int>((target + tiles - 1) / tiles);
+  sp = min(sp, min(4, n_k / 4));
+  return max(sp, 1);
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
+inline void launch_split(GemmParams p, hipStream_t s) {
+  const int sp = splitk_factor(p, BM, BN, BK);
+  if (sp > 1) {
+    const int n_k = (p.K + BK - 1) / BK;
+    const int kt_split = (n_k + sp - 1) / sp;
+    const int used = (n_k + kt_split - 1) / kt_split;  // splits that hold k-tiles
+    void *ws = nullptr;
+    const size_t bytes = static_cast<size_t>(used) * p.M * p.N * sizeof(float);
+    // stream-ordered workspace: concurrent calls on other streams never share it
+    if (keep_pool_memory() && hipMallocAsync(&ws, bytes, s) == hipSuccess) {
+      p.ws = static_cast<float *>(ws);
+      p.kt_split = kt_split;
+      launch_tile<BM, BN, BK, WAVES_M, PF, INT8B, AMODE>(p, s, used);
+      const int64_t groups = static_cast<int64_t>(p.M) * ((p.N + 7) / 8);
+      hipLaunchKernelGGL(gemm_splitk_finalize, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256),
+                         0, s, p, used);
+      (void)hipFreeAsync(ws, s);
+      return;
+    }
+    (void)hipGetLastError();  // allocation failed: run unsplit
+  }
+  p.ws = nullptr;
+  launch_tile<BM, BN, BK, WAVES_M, PF, INT8B, AMODE>(p, s);
+}
+
+template <bool INT8B, int AMODE>
+inline bool big_gemm_fits(const GemmParams &p);
+template <bool INT8B, int AMODE>
+inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
+
+// Tile choice: the 256 x 256 large-tile kernel (gemm_big.hpp) when its
+// tiles fill the chip; else 128 x 128 x 64 when its tiles cover every CU; otherwise
+// 128 x 64 x 32 (half the work per workgroup, twice the workgroups) when
+// those do; otherwise 128 x 128 x 64 split along K.
 template <bool INT8B, int AMODE>
 inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s) {
   if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU) return false;
   p.act = act;
-  if (p.N <= 64) {
+  p.ws = nullptr;
+  const int64_t cus = device_cu_count();
+  bool big = false;
+  if constexpr (AMODE != kAConvScalar) {
+    if (big_gemm_fits<INT8B, AMODE>(p)) {
+      launch_big_gemm<INT8B, AMODE>(p, s);
+      big = true;
+    }
+  }
+  if (big) {
+  } else if (p.N <= 64) {
+    launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
+  } else if (tiles_of(p, 128, 128) >= cus) {
+    launch_tile<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
+  } else if (tiles_of(p, 128, 64) >= cus) {
     launch_tile<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
   } else {
-    launch_tile<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
+    launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
   }
   return true;
 }
 
 }  // namespace teeny
+
+#include "gemm_big.hpp"

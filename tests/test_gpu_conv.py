@@ -79,6 +79,9 @@ BF16_CASES = [
     (1, 12, 20, 7, 7, 3, 3, 1, 1, "relu"),     # C_IN % 8 != 0
     (1, 512, 2048, 7, 7, 1, 1, 1, 0, None),    # deep 1x1 (M = 49)
     (2, 64, 96, 10, 10, 3, 3, 1, 0, None),     # N = 96: BN=128 tile, half-empty
+    (2, 512, 512, 7, 7, 3, 3, 1, 1, "relu"),   # deep 3x3 (ResNet stage 4 shape): split-K
+    (2, 256, 256, 14, 14, 3, 3, 1, 1, "relu"), # ResNet stage 3 shape: split-K
+    (1, 20, 48, 8, 8, 5, 5, 1, 2, None),       # element-wise gather with split-K
 ]
 
 
@@ -98,6 +101,22 @@ def test_bf16_nhwc_mfma(dev, orc, case, with_bias):
     if act == "relu":
         ref = orc.relu(ref)
     check_bf16(got, ref, str(case))
+
+
+def test_bf16_nhwc_large_tile(dev, orc):
+    # batch 64, 56x56, 64 -> 256, 3x3: M = 200704 fills the chip with 256 x 256
+    # tiles (large-tile implicit-GEMM kernel); images 0 and 63 vs the oracle
+    B, H, Cin, Cout = 64, 56, 64, 256
+    rng = np.random.default_rng(56)
+    x = rb(rng.standard_normal((B, H, H, Cin), dtype=np.float32))
+    w = rb((rng.standard_normal((Cout, 3, 3, Cin), dtype=np.float32) * np.sqrt(2.0 / (Cin * 9))).astype(np.float32))
+    b = rb(rng.normal(0, 0.1, Cout).astype(np.float32))
+    print("[conv bf16 large tile] B=64 56x56 64->256 3x3", flush=True)
+    got = K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                   dev.upload(to_bf16(b), tg.bf16), 1, 1, 1, "relu", layout="nhwc").to_host()
+    for i in (0, B - 1):
+        ref = orc.relu(orc.conv2d_nhwc(x[i:i + 1], w, b, stride=1, padding=1))
+        check_bf16(got[i:i + 1], ref, f"image {i}")
 
 
 def test_bf16_nchw_and_grouped_direct(dev, orc):

@@ -38,6 +38,18 @@ def test_linear_bf16(dev, orc, m, n, k):
     check_bf16(got, orc.linear(x, w, b), "linear bf16")
 
 
+def test_linear_bf16_large_tile(dev, orc):
+    # 4096 x 512 x 4096: 256 x 256 tiles fill the chip -> large-tile kernel;
+    # rows 0..31 and the last 32 rows against the oracle
+    m, k, n = 4096, 512, 4096
+    rng = np.random.default_rng(4096)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb(rng.normal(0, 0.05, (n, k)).astype(np.float32))
+    y = K.linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16)).to_host()
+    for lo, hi in ((0, 32), (m - 32, m)):
+        check_bf16(y[lo:hi], orc.linear(x[lo:hi], w), f"rows {lo}..{hi}")
+
+
 def test_linear_bf16_strided_generic(dev, orc):
     # x given as a transposed view (stride_xk = M): the generic kernel path
     rng = np.random.default_rng(3)
