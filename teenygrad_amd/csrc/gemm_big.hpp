@@ -322,6 +322,28 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   // row chunks out (coalesced).
   constexpr int CP = BN + 8;
   bf16 *cs = reinterpret_cast<bf16 *>(smem);
+  // scale / bias per group of four columns (shared by the MB row blocks)
+#pragma clang loop unroll(full)
+  for (int i = 0; i < NB; ++i)
+#pragma clang loop unroll(full)
+    for (int v4 = 0; v4 < 4; ++v4) {
+      float mul[4], add[4];
+      epi_coeffs(p, n0 + wn * 128 + i * 32 + 8 * v4 + 4 * g, mul, add);
+#pragma clang loop unroll(full)
+      for (int j = 0; j < MB; ++j)
+#pragma clang loop unroll(full)
+        for (int e = 0; e < 4; ++e) acc[i][j][4 * v4 + e] = __builtin_fmaf(acc[i][j][4 * v4 + e], mul[e], add[e]);
+    }
+  const EpiAct ea = epi_act(p.act);
+  if (ea.sig) {
+#pragma clang loop unroll(full)
+    for (int i = 0; i < NB; ++i)
+#pragma clang loop unroll(full)
+      for (int j = 0; j < MB; ++j)
+#pragma clang loop unroll(full)
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = epi_sig(acc[i][j][v], ea);
+  }
+  const float lo = ea.relu ? 0.0f : -INFINITY;
 #pragma clang loop unroll(full)
   for (int j = 0; j < MB; ++j) {
     const int ml = wm * 128 + j * 32 + c;
@@ -333,14 +355,8 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
         bf16x4 o4;
 #pragma clang loop unroll(full)
         for (int e = 0; e < 4; ++e) {
-          const int n = n0 + nl + e;
-          float r = acc[i][j][4 * v4 + e];
-          if (n < p.N) {
-            if (p.scale != nullptr) r *= p.scale[n];
-            if (p.bias != nullptr) r += p.bias[n];
-            if (p.bias_bf16 != nullptr) r += static_cast<float>(p.bias_bf16[n]);
-          }
-          o4[e] = static_cast<bf16>(apply_act_rt(r, p.act));
+          const float r = acc[i][j][4 * v4 + e];
+          o4[e] = static_cast<bf16>(r < lo ? lo : r);
         }
         *reinterpret_cast<bf16x4 *>(cs + ml * CP + nl) = o4;
       }

@@ -63,6 +63,50 @@ struct GemmParams {
   int kt_split;
 };
 
+__device__ __forceinline__ void epi_coeffs(const GemmParams &p, int n, float (&mul)[4], float (&add)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int ne = n + e;
+    float m = 1.0f, a = 0.0f;
+    if (ne < p.N) {
+      if (p.scale != nullptr) m = p.scale[ne];
+      if (p.bias != nullptr) a = p.bias[ne];
+      if (p.bias_bf16 != nullptr) a += static_cast<float>(p.bias_bf16[ne]);
+    }
+    mul[e] = m;
+    add[e] = a;
+  }
+}
+
+// ── epilogue helpers ─────────────────────────────────────────────────────
+// y = act(acc * mul[n] + add[n]) with mul = scale (or 1) and add = bias
+// (fp32 or bf16, or 0).  The activation is applied branch-free per element:
+// GELU-tanh and SiLU share y = r / (1 + 2^(r * (k1 + k3 r^2))) (GELU:
+// k1 = -2 sqrt(2/pi) log2 e, k3 = 0.044715 k1; SiLU: k1 = -log2 e, k3 = 0),
+// behind one wave-uniform branch for the whole tile, and ReLU is a clamp
+// that keeps NaN (x < 0 ? 0 : x).  Same functions as act_gelu<true> /
+// act_silu<true> / act_relu.
+struct EpiAct {
+  float k1, k3;
+  bool sig, relu;
+};
+__device__ __forceinline__ EpiAct epi_act(int act) {
+  constexpr float kL2e = 1.4426950408889634f;
+  EpiAct a{0.0f, 0.0f, false, act == TEENY_ACT_RELU};
+  if (act == TEENY_ACT_GELU_TANH) {
+    a.k1 = -1.5957691216057308f * kL2e;
+    a.k3 = a.k1 * 0.044715f;
+    a.sig = true;
+  } else if (act == TEENY_ACT_SILU) {
+    a.k1 = -kL2e;
+    a.sig = true;
+  }
+  return a;
+}
+__device__ __forceinline__ float epi_sig(float r, const EpiAct &a) {
+  return r * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(r * __builtin_fmaf(a.k3, r * r, a.k1)));
+}
+// mul / add for the four consecutive columns n .. n+3 (columns past N: 1 / 0)
 template <int BM, int BN>
 constexpr int gemm_min_waves() {
   return (BM * BN >= 256 * 128) ? 1 : 2;
@@ -379,6 +423,28 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   constexpr int CP = BN + 8;  // C tile pitch in LDS (elements)
   static_assert(BM * CP <= 2 * STAGE, "C tile must fit in LDS");
   bf16 *cs = smem;
+  // scale / bias per group of four columns (shared by the MB row blocks)
+#pragma clang loop unroll(full)
+  for (int i = 0; i < NB; ++i)
+#pragma clang loop unroll(full)
+    for (int v4 = 0; v4 < 4; ++v4) {
+      float mul[4], add[4];
+      epi_coeffs(p, n0 + wn * WN + i * 32 + 8 * v4 + 4 * g, mul, add);
+#pragma clang loop unroll(full)
+      for (int j = 0; j < MB; ++j)
+#pragma clang loop unroll(full)
+        for (int e = 0; e < 4; ++e) acc[i][j][4 * v4 + e] = __builtin_fmaf(acc[i][j][4 * v4 + e], mul[e], add[e]);
+    }
+  const EpiAct ea = epi_act(p.act);
+  if (ea.sig) {
+#pragma clang loop unroll(full)
+    for (int i = 0; i < NB; ++i)
+#pragma clang loop unroll(full)
+      for (int j = 0; j < MB; ++j)
+#pragma clang loop unroll(full)
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = epi_sig(acc[i][j][v], ea);
+  }
+  const float lo = ea.relu ? 0.0f : -INFINITY;
 #pragma clang loop unroll(full)
   for (int j = 0; j < MB; ++j) {
     const int ml = wm * WM + j * 32 + c;
@@ -390,14 +456,8 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
         bf16x4 o4;
 #pragma clang loop unroll(full)
         for (int e = 0; e < 4; ++e) {
-          const int n = n0 + nl + e;
-          float r = acc[i][j][4 * v4 + e];
-          if (n < p.N) {
-            if (p.scale != nullptr) r *= p.scale[n];
-            if (p.bias != nullptr) r += p.bias[n];
-            if (p.bias_bf16 != nullptr) r += static_cast<float>(p.bias_bf16[n]);
-          }
-          o4[e] = static_cast<bf16>(apply_act_rt(r, p.act));
+          const float r = acc[i][j][4 * v4 + e];
+          o4[e] = static_cast<bf16>(r < lo ? lo : r);
         }
         *reinterpret_cast<bf16x4 *>(cs + ml * CP + nl) = o4;
       }
