@@ -195,6 +195,102 @@ static GemmParams conv_gemm_params(const void *x, const void *w, const float *sc
   return p;
 }
 
+// ── stride-2 convs over few input channels (the 3-channel ResNet stem) ───
+// A C_IN that is not a multiple of 8 forces the element-wise gather.  For
+// stride 2 the conv is rewritten exactly as a stride-1 conv on the
+// space-to-depth tensor
+//   xs[b][u][v][(2 dy + dx) C + c] = x_pad[b][2 u + dy][2 v + dx][c]
+// (4 C channels, zero-padded to C2 = a multiple of 8, so the implicit GEMM
+// gathers 16-byte chunks) with a ceil(KH/2) x ceil(KW/2) kernel
+//   ws[n][kh2][kw2][(2 dy + dx) C + c] = w[n][2 kh2 + dy][2 kw2 + dx][c]
+// (0 where 2 kh2 + dy >= KH or 2 kw2 + dx >= KW): output (oh, ow) reads
+// x_pad rows 2 (oh + kh2) + dy = 2 oh + kh, the same taps.  The two repacked
+// tensors live in a stream-ordered workspace.
+__global__ __launch_bounds__(256) void s2d_input_kernel(const bf16 *__restrict__ x, bf16 *__restrict__ xs,
+                                                        int B, int H, int W, int C, int PH, int PW, int Hs,
+                                                        int Ws, int C2) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(B) * Hs * Ws;
+  if (t >= total) return;
+  const int v = static_cast<int>(t % Ws);
+  const int u = static_cast<int>((t / Ws) % Hs);
+  const int b = static_cast<int>(t / (static_cast<int64_t>(Ws) * Hs));
+  bf16 *dst = xs + t * C2;
+  for (int c0 = 0; c0 < C2; c0 += 8) {
+    bf16 e[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ch = c0 + k;
+      float val = 0.0f;
+      if (ch < 4 * C) {
+        const int q = ch / C, c = ch % C;
+        const int ih = 2 * u + (q >> 1) - PH, iw = 2 * v + (q & 1) - PW;
+        if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+          val = static_cast<float>(x[((static_cast<int64_t>(b) * H + ih) * W + iw) * C + c]);
+      }
+      e[k] = static_cast<bf16>(val);
+    }
+    u32x4 pk;
+    __builtin_memcpy(&pk, e, 16);
+    *reinterpret_cast<u32x4 *>(dst + c0) = pk;
+  }
+}
+
+__global__ __launch_bounds__(256) void s2d_weight_kernel(const bf16 *__restrict__ w, bf16 *__restrict__ ws,
+                                                         int N, int KH, int KW, int C, int KH2, int KW2,
+                                                         int C2) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(N) * KH2 * KW2 * C2;
+  if (t >= total) return;
+  const int ch = static_cast<int>(t % C2);
+  const int kw2 = static_cast<int>((t / C2) % KW2);
+  const int kh2 = static_cast<int>((t / (static_cast<int64_t>(C2) * KW2)) % KH2);
+  const int n = static_cast<int>(t / (static_cast<int64_t>(C2) * KW2 * KH2));
+  float val = 0.0f;
+  if (ch < 4 * C) {
+    const int q = ch / C, c = ch % C;
+    const int kh = 2 * kh2 + (q >> 1), kw = 2 * kw2 + (q & 1);
+    if (kh < KH && kw < KW) val = static_cast<float>(w[((static_cast<int64_t>(n) * KH + kh) * KW + kw) * C + c]);
+  }
+  ws[t] = static_cast<bf16>(val);
+}
+
+// Runs the space-to-depth form of a stride-2 bf16 NHWC conv (C_IN % 8 != 0).
+// Returns false (nothing launched) if the workspace cannot be allocated.
+static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, void *y, const ConvGeo &q,
+                          int act, hipStream_t s) {
+  const int C2 = (4 * q.Cin + 7) / 8 * 8;
+  const int KH2 = (q.KH + 1) / 2, KW2 = (q.KW + 1) / 2;
+  const int Hs = q.OH + KH2 - 1, Ws = q.OW + KW2 - 1;
+  const size_t xs_elems = static_cast<size_t>(q.B) * Hs * Ws * C2;
+  const size_t ws_elems = static_cast<size_t>(q.Cout) * KH2 * KW2 * C2;
+  const size_t ws_off = (xs_elems * sizeof(bf16) + 255) / 256 * 256;
+  void *buf = nullptr;
+  if (!keep_pool_memory() || hipMallocAsync(&buf, ws_off + ws_elems * sizeof(bf16), s) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  bf16 *xs = static_cast<bf16 *>(buf);
+  bf16 *wsd = reinterpret_cast<bf16 *>(static_cast<char *>(buf) + ws_off);
+  const int64_t nx = static_cast<int64_t>(q.B) * Hs * Ws;
+  hipLaunchKernelGGL(s2d_input_kernel, dim3(static_cast<unsigned>((nx + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const bf16 *>(x), xs, q.B, q.H, q.W, q.Cin, q.PH, q.PW, Hs, Ws, C2);
+  hipLaunchKernelGGL(s2d_weight_kernel, dim3(static_cast<unsigned>((ws_elems + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const bf16 *>(w), wsd, q.Cout, q.KH, q.KW, q.Cin, KH2, KW2, C2);
+  ConvGeo g2 = q;
+  g2.Cin = C2;
+  g2.H = Hs;
+  g2.W = Ws;
+  g2.KH = KH2;
+  g2.KW = KW2;
+  g2.SH = g2.SW = 1;
+  g2.PH = g2.PW = 0;
+  GemmParams p = conv_gemm_params(xs, wsd, nullptr, nullptr, bias_bf16, y, g2);
+  launch_gemm_mfma<false, kAConvVec>(p, act, s);
+  (void)hipFreeAsync(buf, s);
+  return true;
+}
+
 // bf16 NHWC, groups == 1 -> MFMA implicit GEMM.  Returns false if not taken.
 template <bool INT8B>
 static bool try_conv_mfma(const void *x, const void *w, const float *scale, const float *bias,
@@ -214,6 +310,9 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
     return one_by_one ? launch_gemm_mfma<false, kAPlain>(p, act, s)
                       : launch_gemm_mfma<false, kAConvVec>(p, act, s);
   }
+  if (q.SH == 2 && q.SW == 2 && act >= TEENY_ACT_NONE && act <= TEENY_ACT_SILU && scale == nullptr &&
+      bias == nullptr && conv_s2d_mfma(x, w, bias_bf16, y, q, act, s))
+    return true;
   return launch_gemm_mfma<false, kAConvScalar>(p, act, s);
 }
 

@@ -64,6 +64,33 @@ struct GemmParams {
 };
 
 __device__ __forceinline__ void epi_coeffs(const GemmParams &p, int n, float (&mul)[4], float (&add)[4]) {
+  if (n + 4 <= p.N && (n & 3) == 0) {
+    // four in-range columns: vector loads (n % 4 == 0 keeps them aligned)
+    f32x4 m4 = {1.0f, 1.0f, 1.0f, 1.0f}, a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.scale != nullptr && (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0)
+      m4 = *reinterpret_cast<const f32x4 *>(p.scale + n);
+    else if (p.scale != nullptr)
+      for (int e = 0; e < 4; ++e) m4[e] = p.scale[n + e];
+    if (p.bias != nullptr && (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0)
+      a4 = *reinterpret_cast<const f32x4 *>(p.bias + n);
+    else if (p.bias != nullptr)
+      for (int e = 0; e < 4; ++e) a4[e] = p.bias[n + e];
+    if (p.bias_bf16 != nullptr) {
+      bf16x4 b4;
+      if ((reinterpret_cast<uintptr_t>(p.bias_bf16) & 7) == 0) {
+        b4 = *reinterpret_cast<const bf16x4 *>(p.bias_bf16 + n);
+      } else {
+        for (int e = 0; e < 4; ++e) b4[e] = p.bias_bf16[n + e];
+      }
+      for (int e = 0; e < 4; ++e) a4[e] += static_cast<float>(b4[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mul[e] = m4[e];
+      add[e] = a4[e];
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int ne = n + e;
@@ -136,15 +163,19 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   const int lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
   const int wm = w / WAVES_N, wn = w % WAVES_N;
 
-  // Tile order: consecutive tile ids walk down M within a BN column, so the
-  // run of tiles one XCD receives shares B (weight) tiles through its L2.
   const int tiles_m = (p.M + BM - 1) / BM;
-  const int n_tiles = tiles_m * ((p.N + BN - 1) / BN);
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int n_tiles = tiles_m * tiles_n;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % n_tiles;
   const int split = id / n_tiles;  // 0 unless split-K
-  const int tm = tile % tiles_m;
-  const int tn = tile / tiles_m;
+  // Consecutive tiles (one XCD's run) share an operand through its L2: with
+  // few column tiles (narrow outputs, e.g. 1x1 convs) the column tiles of a
+  // row block are adjacent, so A is read from HBM once; otherwise tiles walk
+  // down M within a column and share B.
+  const bool n_fast = tiles_n <= 4;
+  const int tm = n_fast ? tile / tiles_n : tile % tiles_m;
+  const int tn = n_fast ? tile % tiles_n : tile / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const int n_k_all = (p.K + BK - 1) / BK;
   const int kt_begin = p.ws != nullptr ? split * p.kt_split : 0;

@@ -82,6 +82,10 @@ BF16_CASES = [
     (2, 512, 512, 7, 7, 3, 3, 1, 1, "relu"),   # deep 3x3 (ResNet stage 4 shape): split-K
     (2, 256, 256, 14, 14, 3, 3, 1, 1, "relu"), # ResNet stage 3 shape: split-K
     (1, 20, 48, 8, 8, 5, 5, 1, 2, None),       # element-wise gather with split-K
+    (2, 3, 32, 29, 31, 7, 7, 2, 3, None),      # stride-2 space-to-depth, odd sizes
+    (1, 3, 16, 20, 20, 3, 3, 2, 1, "relu"),    # space-to-depth, 3x3 -> 2x2
+    (1, 1, 8, 15, 15, 5, 5, 2, 2, None),       # space-to-depth, one channel
+    (2, 6, 24, 12, 12, 4, 4, 2, 0, "relu"),    # space-to-depth, C2 = 24, even kernel
 ]
 
 
