@@ -593,17 +593,18 @@ inline int64_t tiles_of(const GemmParams &p, int bm, int bn) {
 // two-tile prefetch.  Measured on MI355X, larger tiles (256 x 128,
 // 256 x 256 with AGPR accumulators and one workgroup per CU) were no faster
 // for these shapes.
-// Split-K factor for a BM x BN x BK tiling: deep-K problems whose tiles do
-// not even cover every CU once (the late ResNet stages: M = 3136 or 12544
-// against K = 1152..4608) are split towards two workgroups per CU, keeping
-// at least four k-tiles per split and at most four splits (the fp32
-// partials cost 8 * S * M * N bytes of extra traffic).
+// Split-K factor for a BM x BN x BK tiling: only deep-K problems (K >= 2048)
+// whose tiles cover fewer than half the CUs (ResNet stage 4: 100 tiles, K =
+// 2048 and 4608) are split, towards two workgroups per CU, with at most
+// four splits (the fp32 partials cost 8 * S * M * N bytes of extra
+// traffic).  Measured on MI355X: at 196 tiles (stage 3) splitting does not
+// pay.
 inline int splitk_factor(const GemmParams &p, int bm, int bn, int bk) {
   const int64_t tiles = tiles_of(p, bm, bn);
   const int n_k = (p.K + bk - 1) / bk;
   const int64_t cus = device_cu_count();
   const int64_t target = 2 * cus;
-  if (tiles >= cus || n_k < 8) return 1;
+  if (2 * tiles >= cus || n_k * bk < 2048) return 1;
   int sp = static_cast<int>((target + tiles - 1) / tiles);
   sp = min(sp, min(4, n_k / 4));
   return max(sp, 1);
@@ -641,9 +642,8 @@ template <bool INT8B, int AMODE>
 inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
 
 // Tile choice: the 256 x 256 large-tile kernel (gemm_big.hpp) when its
-// tiles fill the chip; else 128 x 128 x 64 when its tiles cover every CU; otherwise
-// 128 x 64 x 32 (half the work per workgroup, twice the workgroups) when
-// those do; otherwise 128 x 128 x 64 split along K.
+// tiles fill the chip; else 128 x 64 x 32 for narrow outputs (N <= 64) and
+// 128 x 128 x 64 otherwise, either split along K when badly under-filled.
 template <bool INT8B, int AMODE>
 inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s) {
   if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU) return false;
@@ -657,13 +657,10 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s) {
       big = true;
     }
   }
+  (void)cus;
   if (big) {
   } else if (p.N <= 64) {
     launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
-  } else if (tiles_of(p, 128, 128) >= cus) {
-    launch_tile<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
-  } else if (tiles_of(p, 128, 64) >= cus) {
-    launch_tile<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
   } else {
     launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
   }

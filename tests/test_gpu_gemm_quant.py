@@ -27,7 +27,8 @@ def test_linear_f32_fixture(dev, orc, with_bias):
     check_f32(got, orc.linear(x, w, b if with_bias else None), "linear f32")
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 300, 136), (64, 48, 64), (33, 17, 70), (256, 512, 1000)])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 300, 136), (64, 48, 64), (33, 17, 70), (256, 512, 1000),
+                                   (64, 256, 4096), (96, 200, 3100)])  # last two: split-K (plain, ragged K)
 def test_linear_bf16(dev, orc, m, n, k):
     rng = np.random.default_rng(m + n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
