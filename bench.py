@@ -269,6 +269,16 @@ def resnet50_convs():
     return layers
 
 
+def attach_workspace(tg, dev, stream, sizes):
+    """Gives the stream one caller-owned scratch buffer big enough for every
+    op of the workload (split-K partials, space-to-depth copies); returns
+    its size.  Allocated before timing, as an executor would."""
+    need = max(list(sizes) + [0])
+    if need > 0:
+        stream.set_workspace(dev.buffer(tg.i8, (need,)))
+    return need
+
+
 def bench_resnet(args, tg, dev, stream):
     from teenygrad_amd import kernels as K
     from teenygrad_amd.dtypes import to_bf16
@@ -290,6 +300,10 @@ def bench_resnet(args, tg, dev, stream):
         flops += f
         total_bytes += 2 * (B * h * h * cin + cout * k * k * cin + cout + B * oh * oh * cout)
         bufs.append((name, x, w, b, y, s, p, relu, f))
+    ws = attach_workspace(tg, dev, stream, (
+        K.conv2d_workspace_size((B, h, h, cin), (cout, k, k, cin), s, p, 1, tg.bf16, "nhwc")
+        for name, cin, cout, h, k, s, p, relu in layers))
+    log(f"[bench] stream workspace {ws / 2**20:.1f} MiB")
 
     def step(t):
         for name, x, w, b, y, s, p, relu, _ in bufs:
@@ -330,6 +344,8 @@ def bench_w8a16(args, tg, dev, stream):
         del wf
         y = tg.Buffer(tg.bf16, (m, n))
         problems.append((f"w8a16 {m}x{k}->{n}", x, q, s, y, 2.0 * m * n * k))
+    attach_workspace(tg, dev, stream, (K.linear_workspace_size(m, n, k, tg.i8)
+                                       for k, n in ((4096, 11008), (11008, 4096))))
 
     def step(t):
         for name, x, q, s, y, _ in problems:
@@ -363,6 +379,7 @@ def bench_w8a16_conv(args, tg, dev, stream):
     y = tg.Buffer(tg.bf16, (B, H, H, C))
     flops = 2.0 * B * H * H * C * C * 9
     name = "w8a16_conv3x3"
+    attach_workspace(tg, dev, stream, [K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)])
 
     def step(t):
         launch(t, name, lambda: K.w8a16_conv2d(x, q, s, None, 1, 1, y=y, stream=stream))

@@ -21,7 +21,9 @@
  *     has one) and a stream.  Element counts and dimensions are int64_t where
  *     the reference used i32, so tensors beyond 2^31 elements are addressable.
  *   - Operators never allocate and never synchronize: work is enqueued on the
- *     given stream (NULL = the device's null stream).  Setting the
+ *     given stream (NULL = the device's null stream).  Scratch, where a
+ *     faster path wants it, is a caller-owned buffer attached to the stream
+ *     (teeny_hip_stream_set_workspace).  Setting the
  *     environment variable TEENY_HIP_SYNC=1 makes every operator synchronize
  *     the stream after its launch, reproducing the reference executor's
  *     synchronize-after-every-launch behaviour
@@ -145,6 +147,18 @@ teeny_status teeny_hip_memset(void *dst, int32_t value, size_t bytes, teeny_stre
 teeny_status teeny_hip_stream_create(teeny_stream *stream);
 teeny_status teeny_hip_stream_destroy(teeny_stream stream);
 teeny_status teeny_hip_stream_sync(teeny_stream stream);
+/* Attaches a caller-owned device buffer (256-byte aligned) to a stream as
+ * operator scratch; ptr NULL or bytes 0 detaches.  Operators never allocate:
+ * the paths that need scratch -- split-K partial sums for GEMM and conv grids
+ * too small to fill the device, and the space-to-depth copy of stride-2 NHWC
+ * convs whose C_IN is not a multiple of 8 -- run only when the stream's
+ * workspace is large enough (sizes from teeny_linear_workspace_size and
+ * teeny_conv2d_workspace_size), and otherwise the operator takes a path that
+ * needs none.  Work on one stream runs in order, so every operator on it may
+ * share the buffer; the buffer must outlive the work enqueued while it is
+ * attached.  Destroying the stream detaches it.  Reference counterpart: none
+ * (the reference's ops use no scratch; this mirrors cublasSetWorkspace). */
+teeny_status teeny_hip_stream_set_workspace(teeny_stream stream, void *ptr, size_t bytes);
 teeny_status teeny_hip_event_create(teeny_event *event);
 teeny_status teeny_hip_event_destroy(teeny_event event);
 teeny_status teeny_hip_event_record(teeny_event event, teeny_stream stream);
@@ -304,6 +318,12 @@ teeny_status teeny_linear_forward(const void *x, const void *w, const void *b, v
                                   int64_t stride_ym, int64_t stride_yn, teeny_dtype dtype,
                                   teeny_stream stream);
 
+/* Stream workspace (teeny_hip_stream_set_workspace) that lets linear_forward
+ * (dtype F32/BF16, contiguous operands) or w8a16_linear_forward (dtype I8)
+ * take its fastest plan at this shape; 0 if it uses none. */
+teeny_status teeny_linear_workspace_size(int64_t M, int64_t N, int64_t K, teeny_dtype dtype,
+                                         size_t *bytes);
+
 /* W8A16 linear: y[m,n] = scale[n] * sum_k x[m,k] * q[n,k] (+ bias[n]).
  * x bf16 [M,K] row-major, q int8 [N,K] row-major (teeny-quant per-channel
  * axis-0 symmetric output), scale fp32 [N], bias fp32 [N] or NULL, y bf16
@@ -323,6 +343,13 @@ teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, co
                                         int64_t C_OUT, int64_t H, int64_t W, int64_t OH,
                                         int64_t OW, const teeny_conv2d_params *params,
                                         teeny_stream stream);
+
+/* Stream workspace that lets conv2d_forward / conv2d_bias_forward (dtype
+ * F32/BF16) or w8a16_conv2d_forward (dtype I8, layout NHWC) take its fastest
+ * plan at this shape; 0 if it uses none. */
+teeny_status teeny_conv2d_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                         int64_t OH, int64_t OW, const teeny_conv2d_params *params,
+                                         teeny_dtype dtype, teeny_layout layout, size_t *bytes);
 
 /* ── reference-shaped dispatch ────────────────────────────────────────────
  * Runs an operator from exactly the argument list that the reference's

@@ -98,6 +98,7 @@ _SIGS = {
     "teeny_hip_stream_create": (S, [POINTER(c_void_p)]),
     "teeny_hip_stream_destroy": (S, [P]),
     "teeny_hip_stream_sync": (S, [P]),
+    "teeny_hip_stream_set_workspace": (S, [P, P, c_size_t]),
     "teeny_hip_event_create": (S, [POINTER(c_void_p)]),
     "teeny_hip_event_destroy": (S, [P]),
     "teeny_hip_event_record": (S, [P, P]),
@@ -122,6 +123,8 @@ _SIGS = {
     "teeny_dequantize_affine": (S, [P, P, P, POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, P, P]),
     "teeny_linear_forward": (S, [P, P, P, P] + [c_int64] * 9 + [c_int32, P]),
     "teeny_w8a16_linear_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_int64, c_int32, P]),
+    "teeny_linear_workspace_size": (S, [c_int64, c_int64, c_int64, c_int32, POINTER(c_size_t)]),
+    "teeny_conv2d_workspace_size": (S, [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, POINTER(c_size_t)]),
     "teeny_w8a16_conv2d_forward": (S, [P, P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), P]),
     "teeny_dispatch": (S, [c_char_p, POINTER(c_int64), c_int32, POINTER(TeenyArg), c_int32, POINTER(c_uint32), c_int32, P]),
 }

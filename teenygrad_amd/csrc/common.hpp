@@ -18,9 +18,15 @@ teeny_status hip_fail(hipError_t err, const char *what);
 teeny_status after_launch(const char *what, hipStream_t stream);
 // Compute units of the current device (cached per device ordinal).
 int device_cu_count();
-// Makes the current device's default memory pool keep freed memory (so that
-// per-call hipMallocAsync workspaces are reused, not re-mapped); idempotent.
-bool keep_pool_memory();
+// Caller-owned device scratch attached to a stream with
+// teeny_hip_stream_set_workspace ({nullptr, 0} if none).  Operators never
+// allocate: paths that need scratch (split-K partial sums, the
+// space-to-depth copy of a stride-2 conv) run only when it is large enough.
+struct Scratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+Scratch stream_scratch(hipStream_t stream);
 
 #define TEENY_CHECK_HIP(expr)                                                      \
   do {                                                                             \

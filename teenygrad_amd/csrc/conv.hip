@@ -205,7 +205,7 @@ static GemmParams conv_gemm_params(const void *x, const void *w, const float *sc
 //   ws[n][kh2][kw2][(2 dy + dx) C + c] = w[n][2 kh2 + dy][2 kw2 + dx][c]
 // (0 where 2 kh2 + dy >= KH or 2 kw2 + dx >= KW): output (oh, ow) reads
 // x_pad rows 2 (oh + kh2) + dy = 2 oh + kh, the same taps.  The two repacked
-// tensors live in a stream-ordered workspace.
+// tensors live in the caller's scratch (the stream's workspace).
 __global__ __launch_bounds__(256) void s2d_input_kernel(const bf16 *__restrict__ x, bf16 *__restrict__ xs,
                                                         int B, int H, int W, int C, int PH, int PW, int Hs,
                                                         int Ws, int C2) {
@@ -255,39 +255,85 @@ __global__ __launch_bounds__(256) void s2d_weight_kernel(const bf16 *__restrict_
   ws[t] = static_cast<bf16>(val);
 }
 
-// Runs the space-to-depth form of a stride-2 bf16 NHWC conv (C_IN % 8 != 0).
-// Returns false (nothing launched) if the workspace cannot be allocated.
-static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, void *y, const ConvGeo &q,
-                          int act, hipStream_t s) {
-  const int C2 = (4 * q.Cin + 7) / 8 * 8;
-  const int KH2 = (q.KH + 1) / 2, KW2 = (q.KW + 1) / 2;
-  const int Hs = q.OH + KH2 - 1, Ws = q.OW + KW2 - 1;
-  const size_t xs_elems = static_cast<size_t>(q.B) * Hs * Ws * C2;
-  const size_t ws_elems = static_cast<size_t>(q.Cout) * KH2 * KW2 * C2;
-  const size_t ws_off = (xs_elems * sizeof(bf16) + 255) / 256 * 256;
-  void *buf = nullptr;
-  if (!keep_pool_memory() || hipMallocAsync(&buf, ws_off + ws_elems * sizeof(bf16), s) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  bf16 *xs = static_cast<bf16 *>(buf);
-  bf16 *wsd = reinterpret_cast<bf16 *>(static_cast<char *>(buf) + ws_off);
-  const int64_t nx = static_cast<int64_t>(q.B) * Hs * Ws;
-  hipLaunchKernelGGL(s2d_input_kernel, dim3(static_cast<unsigned>((nx + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16 *>(x), xs, q.B, q.H, q.W, q.Cin, q.PH, q.PW, Hs, Ws, C2);
-  hipLaunchKernelGGL(s2d_weight_kernel, dim3(static_cast<unsigned>((ws_elems + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16 *>(w), wsd, q.Cout, q.KH, q.KW, q.Cin, KH2, KW2, C2);
-  ConvGeo g2 = q;
-  g2.Cin = C2;
-  g2.H = Hs;
-  g2.W = Ws;
-  g2.KH = KH2;
-  g2.KW = KW2;
+// Scratch layout of the space-to-depth form: the rewritten input
+// [B, Hs, Ws, C2], then the rewritten weights [C_OUT, KH2, KW2, C2], then the
+// GEMM's own scratch, each at a 256-byte offset.
+struct S2DPlan {
+  ConvGeo g2;  // the stride-1 conv that the rewrite turns the call into
+  size_t xs_bytes, w_off, gemm_off;
+};
+
+static size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+static S2DPlan s2d_plan(const ConvGeo &q) {
+  S2DPlan sp;
+  ConvGeo &g2 = sp.g2;
+  g2 = q;
+  g2.Cin = (4 * q.Cin + 7) / 8 * 8;
+  g2.KH = (q.KH + 1) / 2;
+  g2.KW = (q.KW + 1) / 2;
+  g2.H = q.OH + g2.KH - 1;
+  g2.W = q.OW + g2.KW - 1;
   g2.SH = g2.SW = 1;
   g2.PH = g2.PW = 0;
+  sp.xs_bytes = static_cast<size_t>(q.B) * g2.H * g2.W * g2.Cin * sizeof(bf16);
+  sp.w_off = round256(sp.xs_bytes);
+  sp.gemm_off = sp.w_off + round256(static_cast<size_t>(q.Cout) * g2.KH * g2.KW * g2.Cin * sizeof(bf16));
+  return sp;
+}
+
+// How a groups == 1 bf16 NHWC conv maps onto the MFMA GEMM.
+enum ConvPath { kConvNoMfma, kConvPlain, kConvVec, kConvS2D, kConvScalarGemm };
+
+template <bool INT8B>
+static ConvPath conv_path(const ConvGeo &q) {
+  if (q.G != 1 || q.B == 0) return kConvNoMfma;
+  const bool one_by_one = q.KH == 1 && q.KW == 1 && q.SH == 1 && q.SW == 1 && q.PH == 0 && q.PW == 0;
+  if (INT8B) {
+    // 16-byte int8 chunks: C_IN must be a multiple of 16.
+    if (q.Cin % 16 != 0) return kConvNoMfma;
+    return one_by_one ? kConvPlain : kConvVec;
+  }
+  if (q.Cin % 8 == 0) return one_by_one ? kConvPlain : kConvVec;
+  return q.SH == 2 && q.SW == 2 ? kConvS2D : kConvScalarGemm;
+}
+
+// Scratch bytes that let a conv take its fastest plan.
+template <bool INT8B>
+static size_t conv_scratch_bytes(const ConvGeo &q) {
+  const GemmParams p = conv_gemm_params(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, q);
+  switch (conv_path<INT8B>(q)) {
+    case kConvPlain: return gemm_scratch_bytes<INT8B, kAPlain>(p);
+    case kConvVec: return gemm_scratch_bytes<INT8B, kAConvVec>(p);
+    case kConvScalarGemm: return gemm_scratch_bytes<INT8B, kAConvScalar>(p);
+    case kConvS2D: {
+      const S2DPlan sp = s2d_plan(q);
+      const GemmParams p2 = conv_gemm_params(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, sp.g2);
+      return sp.gemm_off + gemm_scratch_bytes<false, kAConvVec>(p2);
+    }
+    default: return 0;
+  }
+}
+
+// Runs the space-to-depth form of a stride-2 bf16 NHWC conv (C_IN % 8 != 0)
+// in the caller's scratch.  Returns false (nothing launched) if the scratch
+// is too small for the rewritten input and weights.
+static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, void *y, const ConvGeo &q,
+                          int act, hipStream_t s, Scratch scr) {
+  const S2DPlan sp = s2d_plan(q);
+  if (scr.ptr == nullptr || scr.bytes < sp.gemm_off) return false;
+  const ConvGeo &g2 = sp.g2;
+  bf16 *xs = static_cast<bf16 *>(scr.ptr);
+  bf16 *wsd = reinterpret_cast<bf16 *>(static_cast<char *>(scr.ptr) + sp.w_off);
+  const int64_t nx = static_cast<int64_t>(q.B) * g2.H * g2.W;
+  const int64_t nw = static_cast<int64_t>(q.Cout) * g2.KH * g2.KW * g2.Cin;
+  hipLaunchKernelGGL(s2d_input_kernel, dim3(static_cast<unsigned>((nx + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const bf16 *>(x), xs, q.B, q.H, q.W, q.Cin, q.PH, q.PW, g2.H, g2.W, g2.Cin);
+  hipLaunchKernelGGL(s2d_weight_kernel, dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const bf16 *>(w), wsd, q.Cout, q.KH, q.KW, q.Cin, g2.KH, g2.KW, g2.Cin);
   GemmParams p = conv_gemm_params(xs, wsd, nullptr, nullptr, bias_bf16, y, g2);
-  launch_gemm_mfma<false, kAConvVec>(p, act, s);
-  (void)hipFreeAsync(buf, s);
+  const Scratch rest{static_cast<char *>(scr.ptr) + sp.gemm_off, scr.bytes - sp.gemm_off};
+  launch_gemm_mfma<false, kAConvVec>(p, act, s, rest);
   return true;
 }
 
@@ -296,24 +342,17 @@ template <bool INT8B>
 static bool try_conv_mfma(const void *x, const void *w, const float *scale, const float *bias,
                           const bf16 *bias_bf16, void *y, const ConvGeo &q, int act,
                           hipStream_t s) {
-  if (q.G != 1 || q.B == 0) return false;
   if (!aligned(x, 16) || !aligned(w, 16)) return false;
+  const ConvPath path = conv_path<INT8B>(q);
+  if (path == kConvNoMfma) return false;
+  const Scratch scr = stream_scratch(s);
+  if (path == kConvS2D && conv_s2d_mfma(x, w, bias_bf16, y, q, act, s, scr)) return true;
   GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
-  const bool one_by_one = q.KH == 1 && q.KW == 1 && q.SH == 1 && q.SW == 1 && q.PH == 0 && q.PW == 0;
-  if (INT8B) {
-    // 16-byte int8 chunks: C_IN must be a multiple of 16.
-    if (q.Cin % 16 != 0) return false;
-    return one_by_one ? launch_gemm_mfma<true, kAPlain>(p, act, s)
-                      : launch_gemm_mfma<true, kAConvVec>(p, act, s);
+  switch (path) {
+    case kConvPlain: return launch_gemm_mfma<INT8B, kAPlain>(p, act, s, scr);
+    case kConvVec: return launch_gemm_mfma<INT8B, kAConvVec>(p, act, s, scr);
+    default: return launch_gemm_mfma<INT8B, kAConvScalar>(p, act, s, scr);
   }
-  if (q.Cin % 8 == 0) {
-    return one_by_one ? launch_gemm_mfma<false, kAPlain>(p, act, s)
-                      : launch_gemm_mfma<false, kAConvVec>(p, act, s);
-  }
-  if (q.SH == 2 && q.SW == 2 && act >= TEENY_ACT_NONE && act <= TEENY_ACT_SILU && scale == nullptr &&
-      bias == nullptr && conv_s2d_mfma(x, w, bias_bf16, y, q, act, s))
-    return true;
-  return launch_gemm_mfma<false, kAConvScalar>(p, act, s);
 }
 
 static teeny_status conv_entry(const void *x, const void *w, const void *bias, void *y, int64_t B,
@@ -388,6 +427,22 @@ teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, co
                                 static_cast<bf16 *>(y), q, params->act, s);
   }
   return after_launch(name, s);
+}
+
+teeny_status teeny_conv2d_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                         int64_t OH, int64_t OW, const teeny_conv2d_params *params,
+                                         teeny_dtype dtype, teeny_layout layout, size_t *bytes) {
+  const char *name = "conv2d_workspace_size";
+  TEENY_REQUIRE(bytes != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_workspace_size: bytes");
+  *bytes = 0;
+  ConvGeo q;
+  teeny_status st = make_geo(B, C_IN, C_OUT, H, W, OH, OW, params, layout, &q, name);
+  if (st != TEENY_OK) return st;
+  if (B == 0 || layout != TEENY_NHWC) return TEENY_OK;
+  if (dtype == TEENY_BF16) *bytes = conv_scratch_bytes<false>(q);
+  else if (dtype == TEENY_I8) *bytes = conv_scratch_bytes<true>(q);
+  else TEENY_REQUIRE(dtype == TEENY_F32, TEENY_ERR_UNSUPPORTED_DTYPE, "conv2d_workspace_size: dtype");
+  return TEENY_OK;
 }
 
 }  // extern "C"

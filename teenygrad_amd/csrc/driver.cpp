@@ -5,6 +5,9 @@
 // calls.  Kernels are compiled ahead of time for gfx950, so there is no PTX
 // JIT, no nvrtc and no Triton scratch-pointer convention.
 #include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
 #include <cstdlib>
 #include <cstring>
 
@@ -46,23 +49,28 @@ teeny_status after_launch(const char *what, hipStream_t stream) {
   return TEENY_OK;
 }
 
-bool keep_pool_memory() {
-  // The stream-ordered allocator returns freed memory to the driver at every
-  // synchronize unless the pool keeps it; split-K workspaces are allocated
-  // per call, so keep what was freed (once per device).
-  static std::atomic<int> done[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  if (done[dev].load(std::memory_order_acquire) == 0) {
-    hipMemPool_t pool;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-      uint64_t keep = UINT64_MAX;
-      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-    }
-    (void)hipGetLastError();
-    done[dev].store(1, std::memory_order_release);
-  }
-  return true;
+// Workspace registry: one caller-owned buffer per stream.  The null stream
+// is per device, so it is keyed by the current device as well.
+static std::mutex g_scratch_mu;
+static std::map<std::pair<int, void *>, Scratch> g_scratch;
+
+static std::pair<int, void *> scratch_key(void *stream) {
+  int dev = -1;
+  if (stream == nullptr && hipGetDevice(&dev) != hipSuccess) dev = 0;
+  return {dev, stream};
+}
+
+Scratch stream_scratch(hipStream_t stream) {
+  const auto key = scratch_key(stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch.find(key);
+  return it == g_scratch.end() ? Scratch{} : it->second;
+}
+
+static void drop_scratch(void *stream) {
+  const auto key = scratch_key(stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  g_scratch.erase(key);
 }
 
 int device_cu_count() {
@@ -217,7 +225,21 @@ teeny_status teeny_hip_stream_create(teeny_stream *stream) {
 
 teeny_status teeny_hip_stream_destroy(teeny_stream stream) {
   if (stream == nullptr) return TEENY_OK;
+  drop_scratch(stream);
   TEENY_CHECK_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return TEENY_OK;
+}
+
+teeny_status teeny_hip_stream_set_workspace(teeny_stream stream, void *ptr, size_t bytes) {
+  if (ptr == nullptr || bytes == 0) {
+    drop_scratch(stream);
+    return TEENY_OK;
+  }
+  TEENY_REQUIRE(aligned(ptr, 256), TEENY_ERR_MISALIGNED,
+                "stream_set_workspace: workspace must be 256-byte aligned");
+  const auto key = scratch_key(stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  g_scratch[key] = Scratch{ptr, bytes};
   return TEENY_OK;
 }
 

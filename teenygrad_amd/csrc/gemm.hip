@@ -147,7 +147,7 @@ teeny_status teeny_linear_forward(const void *x, const void *w, const void *b, v
     if (mfma_ok) {
       GemmParams p = plain_params(x, stride_xm, w, stride_wn, y, stride_ym, nullptr, nullptr,
                                   static_cast<const bf16 *>(b), M, N, K);
-      launch_gemm_mfma<false, kAPlain>(p, TEENY_ACT_NONE, s);
+      launch_gemm_mfma<false, kAPlain>(p, TEENY_ACT_NONE, s, stream_scratch(s));
     } else {
       teeny_status st = launch_generic<bf16, bf16, bf16>(
           static_cast<const bf16 *>(x), stride_xm, stride_xk, static_cast<const bf16 *>(w),
@@ -176,7 +176,7 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
   const bool mfma_ok = K > 0 && K % 16 == 0 && aligned(x, 16) && aligned(qweight, 16);
   if (mfma_ok) {
     GemmParams p = plain_params(x, K, qweight, K, y, N, scale, bias, nullptr, M, N, K);
-    launch_gemm_mfma<true, kAPlain>(p, act, s);
+    launch_gemm_mfma<true, kAPlain>(p, act, s, stream_scratch(s));
   } else {
     teeny_status st = launch_generic<bf16, int8_t, bf16>(
         static_cast<const bf16 *>(x), K, 1, qweight, K, 1, static_cast<bf16 *>(y), N, 1, scale,
@@ -184,6 +184,23 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
     if (st != TEENY_OK) return st;
   }
   return after_launch("w8a16_linear_forward", s);
+}
+
+teeny_status teeny_linear_workspace_size(int64_t M, int64_t N, int64_t K, teeny_dtype dtype,
+                                         size_t *bytes) {
+  TEENY_REQUIRE(bytes != nullptr, TEENY_ERR_NULL_POINTER, "linear_workspace_size: bytes");
+  *bytes = 0;
+  TEENY_REQUIRE(M >= 0 && N >= 0 && K >= 0, TEENY_ERR_SHAPE_MISMATCH, "linear_workspace_size: negative size");
+  TEENY_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                "linear_workspace_size: size exceeds 2^31-1");
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16 || dtype == TEENY_I8, TEENY_ERR_UNSUPPORTED_DTYPE,
+                "linear_workspace_size: dtype must be F32, BF16 or I8");
+  if (M == 0 || N == 0 || K == 0 || dtype == TEENY_F32) return TEENY_OK;
+  if (K % (dtype == TEENY_I8 ? 16 : 8) != 0) return TEENY_OK;  // generic kernel, no scratch
+  // contiguous operands, as the MFMA path requires
+  const GemmParams p = plain_params(nullptr, K, nullptr, K, nullptr, N, nullptr, nullptr, nullptr, M, N, K);
+  *bytes = dtype == TEENY_I8 ? gemm_scratch_bytes<true, kAPlain>(p) : gemm_scratch_bytes<false, kAPlain>(p);
+  return TEENY_OK;
 }
 
 }  // extern "C"

@@ -610,27 +610,40 @@ inline int splitk_factor(const GemmParams &p, int bm, int bn, int bk) {
   return max(sp, 1);
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
-inline void launch_split(GemmParams p, hipStream_t s) {
-  const int sp = splitk_factor(p, BM, BN, BK);
-  if (sp > 1) {
+// Split plan: how many K slices hold k-tiles and the bytes of their fp32
+// partial sums (used == 1: no split).
+struct SplitPlan {
+  int used = 1;
+  int kt_split = 0;
+  size_t bytes = 0;
+};
+
+template <int BM, int BN, int BK>
+inline SplitPlan split_plan(const GemmParams &p) {
+  SplitPlan sp;
+  const int f = splitk_factor(p, BM, BN, BK);
+  if (f > 1) {
     const int n_k = (p.K + BK - 1) / BK;
-    const int kt_split = (n_k + sp - 1) / sp;
-    const int used = (n_k + kt_split - 1) / kt_split;  // splits that hold k-tiles
-    void *ws = nullptr;
-    const size_t bytes = static_cast<size_t>(used) * p.M * p.N * sizeof(float);
-    // stream-ordered workspace: concurrent calls on other streams never share it
-    if (keep_pool_memory() && hipMallocAsync(&ws, bytes, s) == hipSuccess) {
-      p.ws = static_cast<float *>(ws);
-      p.kt_split = kt_split;
-      launch_tile<BM, BN, BK, WAVES_M, PF, INT8B, AMODE>(p, s, used);
-      const int64_t groups = static_cast<int64_t>(p.M) * ((p.N + 7) / 8);
-      hipLaunchKernelGGL(gemm_splitk_finalize, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256),
-                         0, s, p, used);
-      (void)hipFreeAsync(ws, s);
-      return;
-    }
-    (void)hipGetLastError();  // allocation failed: run unsplit
+    sp.kt_split = (n_k + f - 1) / f;
+    sp.used = (n_k + sp.kt_split - 1) / sp.kt_split;
+    sp.bytes = static_cast<size_t>(sp.used) * p.M * p.N * sizeof(float);
+  }
+  return sp;
+}
+
+// Runs split along K when the plan splits and the caller's scratch holds the
+// partial sums; otherwise unsplit (same products, one accumulation chain).
+template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
+inline void launch_split(GemmParams p, hipStream_t s, Scratch scr) {
+  const SplitPlan sp = split_plan<BM, BN, BK>(p);
+  if (sp.used > 1 && scr.ptr != nullptr && scr.bytes >= sp.bytes) {
+    p.ws = static_cast<float *>(scr.ptr);
+    p.kt_split = sp.kt_split;
+    launch_tile<BM, BN, BK, WAVES_M, PF, INT8B, AMODE>(p, s, sp.used);
+    const int64_t groups = static_cast<int64_t>(p.M) * ((p.N + 7) / 8);
+    hipLaunchKernelGGL(gemm_splitk_finalize, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
+                       s, p, sp.used);
+    return;
   }
   p.ws = nullptr;
   launch_tile<BM, BN, BK, WAVES_M, PF, INT8B, AMODE>(p, s);
@@ -644,25 +657,37 @@ inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
 // Tile choice: the 256 x 256 large-tile kernel (gemm_big.hpp) when its
 // tiles fill the chip; else 128 x 64 x 32 for narrow outputs (N <= 64) and
 // 128 x 128 x 64 otherwise, either split along K when badly under-filled.
+enum GemmTiles { kTilesBig, kTiles128x64, kTiles128x128 };
+
 template <bool INT8B, int AMODE>
-inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s) {
+inline GemmTiles gemm_tiles(const GemmParams &p) {
+  if constexpr (AMODE != kAConvScalar) {
+    if (big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
+  }
+  return p.N <= 64 ? kTiles128x64 : kTiles128x128;
+}
+
+// Scratch bytes that let launch_gemm_mfma take its split plan (0: none used).
+template <bool INT8B, int AMODE>
+inline size_t gemm_scratch_bytes(const GemmParams &p) {
+  switch (gemm_tiles<INT8B, AMODE>(p)) {
+    case kTiles128x64: return split_plan<128, 64, 32>(p).bytes;
+    case kTiles128x128: return split_plan<128, 128, 64>(p).bytes;
+    default: return 0;
+  }
+}
+
+template <bool INT8B, int AMODE>
+inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) {
   if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU) return false;
   p.act = act;
   p.ws = nullptr;
-  const int64_t cus = device_cu_count();
-  bool big = false;
-  if constexpr (AMODE != kAConvScalar) {
-    if (big_gemm_fits<INT8B, AMODE>(p)) {
-      launch_big_gemm<INT8B, AMODE>(p, s);
-      big = true;
-    }
-  }
-  (void)cus;
-  if (big) {
-  } else if (p.N <= 64) {
-    launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
-  } else {
-    launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
+  switch (gemm_tiles<INT8B, AMODE>(p)) {
+    case kTilesBig:
+      if constexpr (AMODE != kAConvScalar) launch_big_gemm<INT8B, AMODE>(p, s);
+      break;
+    case kTiles128x64: launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s, scr); break;
+    default: launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s, scr); break;
   }
   return true;
 }

@@ -555,6 +555,28 @@ def conv2d(x: Buffer, w: Buffer, bias: Optional[Buffer] = None, stride=(1, 1), p
     return y
 
 
+def conv2d_workspace_size(x_shape, w_shape, stride=(1, 1), padding=(0, 0), groups: int = 1,
+                          dtype=bf16, layout: str = "nhwc") -> int:
+    """Stream workspace bytes that let this conv take its fastest plan (dtype
+    i8 sizes ``w8a16_conv2d``)."""
+    nhwc = layout.lower() == "nhwc"
+    b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw = conv2d_dims(
+        x_shape, w_shape, stride, padding, groups, "nhwc" if nhwc else "nchw")
+    prm = _lib.Conv2dParams(kh, kw, sh, sw, ph, pw, groups, 0)
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_conv2d_workspace_size(b, cin, cout, h, wd, oh, ow, ctypes.byref(prm), from_any(dtype).code,
+                                          _lib.NHWC if nhwc else _lib.NCHW, ctypes.byref(out)))
+    return int(out.value)
+
+
+def linear_workspace_size(m: int, n: int, k: int, dtype=bf16) -> int:
+    """Stream workspace bytes that let ``linear`` (dtype f32/bf16) or
+    ``w8a16_linear`` (dtype i8) take its fastest plan at [m,k] x [n,k]^T."""
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_linear_workspace_size(m, n, k, from_any(dtype).code, ctypes.byref(out)))
+    return int(out.value)
+
+
 def flash_attention(q: Buffer, k: Buffer, v: Buffer, softmax_scale: Optional[float] = None,
                     causal: bool = False, o: Optional[Buffer] = None, lse: Optional[Buffer] = None,
                     stream: Optional[Stream] = None) -> Buffer:

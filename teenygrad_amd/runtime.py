@@ -33,6 +33,7 @@ class Stream:
     def __init__(self, handle: Optional[int] = None, owned: bool = False):
         self.handle = handle
         self._owned = owned
+        self._workspace = None
 
     @classmethod
     def create(cls) -> "Stream":
@@ -42,6 +43,15 @@ class Stream:
 
     def synchronize(self) -> None:
         check(lib.teeny_hip_stream_sync(self.handle))
+
+    def set_workspace(self, buf: Optional["Buffer"]) -> None:
+        """Attaches ``buf`` (caller-owned, kept alive here while attached) as
+        operator scratch for work on this stream; ``None`` detaches."""
+        if buf is None:
+            check(lib.teeny_hip_stream_set_workspace(self.handle, None, 0))
+        else:
+            check(lib.teeny_hip_stream_set_workspace(self.handle, buf.ptr, buf.nbytes))
+        self._workspace = buf
 
     def destroy(self) -> None:
         if self._owned and self.handle:

@@ -12,6 +12,8 @@ on the other side of a rounding boundary from the oracle whenever the two
 fp32 results straddle one.  So bf16 outputs are checked against the fp32
 oracle (unrounded) with |got - ref| <= 2e-2 + 2^-8 |ref|.
 """
+import contextlib
+
 import numpy as np
 
 from teenygrad_amd.dtypes import from_bf16
@@ -56,3 +58,24 @@ def check_f32_elementwise(got, ref, what="", rel=F32_REL, floor=1e-30):
     err = np.abs(got - ref)
     bad = err > rel * np.abs(ref) + floor
     assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {rel} relative"
+
+
+@contextlib.contextmanager
+def stream_workspace(dev, nbytes, stream=None):
+    """Attaches a fresh ``nbytes`` device buffer (NaN-poisoned, so a path that
+    reads scratch it did not write shows up) as the stream's operator
+    workspace for the duration of the block; the null stream by default."""
+    import teenygrad_amd as tg
+    from teenygrad_amd._lib import check, lib
+    from teenygrad_amd.runtime import NULL_STREAM
+
+    st = NULL_STREAM if stream is None else stream
+    buf = dev.buffer(tg.i8, (max(int(nbytes), 256),))
+    check(lib.teeny_hip_memset(buf.ptr, 0xFF, buf.nbytes, st.handle))
+    st.set_workspace(buf)
+    try:
+        yield buf
+    finally:
+        st.set_workspace(None)
+        st.synchronize()
+        buf.free()

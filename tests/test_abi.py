@@ -183,3 +183,27 @@ def test_no_device_paths():
     if tg.device_count() > 0:
         pytest.skip("a device is visible")
     expect(lib.teeny_hip_device_open(0), _lib.ERR_NO_DEVICE)
+
+
+def test_workspace_registry_and_sizes():
+    # attaching is validated on the host; detaching (NULL / 0) always succeeds
+    assert lib.teeny_hip_stream_set_workspace(None, FAKE_ODD, 4096) == _lib.ERR_MISALIGNED
+    assert lib.teeny_hip_stream_set_workspace(None, None, 0) == 0
+    out = ctypes.c_size_t(7)
+    assert lib.teeny_linear_workspace_size(4, 4, 4, _lib.BF16, None) == _lib.ERR_NULL_POINTER
+    assert lib.teeny_linear_workspace_size(-1, 4, 4, _lib.BF16, ctypes.byref(out)) == _lib.ERR_SHAPE_MISMATCH
+    # sizes are pure functions of the shape (a 256-CU device is assumed without a GPU)
+    if tg.device_count() == 0:
+        # 64 x 256 x 4096 bf16: 2 tiles of 128 x 128, K split 4 ways -> 4 fp32 slices of 64 x 256
+        assert tg.kernels.linear_workspace_size(64, 256, 4096, tg.bf16) == 4 * 64 * 256 * 4
+        # 64 x 64 x 4096 int8: 1 tile of 128 x 64 -> 4 slices of 64 x 64
+        assert tg.kernels.linear_workspace_size(64, 64, 4096, tg.i8) == 4 * 64 * 64 * 4
+        # the two configuration GEMMs fill the device: no scratch
+        assert tg.kernels.linear_workspace_size(4096, 11008, 4096, tg.i8) == 0
+        assert tg.kernels.linear_workspace_size(4096, 4096, 11008, tg.i8) == 0
+        # stride-2 3x3 conv, 3 channels, 20 x 20 -> 10 x 10: space-to-depth input
+        # [1, 11, 11, 16] bf16 (3872 B -> 4096) then weights [16, 2, 2, 16] bf16 (2048 B)
+        assert tg.kernels.conv2d_workspace_size((1, 20, 20, 3), (16, 3, 3, 3), 2, 1, 1, tg.bf16) == 4096 + 2048
+        # fp32 and NCHW convs never use scratch
+        assert tg.kernels.conv2d_workspace_size((1, 20, 20, 3), (16, 3, 3, 3), 2, 1, 1, tg.f32) == 0
+        assert tg.kernels.conv2d_workspace_size((1, 3, 20, 20), (16, 3, 3, 3), 2, 1, 1, tg.bf16, "nchw") == 0

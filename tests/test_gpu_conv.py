@@ -4,7 +4,7 @@ import pytest
 
 import teenygrad_amd as tg
 from conftest import load_golden
-from gpu_util import check_bf16, check_f32
+from gpu_util import check_bf16, check_f32, stream_workspace
 from teenygrad_amd import kernels as K
 from teenygrad_amd.dtypes import from_bf16, to_bf16
 
@@ -74,14 +74,14 @@ BF16_CASES = [
     (2, 64, 256, 14, 14, 1, 1, 1, 0, None),    # 1x1 stride 1: plain GEMM
     (2, 256, 512, 14, 14, 1, 1, 2, 0, None),   # strided 1x1 downsample
     (2, 128, 128, 15, 15, 3, 3, 2, 1, "relu"), # strided 3x3
-    (1, 3, 64, 32, 32, 7, 7, 2, 3, "relu"),    # 3-channel stem: element-wise gather
+    (1, 3, 64, 32, 32, 7, 7, 2, 3, "relu"),    # 3-channel stem: space-to-depth or element-wise gather
     (3, 24, 40, 9, 11, 3, 3, 1, 1, None),      # ragged M, N < 64
     (1, 12, 20, 7, 7, 3, 3, 1, 1, "relu"),     # C_IN % 8 != 0
     (1, 512, 2048, 7, 7, 1, 1, 1, 0, None),    # deep 1x1 (M = 49)
     (2, 64, 96, 10, 10, 3, 3, 1, 0, None),     # N = 96: BN=128 tile, half-empty
     (2, 512, 512, 7, 7, 3, 3, 1, 1, "relu"),   # deep 3x3 (ResNet stage 4 shape): split-K
     (2, 256, 256, 14, 14, 3, 3, 1, 1, "relu"), # ResNet stage 3 shape: split-K
-    (1, 20, 48, 8, 8, 5, 5, 1, 2, None),       # element-wise gather with split-K
+    (1, 20, 48, 8, 8, 5, 5, 1, 2, None),       # element-wise gather, 5x5
     (2, 3, 32, 29, 31, 7, 7, 2, 3, None),      # stride-2 space-to-depth, odd sizes
     (1, 3, 16, 20, 20, 3, 3, 2, 1, "relu"),    # space-to-depth, 3x3 -> 2x2
     (1, 1, 8, 15, 15, 5, 5, 2, 2, None),       # space-to-depth, one channel
@@ -89,18 +89,37 @@ BF16_CASES = [
 ]
 
 
+# cases whose fastest plan needs stream scratch (split-K partials or the
+# space-to-depth copy) on a 256-CU device
+SCRATCH_CASES = {BF16_CASES[i] for i in (4, 9, 10, 12, 13, 14, 15)}
+
+
 @pytest.mark.parametrize("case", BF16_CASES)
 @pytest.mark.parametrize("with_bias", [True, False])
-def test_bf16_nhwc_mfma(dev, orc, case, with_bias):
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_bf16_nhwc_mfma(dev, orc, case, with_bias, scratch):
     B, Cin, Cout, H, W, KH, KW, s, p, act = case
-    print(f"[conv bf16] {case} bias={with_bias}", flush=True)
+    print(f"[conv bf16] {case} bias={with_bias} scratch={scratch}", flush=True)
     rng = np.random.default_rng(Cin * 7 + Cout + H)
     x = rb(rng.standard_normal((B, H, W, Cin), dtype=np.float32))
     w = rb((rng.standard_normal((Cout, KH, KW, Cin), dtype=np.float32) * np.sqrt(2.0 / (Cin * KH * KW))).astype(np.float32))
     b = rb(rng.normal(0, 0.1, Cout).astype(np.float32)) if with_bias else None
-    got = K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
-                   dev.upload(to_bf16(b), tg.bf16) if with_bias else None, s, p, 1, act,
-                   layout="nhwc").to_host()
+    need = K.conv2d_workspace_size((B, H, W, Cin), (Cout, KH, KW, Cin), s, p, 1, tg.bf16, "nhwc")
+    if dev.info()["compute_units"] == 256:
+        assert (need > 0) == (case in SCRATCH_CASES), need
+    if scratch == "workspace" and need == 0:
+        pytest.skip("no scratch plan at this shape: same path as scratch=none")
+
+    def run():
+        return K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                        dev.upload(to_bf16(b), tg.bf16) if with_bias else None, s, p, 1, act,
+                        layout="nhwc").to_host()
+
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            got = run()
+    else:
+        got = run()
     ref = orc.conv2d_nhwc(x, w, b, stride=s, padding=p)
     if act == "relu":
         ref = orc.relu(ref)

@@ -4,7 +4,7 @@ import pytest
 
 import teenygrad_amd as tg
 from conftest import load_golden
-from gpu_util import check_bf16, check_f32
+from gpu_util import check_bf16, check_f32, stream_workspace
 from quant_cases import KNOWN
 from teenygrad_amd import _lib, kernels as K
 from teenygrad_amd.dtypes import from_bf16, to_bf16
@@ -27,15 +27,31 @@ def test_linear_f32_fixture(dev, orc, with_bias):
     check_f32(got, orc.linear(x, w, b if with_bias else None), "linear f32")
 
 
+def with_scratch(dev, scratch, need, fn):
+    """Runs fn() with no stream workspace, or with one of ``need`` bytes."""
+    if scratch == "workspace":
+        if need == 0:
+            pytest.skip("no scratch plan at this shape: same path as scratch=none")
+        with stream_workspace(dev, need):
+            return fn()
+    return fn()
+
+
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 300, 136), (64, 48, 64), (33, 17, 70), (256, 512, 1000),
-                                   (64, 256, 4096), (96, 200, 3100)])  # last two: split-K (plain, ragged K)
-def test_linear_bf16(dev, orc, m, n, k):
+                                   (64, 256, 4096), (96, 200, 3100)])
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_linear_bf16(dev, orc, m, n, k, scratch):
+    # (64, 256, 4096) splits along K given a workspace; (33, 17, 70) and
+    # (96, 200, 3100) have K % 8 != 0 and take the generic kernel
     rng = np.random.default_rng(m + n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     w = rb((rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float32))
     b = rb(rng.normal(0, 0.5, n).astype(np.float32))
-    got = K.linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
-                   dev.upload(to_bf16(b), tg.bf16)).to_host()
+    need = K.linear_workspace_size(m, n, k, tg.bf16)
+    if dev.info()["compute_units"] == 256:
+        assert (need > 0) == ((m, n, k) == (64, 256, 4096)), need
+    got = with_scratch(dev, scratch, need, lambda: K.linear(
+        dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16), dev.upload(to_bf16(b), tg.bf16)).to_host())
     check_bf16(got, orc.linear(x, w, b), "linear bf16")
 
 
@@ -72,14 +88,19 @@ def quantized_weight(orc, rng, n, k):
 
 @pytest.mark.parametrize("m,n,k,act", [(100, 200, 256, None), (256, 384, 512, "silu"),
                                        (64, 64, 4096, "gelu"), (37, 70, 40, "relu"), (5, 9, 48, None)])
-def test_w8a16_small(dev, orc, m, n, k, act):
-    # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_w8a16_small(dev, orc, m, n, k, act, scratch):
+    # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA;
+    # (64, 64, 4096) splits along K given a workspace
     rng = np.random.default_rng(m * n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     q, s = quantized_weight(orc, rng, n, k)
     bias = rng.normal(0, 0.1, n).astype(np.float32)
-    got = K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s),
-                         dev.upload(bias), act=act).to_host()
+    need = K.linear_workspace_size(m, n, k, tg.i8)
+    if dev.info()["compute_units"] == 256:
+        assert (need > 0) == ((m, n, k) == (64, 64, 4096)), need
+    got = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(
+        dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), act=act).to_host())
     ref = orc.w8a16_linear(x, q, s, bias)
     if act is not None:
         ref = getattr(orc, act)(ref)
