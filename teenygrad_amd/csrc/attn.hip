@@ -82,291 +82,302 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
 
   // All query blocks of one (b, h) are consecutive logical ids on one XCD,
   // so they run together and read K/V once from HBM into that XCD's L2.
+  // Causal: a query block's work grows with its index, so workgroup p of a
+  // head runs blocks nqb-1-p and then p, and every workgroup does the same
+  // nqb + 1 key tiles (balanced by construction, whatever the dispatch order).
   const int tile_id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = tile_id / nqb;
-  const int qb = nqb - 1 - tile_id % nqb;
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c = lane & 31;
-  const int q0 = qb * BM + w * 32;
-  const int qi = q0 + c;
+  const int per_bh = CAUSAL ? (nqb + 1) / 2 : nqb;
+  const int bh = tile_id / per_bh;
+  const int slot = tile_id % per_bh;
+  const int npass = CAUSAL && slot < nqb - 1 - slot ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qb = pass == 0 ? nqb - 1 - slot : slot;
+    // opaque per pass: nothing derived from the thread id is hoisted out of
+    // the pass loop into registers that would stay live across it
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c = lane & 31;
+    const int q0 = qb * BM + w * 32;
+    const int qi = q0 + c;
 
-  const bf16 *Qb = Q + static_cast<int64_t>(bh) * nq * D;
-  const bf16 *Kb = K + static_cast<int64_t>(bh) * nk * D;
-  const bf16 *Vb = V + static_cast<int64_t>(bh) * nk * D;
+    const bf16 *Qb = Q + static_cast<int64_t>(bh) * nq * D;
+    const bf16 *Kb = K + static_cast<int64_t>(bh) * nk * D;
+    const bf16 *Vb = V + static_cast<int64_t>(bh) * nk * D;
 
-  // A negative softmax scale is applied by negating Q (exact in bf16), so the
-  // score multiplier sc is positive and the running max is a max.  It is at
-  // least FLT_MIN so that a masked -inf score maps to p = 0 even for a zero
-  // scale (where every finite score then gives p = 1 exactly, as it should).
-  const float sc = fmaxf(fabsf(scale_log2), 1.17549435e-38f);
-  const uint32_t qsign = scale_log2 < 0.0f ? 0x80008000u : 0u;
-  bf16x8 qf[NS];
+    // A negative softmax scale is applied by negating Q (exact in bf16), so the
+    // score multiplier sc is positive and the running max is a max.  It is at
+    // least FLT_MIN so that a masked -inf score maps to p = 0 even for a zero
+    // scale (where every finite score then gives p = 1 exactly, as it should).
+    const float sc = fmaxf(fabsf(scale_log2), 1.17549435e-38f);
+    const uint32_t qsign = scale_log2 < 0.0f ? 0x80008000u : 0u;
+    bf16x8 qf[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-    if (qi < nq) raw = *reinterpret_cast<const u32x4 *>(Qb + static_cast<int64_t>(qi) * D + 16 * s + 8 * g);
-    raw ^= qsign;
-    __builtin_memcpy(&qf[s], &raw, 16);
-  }
+    for (int s = 0; s < NS; ++s) {
+      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+      if (qi < nq) raw = *reinterpret_cast<const u32x4 *>(Qb + static_cast<int64_t>(qi) * D + 16 * s + 8 * g);
+      raw ^= qsign;
+      __builtin_memcpy(&qf[s], &raw, 16);
+    }
 
-  f32x16 acc[ND];
+    f32x16 acc[ND];
 #pragma unroll
-  for (int d = 0; d < ND; ++d) acc[d] = zero16();
-  // m_run: reference point of the exponentials (log2 domain, already scaled).
-  // It is raised only when a tile's max exceeds it by more than kRescale, so
-  // p = 2^(sc*s - m_run) <= 2^kRescale and O is rescaled on few tiles.
-  float m_run = -INFINITY, l_run = 0.0f;
-  const int kv_end = CAUSAL ? min(nk, qb * BM + BM) : nk;
-  const int n_tiles = (kv_end + BN - 1) / BN;
-  const int wave_end = CAUSAL ? min(kv_end, q0 + 32) : kv_end;
+    for (int d = 0; d < ND; ++d) acc[d] = zero16();
+    // m_run: reference point of the exponentials (log2 domain, already scaled).
+    // It is raised only when a tile's max exceeds it by more than kRescale, so
+    // p = 2^(sc*s - m_run) <= 2^kRescale and O is rescaled on few tiles.
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int kv_end = CAUSAL ? min(nk, qb * BM + BM) : nk;
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int wave_end = CAUSAL ? min(kv_end, q0 + 32) : kv_end;
 
-  // ── global -> LDS: one 16-byte slot per thread per round, straight into
-  // LDS (global_load_lds_dwordx4: lane j of a wave lands at base + 16 j).
-  // Slot t + 256 i of a tile is row t / CPR + RPI i, position t % CPR; the
-  // source chunk is that position XOR the row's swizzle.  Rows past nk are
-  // zero-filled so that P = 0 never meets stale data in the P*V product.
-  const int ld_row = tid / CPR;
-  const int k_off = ld_row * D + ((tid % CPR) ^ fk(ld_row)) * 8;
-  const int v_off = ld_row * D + ((tid % CPR) ^ fv(ld_row)) * 8;
-  auto load_tile = [&](const bf16 *src, bf16 *dst, int kbase, int off) __attribute__((always_inline)) {
-    const bf16 *tile_src = src + static_cast<int64_t>(kbase) * D + off;
-    typedef __attribute__((address_space(3))) void lds_void;
-    if (kbase + BN <= nk) {
+    // ── global -> LDS: one 16-byte slot per thread per round, straight into
+    // LDS (global_load_lds_dwordx4: lane j of a wave lands at base + 16 j).
+    // Slot t + 256 i of a tile is row t / CPR + RPI i, position t % CPR; the
+    // source chunk is that position XOR the row's swizzle.  Rows past nk are
+    // zero-filled so that P = 0 never meets stale data in the P*V product.
+    const int ld_row = tid / CPR;
+    const int k_off = ld_row * D + ((tid % CPR) ^ fk(ld_row)) * 8;
+    const int v_off = ld_row * D + ((tid % CPR) ^ fv(ld_row)) * 8;
+    auto load_tile = [&](const bf16 *src, bf16 *dst, int kbase, int off) __attribute__((always_inline)) {
+      const bf16 *tile_src = src + static_cast<int64_t>(kbase) * D + off;
+      typedef __attribute__((address_space(3))) void lds_void;
+      if (kbase + BN <= nk) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i)
-        __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
-                                         16, 0, 0);
-    } else {
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        if (kbase + ld_row + RPI * i < nk) {
+        for (int i = 0; i < NLD; ++i)
           __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
                                            16, 0, 0);
-        } else {
-          *reinterpret_cast<u32x4 *>(dst + (256 * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
+      } else {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+          if (kbase + ld_row + RPI * i < nk) {
+            __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
+                                             16, 0, 0);
+          } else {
+            *reinterpret_cast<u32x4 *>(dst + (256 * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
+          }
         }
       }
-    }
-  };
+    };
 
-  // ── LDS -> operands
-  // K (A operand of S^T = K Q^T): lane (g, c) reads row kb*32 + c, chunk
-  // 2 st + g, i.e. element offset koff(st) = kofs ^ (st << 4).
-  // V^T (A operand of O^T += V^T P^T) through ds_read_b64_tr_b16: in each
-  // 16-lane group, lane i receives element i & 3 of the 8-byte pieces
-  // addressed by lanes (i >> 2) + 4 j, j = 0..3.  Lane m of group h points
-  // at key 8 r + 4 g + (m >> 2) (plus kb*32 + 16 tt) and d = 32 dblk +
-  // 16 (h & 1) + 4 (m & 3), so lane l receives d = 32 dblk + l % 32 for the
-  // four keys that its P registers hold; offset voff(dblk) = vofs ^ (dblk << 5).
-  // In both, the step-dependent part is an XOR on offset bits that the row
-  // part does not touch, so each fragment address is one v_xor_b32 from a
-  // single per-lane base (cheaper than holding NS + ND offsets in registers).
-  static_assert(D == 64 || D == 128, "offset XOR layout assumes D of 64 or 128");
-  const int hh = lane >> 4, m16 = lane & 15;
-  const int v_row = 4 * g + (m16 >> 2);
-  int kofs = c * D + ((g ^ fk(c)) << 3);
-  int vofs = v_row * D + ((fv(v_row) | (2 * (hh & 1) + ((m16 & 3) >> 1))) << 3) + (m16 & 1) * 4;
+    // ── LDS -> operands
+    // K (A operand of S^T = K Q^T): lane (g, c) reads row kb*32 + c, chunk
+    // 2 st + g, i.e. element offset koff(st) = kofs ^ (st << 4).
+    // V^T (A operand of O^T += V^T P^T) through ds_read_b64_tr_b16: in each
+    // 16-lane group, lane i receives element i & 3 of the 8-byte pieces
+    // addressed by lanes (i >> 2) + 4 j, j = 0..3.  Lane m of group h points
+    // at key 8 r + 4 g + (m >> 2) (plus kb*32 + 16 tt) and d = 32 dblk +
+    // 16 (h & 1) + 4 (m & 3), so lane l receives d = 32 dblk + l % 32 for the
+    // four keys that its P registers hold; offset voff(dblk) = vofs ^ (dblk << 5).
+    // In both, the step-dependent part is an XOR on offset bits that the row
+    // part does not touch, so each fragment address is one v_xor_b32 from a
+    // single per-lane base (cheaper than holding NS + ND offsets in registers).
+    static_assert(D == 64 || D == 128, "offset XOR layout assumes D of 64 or 128");
+    const int hh = lane >> 4, m16 = lane & 15;
+    const int v_row = 4 * g + (m16 >> 2);
+    int kofs = c * D + ((g ^ fk(c)) << 3);
+    int vofs = v_row * D + ((fv(v_row) | (2 * (hh & 1) + ((m16 & 3) >> 1))) << 3) + (m16 & 1) * 4;
 
-  // S^T for key tile kt (K from LDS as the A operand, Q^T from registers).
-  auto score = [&](auto par, f32x16 (&s)[2]) __attribute__((always_inline)) {
-    const bf16 *ks = kbuf(par);
+    // S^T for key tile kt (K from LDS as the A operand, Q^T from registers).
+    auto score = [&](auto par, f32x16 (&s)[2]) __attribute__((always_inline)) {
+      const bf16 *ks = kbuf(par);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = zero16();
+      for (int kb = 0; kb < 2; ++kb) {
+        s[kb] = zero16();
 #pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + kb * 32 * D + (kofs ^ (st << 4)));
-        s[kb] = mfma32x32x16(a, qf[st], s[kb]);
-      }
-    }
-  };
-
-  // Software pipeline, one barrier per key tile.  Iteration kt starts the
-  // loads of K for tile kt+2 and V for tile kt+1 (each into the buffer whose
-  // last reader finished before the previous barrier), computes the scores
-  // of tile kt+1 on the matrix cores while the softmax of tile kt runs on the
-  // VALU, accumulates P*V of tile kt, and waits for its own loads before the
-  // barrier that publishes them.
-  const std::false_type even{};
-  const std::true_type odd{};
-  load_tile(Kb, kbuf(even), 0, k_off);
-  if (n_tiles > 1) load_tile(Kb, kbuf(odd), BN, k_off);
-  load_tile(Vb, vbuf(even), 0, v_off);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  // Masks tile kt of a wave's scores (keys past nk; causal: keys past the
-  // query) and returns the raw max over the tile for each query lane.
-  auto mask_scores = [&](int kt, f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
-    const int kbase = kt * BN;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kbase + kb * 32 + mfma32_row(v, g);
-        if (key >= nk || (CAUSAL && key > qi)) sc_t[kb][v] = -INFINITY;
-      }
-  };
-  auto tile_max = [&](const f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
-    // pairwise tree (depth 5) rather than a 32-long dependent chain
-    float t[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) t[v] = fmaxf(sc_t[0][v], sc_t[1][v]);
-#pragma unroll
-    for (int n = 8; n > 0; n >>= 1)
-#pragma unroll
-      for (int v = 0; v < n; ++v) t[v] = fmaxf(t[v], t[v + n]);
-    const float mx = t[0];
-    // the keys of a query are split over lanes l and l ^ 32
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-  };
-  auto needs_mask = [&](int kt) {
-    return (kt * BN + BN > nk) || (CAUSAL && kt * BN + BN - 1 > q0);
-  };
-
-  // One pipeline stage.  On entry s_cur holds the masked scores of tile kt
-  // and mx_cur their max; the stage leaves the same for tile kt+1 in s_nx and
-  // mx_cur.  The scores of tile kt+1 are computed unconditionally (past the
-  // last tile they read a stale, in-bounds K buffer and are never used).  The
-  // loop below is unrolled by two so that the two score buffers swap roles
-  // without register copies, and each stage body is one straight-line block
-  // in which the VALU work (this tile's exponentials) can issue in the
-  // shadow of the 32 MFMAs; the next tile's max closes the stage.
-  float mx_cur = -INFINITY;
-  // par is the parity of kt (compile time: the loop is unrolled by two).
-  auto stage = [&](auto par, int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
-    constexpr bool P = decltype(par)::value;
-    const std::integral_constant<bool, !P> npar{};
-    if (kt + 2 < n_tiles) load_tile(Kb, kbuf(par), (kt + 2) * BN, k_off);
-    if (kt + 1 < n_tiles) load_tile(Vb, vbuf(npar), (kt + 1) * BN, v_off);
-
-    if (kt * BN < wave_end) {  // causal: later tiles are beyond this wave's last query
-      const float mx_s = mx_cur * sc;  // sc > 0: -inf stays -inf
-      if (__any(mx_s > m_run + kRescale)) {
-        const float m_new = fmaxf(m_run, mx_s);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
-        m_run = m_new;
-      }
-      const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
-
-      auto body = [&]() __attribute__((always_inline)) {
-        // Hand-pipelined block of 2 NS score MFMAs (next tile) followed by
-        // 4 ND P*V MFMAs (this tile).  Each bundle is one MFMA, the LDS
-        // read(s) for the MFMA kLA bundles later (into a rotating window of
-        // kW fragments) and a slice of the softmax VALU work; a
-        // sched_barrier after each bundle keeps this order, so the reads
-        // stay kLA MFMAs ahead and the window registers are never reused
-        // while a read into them is in flight.
-        constexpr int kLA = ATTN_LA, kW = kLA + 1;
-        constexpr int nS = 2 * NS, nPV = 4 * ND;
-        constexpr int PPB = 16 / nS;  // softmax value pairs per score bundle
-        const bf16 *ks = kbuf(npar);
-        const bf16 *vs = vbuf(par);
-        // opaque per stage: the fragment addresses are re-derived here (one
-        // XOR each) rather than hoisted out of the loop into registers
-        int kofs_s = kofs, vofs_s = vofs;
-        asm volatile("" : "+v"(kofs_s), "+v"(vofs_s));
-        bf16x8 kw[kW];
-        bf16x4 vw[kW][2];
-        // score MFMA i: key block kb = i / NS, k-step st = i % NS
-        auto kread = [&](int i) __attribute__((always_inline)) {
-          kw[i % kW] = *reinterpret_cast<const bf16x8 *>(ks + (i / NS) * 32 * D + (kofs_s ^ ((i % NS) << 4)));
-        };
-        // P*V MFMA j: d-block d = j % ND, then tt, then kb
-        auto vread = [&](int j) __attribute__((always_inline)) {
-          const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
-          const bf16 *vp = vs + (kb * 32 + 16 * tt) * D + (vofs_s ^ (d << 5));
-          vw[j % kW][0] = ds_read_tr16(vp);
-          vw[j % kW][1] = ds_read_tr16(vp + 8 * D);
-        };
-        // p = 2^(sc * s - m_run) (0 for masked keys), rounded to bf16
-        // pairwise into exactly the registers of the B operand of the P*V
-        // product; the row sum stays in fp32 so that L = m + log(l) keeps
-        // fp32 accuracy.
-        u32x4 pw[2][2];
-        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto softmax_pair = [&](int q) __attribute__((always_inline)) {
-          const int kb = q >> 3, v = 2 * (q & 7);
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v], sc, neg_m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
-          ps[(v >> 1) & 3] += p0 + p1;
-          const bf16x2 pair = cvt_pk_bf16(p0, p1);
-          uint32_t word;
-          __builtin_memcpy(&word, &pair, 4);
-          pw[kb][v >> 3][(v & 7) >> 1] = word;
-        };
-
-#pragma unroll
-        for (int i = 0; i < kLA; ++i) kread(i);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < nS; ++i) {
-          const int ahead = i + kLA;
-          if (ahead < nS) kread(ahead);
-          else vread(ahead - nS);
-          const int kb = i / NS, st = i % NS;
-          s_nx[kb] = mfma32x32x16(kw[i % kW], qf[st], st == 0 ? zero16() : s_nx[kb]);
-#pragma unroll
-          for (int q = 0; q < PPB; ++q) softmax_pair(i * PPB + q);
-          __builtin_amdgcn_sched_barrier(0);
+        for (int st = 0; st < NS; ++st) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ks + kb * 32 * D + (kofs ^ (st << 4)));
+          s[kb] = mfma32x32x16(a, qf[st], s[kb]);
         }
-        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-#pragma unroll
-        for (int j = 0; j < nPV; ++j) {
-          if (j + kLA < nPV) vread(j + kLA);
-          const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
-          bf16x8 pb;
-          __builtin_memcpy(&pb, &pw[kb][tt], 16);
-          acc[d] = mfma32x32x16(cat8(vw[j % kW][0], vw[j % kW][1]), pb, acc[d]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      }
+    };
 
-        // rare (last tile, causal diagonal): a wave-uniform branch after
-        // every MFMA of the stage has issued
-        if (needs_mask(kt + 1)) {
-          asm volatile("" ::: "memory");
-          mask_scores(kt + 1, s_nx);
-        }
-        mx_cur = tile_max(s_nx);
-      };
-      body();
-    }
+    // Software pipeline, one barrier per key tile.  Iteration kt starts the
+    // loads of K for tile kt+2 and V for tile kt+1 (each into the buffer whose
+    // last reader finished before the previous barrier), computes the scores
+    // of tile kt+1 on the matrix cores while the softmax of tile kt runs on the
+    // VALU, accumulates P*V of tile kt, and waits for its own loads before the
+    // barrier that publishes them.
+    const std::false_type even{};
+    const std::true_type odd{};
+    load_tile(Kb, kbuf(even), 0, k_off);
+    if (n_tiles > 1) load_tile(Kb, kbuf(odd), BN, k_off);
+    load_tile(Vb, vbuf(even), 0, v_off);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-  };
+    // Masks tile kt of a wave's scores (keys past nk; causal: keys past the
+    // query) and returns the raw max over the tile for each query lane.
+    auto mask_scores = [&](int kt, f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
+      const int kbase = kt * BN;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kbase + kb * 32 + mfma32_row(v, g);
+          if (key >= nk || (CAUSAL && key > qi)) sc_t[kb][v] = -INFINITY;
+        }
+    };
+    auto tile_max = [&](const f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
+      // pairwise tree (depth 5) rather than a 32-long dependent chain
+      float t[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) t[v] = fmaxf(sc_t[0][v], sc_t[1][v]);
+#pragma unroll
+      for (int n = 8; n > 0; n >>= 1)
+#pragma unroll
+        for (int v = 0; v < n; ++v) t[v] = fmaxf(t[v], t[v + n]);
+      const float mx = t[0];
+      // the keys of a query are split over lanes l and l ^ 32
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    };
+    auto needs_mask = [&](int kt) {
+      return (kt * BN + BN > nk) || (CAUSAL && kt * BN + BN - 1 > q0);
+    };
 
-  f32x16 sa[2], sb[2];
-  score(even, sa);
-  if (needs_mask(0)) mask_scores(0, sa);
-  mx_cur = tile_max(sa);
-  __syncthreads();  // K buffer 0 is reloaded (tile 2) at the start of stage 0
-  for (int kt = 0; kt < n_tiles; kt += 2) {
-    stage(even, kt, sa, sb);
-    if (kt + 1 >= n_tiles) break;
-    stage(odd, kt + 1, sb, sa);
-  }
+    // One pipeline stage.  On entry s_cur holds the masked scores of tile kt
+    // and mx_cur their max; the stage leaves the same for tile kt+1 in s_nx and
+    // mx_cur.  The scores of tile kt+1 are computed unconditionally (past the
+    // last tile they read a stale, in-bounds K buffer and are never used).  The
+    // loop below is unrolled by two so that the two score buffers swap roles
+    // without register copies, and each stage body is one straight-line block
+    // in which the VALU work (this tile's exponentials) can issue in the
+    // shadow of the 32 MFMAs; the next tile's max closes the stage.
+    float mx_cur = -INFINITY;
+    // par is the parity of kt (compile time: the loop is unrolled by two).
+    auto stage = [&](auto par, int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
+      constexpr bool P = decltype(par)::value;
+      const std::integral_constant<bool, !P> npar{};
+      if (kt + 2 < n_tiles) load_tile(Kb, kbuf(par), (kt + 2) * BN, k_off);
+      if (kt + 1 < n_tiles) load_tile(Vb, vbuf(npar), (kt + 1) * BN, v_off);
 
-  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-  const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
-  if (qi < nq) {
-    const float inv = 1.0f / l_tot;
-    bf16 *orow = O + (static_cast<int64_t>(bh) * nq + qi) * D;
+      if (kt * BN < wave_end) {  // causal: later tiles are beyond this wave's last query
+        const float mx_s = mx_cur * sc;  // sc > 0: -inf stays -inf
+        if (__any(mx_s > m_run + kRescale)) {
+          const float m_new = fmaxf(m_run, mx_s);
+          const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+          l_run *= alpha;
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
+          for (int d = 0; d < ND; ++d)
 #pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        bf16x4 o4;
+            for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
+          m_run = m_new;
+        }
+        const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
+
+        auto body = [&]() __attribute__((always_inline)) {
+          // Hand-pipelined block of 2 NS score MFMAs (next tile) followed by
+          // 4 ND P*V MFMAs (this tile).  Each bundle is one MFMA, the LDS
+          // read(s) for the MFMA kLA bundles later (into a rotating window of
+          // kW fragments) and a slice of the softmax VALU work; a
+          // sched_barrier after each bundle keeps this order, so the reads
+          // stay kLA MFMAs ahead and the window registers are never reused
+          // while a read into them is in flight.
+          constexpr int kLA = ATTN_LA, kW = kLA + 1;
+          constexpr int nS = 2 * NS, nPV = 4 * ND;
+          constexpr int PPB = 16 / nS;  // softmax value pairs per score bundle
+          const bf16 *ks = kbuf(npar);
+          const bf16 *vs = vbuf(par);
+          // opaque per stage: the fragment addresses are re-derived here (one
+          // XOR each) rather than hoisted out of the loop into registers
+          int kofs_s = kofs, vofs_s = vofs;
+          asm volatile("" : "+v"(kofs_s), "+v"(vofs_s));
+          bf16x8 kw[kW];
+          bf16x4 vw[kW][2];
+          // score MFMA i: key block kb = i / NS, k-step st = i % NS
+          auto kread = [&](int i) __attribute__((always_inline)) {
+            kw[i % kW] = *reinterpret_cast<const bf16x8 *>(ks + (i / NS) * 32 * D + (kofs_s ^ ((i % NS) << 4)));
+          };
+          // P*V MFMA j: d-block d = j % ND, then tt, then kb
+          auto vread = [&](int j) __attribute__((always_inline)) {
+            const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
+            const bf16 *vp = vs + (kb * 32 + 16 * tt) * D + (vofs_s ^ (d << 5));
+            vw[j % kW][0] = ds_read_tr16(vp);
+            vw[j % kW][1] = ds_read_tr16(vp + 8 * D);
+          };
+          // p = 2^(sc * s - m_run) (0 for masked keys), rounded to bf16
+          // pairwise into exactly the registers of the B operand of the P*V
+          // product; the row sum stays in fp32 so that L = m + log(l) keeps
+          // fp32 accuracy.
+          u32x4 pw[2][2];
+          float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          auto softmax_pair = [&](int q) __attribute__((always_inline)) {
+            const int kb = q >> 3, v = 2 * (q & 7);
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v], sc, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
+            ps[(v >> 1) & 3] += p0 + p1;
+            const bf16x2 pair = cvt_pk_bf16(p0, p1);
+            uint32_t word;
+            __builtin_memcpy(&word, &pair, 4);
+            pw[kb][v >> 3][(v & 7) >> 1] = word;
+          };
+
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = static_cast<bf16>(acc[d][4 * v4 + i] * inv);
-        *reinterpret_cast<bf16x4 *>(orow + d * 32 + 8 * v4 + 4 * g) = o4;
+          for (int i = 0; i < kLA; ++i) kread(i);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < nS; ++i) {
+            const int ahead = i + kLA;
+            if (ahead < nS) kread(ahead);
+            else vread(ahead - nS);
+            const int kb = i / NS, st = i % NS;
+            s_nx[kb] = mfma32x32x16(kw[i % kW], qf[st], st == 0 ? zero16() : s_nx[kb]);
+#pragma unroll
+            for (int q = 0; q < PPB; ++q) softmax_pair(i * PPB + q);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+#pragma unroll
+          for (int j = 0; j < nPV; ++j) {
+            if (j + kLA < nPV) vread(j + kLA);
+            const int d = j % ND, tt = (j / ND) & 1, kb = j / (2 * ND);
+            bf16x8 pb;
+            __builtin_memcpy(&pb, &pw[kb][tt], 16);
+            acc[d] = mfma32x32x16(cat8(vw[j % kW][0], vw[j % kW][1]), pb, acc[d]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+
+          // rare (last tile, causal diagonal): a wave-uniform branch after
+          // every MFMA of the stage has issued
+          if (needs_mask(kt + 1)) {
+            asm volatile("" ::: "memory");
+            mask_scores(kt + 1, s_nx);
+          }
+          mx_cur = tile_max(s_nx);
+        };
+        body();
       }
-    if (L != nullptr && g == 0) L[static_cast<int64_t>(bh) * nq + qi] = (m_run + log2f(l_tot)) * kLn2;
-  }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+
+    f32x16 sa[2], sb[2];
+    score(even, sa);
+    if (needs_mask(0)) mask_scores(0, sa);
+    mx_cur = tile_max(sa);
+    __syncthreads();  // K buffer 0 is reloaded (tile 2) at the start of stage 0
+    for (int kt = 0; kt < n_tiles; kt += 2) {
+      stage(even, kt, sa, sb);
+      if (kt + 1 >= n_tiles) break;
+      stage(odd, kt + 1, sb, sa);
+    }
+
+    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+    if (qi < nq) {
+      const float inv = 1.0f / l_tot;
+      bf16 *orow = O + (static_cast<int64_t>(bh) * nq + qi) * D;
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          bf16x4 o4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o4[i] = static_cast<bf16>(acc[d][4 * v4 + i] * inv);
+          *reinterpret_cast<bf16x4 *>(orow + d * 32 + 8 * v4 + 4 * g) = o4;
+        }
+      if (L != nullptr && g == 0) L[static_cast<int64_t>(bh) * nq + qi] = (m_run + log2f(l_tot)) * kLn2;
+    }
+  }  // pass
 }
 
 // fp32 path: grid (nq, BH), one wave per query row (flash_attn2.rs:48-51).
@@ -444,7 +455,7 @@ static void launch_bf16(const void *q, const void *k, const void *v, void *o, fl
                         int nk, float scale, int BH, int causal, hipStream_t s) {
   const int nqb = (nq + 127) / 128;
   const float scale_log2 = scale * kLog2e;
-  const dim3 grid(BH * nqb);
+  const dim3 grid(BH * (causal ? (nqb + 1) / 2 : nqb));
   if (causal) {
     hipLaunchKernelGGL((fa_fwd_bf16<D, true>), grid, dim3(256), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
