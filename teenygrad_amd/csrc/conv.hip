@@ -288,14 +288,18 @@ enum ConvPath { kConvNoMfma, kConvPlain, kConvVec, kConvS2D, kConvScalarGemm };
 template <bool INT8B>
 static ConvPath conv_path(const ConvGeo &q) {
   if (q.G != 1 || q.B == 0) return kConvNoMfma;
+  // the vector gather addresses whole images with 32-bit byte offsets
+  const bool small_image = static_cast<int64_t>(q.H) * q.W * q.Cin < (int64_t{1} << 30);
   const bool one_by_one = q.KH == 1 && q.KW == 1 && q.SH == 1 && q.SW == 1 && q.PH == 0 && q.PW == 0;
   if (INT8B) {
     // 16-byte int8 chunks: C_IN must be a multiple of 16.
-    if (q.Cin % 16 != 0) return kConvNoMfma;
+    if (q.Cin % 16 != 0 || (!one_by_one && !small_image)) return kConvNoMfma;
     return one_by_one ? kConvPlain : kConvVec;
   }
-  if (q.Cin % 8 == 0) return one_by_one ? kConvPlain : kConvVec;
-  return q.SH == 2 && q.SW == 2 ? kConvS2D : kConvScalarGemm;
+  if (q.Cin % 8 == 0 && (one_by_one || small_image)) return one_by_one ? kConvPlain : kConvVec;
+  if (q.Cin % 8 == 0 || q.SH != 2 || q.SW != 2) return kConvScalarGemm;
+  const ConvGeo &g2 = s2d_plan(q).g2;
+  return static_cast<int64_t>(g2.H) * g2.W * g2.Cin < (int64_t{1} << 30) ? kConvS2D : kConvScalarGemm;
 }
 
 // Scratch bytes that let a conv take its fastest plan.

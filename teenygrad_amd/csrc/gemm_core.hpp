@@ -31,9 +31,15 @@
 // that XCD's L2.
 #pragma once
 
+#include <algorithm>
+
 #include "mfma.hpp"
 
 namespace teeny {
+
+// 16 zero bytes in device memory: the load source for chunks that must read
+// as zero (k past K, padding taps), so that loads need no branch.
+__device__ __attribute__((aligned(16))) const uint32_t kGemmZero16[4] = {0u, 0u, 0u, 0u};
 
 enum GemmAMode : int {
   kAPlain = 0,     // A[m*lda + k]
@@ -61,7 +67,23 @@ struct GemmParams {
   // and applies the epilogue.
   float *ws;
   int kt_split;
+  // byte extents of A and B (each below 2^31: the vector loads address them
+  // through buffer resources with 32-bit offsets; larger problems are split
+  // on the host)
+  int a_bytes, b_bytes;
 };
+
+// Raw buffer resource over [base, base + bytes): a load at an offset past
+// the extent returns zeros.  kOffNone is such an offset for any extent below
+// 2^31.  Word 3 is the gfx9 raw-buffer format (32-bit data, no swizzle).
+constexpr uint32_t kBufWord3 = 0x00020000u;
+constexpr int kOffNone = static_cast<int>(0x80000000u);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 __device__ __forceinline__ void epi_coeffs(const GemmParams &p, int n, float (&mul)[4], float (&add)[4]) {
   if (n + 4 <= p.N && (n & 3) == 0) {
@@ -183,47 +205,90 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   const int k_first = kt_begin * BK;
 
   // ── per-thread A row state ────────────────────────────────────────────
+  // The vector paths load through buffer resources, unconditionally: a
+  // chunk that must read as zero (k past K, a padding tap of the conv
+  // gather) gets the offset kOffNone, and rows past M (past N for B) read
+  // the last valid row, whose products only reach discarded outputs.  No
+  // branches, no zeroing moves, exact vmcnt counts for the compiler.
   const int a_col = (tid % CPR_A) * 8;  // k offset of this thread's chunk inside the tile
+  const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(p.A, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t b_rsrc = buffer_rsrc(p.B, p.b_bytes);
   int a_row[A_CH];
   bool a_ok[A_CH];
-  const bf16 *a_base[A_CH];
+  const bf16 *a_base[A_CH];  // element paths: plain row / the row's image
   int a_ih0[A_CH], a_iw0[A_CH];
+  int a_off[A_CH];  // vector paths, bytes: plain row start / conv tap (0, 0), channel 0
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
     a_row[i] = tid / CPR_A + RPP_A * i;
     const int m = m0 + a_row[i];
     a_ok[i] = m < p.M;
+    const int mm = a_ok[i] ? m : p.M - 1;
     if constexpr (AMODE == kAPlain) {
-      a_base[i] = p.A + static_cast<int64_t>(a_ok[i] ? m : 0) * p.lda;
+      a_base[i] = p.A + static_cast<int64_t>(mm) * p.lda;
       a_ih0[i] = a_iw0[i] = 0;
+      a_off[i] = static_cast<int>(static_cast<int64_t>(mm) * p.lda * 2);
     } else {
-      const int mm = a_ok[i] ? m : 0;
       const int ow = mm % p.OW;
       const int t = mm / p.OW;
       const int oh = t % p.OH;
       const int b = t / p.OH;
       a_ih0[i] = oh * p.SH - p.PH;
       a_iw0[i] = ow * p.SW - p.PW;
-      a_base[i] = p.A + static_cast<int64_t>(b) * p.H * p.W * p.Cin;
+      const int64_t img = static_cast<int64_t>(b) * p.H * p.W * p.Cin;
+      a_base[i] = p.A + img;
+      a_off[i] = static_cast<int>(2 * (img + static_cast<int64_t>(a_ih0[i] * p.W + a_iw0[i]) * p.Cin));
     }
   }
-  // implicit-GEMM k decomposition of this thread's chunk column (vector mode)
-  int k_ci = 0, k_kw = 0, k_kh = 0;
+  // Implicit-GEMM k decomposition (vector mode), stepped per k-tile: tap
+  // (kh, kw), channel ci and the byte offset 2 ((kh W + kw) C_IN + ci).  When
+  // C_IN is a multiple of BK a k-tile never straddles a tap, so the state of
+  // the tile's first column is wave-uniform (scalar registers, scalar
+  // branches) and a thread adds its column a_col; otherwise each thread
+  // steps its own column.
+  const bool tap_uniform = AMODE == kAConvVec && p.Cin % BK == 0;
+  struct TapState {
+    int ci, kw, kh, off;
+  };
+  auto tap_at = [&](int k) {
+    TapState t;
+    t.ci = k % p.Cin;
+    const int r = k / p.Cin;
+    t.kw = r % p.KW;
+    t.kh = r / p.KW;
+    t.off = 2 * ((t.kh * p.W + t.kw) * p.Cin + t.ci);
+    return t;
+  };
+  // u: the k-tile's first column (uniform); v: this thread's column
+  TapState u_tap{0, 0, 0, 0}, v_tap{0, 0, 0, 0};
   if constexpr (AMODE == kAConvVec) {
-    k_ci = (k_first + a_col) % p.Cin;
-    const int r = (k_first + a_col) / p.Cin;
-    k_kw = r % p.KW;
-    k_kh = r / p.KW;
+    if (tap_uniform) u_tap = tap_at(k_first);
+    else v_tap = tap_at(k_first + a_col);
   }
+  // advance by one k-tile: the offset moves by BK elements, plus
+  // (W - KW) C_IN each time kh steps
+  auto tap_step = [&](TapState &t, bool once) __attribute__((always_inline)) {
+    t.ci += BK;
+    t.off += 2 * BK;
+    while (t.ci >= p.Cin) {
+      t.ci -= p.Cin;
+      if (++t.kw == p.KW) {
+        t.kw = 0;
+        ++t.kh;
+        t.off += 2 * (p.W - p.KW) * p.Cin;
+      }
+      if (once) break;  // uniform case: C_IN % BK == 0, at most one step
+    }
+  };
 
   auto load_a = [&](int k0, u32x4 (&areg)[A_CH]) __attribute__((always_inline)) {
+    const int k = k0 + a_col;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
-      const int k = k0 + a_col;
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
       if constexpr (AMODE == kAPlain && KVEC) {
-        if (a_ok[i] && k < p.K) v = *reinterpret_cast<const u32x4 *>(a_base[i] + k);
+        areg[i] = buffer_load16(a_rsrc, k < p.K ? a_off[i] + 2 * k : kOffNone);
       } else if constexpr (AMODE == kAPlain) {
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (a_ok[i] && k + 8 <= p.K) {
           v = *reinterpret_cast<const u32x4 *>(a_base[i] + k);
         } else if (a_ok[i] && k < p.K) {
@@ -232,13 +297,20 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
           for (int j = 0; j < 8; ++j) e[j] = k + j < p.K ? a_base[i][k + j] : static_cast<bf16>(0.0f);
           __builtin_memcpy(&v, e, 16);
         }
+        areg[i] = v;
       } else if constexpr (AMODE == kAConvVec) {
-        const int ih = a_ih0[i] + k_kh, iw = a_iw0[i] + k_kw;
-        if (a_ok[i] && k < p.K && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-          v = *reinterpret_cast<const u32x4 *>(a_base[i] + (static_cast<int64_t>(ih) * p.W + iw) * p.Cin + k_ci);
+        // (non-short-circuit: no branch)
+        auto gather = [&](const TapState &t, int col_bytes) __attribute__((always_inline)) {
+          const int ih = a_ih0[i] + t.kh, iw = a_iw0[i] + t.kw;
+          const bool ok = (k < p.K) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
+                          (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
+          return buffer_load16(a_rsrc, ok ? a_off[i] + t.off + col_bytes : kOffNone);
+        };
+        areg[i] = tap_uniform ? gather(u_tap, 2 * a_col) : gather(v_tap, 0);
       } else {
         // element-wise gather (C_IN % 8 != 0, e.g. the 3-channel stem): the
         // chunk's first (ci, kw, kh) is decoded once, then stepped
+        u32x4 v;
         bf16 e[8];
         int ci = k % p.Cin;
         const int r = k / p.Cin;
@@ -258,40 +330,44 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
           }
         }
         __builtin_memcpy(&v, e, 16);
+        areg[i] = v;
       }
-      areg[i] = v;
     }
     if constexpr (AMODE == kAConvVec) {
-      // advance this thread's (kh, kw, ci) by one k-tile
-      k_ci += BK;
-      while (k_ci >= p.Cin) {
-        k_ci -= p.Cin;
-        if (++k_kw == p.KW) {
-          k_kw = 0;
-          ++k_kh;
-        }
-      }
+      if (tap_uniform) tap_step(u_tap, true);
+      else tap_step(v_tap, false);
     }
   };
 
+  // B rows (clamped into [0, N)), resolved once; a k-tile adds its k offset
+  constexpr int B_ES = INT8B ? 1 : 2;  // bytes per B element
+  int b_off[B_CH];
+  const char *b_row_ptr[B_CH];
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int row = tid / CPR_B + RPP_B * i;
+    const int n = min(n0 + row, p.N - 1);
+    b_off[i] = static_cast<int>(static_cast<int64_t>(n) * p.ldb * B_ES);
+    b_row_ptr[i] = static_cast<const char *>(p.B) + static_cast<int64_t>(n) * p.ldb * B_ES;
+  }
   auto load_b = [&](int k0, u32x4 (&breg)[B_CH]) __attribute__((always_inline)) {
+    const int k = k0 + (tid % CPR_B) * (16 / B_ES);
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
       const int row = tid / CPR_B + RPP_B * i;
-      const int n = row < BN ? n0 + row : p.N;
-      if constexpr (INT8B) {
-        const int k = k0 + (tid % CPR_B) * 16;
-        if (n < p.N && k < p.K)
-          v = *reinterpret_cast<const u32x4 *>(static_cast<const int8_t *>(p.B) + static_cast<int64_t>(n) * p.ldb + k);
+      if (RPP_B * (i + 1) > BN && row >= BN) {  // only when BN is not a whole number of passes
+        breg[i] = u32x4{0u, 0u, 0u, 0u};
+        continue;
+      }
+      if (INT8B || (KVEC && AMODE != kAConvScalar)) {
+        breg[i] = buffer_load16(b_rsrc, k < p.K ? b_off[i] + B_ES * k : kOffNone);
       } else {
-        const int k = k0 + (tid % CPR_B) * 8;
-        const bf16 *brow = static_cast<const bf16 *>(p.B) + static_cast<int64_t>(n) * p.ldb;
-        // Element-wise when rows are not 16-byte aligned (scalar-gather conv,
-        // where ldb = KH*KW*C_IN is arbitrary) or the chunk straddles K.
-        if (KVEC && AMODE != kAConvScalar) {
-          if (n < p.N && k < p.K) v = *reinterpret_cast<const u32x4 *>(brow + k);
-        } else if (AMODE != kAConvScalar && n < p.N && k + 8 <= p.K) {
+        // element-wise when rows are not 16-byte aligned (scalar-gather conv,
+        // where ldb = KH*KW*C_IN is arbitrary) or the chunk straddles K
+        const int n = n0 + row;
+        const bf16 *brow = reinterpret_cast<const bf16 *>(b_row_ptr[i]);
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (AMODE != kAConvScalar && n < p.N && k + 8 <= p.K) {
           v = *reinterpret_cast<const u32x4 *>(brow + k);
         } else if (n < p.N && k < p.K) {
           bf16 e[8];
@@ -299,8 +375,8 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
           for (int j = 0; j < 8; ++j) e[j] = k + j < p.K ? brow[k + j] : static_cast<bf16>(0.0f);
           __builtin_memcpy(&v, e, 16);
         }
+        breg[i] = v;
       }
-      breg[i] = v;
     }
   };
 
@@ -312,7 +388,7 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int row = tid / CPR_B + RPP_B * i;
-      if (row >= BN) continue;
+      if (RPP_B * (i + 1) > BN && row >= BN) continue;
       if constexpr (INT8B) {
         const int col = (tid % CPR_B) * 16;
         bf16 e[16];
@@ -654,7 +730,7 @@ inline bool big_gemm_fits(const GemmParams &p);
 template <bool INT8B, int AMODE>
 inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
 
-// Tile choice: the 256 x 256 large-tile kernel (gemm_big.hpp) when its
+// Tile choice: the 256 x 256 large-tile kernel (gemm_dma.hpp) when its
 // tiles fill the chip; else 128 x 64 x 32 for narrow outputs (N <= 64) and
 // 128 x 128 x 64 otherwise, either split along K when badly under-filled.
 enum GemmTiles { kTilesBig, kTiles128x64, kTiles128x128 };
@@ -677,9 +753,55 @@ inline size_t gemm_scratch_bytes(const GemmParams &p) {
   }
 }
 
+// Byte extents of the A and B operands as the kernels address them.
+template <bool INT8B, int AMODE>
+inline int64_t gemm_a_extent(const GemmParams &p) {
+  if (AMODE == kAPlain) return (static_cast<int64_t>(p.M - 1) * p.lda + p.K) * 2;
+  return static_cast<int64_t>(p.M / (p.OH * p.OW)) * p.H * p.W * p.Cin * 2;  // whole images
+}
+template <bool INT8B>
+inline int64_t gemm_b_extent(const GemmParams &p) {
+  return (static_cast<int64_t>(p.N - 1) * p.ldb + p.K) * (INT8B ? 1 : 2);
+}
+
 template <bool INT8B, int AMODE>
 inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) {
   if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU) return false;
+  constexpr int64_t kMaxExtent = 0x7fffffff;
+  // Operands past 2^31 bytes (32-bit buffer offsets): run the problem as
+  // row chunks of A (whole images for a conv) or column chunks of B, each
+  // within the limit; the outputs are disjoint.
+  if (gemm_a_extent<INT8B, AMODE>(p) > kMaxExtent) {
+    const int64_t unit = AMODE == kAPlain ? 1 : static_cast<int64_t>(p.OH) * p.OW;  // rows per unit
+    const int64_t unit_bytes = AMODE == kAPlain ? p.lda * 2 : static_cast<int64_t>(p.H) * p.W * p.Cin * 2;
+    const int64_t per = std::max<int64_t>(1, (kMaxExtent - 2 * static_cast<int64_t>(p.K)) / unit_bytes);
+    for (int64_t u0 = 0; u0 * unit < p.M; u0 += per) {
+      GemmParams q = p;
+      const int64_t m0 = u0 * unit;
+      q.M = static_cast<int>(std::min<int64_t>(p.M - m0, per * unit));
+      q.A = p.A + u0 * (AMODE == kAPlain ? p.lda : static_cast<int64_t>(p.H) * p.W * p.Cin);
+      q.C = p.C + m0 * p.ldc;
+      launch_gemm_mfma<INT8B, AMODE>(q, act, s, scr);
+    }
+    return true;
+  }
+  if (gemm_b_extent<INT8B>(p) > kMaxExtent) {
+    const int64_t row_bytes = p.ldb * (INT8B ? 1 : 2);
+    const int64_t per = std::max<int64_t>(8, (kMaxExtent - row_bytes) / row_bytes / 8 * 8);
+    for (int64_t n0 = 0; n0 < p.N; n0 += per) {
+      GemmParams q = p;
+      q.N = static_cast<int>(std::min<int64_t>(p.N - n0, per));
+      q.B = static_cast<const char *>(p.B) + n0 * row_bytes;
+      q.C = p.C + n0;
+      if (p.scale != nullptr) q.scale = p.scale + n0;
+      if (p.bias != nullptr) q.bias = p.bias + n0;
+      if (p.bias_bf16 != nullptr) q.bias_bf16 = p.bias_bf16 + n0;
+      launch_gemm_mfma<INT8B, AMODE>(q, act, s, scr);
+    }
+    return true;
+  }
+  p.a_bytes = static_cast<int>(gemm_a_extent<INT8B, AMODE>(p));
+  p.b_bytes = static_cast<int>(gemm_b_extent<INT8B>(p));
   p.act = act;
   p.ws = nullptr;
   switch (gemm_tiles<INT8B, AMODE>(p)) {
@@ -694,4 +816,4 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
 
 }  // namespace teeny
 
-#include "gemm_big.hpp"
+#include "gemm_dma.hpp"

@@ -1,31 +1,37 @@
-// Large-tile MFMA GEMM for problems that fill the chip with 256 x 256 tiles
-// (the W8A16 linears, big implicit-GEMM convs).  Same contract as
-// gemm_mfma_kernel (gemm_core.hpp):
+// LDS-DMA pipelined MFMA GEMM, two instantiations:
+//
+//   256 x 256 tiles, one workgroup per CU, for problems that fill the chip
+//   with them (the W8A16 linears, big implicit-GEMM convs);
+//   128 x 128 tiles, two workgroups per CU, for the deep implicit-GEMM convs
+//   with small spatial extent (few, long k-loops).
+//
+// Same contract as gemm_mfma_kernel (gemm_core.hpp):
 //
 //   C[m, n] = act( scale[n] * sum_k A[m, k] * B[n, k] + bias[n] )
 //
 // with A bf16 (plain rows or the NHWC implicit-GEMM gather, C_IN % 8 == 0)
-// and B bf16 or int8 [N][K].
+// and B bf16 or int8 [N][K], including the split-K partial output.
 //
-// Why a second kernel: a 128 x 128 tile reads 1 KiB of LDS fragments per
-// v_mfma_f32_32x32x16_bf16 (four waves, 64 x 64 each), which is the LDS
-// bandwidth of a CU at the MFMA rate, so that kernel saturates LDS well
-// before the matrix cores.  Here one workgroup of four waves owns a
-// 256 x 256 tile and each wave a 128 x 128 block (16 MFMAs per k-step from
-// 8 fragments: 0.5 KiB per MFMA).  Its accumulators (256 per lane) live in
-// AGPRs, so there is one wave per SIMD and latency is hidden inside the
-// wave instead of across waves:
+// Why a second kernel family: the register-staged kernel's loads are
+// conditional (bounds, padding), so the compiler waits for all of them
+// (vmcnt(0)) before each k-tile's LDS store, and every k-tile pays the full
+// global-memory latency.  Here:
 //
 //  * global -> LDS moves by LDS-DMA (global_load_lds_dwordx4, no staging
 //    registers), issued from inline asm so the compiler neither counts it
-//    nor waits on it before LDS reads of other stages; four LDS stages, the
-//    DMA two k-tiles ahead, one barrier per k-tile (after an explicit
-//    s_waitcnt vmcnt that leaves only this k-tile's DMA in flight).
-//  * a k-tile is 32 fenced bundles, each one MFMA plus a share of the
-//    other work: the DMA of k-tile kt+3, LDS reads that refill the one
-//    fragment set in place 1..16 MFMAs ahead of use (k-tile kt+1's data is
-//    complete and published once tile kt starts), and the int8 -> bf16
-//    weight conversion.
+//    nor waits on it before LDS reads of other stages.  Every k-tile issues
+//    the same DMA count (out-of-range chunks read a zero block), so an
+//    explicit s_waitcnt vmcnt leaves the newer tiles in flight: NST LDS
+//    stages, the DMA NST-1 k-tiles ahead, one barrier per k-tile.
+//  * waves are 2 x 2 over the tile; a k-tile (BK = 32, two MFMA k-steps) is
+//    2 MB NB fenced bundles, each one MFMA plus a share of the other work:
+//    the DMA of k-tile kt+NST-1, LDS reads that refill the one fragment set
+//    in place ahead of use (k-tile kt+1's data is complete and published
+//    once tile kt starts), and the int8 -> bf16 weight conversion.
+//  * 256 x 256: each wave owns 128 x 128 (16 MFMAs per k-step from 8
+//    fragments: 0.5 KiB of LDS reads per MFMA, against 1 KiB for 64 x 64
+//    wave tiles, which is the CU's LDS bandwidth at the MFMA rate); its 256
+//    accumulators per lane live in AGPRs, one wave per SIMD.
 //  * int8 weights stay int8 in LDS (half the DMA and LDS bytes) and become
 //    bf16 in registers (exact: |q| <= 128 fits bf16's significand); the
 //    per-channel scale is applied to the fp32 accumulator.
@@ -40,10 +46,6 @@
 #include "gemm_core.hpp"
 
 namespace teeny {
-
-// 16 zero bytes in device memory: the DMA source for rows past M / N and k
-// past K, so that every k-tile issues the same number of DMA instructions.
-__device__ __attribute__((aligned(16))) const uint32_t kGemmZero16[4] = {0u, 0u, 0u, 0u};
 
 __device__ __forceinline__ uint32_t lds_address(const void *p) {
   typedef __attribute__((address_space(3))) const char lds_char;
@@ -65,42 +67,62 @@ __device__ __forceinline__ void lds_dma16(const void *src, uint32_t wave_lds) {
       : "memory");
 }
 
-constexpr int kBigBM = 256, kBigBN = 256, kBigBK = 32, kBigStages = 4;
+constexpr int kDmaBK = 32;
 
-template <bool INT8B>
-constexpr int big_stage_bytes() {
-  return kBigBM * kBigBK * 2 + kBigBN * kBigBK * (INT8B ? 1 : 2);
+template <int BM, int BN, bool INT8B>
+constexpr int dma_stage_bytes() {
+  return BM * kDmaBK * 2 + BN * kDmaBK * (INT8B ? 1 : 2);
 }
-template <bool INT8B>
-constexpr int big_lds_bytes() {
+template <int BM, int BN, int NST, bool INT8B>
+constexpr int dma_lds_bytes() {
   // pipeline stages, or the bf16 C tile of the epilogue, whichever is larger
-  return kBigStages * big_stage_bytes<INT8B>() > kBigBM * (kBigBN + 8) * 2
-             ? kBigStages * big_stage_bytes<INT8B>()
-             : kBigBM * (kBigBN + 8) * 2;
+  return NST * dma_stage_bytes<BM, BN, INT8B>() > BM * (BN + 8) * 2 ? NST * dma_stage_bytes<BM, BN, INT8B>()
+                                                                    : BM * (BN + 8) * 2;
 }
 
-template <bool INT8B, int AMODE>
-__global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
-  constexpr int BM = kBigBM, BN = kBigBN, BK = kBigBK, NST = kBigStages;
-  constexpr int LA = 2;                                // DMA lookahead (k-tiles)
-  constexpr int A_BYTES = BM * BK * 2;                 // 16 KiB
-  constexpr int B_BYTES = BN * BK * (INT8B ? 1 : 2);   // 8 or 16 KiB
+// BM x BN tile, NST LDS stages, MINW workgroups per CU; SPLIT: split-K
+// partial output when p.ws is set (a separate instantiation: the partial
+// store path alone costs the 256 x 256 tile spills).
+template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT>
+__global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
+  constexpr int BK = kDmaBK;
+  constexpr int WM = BM / 2, WN = BN / 2;              // wave block (2 x 2 waves)
+  constexpr int MB = WM / 32, NB = WN / 32;            // 32 x 32 MFMA blocks per wave
+  constexpr int H = MB * NB;                           // MFMA bundles per k-step
+  constexpr int A_BYTES = BM * BK * 2;
+  constexpr int B_BYTES = BN * BK * (INT8B ? 1 : 2);
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int A_LD = A_BYTES / 16 / 256;             // DMA rounds per k-tile (A)
   constexpr int B_LD = B_BYTES / 16 / 256;             // DMA rounds per k-tile (B)
   constexpr int DMA_PER_KT = A_LD + B_LD;
-  constexpr int MB = 4, NB = 4;                        // 32 x 32 blocks per wave
+  // k-tiles whose DMA may still fly at the end of a k-tile (kt+3 .. kt+NST-1)
+  constexpr int INFLIGHT = DMA_PER_KT * (NST - 3);
   static_assert(AMODE == kAPlain || AMODE == kAConvVec, "16-byte gather only");
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA rounds per k-tile");
+  static_assert(MB >= 2 && NB >= 2 && MB + NB <= H && DMA_PER_KT <= 2 * H, "bundle schedule");
+  static_assert(NST >= 4 && INFLIGHT < 16, "stages / vmcnt field");
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
-  const int wm = w >> 1, wn = w & 1;  // wave block: rows wm*128.. of m, wn*128.. of n
+  const int wm = w >> 1, wn = w & 1;  // wave block: rows wm*WM.. of m, wn*WN.. of n
 
   const int tiles_m = (p.M + BM - 1) / BM;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (tile % tiles_m) * BM, n0 = (tile / tiles_m) * BN;
-  const int n_k = (p.K + BK - 1) / BK;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int n_tiles = tiles_m * tiles_n;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = id % n_tiles;
+  const int split = id / n_tiles;  // 0 unless split-K
+  // consecutive tiles (one XCD's run) share A when there are few column
+  // tiles, else walk down M and share B
+  const bool n_fast = tiles_n <= 4;
+  const int m0 = (n_fast ? tile / tiles_n : tile % tiles_m) * BM;
+  const int n0 = (n_fast ? tile % tiles_n : tile / tiles_m) * BN;
+  const int n_k_all = (p.K + BK - 1) / BK;
+  const bool split_k = SPLIT && p.ws != nullptr;
+  const int kt_begin = split_k ? split * p.kt_split : 0;
+  const int n_k = (split_k ? min(n_k_all, kt_begin + p.kt_split) : n_k_all) - kt_begin;
+  const int k_first = kt_begin * BK;
 
   // ── DMA mapping.  A / bf16 B stage: 1024 slots of 16 B; slot t + 256 i is
   // row t / 4 + 64 i at chunk position t % 4 and holds data chunk
@@ -138,8 +160,8 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   // implicit-GEMM (kh, kw, ci) of this thread's chunk column, stepped by BK
   int k_ci = 0, k_kw = 0, k_kh = 0;
   if constexpr (AMODE == kAConvVec) {
-    k_ci = a_col % p.Cin;
-    const int r = a_col / p.Cin;
+    k_ci = (k_first + a_col) % p.Cin;
+    const int r = (k_first + a_col) / p.Cin;
     k_kw = r % p.KW;
     k_kh = r / p.KW;
   }
@@ -150,7 +172,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   // k-tile kt: advance_k() steps it once the k-tile's A rounds are out.
   auto dma_one = [&](int kt, int d) __attribute__((always_inline)) {
     const uint32_t st_base = lds0 + (kt % NST) * STAGE;
-    const int k0 = kt * BK;
+    const int k0 = k_first + kt * BK;
     const bool live = kt < n_k;
     const void *src = kGemmZero16;
     uint32_t dst;
@@ -200,14 +222,14 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   };
 
   // ── fragment offsets (bytes within a stage).  Activations (B operand):
-  // block j row wm*128 + 32 j + c, chunk 2 g + st at position
+  // block j row wm*WM + 32 j + c, chunk 2 g + st at position
   // chunk ^ ((row >> 2) & 3) = chunk ^ ((c >> 2) & 3).  bf16 weights (A
-  // operand) likewise with wn.  int8 weights: row wn*128 + 32 i + c, chunk g
+  // operand) likewise with wn.  int8 weights: row wn*WN + 32 i + c, chunk g
   // at position g ^ ((c >> 3) & 1), 16 bytes = both k-steps.
   const int sw_a = (c >> 2) & 3;
-  const int x_off = (wm * 128 + c) * 64;
-  const int w_off = INT8B ? A_BYTES + (wn * 128 + c) * 32 + ((g ^ ((c >> 3) & 1)) << 4)
-                          : A_BYTES + (wn * 128 + c) * 64;
+  const int x_off = (wm * WM + c) * 64;
+  const int w_off = INT8B ? A_BYTES + (wn * WN + c) * 32 + ((g ^ ((c >> 3) & 1)) << 4)
+                          : A_BYTES + (wn * WN + c) * 64;
 
   f32x16 acc[NB][MB];
 #pragma unroll
@@ -243,16 +265,28 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
     }
     __builtin_memcpy(&f.w[st][i], e, 16);
   };
-  // One k-tile as 32 fenced bundles.  Bundle b issues MFMA (st, i, j) =
-  // (b / 16, (b / 4) % 4, b % 4) plus a share of the other work: the DMA of
-  // k-tile kt+3 (first bundles) and LDS reads that refill the single
+  // One k-tile as 2H fenced bundles.  Bundle b issues MFMA (st, i, j) =
+  // (b / H, (b % H) / MB, b % MB) plus a share of the other work: the DMA of
+  // k-tile kt+NST-1 (first bundles) and LDS reads that refill the single
   // fragment set in place: during the k-step-0 MFMAs the k-step-1 slots
   // (free since the previous k-tile) receive this k-tile's k-step-1
   // fragments; during the k-step-1 MFMAs the k-step-0 slots (just freed)
   // receive k-tile kt+1's (complete and published once tile kt starts).
   // int8 weights: one 16-byte read per n-block (q) serves both k-steps; its
-  // k-step-0 half is converted for tile kt+1 during the second half and its
-  // k-step-1 half during the first half of tile kt+1.
+  // k-step-1 half is converted during the first half of the k-tile, then q
+  // is refilled with k-tile kt+1's chunks, whose k-step-0 half is converted
+  // in the second half, after the last k-step-0 MFMA that reads the slot.
+  // Bundles of the int8 work (c1: k-step-1 conversion of n-block i; qr: read
+  // of k-tile kt+1's chunk i; xr: its k-step-0 activation fragment j; c0: its
+  // k-step-0 conversion of n-block i):
+  //   H = 16 (256 x 256): c1 = 4 + 2i, qr = 16 + i, xr = 20 + j, c0 = 24 + 2i
+  //   H = 4  (128 x 128): c1 = i,      qr = 2 + i,  xr = 4 + j,  c0 = 6 + i
+  constexpr bool kWide = H >= 16;
+  static_assert(kWide || (H == 4 && MB == 2 && NB == 2), "int8 schedule covers H = 4 and H >= 16");
+  auto c1_at = [](int i) { return kWide ? 4 + 2 * i : i; };
+  auto qr_at = [](int i) { return kWide ? 16 + i : 2 + i; };
+  auto xr_at = [](int j) { return kWide ? 20 + j : 4 + j; };
+  auto c0_at = [](int i) { return kWide ? 24 + 2 * i : 6 + i; };
   FragSet f;
   u32x4 q[NB];
   auto ktile = [&](int kt) __attribute__((always_inline)) {
@@ -260,47 +294,49 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
     const char *nx = smem + ((kt + 1) % NST) * STAGE;
     const bool more = kt + 1 < n_k;
 #pragma unroll
-    for (int b = 0; b < 32; ++b) {
-      const int st = b >> 4, i = (b >> 2) & 3, j = b & 3;
+    for (int b = 0; b < 2 * H; ++b) {
+      const int st = b / H, i = (b % H) / MB, j = b % MB;
       if (b < DMA_PER_KT) {
-        dma_one(kt + 3, b);
+        dma_one(kt + NST - 1, b);
         if (b == A_LD - 1) advance_k();
       }
-      if (b < 16) {
-        // this k-tile's k-step 1: MB activation reads (+ NB weight reads for bf16)
-        if (b < MB) read_x(cu, 1, b, f);
-        else if (!INT8B && b < MB + NB) read_w(cu, 1, b - MB, f);
-      } else if (more) {
-        // next k-tile's k-step 0 (int8: the weight chunks first)
-        const int r = b - 16;
-        if constexpr (INT8B) {
-          if (r < NB) q[r] = read_q(nx, r);
-          else if (r < NB + MB) read_x(nx, 0, r - NB, f);
-        } else {
+      if constexpr (INT8B) {
+        if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+          if (b == c1_at(t)) convert_q(q[t], 1, t, f);
+          if (more && b == qr_at(t)) q[t] = read_q(nx, t);
+          if (more && b == c0_at(t)) convert_q(q[t], 0, t, f);
+        }
+#pragma unroll
+        for (int t = 0; t < MB; ++t)
+          if (more && b == xr_at(t)) read_x(nx, 0, t, f);
+      } else {
+        if (b < H) {
+          // this k-tile's k-step 1: MB activation and NB weight reads
+          if (b < MB) read_x(cu, 1, b, f);
+          else if (b < MB + NB) read_w(cu, 1, b - MB, f);
+        } else if (more) {
+          // next k-tile's k-step 0
+          const int r = b - H;
           if (r < MB) read_x(nx, 0, r, f);
           else if (r < MB + NB) read_w(nx, 0, r - MB, f);
         }
       }
       acc[i][j] = mfma32x32x16(f.w[st][i], f.x[st][j], acc[i][j]);
-      if constexpr (INT8B) {
-        // k-step-1 halves of this k-tile's chunks in bundles 4, 6, 8, 10;
-        // k-step-0 halves of the next k-tile's in bundles 24, 26, 28, 30
-        if (b >= 4 && b < 12 && (b & 1) == 0) convert_q(q[(b - 4) >> 1], 1, (b - 4) >> 1, f);
-        if (more && b >= 24 && (b & 1) == 0) convert_q(q[(b - 24) >> 1], 0, (b - 24) >> 1, f);
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // own DMA of earlier k-tiles complete (this k-tile's may still fly),
-    // then the barrier that publishes them
-    __builtin_amdgcn_s_waitcnt(0xF70 | DMA_PER_KT);
+    // DMA of k-tiles <= kt+2 complete (newer ones may still fly), then the
+    // barrier that publishes them
+    __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
     __syncthreads();
   };
 
-  // prologue: k-tiles 0..LA in flight, then all complete and published;
+  // prologue: k-tiles 0 .. NST-2 in flight, 0 and 1 complete and published;
   // k-step 0 of k-tile 0 into the fragment set (int8: with its chunks in q)
 #pragma unroll
-  for (int t = 0; t <= LA; ++t) dma_tile(t);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  for (int t = 0; t < NST - 1; ++t) dma_tile(t);
+  __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < MB; ++j) read_x(smem, 0, j, f);
@@ -318,6 +354,32 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
   __syncthreads();
 
+  if (split_k) {
+    // split-K partial: raw fp32 accumulators, four consecutive n per lane
+    float *wsp = p.ws + static_cast<int64_t>(split) * p.M * p.N;
+#pragma clang loop unroll(full)
+    for (int j = 0; j < MB; ++j) {
+      const int m = m0 + wm * WM + j * 32 + c;
+#pragma clang loop unroll(full)
+      for (int i = 0; i < NB; ++i) {
+#pragma clang loop unroll(full)
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int n = n0 + wn * WN + i * 32 + 8 * v4 + 4 * g;
+          if (m < p.M && n < p.N) {
+            float *dst = wsp + static_cast<int64_t>(m) * p.N + n;
+            if (n + 4 <= p.N && (p.N & 3) == 0) {
+              f32x4 v{acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2], acc[i][j][4 * v4 + 3]};
+              *reinterpret_cast<f32x4 *>(dst) = v;
+            } else {
+              for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = acc[i][j][4 * v4 + e];
+            }
+          }
+        }
+      }
+    }
+    return;
+  }
+
   // ── epilogue: scale / bias / activation, bf16 C tile through LDS, 16-byte
   // row chunks out (coalesced).
   constexpr int CP = BN + 8;
@@ -328,7 +390,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
 #pragma clang loop unroll(full)
     for (int v4 = 0; v4 < 4; ++v4) {
       float mul[4], add[4];
-      epi_coeffs(p, n0 + wn * 128 + i * 32 + 8 * v4 + 4 * g, mul, add);
+      epi_coeffs(p, n0 + wn * WN + i * 32 + 8 * v4 + 4 * g, mul, add);
 #pragma clang loop unroll(full)
       for (int j = 0; j < MB; ++j)
 #pragma clang loop unroll(full)
@@ -346,12 +408,12 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   const float lo = ea.relu ? 0.0f : -INFINITY;
 #pragma clang loop unroll(full)
   for (int j = 0; j < MB; ++j) {
-    const int ml = wm * 128 + j * 32 + c;
+    const int ml = wm * WM + j * 32 + c;
 #pragma clang loop unroll(full)
     for (int i = 0; i < NB; ++i) {
 #pragma clang loop unroll(full)
       for (int v4 = 0; v4 < 4; ++v4) {
-        const int nl = wn * 128 + i * 32 + 8 * v4 + 4 * g;
+        const int nl = wn * WN + i * 32 + 8 * v4 + 4 * g;
         bf16x4 o4;
 #pragma clang loop unroll(full)
         for (int e = 0; e < 4; ++e) {
@@ -384,33 +446,44 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p) {
   }
 }
 
-// Whether the large-tile kernel takes this problem: 16-byte chunks must
+// Whether the LDS-DMA kernels can take this problem: 16-byte chunks must
 // never straddle a row or K (bf16: K % 8, int8: K % 16, 16-byte aligned
-// operands and leading dimensions), the gather must be the vector one, N
-// must fill a 256-wide tile, the k-loop must be long enough (K >= 512) for
-// the pipeline to outweigh the 256 x 256 epilogue, and 256 x 256 tiles must
-// still give every CU a workgroup.
+// operands and leading dimensions) and the gather must be the vector one.
 template <bool INT8B, int AMODE>
-inline bool big_gemm_fits(const GemmParams &p) {
+inline bool dma_gemm_ok(const GemmParams &p) {
   if (AMODE != kAPlain && AMODE != kAConvVec) return false;
-  if (p.K % (INT8B ? 16 : 8) != 0 || p.K < 16 * kBigBK) return false;
+  if (p.K % (INT8B ? 16 : 8) != 0) return false;
   if (!aligned(p.A, 16) || !aligned(p.B, 16)) return false;
   if (AMODE == kAPlain && p.lda % 8 != 0) return false;
-  if (p.ldb % (INT8B ? 16 : 8) != 0) return false;
-  if (p.N < kBigBN) return false;  // narrower outputs would leave most of each tile idle
-  return tiles_of(p, kBigBM, kBigBN) >= device_cu_count();
+  return p.ldb % (INT8B ? 16 : 8) == 0;
+}
+
+// The 256 x 256 kernel: N must fill a 256-wide tile, the k-loop must be
+// long enough (K >= 512) for the pipeline to outweigh the 256 x 256
+// epilogue, and 256 x 256 tiles must still give every CU a workgroup.
+template <bool INT8B, int AMODE>
+inline bool big_gemm_fits(const GemmParams &p) {
+  return dma_gemm_ok<INT8B, AMODE>(p) && p.K >= 16 * kDmaBK && p.N >= 256 &&
+         tiles_of(p, 256, 256) >= device_cu_count();
+}
+
+template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT>
+inline void launch_dma_gemm(const GemmParams &p, hipStream_t s, int splits = 1) {
+  constexpr int bytes = dma_lds_bytes<BM, BN, NST, INT8B>();
+  static const bool attr_set = [] {
+    return hipFuncSetAttribute(
+               reinterpret_cast<const void *>(&gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT>),
+               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+  }();
+  (void)attr_set;
+  const int grid = static_cast<int>(tiles_of(p, BM, BN)) * (SPLIT ? splits : 1);
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT>), dim3(grid), dim3(256), bytes, s,
+                     p);
 }
 
 template <bool INT8B, int AMODE>
 inline void launch_big_gemm(const GemmParams &p, hipStream_t s) {
-  constexpr int bytes = big_lds_bytes<INT8B>();
-  static const bool attr_set = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_big_kernel<INT8B, AMODE>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
-  }();
-  (void)attr_set;
-  const int grid = static_cast<int>(tiles_of(p, kBigBM, kBigBN));
-  hipLaunchKernelGGL((gemm_big_kernel<INT8B, AMODE>), dim3(grid), dim3(256), bytes, s, p);
+  launch_dma_gemm<256, 256, 4, 1, INT8B, AMODE, false>(p, s);
 }
 
 }  // namespace teeny
