@@ -730,17 +730,26 @@ inline bool big_gemm_fits(const GemmParams &p);
 template <bool INT8B, int AMODE>
 inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
 
-// Tile choice: the 256 x 256 large-tile kernel (gemm_dma.hpp) when its
-// tiles fill the chip; else 128 x 64 x 32 for narrow outputs (N <= 64) and
-// 128 x 128 x 64 otherwise, either split along K when badly under-filled.
-enum GemmTiles { kTilesBig, kTiles128x64, kTiles128x128 };
+// Tile choice (measured on MI355X over the ResNet-50 and W8A16 shapes):
+//  * the 256 x 256 LDS-DMA kernel (gemm_dma.hpp) when its tiles fill the chip;
+//  * narrow outputs (N <= 64): 64 x 64 x 64 tiles for deep K (more
+//    workgroups to hide latency), else 128 x 64 x 32;
+//  * short K (<= 256, the 1x1 convs): 128 x 128 x 32 with a two-tile
+//    prefetch, so the few k-tiles still overlap loads with MFMAs;
+//  * grids of 128 x 128 tiles that leave CUs idle and do not split along K:
+//    128 x 64 x 64 (twice the workgroups);
+//  * otherwise 128 x 128 x 64, split along K when badly under-filled.
+enum GemmTiles { kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
 
 template <bool INT8B, int AMODE>
 inline GemmTiles gemm_tiles(const GemmParams &p) {
   if constexpr (AMODE != kAConvScalar) {
     if (big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
   }
-  return p.N <= 64 ? kTiles128x64 : kTiles128x128;
+  if (p.N <= 64) return p.K >= 512 ? kTiles64x64 : kTiles128x64;
+  if (p.K <= 256) return kTiles128x128Short;
+  if (tiles_of(p, 128, 128) < device_cu_count() && split_plan<128, 128, 64>(p).used == 1) return kTiles128x64Deep;
+  return kTiles128x128;
 }
 
 // Scratch bytes that let launch_gemm_mfma take its split plan (0: none used).
@@ -748,6 +757,9 @@ template <bool INT8B, int AMODE>
 inline size_t gemm_scratch_bytes(const GemmParams &p) {
   switch (gemm_tiles<INT8B, AMODE>(p)) {
     case kTiles128x64: return split_plan<128, 64, 32>(p).bytes;
+    case kTiles64x64: return split_plan<64, 64, 64>(p).bytes;
+    case kTiles128x128Short: return split_plan<128, 128, 32>(p).bytes;
+    case kTiles128x64Deep: return split_plan<128, 64, 64>(p).bytes;
     case kTiles128x128: return split_plan<128, 128, 64>(p).bytes;
     default: return 0;
   }
@@ -809,6 +821,9 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
       if constexpr (AMODE != kAConvScalar) launch_big_gemm<INT8B, AMODE>(p, s);
       break;
     case kTiles128x64: launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s, scr); break;
+    case kTiles64x64: launch_split<64, 64, 64, 2, 2, INT8B, AMODE>(p, s, scr); break;
+    case kTiles128x128Short: launch_split<128, 128, 32, 2, 2, INT8B, AMODE>(p, s, scr); break;
+    case kTiles128x64Deep: launch_split<128, 64, 64, 2, 1, INT8B, AMODE>(p, s, scr); break;
     default: launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s, scr); break;
   }
   return true;
