@@ -123,6 +123,145 @@ static void launch_direct(const T *x, const WT *w, const float *wscale, const T 
 }
 
 // Validates geometry (conv2d.rs:28-42 shape rules) and fills strides for the layout.
+// ── fp32 NCHW, groups == 1: implicit GEMM on the fp32 matrix cores ─────────
+// y[b, n, oh, ow] = sum_k W[n, k] X[k, m] over k = (ci, tap), m = (b, oh, ow),
+// with v_mfma_f32_16x16x4_f32 (D = A B, A 16 x 4, B 4 x 16; lane l holds
+// A[l % 16][l / 16], B[l / 16][l % 16] and D[4 (l / 16) + v][l % 16]).  The
+// weights are the A operand and the activations the B operand, so a D
+// register holds 16 consecutive output pixels of one channel (coalesced
+// NCHW stores).  The reference's sum over (ci, kh, kw) is reassociated
+// (fp32 products and accumulation).
+//
+// A workgroup owns one 16 (channels) x 16 (pixels) block.  Its weight rows
+// W[n0 .. n0+15][k] are contiguous in k, so they are staged in LDS by
+// coalesced loads, a chunk of input channels (all taps) at a time; in the
+// product, a lane reads W[n][(ci, tap)] from LDS, where four channels of
+// one tap are KH*KW floats apart (row pitch = 4 mod 64 banks keeps the 64
+// reads of a wave on distinct banks for odd KH*KW).  Activations are read
+// straight from global memory: for one tap a lane's address advances by
+// whole channel planes, and padding is resolved once per tap by an offset
+// past the buffer extent (which reads zero).  The four waves split the
+// channels of a chunk (wave v takes groups of four starting at 4 v, every
+// 16), and their partial sums meet in LDS in a fixed order.
+template <int ACT>
+__global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x, const float *__restrict__ w,
+                                                     const float *__restrict__ bias, float *__restrict__ y,
+                                                     ConvGeo q, int x_bytes, int chunk, int pitch) {
+  extern __shared__ __attribute__((aligned(16))) float wl[];  // [16][pitch]
+  __shared__ f32x4 part[3][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int r = lane & 15, kk = lane >> 4;
+  const int M = q.B * q.OH * q.OW;
+  const int m = blockIdx.x * 16 + r;  // this lane's output pixel (B operand column)
+  const int n0 = blockIdx.y * 16;
+  const bool m_ok = m < M;
+  const int mm = m_ok ? m : 0;
+  const int ow = mm % q.OW, t = mm / q.OW, oh = t % q.OH, b = t / q.OH;
+  const int ih0 = oh * q.SH - q.PH, iw0 = ow * q.SW - q.PW;
+  const int HW = q.H * q.W, KHW = q.KH * q.KW;
+  const int64_t K = static_cast<int64_t>(q.Cin) * KHW;
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x, x_bytes);
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int cb = 0; cb < q.Cin; cb += chunk) {
+    const int ce = min(q.Cin, cb + chunk);
+    const int len = (ce - cb) * KHW;  // floats per weight row in this chunk
+    __syncthreads();                  // the previous chunk's LDS reads are done
+    {
+      // row i = tid / 16 of the block, 16 consecutive floats per step
+      const int i = threadIdx.x >> 4, j0 = threadIdx.x & 15;
+      const int n = n0 + i;
+      const float *src = w + (static_cast<int64_t>(n < q.Cout ? n : 0) * K + static_cast<int64_t>(cb) * KHW);
+      for (int j = j0; j < len; j += 16) wl[i * pitch + j] = n < q.Cout ? src[j] : 0.0f;
+    }
+    __syncthreads();
+    for (int kh = 0; kh < q.KH; ++kh) {
+      for (int kw = 0; kw < q.KW; ++kw) {
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        const bool xv = m_ok & (static_cast<unsigned>(ih) < static_cast<unsigned>(q.H)) &
+                        (static_cast<unsigned>(iw) < static_cast<unsigned>(q.W));
+        const int tap = kh * q.KW + kw;
+        // channel c0 + kk, c0 = cb + 4 wv + 16 j: activation bytes and LDS index
+        int xo = 4 * ((b * q.Cin + cb + 4 * wv + kk) * HW + ih * q.W + iw);
+        int li = r * pitch + (4 * wv + kk) * KHW + tap;
+#pragma unroll 4
+        for (int c0 = cb + 4 * wv; c0 < ce; c0 += 16) {
+          const bool live = c0 + kk < ce;
+          const float a = live ? wl[li] : 0.0f;
+          const float bx =
+              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, live & xv ? xo : kOffNone, 0, 0));
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bx, acc, 0, 0, 0);
+          xo += 64 * HW;
+          li += 16 * KHW;
+        }
+      }
+    }
+  }
+  if (wv > 0) part[wv - 1][lane] = acc;
+  __syncthreads();
+  if (wv > 0 || !m_ok) return;
+  acc += part[0][lane];
+  acc += part[1][lane];
+  acc += part[2][lane];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int co = n0 + 4 * kk + v;
+    if (co < q.Cout) {
+      float val = acc[v];
+      if (bias != nullptr) val += bias[co];
+      y[(static_cast<int64_t>(b) * q.Cout + co) * q.OH * q.OW + static_cast<int64_t>(oh) * q.OW + ow] =
+          apply_act<ACT, false>(val);
+    }
+  }
+}
+
+// Takes an fp32 NCHW conv with groups == 1 whose input fits 32-bit byte
+// offsets and whose staged weight chunk fits LDS; returns false (nothing
+// launched) otherwise.
+static bool try_conv_f32_mfma(const float *x, const float *w, const float *bias, float *y, const ConvGeo &q,
+                              int act, hipStream_t s) {
+  const int64_t xb = static_cast<int64_t>(q.B) * q.Cin * q.H * q.W * 4;
+  const int khw = q.KH * q.KW;
+  if (q.G != 1 || xb >= (int64_t{1} << 31) || khw > 128) return false;
+  // channels per staged chunk: a multiple of 16 (whole groups for the four
+  // waves) with 16 * chunk * KH * KW floats within about 40 KiB
+  int chunk = (640 / khw) / 16 * 16;
+  if (chunk < 16) chunk = 16;
+  if (chunk > q.Cin) chunk = q.Cin;
+  int pitch = chunk * khw;
+  pitch += ((4 - pitch % 64) % 64 + 64) % 64;  // pitch = 4 (mod 64)
+  const size_t lds = static_cast<size_t>(16) * pitch * sizeof(float);
+  static const bool attr_set = [] {
+    bool ok = true;
+    const void *fns[] = {reinterpret_cast<const void *>(&conv_f32_mfma<TEENY_ACT_NONE>),
+                         reinterpret_cast<const void *>(&conv_f32_mfma<TEENY_ACT_RELU>),
+                         reinterpret_cast<const void *>(&conv_f32_mfma<TEENY_ACT_GELU_TANH>),
+                         reinterpret_cast<const void *>(&conv_f32_mfma<TEENY_ACT_SILU>)};
+    for (const void *f : fns)
+      ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) == hipSuccess;
+    return ok;
+  }();
+  if (!attr_set || lds > 150 * 1024) return false;
+  const int64_t M = static_cast<int64_t>(q.B) * q.OH * q.OW;
+  const dim3 grid(static_cast<unsigned>(cdiv(M, 16)), static_cast<unsigned>(cdiv(q.Cout, 16)));
+  const int xi = static_cast<int>(xb);
+  switch (act) {
+    case TEENY_ACT_RELU:
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_RELU>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
+      break;
+    case TEENY_ACT_GELU_TANH:
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_GELU_TANH>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk,
+                         pitch);
+      break;
+    case TEENY_ACT_SILU:
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_SILU>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
+      break;
+    default:
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_NONE>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
+      break;
+  }
+  return true;
+}
+
 static teeny_status make_geo(int64_t B, int64_t Cin, int64_t Cout, int64_t H, int64_t W,
                              int64_t OH, int64_t OW, const teeny_conv2d_params *prm,
                              teeny_layout layout, ConvGeo *q, const char *name) {
@@ -371,9 +510,13 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
                 std::string(name) + ": x/w/y");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TEENY_F32) {
-    launch_direct<float, float>(static_cast<const float *>(x), static_cast<const float *>(w),
-                                nullptr, static_cast<const float *>(bias), nullptr,
-                                static_cast<float *>(y), q, prm->act, s);
+    if (!(layout == TEENY_NCHW &&
+          try_conv_f32_mfma(static_cast<const float *>(x), static_cast<const float *>(w),
+                            static_cast<const float *>(bias), static_cast<float *>(y), q, prm->act, s))) {
+      launch_direct<float, float>(static_cast<const float *>(x), static_cast<const float *>(w),
+                                  nullptr, static_cast<const float *>(bias), nullptr,
+                                  static_cast<float *>(y), q, prm->act, s);
+    }
     return after_launch(name, s);
   }
   if (dtype == TEENY_BF16) {
