@@ -37,10 +37,6 @@
 
 namespace teeny {
 
-// 16 zero bytes in device memory: the load source for chunks that must read
-// as zero (k past K, padding taps), so that loads need no branch.
-__device__ __attribute__((aligned(16))) const uint32_t kGemmZero16[4] = {0u, 0u, 0u, 0u};
-
 enum GemmAMode : int {
   kAPlain = 0,     // A[m*lda + k]
   kAConvVec = 1,   // NHWC gather, C_IN % 8 == 0 (16-byte chunks never straddle a tap)
@@ -71,6 +67,9 @@ struct GemmParams {
   // through buffer resources with 32-bit offsets; larger problems are split
   // on the host)
   int a_bytes, b_bytes;
+  // grid order: consecutive tiles (one XCD's run, one L2) walk along N and
+  // share their A row block (1), or walk along M and share B (0)
+  int n_fast;
 };
 
 // Raw buffer resource over [base, base + bytes): a load at an offset past
@@ -191,11 +190,9 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % n_tiles;
   const int split = id / n_tiles;  // 0 unless split-K
-  // Consecutive tiles (one XCD's run) share an operand through its L2: with
-  // few column tiles (narrow outputs, e.g. 1x1 convs) the column tiles of a
-  // row block are adjacent, so A is read from HBM once; otherwise tiles walk
-  // down M within a column and share B.
-  const bool n_fast = tiles_n <= 4;
+  // Consecutive tiles (one XCD's run) share an operand through its L2
+  // (p.n_fast: the larger operand, chosen on the host).
+  const bool n_fast = p.n_fast != 0;
   const int tm = n_fast ? tile / tiles_n : tile % tiles_m;
   const int tn = n_fast ? tile % tiles_n : tile / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
@@ -814,6 +811,9 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
   }
   p.a_bytes = static_cast<int>(gemm_a_extent<INT8B, AMODE>(p));
   p.b_bytes = static_cast<int>(gemm_b_extent<INT8B>(p));
+  // Share the larger operand between neighbouring tiles: A as the tiles
+  // read it (M x K bf16, the implicit-GEMM view for a conv) against B.
+  p.n_fast = static_cast<int64_t>(p.M) * p.K * 2 > static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2);
   p.act = act;
   p.ws = nullptr;
   switch (gemm_tiles<INT8B, AMODE>(p)) {

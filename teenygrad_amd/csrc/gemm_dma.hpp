@@ -52,18 +52,19 @@ __device__ __forceinline__ uint32_t lds_address(const void *p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)(p)));
 }
 
-// One 16-byte LDS-DMA per lane: lane j writes wave_lds + 16 j.  M0 carries
+// One 16-byte LDS-DMA per lane from a buffer resource: lane j writes
+// lds + 16 j, reading [voff, voff + 16) (zeros past the extent).  M0 carries
 // the wave's LDS base and is restored afterwards.
-__device__ __forceinline__ void lds_dma16(const void *src, uint32_t wave_lds) {
+__device__ __forceinline__ void buffer_lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, uint32_t lds) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
+      "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(src), "s"(wave_lds)
+      : "v"(voff), "s"(r), "s"(lds)
       : "memory");
 }
 
@@ -113,9 +114,8 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % n_tiles;
   const int split = id / n_tiles;  // 0 unless split-K
-  // consecutive tiles (one XCD's run) share A when there are few column
-  // tiles, else walk down M and share B
-  const bool n_fast = tiles_n <= 4;
+  // consecutive tiles (one XCD's run) share the larger operand (p.n_fast)
+  const bool n_fast = p.n_fast != 0;
   const int m0 = (n_fast ? tile / tiles_n : tile % tiles_m) * BM;
   const int n0 = (n_fast ? tile % tiles_n : tile / tiles_m) * BN;
   const int n_k_all = (p.K + BK - 1) / BK;
@@ -136,81 +136,108 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
                           : a_col;
   constexpr int B_RSTEP = INT8B ? 128 : 64;
 
-  const bf16 *a_base[A_LD];
-  bool a_ok[A_LD];
+  // Sources are buffer offsets (bytes): rows past M / N read the last valid
+  // row (their products only reach discarded outputs) and a chunk that must
+  // read as zero (k past K, a padding tap, k-tiles past the end) gets an
+  // offset past the buffer extent, which the hardware returns as zeros.
+  const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(p.A, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t b_rsrc = buffer_rsrc(p.B, p.b_bytes);
+  int a_off[A_LD];  // plain: row start; conv: tap (0, 0), channel 0 of the row's window
   int a_ih0[A_LD], a_iw0[A_LD];
 #pragma unroll
   for (int i = 0; i < A_LD; ++i) {
-    const int m = m0 + a_row0 + 64 * i;
-    a_ok[i] = m < p.M;
-    const int mm = a_ok[i] ? m : 0;
+    const int m = min(m0 + a_row0 + 64 * i, p.M - 1);
     if constexpr (AMODE == kAPlain) {
-      a_base[i] = p.A + static_cast<int64_t>(mm) * p.lda;
+      a_off[i] = static_cast<int>(static_cast<int64_t>(m) * p.lda * 2);
       a_ih0[i] = a_iw0[i] = 0;
     } else {
-      const int ow = mm % p.OW;
-      const int t = mm / p.OW;
+      const int ow = m % p.OW;
+      const int t = m / p.OW;
       const int oh = t % p.OH;
       const int b = t / p.OH;
       a_ih0[i] = oh * p.SH - p.PH;
       a_iw0[i] = ow * p.SW - p.PW;
-      a_base[i] = p.A + static_cast<int64_t>(b) * p.H * p.W * p.Cin;
+      a_off[i] = static_cast<int>(
+          2 * (static_cast<int64_t>(b) * p.H * p.W * p.Cin + static_cast<int64_t>(a_ih0[i] * p.W + a_iw0[i]) * p.Cin));
     }
   }
-  // implicit-GEMM (kh, kw, ci) of this thread's chunk column, stepped by BK
-  int k_ci = 0, k_kw = 0, k_kh = 0;
-  if constexpr (AMODE == kAConvVec) {
-    k_ci = (k_first + a_col) % p.Cin;
-    const int r = (k_first + a_col) / p.Cin;
-    k_kw = r % p.KW;
-    k_kh = r / p.KW;
+  int b_off[B_LD];
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const int n = min(n0 + b_row0 + B_RSTEP * i, p.N - 1);
+    b_off[i] = static_cast<int>(static_cast<int64_t>(n) * p.ldb * (INT8B ? 1 : 2));
   }
+  // Implicit-GEMM k decomposition, stepped per k-tile: tap (kh, kw), channel
+  // ci and the byte offset 2 ((kh W + kw) C_IN + ci).  When C_IN % BK == 0 a
+  // k-tile never straddles a tap and the state of its first column is
+  // wave-uniform (scalar registers); otherwise each thread steps its own.
+  const bool tap_uniform = AMODE == kAConvVec && p.Cin % BK == 0;
+  struct TapState {
+    int ci, kw, kh, off;
+  };
+  auto tap_at = [&](int k) {
+    TapState t;
+    t.ci = k % p.Cin;
+    const int r = k / p.Cin;
+    t.kw = r % p.KW;
+    t.kh = r / p.KW;
+    t.off = 2 * ((t.kh * p.W + t.kw) * p.Cin + t.ci);
+    return t;
+  };
+  TapState u_tap{0, 0, 0, 0}, v_tap{0, 0, 0, 0};
+  if constexpr (AMODE == kAConvVec) {
+    if (tap_uniform) u_tap = tap_at(k_first);
+    else v_tap = tap_at(k_first + a_col);
+  }
+  auto tap_step = [&](TapState &t, bool once) __attribute__((always_inline)) {
+    t.ci += BK;
+    t.off += 2 * BK;
+    while (t.ci >= p.Cin) {
+      t.ci -= p.Cin;
+      if (++t.kw == p.KW) {
+        t.kw = 0;
+        ++t.kh;
+        t.off += 2 * (p.W - p.KW) * p.Cin;
+      }
+      if (once) break;
+    }
+  };
   const uint32_t lds0 = lds_address(smem);
   // DMA instruction d (0 .. DMA_PER_KT-1) of k-tile kt into stage kt % NST
   // (zeros past n_k): d < A_LD are activation rounds, the rest weight rounds.
-  // The activation gather of a conv needs this thread's (kh, kw, ci) for
-  // k-tile kt: advance_k() steps it once the k-tile's A rounds are out.
+  // The activation gather of a conv needs (kh, kw, ci) for k-tile kt:
+  // advance_k() steps it once the k-tile's A rounds are out.
   auto dma_one = [&](int kt, int d) __attribute__((always_inline)) {
     const uint32_t st_base = lds0 + (kt % NST) * STAGE;
     const int k0 = k_first + kt * BK;
     const bool live = kt < n_k;
-    const void *src = kGemmZero16;
-    uint32_t dst;
     if (d < A_LD) {
       const int i = d;
       const int k = k0 + a_col;
+      int off;
       if constexpr (AMODE == kAPlain) {
-        if (live && a_ok[i] && k < p.K) src = a_base[i] + k;
+        off = live & (k < p.K) ? a_off[i] + 2 * k : kOffNone;
       } else {
-        const int ih = a_ih0[i] + k_kh, iw = a_iw0[i] + k_kw;
-        if (live && a_ok[i] && k < p.K && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-          src = a_base[i] + (static_cast<int64_t>(ih) * p.W + iw) * p.Cin + k_ci;
+        auto gather = [&](const TapState &t, int col_bytes) __attribute__((always_inline)) {
+          const int ih = a_ih0[i] + t.kh, iw = a_iw0[i] + t.kw;
+          const bool ok = live & (k < p.K) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
+                          (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
+          return ok ? a_off[i] + t.off + col_bytes : kOffNone;
+        };
+        off = tap_uniform ? gather(u_tap, 2 * a_col) : gather(v_tap, 0);
       }
-      dst = st_base + i * 4096 + w * 1024;
+      buffer_lds_dma16(a_rsrc, off, __builtin_amdgcn_readfirstlane(st_base + i * 4096 + w * 1024));
     } else {
       const int i = d - A_LD;
-      const int n = n0 + b_row0 + B_RSTEP * i;
       const int k = k0 + b_col;
-      if (live && n < p.N && k < p.K) {
-        if constexpr (INT8B)
-          src = static_cast<const int8_t *>(p.B) + static_cast<int64_t>(n) * p.ldb + k;
-        else
-          src = static_cast<const bf16 *>(p.B) + static_cast<int64_t>(n) * p.ldb + k;
-      }
-      dst = st_base + A_BYTES + i * 4096 + w * 1024;
+      const int off = live & (k < p.K) ? b_off[i] + k * (INT8B ? 1 : 2) : kOffNone;
+      buffer_lds_dma16(b_rsrc, off, __builtin_amdgcn_readfirstlane(st_base + A_BYTES + i * 4096 + w * 1024));
     }
-    lds_dma16(src, __builtin_amdgcn_readfirstlane(dst));
   };
   auto advance_k = [&]() __attribute__((always_inline)) {
     if constexpr (AMODE == kAConvVec) {
-      k_ci += BK;
-      while (k_ci >= p.Cin) {
-        k_ci -= p.Cin;
-        if (++k_kw == p.KW) {
-          k_kw = 0;
-          ++k_kh;
-        }
-      }
+      if (tap_uniform) tap_step(u_tap, true);
+      else tap_step(v_tap, false);
     }
   };
   auto dma_tile = [&](int kt) __attribute__((always_inline)) {
