@@ -307,13 +307,20 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   // of k-tile kt+1's chunk i; xr: its k-step-0 activation fragment j; c0: its
   // k-step-0 conversion of n-block i):
   //   H = 16 (256 x 256): c1 = 4 + 2i, qr = 16 + i, xr = 20 + j, c0 = 24 + 2i
+  //   H = 8  (256 x 128): c1 = 4 + i,  qr = 8 + i,  xr = 10 + j, c0 = 14 + i
   //   H = 4  (128 x 128): c1 = i,      qr = 2 + i,  xr = 4 + j,  c0 = 6 + i
-  constexpr bool kWide = H >= 16;
-  static_assert(kWide || (H == 4 && MB == 2 && NB == 2), "int8 schedule covers H = 4 and H >= 16");
-  auto c1_at = [](int i) { return kWide ? 4 + 2 * i : i; };
-  auto qr_at = [](int i) { return kWide ? 16 + i : 2 + i; };
-  auto xr_at = [](int j) { return kWide ? 20 + j : 4 + j; };
-  auto c0_at = [](int i) { return kWide ? 24 + 2 * i : 6 + i; };
+  // (c1 before the first k-step-1 MFMA of block i at H + MB i; qr after c1;
+  // xr after the last k-step-0 MFMA reading slot j, (NB - 1) MB + j; c0
+  // after the last one reading block i, MB i + MB - 1.)
+  // The bundle -> block maps are plain index arithmetic on the (unrolled)
+  // bundle number, so every fragment index is a compile-time constant
+  // (a run-time index would put the fragment set in scratch memory).
+  static_assert(H == 16 || (H == 8 && MB == 4 && NB == 2) || (H == 4 && MB == 2 && NB == 2),
+                "int8 schedule covers H = 4, 8, 16");
+  constexpr int kC1 = H == 16 ? 4 : H == 8 ? 4 : 0, kC1Step = H == 16 ? 2 : 1;
+  constexpr int kQr = H == 16 ? 16 : H == 8 ? 8 : 2;
+  constexpr int kXr = H == 16 ? 20 : H == 8 ? 10 : 4;
+  constexpr int kC0 = H == 16 ? 24 : H == 8 ? 14 : 6, kC0Step = H == 16 ? 2 : 1;
   FragSet f;
   u32x4 q[NB];
   auto ktile = [&](int kt) __attribute__((always_inline)) {
@@ -329,15 +336,12 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
       }
       if constexpr (INT8B) {
         if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
-#pragma unroll
-        for (int t = 0; t < NB; ++t) {
-          if (b == c1_at(t)) convert_q(q[t], 1, t, f);
-          if (more && b == qr_at(t)) q[t] = read_q(nx, t);
-          if (more && b == c0_at(t)) convert_q(q[t], 0, t, f);
-        }
-#pragma unroll
-        for (int t = 0; t < MB; ++t)
-          if (more && b == xr_at(t)) read_x(nx, 0, t, f);
+        if (b >= kC1 && b < kC1 + kC1Step * NB && (b - kC1) % kC1Step == 0)
+          convert_q(q[(b - kC1) / kC1Step], 1, (b - kC1) / kC1Step, f);
+        if (more && b >= kQr && b < kQr + NB) q[b - kQr] = read_q(nx, b - kQr);
+        if (more && b >= kXr && b < kXr + MB) read_x(nx, 0, b - kXr, f);
+        if (more && b >= kC0 && b < kC0 + kC0Step * NB && (b - kC0) % kC0Step == 0)
+          convert_q(q[(b - kC0) / kC0Step], 0, (b - kC0) / kC0Step, f);
       } else {
         if (b < H) {
           // this k-tile's k-step 1: MB activation and NB weight reads

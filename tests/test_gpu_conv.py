@@ -190,3 +190,21 @@ def test_w8a16_conv_config_batch32(dev, orc):
     for b in (0, B - 1):
         ref = orc.conv2d_nhwc(x[b:b + 1], wdeq, None, stride=1, padding=1)
         check_bf16(got[b:b + 1], ref, f"image {b}")
+
+
+def test_w8a16_conv_large_tile(dev, orc):
+    # 128 x 256 x 28 x 28, 3x3 p1, with bias and ReLU: M = 100352 gives 392
+    # 256 x 256 tiles, so the int8 implicit GEMM takes the large-tile LDS-DMA
+    # kernel; images 0, 77 and 127 against the oracle
+    B, C, H = 128, 256, 28
+    rng = np.random.default_rng(0x7EE70128)
+    x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
+    q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
+    bias = rng.normal(0, 0.1, C).astype(np.float32)
+    print("[w8a16 conv large tile] 128x256x28x28", flush=True)
+    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), 1, 1,
+                         act="relu").to_host()
+    wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
+    for b in (0, 77, B - 1):
+        ref = orc.relu(orc.conv2d_nhwc(x[b:b + 1], wdeq, bias, stride=1, padding=1))
+        check_bf16(got[b:b + 1], ref, f"image {b}")
