@@ -163,7 +163,13 @@ constexpr int gemm_min_waves() {
 // BK: k-tile depth (32 or 64).  PF: global->register prefetch depth in k-tiles (1 or 2).
 template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE, bool KVEC = true>
 __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_kernel(GemmParams p) {
-  constexpr int P = BK + 8;                      // LDS row pitch (elements)
+  // LDS rows.  k-depth 64: padded to 72 elements.  k-depth 32: dense
+  // 32-element (64-byte) rows whose 16-byte chunk c sits at position
+  // c ^ ((row >> 2) & 3), so that both the row-chunk stores (16 lanes: 4
+  // rows x 4 chunks) and the fragment reads (16 lanes: 16 rows, one chunk)
+  // cover distinct banks (80-byte padded rows cost 2-way store conflicts).
+  constexpr bool SWZ = BK == 32;
+  constexpr int P = SWZ ? BK : BK + 8;           // LDS row pitch (elements)
   constexpr int A_ELEMS = BM * P;
   constexpr int B_ELEMS = BN * P;
   constexpr int STAGE = A_ELEMS + B_ELEMS;
@@ -178,7 +184,11 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   constexpr int MB = WM / 32, NB = WN / 32;            // MFMA blocks per wave
   static_assert(MB >= 1 && NB >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
   static_assert(PF == 1 || PF == 2, "prefetch depth");
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
+  constexpr int CP = BN + 8;  // C tile pitch in LDS (elements), epilogue
+  constexpr int SMEM = 2 * STAGE > BM * CP ? 2 * STAGE : BM * CP;
+  __shared__ __attribute__((aligned(16))) bf16 smem[SMEM];
+  // element offset of 16-byte chunk `chunk` within LDS row `row`
+  auto chunk_at = [](int row, int chunk) { return (SWZ ? chunk ^ ((row >> 2) & 3) : chunk) * 8; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
@@ -381,7 +391,8 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     bf16 *as = smem + buf * STAGE;
     bf16 *bs = as + A_ELEMS;
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<u32x4 *>(as + a_row[i] * P + a_col) = areg[i];
+    for (int i = 0; i < A_CH; ++i)
+      *reinterpret_cast<u32x4 *>(as + a_row[i] * P + chunk_at(a_row[i], tid % CPR_A)) = areg[i];
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int row = tid / CPR_B + RPP_B * i;
@@ -397,10 +408,10 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
         u32x4 lo, hi;
         __builtin_memcpy(&lo, e, 16);
         __builtin_memcpy(&hi, e + 8, 16);
-        *reinterpret_cast<u32x4 *>(bs + row * P + col) = lo;
-        *reinterpret_cast<u32x4 *>(bs + row * P + col + 8) = hi;
+        *reinterpret_cast<u32x4 *>(bs + row * P + chunk_at(row, col / 8)) = lo;
+        *reinterpret_cast<u32x4 *>(bs + row * P + chunk_at(row, col / 8 + 1)) = hi;
       } else {
-        *reinterpret_cast<u32x4 *>(bs + row * P + (tid % CPR_B) * 8) = breg[i];
+        *reinterpret_cast<u32x4 *>(bs + row * P + chunk_at(row, tid % CPR_B)) = breg[i];
       }
     }
   };
@@ -420,10 +431,10 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     auto read_frags = [&](int s, bf16x8 (&wf)[NB], bf16x8 (&xf)[MB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
-        wf[i] = *reinterpret_cast<const bf16x8 *>(bs + (wn * WN + i * 32 + c) * P + 16 * s + 8 * g);
+        wf[i] = *reinterpret_cast<const bf16x8 *>(bs + (wn * WN + i * 32 + c) * P + chunk_at(c, 2 * s + g));
 #pragma unroll
       for (int j = 0; j < MB; ++j)
-        xf[j] = *reinterpret_cast<const bf16x8 *>(as + (wm * WM + j * 32 + c) * P + 16 * s + 8 * g);
+        xf[j] = *reinterpret_cast<const bf16x8 *>(as + (wm * WM + j * 32 + c) * P + chunk_at(c, 2 * s + g));
     };
     auto mma = [&](const bf16x8 (&wf)[NB], const bf16x8 (&xf)[MB]) __attribute__((always_inline)) {
 #pragma unroll
@@ -524,8 +535,7 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     }
     return;
   }
-  constexpr int CP = BN + 8;  // C tile pitch in LDS (elements)
-  static_assert(BM * CP <= 2 * STAGE, "C tile must fit in LDS");
+  static_assert(WN % 16 == 0 && WM % 16 == 0, "fragment rows keep the swizzle of lane c");
   bf16 *cs = smem;
   // scale / bias per group of four columns (shared by the MB row blocks)
 #pragma clang loop unroll(full)
@@ -563,7 +573,9 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
           const float r = acc[i][j][4 * v4 + e];
           o4[e] = static_cast<bf16>(r < lo ? lo : r);
         }
-        *reinterpret_cast<bf16x4 *>(cs + ml * CP + nl) = o4;
+        // 16-byte chunk nl / 8 of row ml sits at chunk (nl / 8) ^ ((ml >> 4) & 1):
+        // rows c and c + 16 of one write instruction then use different banks
+        *reinterpret_cast<bf16x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3) + (nl & 7)) = o4;
       }
     }
   }
@@ -576,7 +588,7 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     const int ml = r0 + tid / CPR_C, nl = (tid % CPR_C) * 8;
     const int m = m0 + ml, n = n0 + nl;
     if (m < p.M && n < p.N) {
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + nl);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3));
       bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
       if (vec16 && n + 8 <= p.N) {
         *reinterpret_cast<u32x4 *>(dst) = v;

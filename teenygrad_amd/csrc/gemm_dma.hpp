@@ -451,7 +451,9 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
           const float r = acc[i][j][4 * v4 + e];
           o4[e] = static_cast<bf16>(r < lo ? lo : r);
         }
-        *reinterpret_cast<bf16x4 *>(cs + ml * CP + nl) = o4;
+        // 16-byte chunk nl / 8 of row ml sits at chunk (nl / 8) ^ ((ml >> 4) & 1):
+        // rows c and c + 16 of one write instruction then use different banks
+        *reinterpret_cast<bf16x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3) + (nl & 7)) = o4;
       }
     }
   }
@@ -464,7 +466,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
     const int ml = r0 + tid / CPR_C, nl = (tid % CPR_C) * 8;
     const int m = m0 + ml, n = n0 + nl;
     if (m < p.M && n < p.N) {
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + nl);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3));
       bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
       if (vec16 && n + 8 <= p.N) {
         *reinterpret_cast<u32x4 *>(dst) = v;
