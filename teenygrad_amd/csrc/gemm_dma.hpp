@@ -292,6 +292,15 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
     }
     __builtin_memcpy(&f.w[st][i], e, 16);
   };
+  // ... or a quarter of it: weights 2r, 2r + 1 of that fragment
+  auto convert_q2 = [&](const u32x4 &q, int st, int i, int r, FragSet &f) __attribute__((always_inline)) {
+    const int byte = 8 * st + 2 * r;
+    const uint32_t word = q[byte >> 2] >> (8 * (byte & 3));
+    const bf16x2 pair = cvt_pk_bf16(static_cast<float>(static_cast<int8_t>(word & 0xffu)),
+                                    static_cast<float>(static_cast<int8_t>((word >> 8) & 0xffu)));
+    f.w[st][i][2 * r] = pair[0];
+    f.w[st][i][2 * r + 1] = pair[1];
+  };
   // One k-tile as 2H fenced bundles.  Bundle b issues MFMA (st, i, j) =
   // (b / H, (b % H) / MB, b % MB) plus a share of the other work: the DMA of
   // k-tile kt+NST-1 (first bundles) and LDS reads that refill the single
@@ -306,7 +315,10 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   // Bundles of the int8 work (c1: k-step-1 conversion of n-block i; qr: read
   // of k-tile kt+1's chunk i; xr: its k-step-0 activation fragment j; c0: its
   // k-step-0 conversion of n-block i):
-  //   H = 16 (256 x 256): c1 = 4 + 2i, qr = 16 + i, xr = 20 + j, c0 = 24 + 2i
+  //   H = 16 (256 x 256): each conversion in four quarters (two weights, a
+  //            few VALU instructions) spread over the 32 bundles, so that no
+  //            bundle's VALU work outlasts its MFMA: c1 quarter r at 4i + r,
+  //            qr = 4i + 4, xr = 20 + j, c0 quarter r at 16 + 4i + r
   //   H = 8  (256 x 128): c1 = 4 + i,  qr = 8 + i,  xr = 10 + j, c0 = 14 + i
   //   H = 4  (128 x 128): c1 = i,      qr = 2 + i,  xr = 4 + j,  c0 = 6 + i
   // (c1 before the first k-step-1 MFMA of block i at H + MB i; qr after c1;
@@ -334,7 +346,13 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
         dma_one(kt + NST - 1, b);
         if (b == A_LD - 1) advance_k();
       }
-      if constexpr (INT8B) {
+      if constexpr (INT8B && H == 16) {
+        if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
+        if (b < 16) convert_q2(q[b >> 2], 1, b >> 2, b & 3, f);
+        if (more && b >= 4 && b <= 16 && (b & 3) == 0) q[(b >> 2) - 1] = read_q(nx, (b >> 2) - 1);
+        if (more && b >= 20 && b < 24) read_x(nx, 0, b - 20, f);
+        if (more && b >= 16) convert_q2(q[(b - 16) >> 2], 0, (b - 16) >> 2, b & 3, f);
+      } else if constexpr (INT8B) {
         if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
         if (b >= kC1 && b < kC1 + kC1Step * NB && (b - kC1) % kC1Step == 0)
           convert_q(q[(b - kC1) / kC1Step], 1, (b - kC1) / kC1Step, f);
