@@ -162,15 +162,30 @@ def quantized_conv_weight(orc, rng, cout, kh, kw, cin):
 
 
 @pytest.mark.parametrize("B,Cin,Cout,H,act", [(2, 256, 256, 28, None), (1, 64, 96, 9, "relu"),
-                                              (1, 24, 16, 8, None)])
-def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act):
-    # int8 3x3 conv (the W8A16 conv workload at reduced batch; Cin=24 takes the fallback kernel)
+                                              (1, 24, 16, 8, None), (3, 32, 48, 14, "relu")])
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act, scratch):
+    # int8 3x3 conv (the W8A16 conv workload at reduced batch; Cin=24 takes the
+    # fallback kernel); given a workspace, M = B*H*W >= 512 runs on weights
+    # dequantized once to bf16 (and the first case also splits along K)
+    print(f"[w8a16 conv] B={B} Cin={Cin} Cout={Cout} H={H} scratch={scratch}", flush=True)
     rng = np.random.default_rng(Cin + H)
     x = rb(rng.standard_normal((B, H, H, Cin), dtype=np.float32))
     q, s = quantized_conv_weight(orc, rng, Cout, 3, 3, Cin)
     bias = rng.normal(0, 0.1, Cout).astype(np.float32)
-    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s),
-                         dev.upload(bias), 1, 1, act=act).to_host()
+    need = K.conv2d_workspace_size((B, H, H, Cin), (Cout, 3, 3, Cin), 1, 1, 1, tg.i8)
+    if scratch == "workspace" and need == 0:
+        pytest.skip("no scratch plan at this shape: same path as scratch=none")
+
+    def run():
+        return K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s),
+                              dev.upload(bias), 1, 1, act=act).to_host()
+
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            got = run()
+    else:
+        got = run()
     wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
     ref = orc.conv2d_nhwc(x, wdeq, bias, stride=1, padding=1)
     if act == "relu":

@@ -87,18 +87,20 @@ def quantized_weight(orc, rng, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,act", [(100, 200, 256, None), (256, 384, 512, "silu"),
-                                       (64, 64, 4096, "gelu"), (37, 70, 40, "relu"), (5, 9, 48, None)])
+                                       (64, 64, 4096, "gelu"), (37, 70, 40, "relu"), (5, 9, 48, None),
+                                       (600, 96, 128, "relu"), (530, 200, 64, None)])
 @pytest.mark.parametrize("scratch", ["none", "workspace"])
 def test_w8a16_small(dev, orc, m, n, k, act, scratch):
     # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA;
-    # (64, 64, 4096) splits along K given a workspace
+    # given a workspace, (64, 64, 4096) splits along K and the M >= 512 cases
+    # run on weights dequantized once to bf16
     rng = np.random.default_rng(m * n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     q, s = quantized_weight(orc, rng, n, k)
     bias = rng.normal(0, 0.1, n).astype(np.float32)
     need = K.linear_workspace_size(m, n, k, tg.i8)
     if dev.info()["compute_units"] == 256:
-        assert (need > 0) == ((m, n, k) == (64, 64, 4096)), need
+        assert (need > 0) == ((m, n, k) in ((64, 64, 4096), (600, 96, 128), (530, 200, 64))), need
     got = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(
         dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), act=act).to_host())
     ref = orc.w8a16_linear(x, q, s, bias)
@@ -108,19 +110,23 @@ def test_w8a16_small(dev, orc, m, n, k, act, scratch):
 
 
 @pytest.mark.parametrize("k,n", [(4096, 11008), (11008, 4096)])
-def test_w8a16_config(dev, orc, k, n):
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_w8a16_config(dev, orc, k, n, scratch):
     # M = 4096 tokens; weights N(0, 0.02) quantised per output channel on the GPU
     # (bit-exact with the oracle); output rows 0..31 and M-32..M-1 vs the oracle
     m = 4096
     rng = np.random.default_rng(0x7EE70005 + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
-    print(f"[w8a16 config] M={m} K={k} N={n}", flush=True)
+    print(f"[w8a16 config] M={m} K={k} N={n} scratch={scratch}", flush=True)
     qg, sg, zg, _ = K.quantize_affine(dev.upload(wf), [n, k], "channel", 0)
     q, s, z, _ = orc.quantize_affine(wf, [n, k], "channel", 0)
     np.testing.assert_array_equal(qg.to_host().reshape(-1), q)
     np.testing.assert_array_equal(sg.to_host(), s)
-    y = K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), qg, sg).to_host()
+    # with a workspace the int8 weights are dequantized once and the bf16
+    # kernel runs; without, the kernel converts them per tile
+    need = K.linear_workspace_size(m, n, k, tg.i8)
+    y = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), qg, sg).to_host())
     assert np.all(np.isfinite(from_bf16(y)))
     wdeq = orc.dequantize_affine(q, s, None, [n, k], "channel", 0)
     for lo, hi in ((0, 32), (m - 32, m)):
