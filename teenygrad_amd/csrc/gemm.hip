@@ -177,7 +177,7 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
   if (mfma_ok) {
     GemmParams p = plain_params(x, K, qweight, K, y, N, scale, bias, nullptr, M, N, K);
     const Scratch scr = stream_scratch(s);
-    if (M >= kW8DequantMinM && scr.ptr != nullptr && scr.bytes >= dequant_scratch_bytes(N * K)) {
+    if (w8_dequant_pays<kAPlain>(p) && scr.ptr != nullptr && scr.bytes >= dequant_scratch_bytes(N * K)) {
       // compute-bound: dequantize the weights once, then the bf16 kernels
       Scratch rest;
       p.B = dequant_weights(qweight, N * K, scr, &rest, s);
@@ -207,7 +207,7 @@ teeny_status teeny_linear_workspace_size(int64_t M, int64_t N, int64_t K, teeny_
   if (K % (dtype == TEENY_I8 ? 16 : 8) != 0) return TEENY_OK;  // generic kernel, no scratch
   // contiguous operands, as the MFMA path requires
   const GemmParams p = plain_params(nullptr, K, nullptr, K, nullptr, N, nullptr, nullptr, nullptr, M, N, K);
-  if (dtype == TEENY_I8 && M >= kW8DequantMinM)
+  if (dtype == TEENY_I8 && w8_dequant_pays<kAPlain>(p))
     *bytes = dequant_scratch_bytes(N * K) + gemm_scratch_bytes<false, kAPlain>(p);
   else
     *bytes = dtype == TEENY_I8 ? gemm_scratch_bytes<true, kAPlain>(p) : gemm_scratch_bytes<false, kAPlain>(p);

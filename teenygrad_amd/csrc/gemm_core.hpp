@@ -673,10 +673,12 @@ static __global__ __launch_bounds__(256) void i8_to_bf16_kernel(const int8_t *__
   reinterpret_cast<u32x4 *>(out)[2 * t + 1] = hi;
 }
 
-// W8A16 with at least this many rows runs as a bf16 GEMM on weights
-// dequantized once into the stream's scratch (when it is large enough):
-// past about 500 rows the GEMM is compute-bound, so the extra 3 bytes of
-// traffic per weight cost less than converting every weight per row tile.
+// W8A16 problems that take the 256 x 256 LDS-DMA kernel (so compute-bound:
+// at least 512 rows) run as a bf16 GEMM on weights dequantized once into
+// the stream's scratch (when it is large enough): converting in the MFMA
+// loop costs that kernel ~20 %, the dequant pass ~3 bytes of traffic per
+// weight.  The register-staged kernels convert while staging to LDS, where
+// it is nearly free, so there the pass would only add a launch.
 constexpr int64_t kW8DequantMinM = 512;
 inline size_t dequant_scratch_bytes(int64_t n_weights) { return (static_cast<size_t>(n_weights) * 2 + 255) / 256 * 256; }
 
@@ -797,6 +799,12 @@ inline GemmTiles gemm_tiles(const GemmParams &p) {
   if (p.K <= 256) return kTiles128x128Short;
   if (tiles_of(p, 128, 128) < device_cu_count() && split_plan<128, 128, 64>(p).used == 1) return kTiles128x64Deep;
   return kTiles128x128;
+}
+
+// Whether a W8A16 problem runs on dequantized weights (see kW8DequantMinM).
+template <int AMODE>
+inline bool w8_dequant_pays(const GemmParams &p) {
+  return p.M >= kW8DequantMinM && gemm_tiles<true, AMODE>(p) == kTilesBig;
 }
 
 // Scratch bytes that let launch_gemm_mfma take its split plan (0: none used).

@@ -166,8 +166,7 @@ def quantized_conv_weight(orc, rng, cout, kh, kw, cin):
 @pytest.mark.parametrize("scratch", ["none", "workspace"])
 def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act, scratch):
     # int8 3x3 conv (the W8A16 conv workload at reduced batch; Cin=24 takes the
-    # fallback kernel); given a workspace, M = B*H*W >= 512 runs on weights
-    # dequantized once to bf16 (and the first case also splits along K)
+    # fallback kernel); given a workspace, the first case splits along K
     print(f"[w8a16 conv] B={B} Cin={Cin} Cout={Cout} H={H} scratch={scratch}", flush=True)
     rng = np.random.default_rng(Cin + H)
     x = rb(rng.standard_normal((B, H, H, Cin), dtype=np.float32))
@@ -207,18 +206,31 @@ def test_w8a16_conv_config_batch32(dev, orc):
         check_bf16(got[b:b + 1], ref, f"image {b}")
 
 
-def test_w8a16_conv_large_tile(dev, orc):
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_w8a16_conv_large_tile(dev, orc, scratch):
     # 128 x 256 x 28 x 28, 3x3 p1, with bias and ReLU: M = 100352 gives 392
-    # 256 x 256 tiles, so the int8 implicit GEMM takes the large-tile LDS-DMA
-    # kernel; images 0, 77 and 127 against the oracle
+    # 256 x 256 tiles, so the implicit GEMM takes the large-tile LDS-DMA
+    # kernel, on int8 weights or, given a workspace, on weights dequantized
+    # once to bf16; images 0, 77 and 127 against the oracle
     B, C, H = 128, 256, 28
     rng = np.random.default_rng(0x7EE70128)
     x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
     q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
     bias = rng.normal(0, 0.1, C).astype(np.float32)
-    print("[w8a16 conv large tile] 128x256x28x28", flush=True)
-    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), 1, 1,
-                         act="relu").to_host()
+    need = K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)
+    if dev.info()["compute_units"] == 256:
+        assert need == C * 9 * C * 2, need
+    print(f"[w8a16 conv large tile] 128x256x28x28 scratch={scratch}", flush=True)
+
+    def run():
+        return K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), 1, 1,
+                              act="relu").to_host()
+
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            got = run()
+    else:
+        got = run()
     wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
     for b in (0, 77, B - 1):
         ref = orc.relu(orc.conv2d_nhwc(x[b:b + 1], wdeq, bias, stride=1, padding=1))

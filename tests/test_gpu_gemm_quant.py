@@ -92,15 +92,15 @@ def quantized_weight(orc, rng, n, k):
 @pytest.mark.parametrize("scratch", ["none", "workspace"])
 def test_w8a16_small(dev, orc, m, n, k, act, scratch):
     # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA;
-    # given a workspace, (64, 64, 4096) splits along K and the M >= 512 cases
-    # run on weights dequantized once to bf16
+    # given a workspace, (64, 64, 4096) splits along K (the dequantized-weight
+    # path needs 256 x 256 tiles to fill the device: test_w8a16_config)
     rng = np.random.default_rng(m * n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     q, s = quantized_weight(orc, rng, n, k)
     bias = rng.normal(0, 0.1, n).astype(np.float32)
     need = K.linear_workspace_size(m, n, k, tg.i8)
     if dev.info()["compute_units"] == 256:
-        assert (need > 0) == ((m, n, k) in ((64, 64, 4096), (600, 96, 128), (530, 200, 64))), need
+        assert (need > 0) == ((m, n, k) == (64, 64, 4096)), need
     got = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(
         dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), act=act).to_host())
     ref = orc.w8a16_linear(x, q, s, bias)
