@@ -49,22 +49,23 @@ constexpr float kRescale = 8.0f;
 #define ATTN_LA 3
 #endif
 
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q,
+template <int D, bool CAUSAL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 *__restrict__ Q,
                                                       const bf16 *__restrict__ K,
                                                       const bf16 *__restrict__ V,
                                                       bf16 *__restrict__ O, float *__restrict__ L,
                                                       int nq, int nk, float scale_log2, int nqb) {
-  constexpr int BM = 128;          // queries per workgroup
+  constexpr int NT = 64 * WAVES;   // threads per workgroup
+  constexpr int BM = 32 * WAVES;   // queries per workgroup (32 per wave)
   constexpr int BN = 64;           // keys per tile
   constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
   constexpr int RPB = 128 / D;     // rows per 256-byte LDS bank window
-  constexpr int RPI = 256 / CPR;   // rows covered by one load round of the workgroup
-  constexpr int NLD = BN * CPR / 256;  // load rounds per tile
+  constexpr int RPI = NT / CPR;    // rows covered by one load round of the workgroup
+  constexpr int NLD = BN * CPR / NT;  // load rounds per tile
   constexpr int TILE = BN * D;     // elements of one K or V tile
   constexpr int NS = D / 16;       // k-steps of the score MFMA
   constexpr int ND = D / 32;       // d-blocks of the output
-  static_assert(NLD >= 1 && BN * CPR % 256 == 0, "tile must be a whole number of load rounds");
+  static_assert(NLD >= 1 && BN * CPR % NT == 0, "tile must be a whole number of load rounds");
   // K tiles (t & 1) then V tiles (t & 1), dense rows with XOR-swizzled
   // 16-byte chunks: chunk j of row r sits at position j ^ fk(r) (K) or
   // j ^ fv(r) (V).  fk spreads the 16 rows that one ds_read_b128 quarter-wave
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
 
     // ── global -> LDS: one 16-byte slot per thread per round, straight into
     // LDS (global_load_lds_dwordx4: lane j of a wave lands at base + 16 j).
-    // Slot t + 256 i of a tile is row t / CPR + RPI i, position t % CPR; the
+    // Slot t + NT i of a tile is row t / CPR + RPI i, position t % CPR; the
     // source chunk is that position XOR the row's swizzle.  Rows past nk are
     // zero-filled so that P = 0 never meets stale data in the P*V product.
     const int ld_row = tid / CPR;
@@ -144,16 +145,16 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
       if (kbase + BN <= nk) {
 #pragma unroll
         for (int i = 0; i < NLD; ++i)
-          __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
+          __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (NT * i + 64 * w) * 8),
                                            16, 0, 0);
       } else {
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
           if (kbase + ld_row + RPI * i < nk) {
-            __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (256 * i + 64 * w) * 8),
+            __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (NT * i + 64 * w) * 8),
                                              16, 0, 0);
           } else {
-            *reinterpret_cast<u32x4 *>(dst + (256 * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4 *>(dst + (NT * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
           }
         }
       }
@@ -217,18 +218,27 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
         }
     };
     auto tile_max = [&](const f32x16 (&sc_t)[2]) __attribute__((always_inline)) {
-      // pairwise tree (depth 5) rather than a 32-long dependent chain
-      float t[16];
+      // Three-input tree (v_maximum3_f32: 17 instructions for 32 values).
+      // IEEE maximum rather than fmaxf: fmaxf's NaN-dropping form makes the
+      // compiler canonicalize every MFMA result first (one extra VALU op per
+      // score); a NaN score gives a NaN row either way, through p.
+      auto mx2 = [](float a, float b) { return __builtin_elementwise_maximum(a, b); };
+      auto mx3 = [&](float a, float b, float c) { return mx2(mx2(a, b), c); };
+      float x[32];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) t[v] = fmaxf(sc_t[0][v], sc_t[1][v]);
+      for (int v = 0; v < 16; ++v) {
+        x[v] = sc_t[0][v];
+        x[16 + v] = sc_t[1][v];
+      }
+      float u[11];
 #pragma unroll
-      for (int n = 8; n > 0; n >>= 1)
-#pragma unroll
-        for (int v = 0; v < n; ++v) t[v] = fmaxf(t[v], t[v + n]);
-      const float mx = t[0];
+      for (int i = 0; i < 10; ++i) u[i] = mx3(x[3 * i], x[3 * i + 1], x[3 * i + 2]);
+      u[10] = mx2(x[30], x[31]);
+      const float w0 = mx3(u[0], u[1], u[2]), w1 = mx3(u[3], u[4], u[5]), w2 = mx3(u[6], u[7], u[8]);
+      const float mx = mx3(mx3(w0, w1, w2), u[9], u[10]);
       // the keys of a query are split over lanes l and l ^ 32
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      return mx2(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     };
     auto needs_mask = [&](int kt) {
       return (kt * BN + BN > nk) || (CAUSAL && kt * BN + BN - 1 > q0);
@@ -299,12 +309,15 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16(const bf16 *__restrict__ Q
           // product; the row sum stays in fp32 so that L = m + log(l) keeps
           // fp32 accuracy.
           u32x4 pw[2][2];
-          float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          // four partial sums, each started by its first pair (no + 0.0f,
+          // which the compiler must keep for a -0.0 operand)
+          float ps[4];
           auto softmax_pair = [&](int q) __attribute__((always_inline)) {
             const int kb = q >> 3, v = 2 * (q & 7);
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v], sc, neg_m));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
-            ps[(v >> 1) & 3] += p0 + p1;
+            if (q < 4) ps[q & 3] = p0 + p1;
+            else ps[q & 3] += p0 + p1;
             const bf16x2 pair = cvt_pk_bf16(p0, p1);
             uint32_t word;
             __builtin_memcpy(&word, &pair, 4);
@@ -453,16 +466,17 @@ static void launch_f32(const void *q, const void *k, const void *v, void *o, flo
 template <int D>
 static void launch_bf16(const void *q, const void *k, const void *v, void *o, float *l, int nq,
                         int nk, float scale, int BH, int causal, hipStream_t s) {
-  const int nqb = (nq + 127) / 128;
+  constexpr int WAVES = 4;
+  const int nqb = (nq + 32 * WAVES - 1) / (32 * WAVES);
   const float scale_log2 = scale * kLog2e;
   const dim3 grid(BH * (causal ? (nqb + 1) / 2 : nqb));
   if (causal) {
-    hipLaunchKernelGGL((fa_fwd_bf16<D, true>), grid, dim3(256), 0, s,
+    hipLaunchKernelGGL((fa_fwd_bf16<D, true, WAVES>), grid, dim3(64 * WAVES), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
                        static_cast<const bf16 *>(v), static_cast<bf16 *>(o), l, nq, nk, scale_log2,
                        nqb);
   } else {
-    hipLaunchKernelGGL((fa_fwd_bf16<D, false>), grid, dim3(256), 0, s,
+    hipLaunchKernelGGL((fa_fwd_bf16<D, false, WAVES>), grid, dim3(64 * WAVES), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
                        static_cast<const bf16 *>(v), static_cast<bf16 *>(o), l, nq, nk, scale_log2,
                        nqb);

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
       const int k = k0 + a_col;
       int off;
       if constexpr (AMODE == kAPlain) {
-        off = live & (k < p.K) ? a_off[i] + 2 * k : kOffNone;
+        off = (live & (k < p.K)) ? a_off[i] + 2 * k : kOffNone;
       } else {
         auto gather = [&](const TapState &t, int col_bytes) __attribute__((always_inline)) {
           const int ih = a_ih0[i] + t.kh, iw = a_iw0[i] + t.kw;
