@@ -475,30 +475,40 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     }
   } else {
     // two register sets (loop unrolled by two so the sets are named
-    // statically): a tile's loads have two k-tiles of MFMA work to land
+    // statically): a tile's loads have two k-tiles of MFMA work to land.
+    // With the buffer-load paths the loads are issued unconditionally: past
+    // the last k-tile they are given k = K, which puts every lane's offset
+    // out of range (zeros, no memory access).  A branch around the loads
+    // would make the compiler's wait before the LDS stores assume the path
+    // without them and drain the set just issued too (depth 1, not 2).
+    constexpr bool kDeadLoads = AMODE == kAConvVec || (AMODE == kAPlain && KVEC);
     u32x4 ra0[A_CH], rb0[B_CH], ra1[A_CH], rb1[B_CH];
     load_a(k_first, ra0);
     load_b(k_first, rb0);
-    if (n_k > 1) {
-      load_a(k_first + BK, ra1);
-      load_b(k_first + BK, rb1);
+    if (kDeadLoads || n_k > 1) {
+      const int k1 = n_k > 1 ? k_first + BK : p.K;
+      load_a(k1, ra1);
+      load_b(k1, rb1);
     }
     store_stage(0, ra0, rb0);
     __syncthreads();
     // next_*: the set holding tile kt+1; free_*: the set tile kt+2 is loaded into
     auto step = [&](int kt, const u32x4 (&next_a)[A_CH], const u32x4 (&next_b)[B_CH],
                     u32x4 (&free_a)[A_CH], u32x4 (&free_b)[B_CH]) __attribute__((always_inline)) {
-      if (kt + 2 < n_k) {
-        load_a(k_first + (kt + 2) * BK, free_a);
-        load_b(k_first + (kt + 2) * BK, free_b);
+      if (kDeadLoads || kt + 2 < n_k) {
+        const int k2 = kt + 2 < n_k ? k_first + (kt + 2) * BK : p.K;
+        load_a(k2, free_a);
+        load_b(k2, free_b);
       }
-      compute(kt & 1);
-      if (kt + 1 < n_k) store_stage((kt + 1) & 1, next_a, next_b);
-      __syncthreads();
+      if (!kDeadLoads || kt < n_k) {
+        compute(kt & 1);
+        if (kt + 1 < n_k) store_stage((kt + 1) & 1, next_a, next_b);
+        __syncthreads();
+      }
     };
     for (int kt = 0; kt < n_k; kt += 2) {
       step(kt, ra1, rb1, ra0, rb0);
-      if (kt + 1 < n_k) step(kt + 1, ra0, rb0, ra1, rb1);
+      if (kDeadLoads || kt + 1 < n_k) step(kt + 1, ra0, rb0, ra1, rb1);
     }
   }
 
