@@ -132,32 +132,23 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
     const int wave_end = CAUSAL ? min(kv_end, q0 + 32) : kv_end;
 
     // ── global -> LDS: one 16-byte slot per thread per round, straight into
-    // LDS (global_load_lds_dwordx4: lane j of a wave lands at base + 16 j).
-    // Slot t + NT i of a tile is row t / CPR + RPI i, position t % CPR; the
-    // source chunk is that position XOR the row's swizzle.  Rows past nk are
-    // zero-filled so that P = 0 never meets stale data in the P*V product.
+    // LDS by buffer loads with the lds flag (lane j of a wave lands at
+    // base + 16 j).  Slot t + NT i of a tile is row t / CPR + RPI i, position
+    // t % CPR; the source chunk is that position XOR the row's swizzle.  The
+    // buffer extent is the head's nk rows, so rows past nk read as zeros and
+    // P = 0 never meets stale data in the P*V product.  The DMA is issued from
+    // inline assembly: the compiler's own tracking of an LDS DMA in flight
+    // turns every LDS-read wait of the stage into lgkmcnt(0).
     const int ld_row = tid / CPR;
-    const int k_off = ld_row * D + ((tid % CPR) ^ fk(ld_row)) * 8;
-    const int v_off = ld_row * D + ((tid % CPR) ^ fv(ld_row)) * 8;
-    auto load_tile = [&](const bf16 *src, bf16 *dst, int kbase, int off) __attribute__((always_inline)) {
-      const bf16 *tile_src = src + static_cast<int64_t>(kbase) * D + off;
-      typedef __attribute__((address_space(3))) void lds_void;
-      if (kbase + BN <= nk) {
+    const int k_off = 2 * (ld_row * D + ((tid % CPR) ^ fk(ld_row)) * 8);
+    const int v_off = 2 * (ld_row * D + ((tid % CPR) ^ fv(ld_row)) * 8);
+    const __amdgpu_buffer_rsrc_t k_rsrc = buffer_rsrc(Kb, nk * D * 2);
+    const __amdgpu_buffer_rsrc_t v_rsrc = buffer_rsrc(Vb, nk * D * 2);
+    auto load_tile = [&](__amdgpu_buffer_rsrc_t r, bf16 *dst, int kbase, int off) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < NLD; ++i)
-          __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (NT * i + 64 * w) * 8),
-                                           16, 0, 0);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NLD; ++i) {
-          if (kbase + ld_row + RPI * i < nk) {
-            __builtin_amdgcn_global_load_lds(tile_src + RPI * i * D, (lds_void *)(dst + (NT * i + 64 * w) * 8),
-                                             16, 0, 0);
-          } else {
-            *reinterpret_cast<u32x4 *>(dst + (NT * i + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-      }
+      for (int i = 0; i < NLD; ++i)
+        buffer_lds_dma16(r, off + 2 * (kbase + RPI * i) * D,
+                         __builtin_amdgcn_readfirstlane(lds_address(dst + (NT * i + 64 * w) * 8)));
     };
 
     // ── LDS -> operands
@@ -200,9 +191,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
     // barrier that publishes them.
     const std::false_type even{};
     const std::true_type odd{};
-    load_tile(Kb, kbuf(even), 0, k_off);
-    if (n_tiles > 1) load_tile(Kb, kbuf(odd), BN, k_off);
-    load_tile(Vb, vbuf(even), 0, v_off);
+    load_tile(k_rsrc, kbuf(even), 0, k_off);
+    if (n_tiles > 1) load_tile(k_rsrc, kbuf(odd), BN, k_off);
+    load_tile(v_rsrc, vbuf(even), 0, v_off);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // Masks tile kt of a wave's scores (keys past nk; causal: keys past the
@@ -257,8 +248,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
     auto stage = [&](auto par, int kt, f32x16 (&s_cur)[2], f32x16 (&s_nx)[2]) __attribute__((always_inline)) {
       constexpr bool P = decltype(par)::value;
       const std::integral_constant<bool, !P> npar{};
-      if (kt + 2 < n_tiles) load_tile(Kb, kbuf(par), (kt + 2) * BN, k_off);
-      if (kt + 1 < n_tiles) load_tile(Vb, vbuf(npar), (kt + 1) * BN, v_off);
+      if (kt + 2 < n_tiles) load_tile(k_rsrc, kbuf(par), (kt + 2) * BN, k_off);
+      if (kt + 1 < n_tiles) load_tile(v_rsrc, vbuf(npar), (kt + 1) * BN, v_off);
 
       if (kt * BN < wave_end) {  // causal: later tiles are beyond this wave's last query
         const float mx_s = mx_cur * sc;  // sc > 0: -inf stays -inf
@@ -318,6 +309,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][v + 1], sc, neg_m));
             if (q < 4) ps[q & 3] = p0 + p1;
             else ps[q & 3] += p0 + p1;
+            // the sum is taken here, not after the last MFMA: otherwise all
+            // 32 fp32 p of the tile stay live across the stage
+            asm volatile("" : "+v"(ps[q & 3]));
             const bf16x2 pair = cvt_pk_bf16(p0, p1);
             uint32_t word;
             __builtin_memcpy(&word, &pair, 4);

@@ -72,17 +72,6 @@ struct GemmParams {
   int n_fast;
 };
 
-// Raw buffer resource over [base, base + bytes): a load at an offset past
-// the extent returns zeros.  kOffNone is such an offset for any extent below
-// 2^31.  Word 3 is the gfx9 raw-buffer format (32-bit data, no swizzle).
-constexpr uint32_t kBufWord3 = 0x00020000u;
-constexpr int kOffNone = static_cast<int>(0x80000000u);
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufWord3);
-}
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 __device__ __forceinline__ void epi_coeffs(const GemmParams &p, int n, float (&mul)[4], float (&add)[4]) {
   if (n + 4 <= p.N && (n & 3) == 0) {

@@ -47,26 +47,6 @@
 
 namespace teeny {
 
-__device__ __forceinline__ uint32_t lds_address(const void *p) {
-  typedef __attribute__((address_space(3))) const char lds_char;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)(p)));
-}
-
-// One 16-byte LDS-DMA per lane from a buffer resource: lane j writes
-// lds + 16 j, reading [voff, voff + 16) (zeros past the extent).  M0 carries
-// the wave's LDS base and is restored afterwards.
-__device__ __forceinline__ void buffer_lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(r), "s"(lds)
-      : "memory");
-}
 
 constexpr int kDmaBK = 32;
 

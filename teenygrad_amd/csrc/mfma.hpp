@@ -13,6 +13,41 @@
 
 namespace teeny {
 
+// Raw buffer resource over [base, base + bytes): a load at an offset past
+// the extent returns zeros.  kOffNone is such an offset for any extent below
+// 2^31.  Word 3 is the gfx9 raw-buffer format (32-bit data, no swizzle).
+constexpr uint32_t kBufWord3 = 0x00020000u;
+constexpr int kOffNone = static_cast<int>(0x80000000u);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  typedef __attribute__((address_space(3))) const char lds_char;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)(p)));
+}
+
+// One 16-byte LDS-DMA per lane from a buffer resource: lane j writes
+// lds + 16 j, reading [voff, voff + 16) (zeros past the extent).  M0 carries
+// the wave's LDS base and is restored afterwards.  Issued from inline
+// assembly, so the compiler neither tracks it (the caller waits on vmcnt
+// itself) nor lets it degrade its own LDS-read waits to lgkmcnt(0).
+__device__ __forceinline__ void buffer_lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(r), "s"(lds)
+      : "memory");
+}
+
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
