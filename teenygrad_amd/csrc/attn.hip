@@ -320,6 +320,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
 
 #pragma unroll
           for (int i = 0; i < kLA; ++i) kread(i);
+          // Wave priority 1 over the score bundles, 0 over P*V and the tail:
+          // of the two waves on a SIMD, the one issuing score MFMAs with
+          // exponentials in between is issued first, and the P*V MFMAs of
+          // the other fill the matrix core around it (5% fewer cycles per
+          // tile measured).
+          __builtin_amdgcn_s_setprio(1);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int i = 0; i < nS; ++i) {
@@ -333,6 +339,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
             __builtin_amdgcn_sched_barrier(0);
           }
           l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+          __builtin_amdgcn_s_setprio(0);
 #pragma unroll
           for (int j = 0; j < nPV; ++j) {
             if (j + kLA < nPV) vread(j + kLA);
