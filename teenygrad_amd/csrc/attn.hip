@@ -8,26 +8,25 @@
 //
 // Two kernels:
 //
-// fa_fwd_bf16 (the MI355X path).  One workgroup = 4 waves = 128 queries of
-// one (b, h); each wave owns 32 queries.  K and V tiles of 64 keys are
-// staged in LDS (double-buffered, next tile prefetched into registers while
-// the current one is consumed).  Scores are computed transposed,
-// S^T = K * Q^T, with v_mfma_f32_32x32x16_bf16: Q^T is the B operand and
-// stays in registers for the whole key loop, and each lane's accumulator
-// column is one query, so the softmax max/sum over keys is an in-lane
-// reduction plus one exchange with lane ^ 32.  The probabilities are
-// rounded to bf16 and fed, in exactly the registers the score MFMA wrote
-// them to, as the B operand of O^T += V^T * P^T; V is written to LDS
-// transposed ([d][key]) so that the matching A operand is two 8-byte LDS
-// reads per MFMA.  The loop is bound by VALU issue as much as by the matrix
-// cores (32 MFMAs vs 32 quarter-rate exps per lane per tile), so the softmax
-// is pared down: the tile max is taken on raw scores, scale * log2 e and the
-// max subtraction are one FMA ahead of v_exp_f32, the running output is
-// rescaled only when the max grows by more than 2^8 (a wave-uniform branch,
-// normally taken on the first tile only), and probabilities are rounded to
-// bf16 two per v_cvt_pk_bf16_f32.  fp32 throughout; the output is
-// normalised once at the end.  Causal tiles beyond a wave's last query are skipped per wave and
-// the query-block order is reversed so the heaviest blocks start first.
+// fa_fwd_bf16 (the MI355X path).  One workgroup = WAVES waves (4 as
+// launched) of 32 queries of one (b, h).  K and V tiles of 64 keys are
+// double-buffered in LDS, moved there by LDS-DMA one tile ahead.  Scores are
+// computed transposed, S^T = K * Q^T, with v_mfma_f32_32x32x16_bf16: Q^T is
+// the B operand and stays in registers for the whole key loop, and each
+// lane's accumulator column is one query, so the softmax max/sum over keys is
+// an in-lane reduction plus one exchange with lane ^ 32.  The probabilities
+// are rounded to bf16 and fed, in exactly the registers the score MFMA wrote
+// them to, as the B operand of O^T += V^T * P^T; V stays row-major in LDS and
+// the V^T operand is read with ds_read_b64_tr_b16 (two 8-byte transposing
+// reads per MFMA).  A wave's VALU work does not overlap its own MFMAs, only
+// another wave's, so the softmax is pared down: the tile max is taken on raw
+// scores, scale * log2 e and the max subtraction are one FMA ahead of
+// v_exp_f32, the running output is rescaled only when the max grows by more
+// than 2^8 (a wave-uniform branch, normally taken on the first tile only),
+// and probabilities are rounded to bf16 two per v_cvt_pk_bf16_f32.  fp32
+// throughout; the output is normalised once at the end.  Causal tiles beyond
+// a wave's last query are skipped per wave and the query-block order is
+// reversed so the heaviest blocks start first.
 // The 1-D grid is remapped so that each XCD runs the query blocks of a few
 // (b, h) pairs at a time: they stream the same K/V tiles, which then come
 // from that XCD's L2 rather than once per workgroup from HBM.
