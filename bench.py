@@ -241,7 +241,9 @@ def bench_attention(args, tg, dev, stream, s, causal, idx):
             "config": {"workload": f"sdpa {'causal' if causal else 'non-causal'} bf16 B*H=256 S={s} D=128",
                        "flop_per_step": flops},
             "roofline": {"bound": "mfma", "kernel": name, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                         "traffic": load_traffic(args.workload),
+                         "algorithmic_bytes": 4 * bh * s * d * 2 + bh * s * 4,
                          "avg_us": round(per[name] * 1e3, 2)},
             "cpu_baseline": cpu, "wall_s": round(wall, 3)}
 
@@ -343,12 +345,12 @@ def bench_w8a16(args, tg, dev, stream):
         q, s, _, _ = K.quantize_affine(wf, [n, k], "channel", 0)
         del wf
         y = tg.Buffer(tg.bf16, (m, n))
-        problems.append((f"w8a16 {m}x{k}->{n}", x, q, s, y, 2.0 * m * n * k))
+        problems.append((f"w8a16 {m}x{k}->{n}", x, q, s, y, 2 * m * k + n * k + 4 * n + 2 * m * n, 2.0 * m * n * k))
     attach_workspace(tg, dev, stream, (K.linear_workspace_size(m, n, k, tg.i8)
                                        for k, n in ((4096, 11008), (11008, 4096))))
 
     def step(t):
-        for name, x, q, s, y, _ in problems:
+        for name, x, q, s, y, _, _ in problems:
             launch(t, name, lambda: K.w8a16_linear(x, q, s, y=y, stream=stream))
 
     ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, len(problems))
@@ -358,13 +360,15 @@ def bench_w8a16(args, tg, dev, stream):
            for p in problems}
     dom = max(per, key=per.get)
     fdom = [p[-1] for p in problems if p[0] == dom][0]
+    dom_bytes = [p[-2] for p in problems if p[0] == dom][0]  # x bf16 + int8 q + fp32 scales + y bf16
     ach = fdom / (per[dom] * 1e-3) / 1e12
     return {"metric": METRIC, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
             "dtype": "bf16", "scaling": "weak",
             "config": {"workload": "w8a16 GEMMs M=4096: K=4096->N=11008 and K=11008->N=4096, int8 per-channel weights",
                        "flop_per_step": flops},
             "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                         "traffic": load_traffic(args.workload), "algorithmic_bytes": dom_bytes},
             "ops": ops, "cpu_baseline": None, "wall_s": round(wall, 3)}
 
 

@@ -70,6 +70,11 @@ struct GemmParams {
   // grid order: consecutive tiles (one XCD's run, one L2) walk along N and
   // share their A row block (1), or walk along M and share B (0)
   int n_fast;
+  // LDS-DMA kernel only: when > 0, consecutive tiles first cover `group`
+  // tiles of the other dimension (a group x run block of tiles per XCD, so
+  // both operands are shared through its L2), then step along n_fast's
+  // dimension
+  int group;
 };
 
 
@@ -776,7 +781,7 @@ inline void launch_split(GemmParams p, hipStream_t s, Scratch scr) {
 template <bool INT8B, int AMODE>
 inline bool big_gemm_fits(const GemmParams &p);
 template <bool INT8B, int AMODE>
-inline void launch_big_gemm(const GemmParams &p, hipStream_t s);
+inline void launch_big_gemm(GemmParams p, hipStream_t s);
 
 // Tile choice (measured on MI355X over the ResNet-50 and W8A16 shapes):
 //  * the 256 x 256 LDS-DMA kernel (gemm_dma.hpp) when its tiles fill the chip;
