@@ -263,7 +263,9 @@ teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void 
  * head_dim are arguments, neg_inf is internal, and `causal` != 0 masks key j
  * from query i when j > i (top-left aligned, as torch's is_causal).
  * l is fp32 for every dtype and may be NULL.  dtype F32: head_dim a power of
- * two <= 256.  dtype BF16: MFMA flash kernel, head_dim 64 or 128. */
+ * two <= 256.  dtype BF16: MFMA flash kernel, head_dim 64 or 128, 16-byte
+ * aligned q/k/v/o, and one head's K (and V) below 2 GiB (n_ctx_k * head_dim
+ * * 2 bytes; TEENY_ERR_SHAPE_MISMATCH otherwise). */
 teeny_status teeny_flash_attention2_forward(const void *q, const void *k, const void *v, void *o,
                                             float *l, int64_t n_ctx_q, int64_t n_ctx_k,
                                             float softmax_scale, int64_t BH, int64_t head_dim,

@@ -111,6 +111,9 @@ def test_attention_errors():
            _lib.ERR_NULL_POINTER)
     expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 8, 0.125, 4, 64, 0, _lib.I8, None),
            _lib.ERR_UNSUPPORTED_DTYPE)
+    # bf16 K/V of one head are addressed with 32-bit offsets: 2^23 keys of 128 bf16 are 2 GiB
+    expect(fa(FAKE, FAKE, FAKE, FAKE, None, 8, 1 << 23, 0.125, 4, 128, 0, _lib.BF16, None),
+           _lib.ERR_SHAPE_MISMATCH)
 
 
 def shape_arr(*s):
