@@ -525,6 +525,9 @@ extern "C" teeny_status teeny_flash_attention2_forward(const void *q, const void
   if (dtype == TEENY_BF16) {
     TEENY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
                   TEENY_ERR_MISALIGNED, "flash_attention2_forward: bf16 q/k/v/o must be 16-byte aligned");
+    // K and V of one (batch, head) are read through 32-bit buffer offsets
+    TEENY_REQUIRE(n_ctx_k * head_dim * 2 <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                  "flash_attention2_forward: bf16 K/V of one head must be below 2 GiB");
     switch (head_dim) {
       case 64: launch_bf16<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
       case 128: launch_bf16<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
