@@ -801,7 +801,12 @@ inline GemmTiles gemm_tiles(const GemmParams &p) {
   }
   if (p.N <= 64) return p.K >= 512 ? kTiles64x64 : kTiles128x64;
   if (p.K <= 256) return kTiles128x128Short;
-  if (tiles_of(p, 128, 128) < device_cu_count() && split_plan<128, 128, 64>(p).used == 1) return kTiles128x64Deep;
+  // 128 x 64 tiles with a two-tile prefetch when 128 x 128 tiles leave CUs
+  // idle: unsplit up to K = 2048 (7x7 2048 -> 512: 17.5 us against 25 us
+  // for four K slices plus their reduction), split beyond (a 4608-deep K
+  // chain of 72 k-tiles is long enough that slicing it wins)
+  if (tiles_of(p, 128, 128) < device_cu_count() && (split_plan<128, 128, 64>(p).used == 1 || p.K <= 2048))
+    return kTiles128x64Deep;
   return kTiles128x128;
 }
 
@@ -885,7 +890,7 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
     case kTiles128x64: launch_split<128, 64, 32, 2, 2, INT8B, AMODE>(p, s, scr); break;
     case kTiles64x64: launch_split<64, 64, 64, 2, 2, INT8B, AMODE>(p, s, scr); break;
     case kTiles128x128Short: launch_split<128, 128, 32, 2, 2, INT8B, AMODE>(p, s, scr); break;
-    case kTiles128x64Deep: launch_split<128, 64, 64, 2, 1, INT8B, AMODE>(p, s, scr); break;
+    case kTiles128x64Deep: launch_split<128, 64, 64, 2, 2, INT8B, AMODE>(p, s, scr); break;
     default: launch_split<128, 128, 64, 2, 1, INT8B, AMODE>(p, s, scr); break;
   }
   return true;
