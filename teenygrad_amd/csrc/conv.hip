@@ -167,11 +167,23 @@ __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x
     const int len = (ce - cb) * KHW;  // floats per weight row in this chunk
     __syncthreads();                  // the previous chunk's LDS reads are done
     {
-      // row i = tid / 16 of the block, 16 consecutive floats per step
+      // row i = tid / 16 of the block, 16 consecutive floats per step (four
+      // per thread and step as one 16-byte load when the row allows it: the
+      // LDS row starts at a multiple of 4 floats since pitch = 4 mod 64)
       const int i = threadIdx.x >> 4, j0 = threadIdx.x & 15;
       const int n = n0 + i;
-      const float *src = w + (static_cast<int64_t>(n < q.Cout ? n : 0) * K + static_cast<int64_t>(cb) * KHW);
-      for (int j = j0; j < len; j += 16) wl[i * pitch + j] = n < q.Cout ? src[j] : 0.0f;
+      const int64_t src_off = static_cast<int64_t>(n < q.Cout ? n : 0) * K + static_cast<int64_t>(cb) * KHW;
+      const float *src = w + src_off;
+      if (((reinterpret_cast<uintptr_t>(w) >> 2) + src_off) % 4 == 0) {
+        const int len4 = len & ~3;
+        for (int j = 4 * j0; j < len4; j += 64) {
+          f32x4 v4 = n < q.Cout ? *reinterpret_cast<const f32x4 *>(src + j) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          *reinterpret_cast<f32x4 *>(&wl[i * pitch + j]) = v4;
+        }
+        for (int j = len4 + j0; j < len; j += 16) wl[i * pitch + j] = n < q.Cout ? src[j] : 0.0f;
+      } else {
+        for (int j = j0; j < len; j += 16) wl[i * pitch + j] = n < q.Cout ? src[j] : 0.0f;
+      }
     }
     __syncthreads();
     for (int kh = 0; kh < q.KH; ++kh) {
