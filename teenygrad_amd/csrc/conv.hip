@@ -357,40 +357,46 @@ static GemmParams conv_gemm_params(const void *x, const void *w, const float *sc
 // (0 where 2 kh2 + dy >= KH or 2 kw2 + dx >= KW): output (oh, ow) reads
 // x_pad rows 2 (oh + kh2) + dy = 2 oh + kh, the same taps.  The two repacked
 // tensors live in the caller's scratch (the stream's workspace).
-__global__ __launch_bounds__(256) void s2d_input_kernel(const bf16 *__restrict__ x, bf16 *__restrict__ xs,
-                                                        int B, int H, int W, int C, int PH, int PW, int Hs,
-                                                        int Ws, int C2) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(B) * Hs * Ws;
-  if (t >= total) return;
-  const int v = static_cast<int>(t % Ws);
-  const int u = static_cast<int>((t / Ws) % Hs);
-  const int b = static_cast<int>(t / (static_cast<int64_t>(Ws) * Hs));
-  bf16 *dst = xs + t * C2;
-  for (int c0 = 0; c0 < C2; c0 += 8) {
-    bf16 e[8];
+// One launch for both rewrites: blocks [0, nbx) write the input, one output
+// pixel per thread; the rest write the weights, one element per thread.
+// Channel ch of the rewritten tensors is sub-pixel q = ch / C, channel
+// c = ch % C; both are stepped along a pixel's channels instead of divided.
+__global__ __launch_bounds__(256) void s2d_kernel(const bf16 *__restrict__ x, bf16 *__restrict__ xs,
+                                                  const bf16 *__restrict__ w, bf16 *__restrict__ ws, int nbx,
+                                                  int B, int H, int W, int C, int PH, int PW, int Hs, int Ws,
+                                                  int N, int KH, int KW, int KH2, int KW2, int C2) {
+  if (static_cast<int>(blockIdx.x) < nbx) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(B) * Hs * Ws;
+    if (t >= total) return;
+    const int v = static_cast<int>(t % Ws);
+    const int u = static_cast<int>((t / Ws) % Hs);
+    const int b = static_cast<int>(t / (static_cast<int64_t>(Ws) * Hs));
+    bf16 *dst = xs + t * C2;
+    int q = 0, c = 0;  // sub-pixel and channel of output channel c0 + k
+    for (int c0 = 0; c0 < C2; c0 += 8) {
+      bf16 e[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int ch = c0 + k;
-      float val = 0.0f;
-      if (ch < 4 * C) {
-        const int q = ch / C, c = ch % C;
-        const int ih = 2 * u + (q >> 1) - PH, iw = 2 * v + (q & 1) - PW;
-        if (ih >= 0 && ih < H && iw >= 0 && iw < W)
-          val = static_cast<float>(x[((static_cast<int64_t>(b) * H + ih) * W + iw) * C + c]);
+      for (int k = 0; k < 8; ++k) {
+        float val = 0.0f;
+        if (q < 4) {
+          const int ih = 2 * u + (q >> 1) - PH, iw = 2 * v + (q & 1) - PW;
+          if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+            val = static_cast<float>(x[((static_cast<int64_t>(b) * H + ih) * W + iw) * C + c]);
+          if (++c == C) {
+            c = 0;
+            ++q;
+          }
+        }
+        e[k] = static_cast<bf16>(val);
       }
-      e[k] = static_cast<bf16>(val);
+      u32x4 pk;
+      __builtin_memcpy(&pk, e, 16);
+      *reinterpret_cast<u32x4 *>(dst + c0) = pk;
     }
-    u32x4 pk;
-    __builtin_memcpy(&pk, e, 16);
-    *reinterpret_cast<u32x4 *>(dst + c0) = pk;
+    return;
   }
-}
-
-__global__ __launch_bounds__(256) void s2d_weight_kernel(const bf16 *__restrict__ w, bf16 *__restrict__ ws,
-                                                         int N, int KH, int KW, int C, int KH2, int KW2,
-                                                         int C2) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t t = static_cast<int64_t>(blockIdx.x - nbx) * 256 + threadIdx.x;
   const int64_t total = static_cast<int64_t>(N) * KH2 * KW2 * C2;
   if (t >= total) return;
   const int ch = static_cast<int>(t % C2);
@@ -489,10 +495,10 @@ static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, v
   bf16 *wsd = reinterpret_cast<bf16 *>(static_cast<char *>(scr.ptr) + sp.w_off);
   const int64_t nx = static_cast<int64_t>(q.B) * g2.H * g2.W;
   const int64_t nw = static_cast<int64_t>(q.Cout) * g2.KH * g2.KW * g2.Cin;
-  hipLaunchKernelGGL(s2d_input_kernel, dim3(static_cast<unsigned>((nx + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16 *>(x), xs, q.B, q.H, q.W, q.Cin, q.PH, q.PW, g2.H, g2.W, g2.Cin);
-  hipLaunchKernelGGL(s2d_weight_kernel, dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16 *>(w), wsd, q.Cout, q.KH, q.KW, q.Cin, g2.KH, g2.KW, g2.Cin);
+  const int nbx = static_cast<int>((nx + 255) / 256), nbw = static_cast<int>((nw + 255) / 256);
+  hipLaunchKernelGGL(s2d_kernel, dim3(static_cast<unsigned>(nbx + nbw)), dim3(256), 0, s,
+                     static_cast<const bf16 *>(x), xs, static_cast<const bf16 *>(w), wsd, nbx, q.B, q.H, q.W,
+                     q.Cin, q.PH, q.PW, g2.H, g2.W, q.Cout, q.KH, q.KW, g2.KH, g2.KW, g2.Cin);
   GemmParams p = conv_gemm_params(xs, wsd, nullptr, nullptr, bias_bf16, y, g2);
   const Scratch rest{static_cast<char *>(scr.ptr) + sp.gemm_off, scr.bytes - sp.gemm_off};
   launch_gemm_mfma<false, kAConvVec>(p, act, s, rest);
