@@ -782,8 +782,13 @@ template <bool INT8B, int AMODE>
 inline bool big_gemm_fits(const GemmParams &p);
 template <bool INT8B, int AMODE>
 inline void launch_big_gemm(GemmParams p, hipStream_t s);
+template <bool INT8B, int AMODE>
+inline bool stream_gemm_fits(const GemmParams &p);
+inline void launch_stream_gemm(const GemmParams &p, hipStream_t s);
 
 // Tile choice (measured on MI355X over the ResNet-50 and W8A16 shapes):
+//  * the streaming kernel (gemm_stream.hpp) for long, HBM-bound problems
+//    with K, N <= 256 and bf16 weights (the full-resolution 1x1 convs);
 //  * the 256 x 256 LDS-DMA kernel (gemm_dma.hpp) when its tiles fill the chip;
 //  * narrow outputs (N <= 64): 64 x 64 x 64 tiles for deep K (more
 //    workgroups to hide latency), else 128 x 64 x 32;
@@ -792,10 +797,11 @@ inline void launch_big_gemm(GemmParams p, hipStream_t s);
 //  * grids of 128 x 128 tiles that leave CUs idle and do not split along K:
 //    128 x 64 x 64 (twice the workgroups);
 //  * otherwise 128 x 128 x 64, split along K when badly under-filled.
-enum GemmTiles { kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
+enum GemmTiles { kTilesStream, kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
 
 template <bool INT8B, int AMODE>
 inline GemmTiles gemm_tiles(const GemmParams &p) {
+  if (stream_gemm_fits<INT8B, AMODE>(p)) return kTilesStream;
   if constexpr (AMODE != kAConvScalar) {
     if (big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
   }
@@ -884,6 +890,7 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
   p.act = act;
   p.ws = nullptr;
   switch (gemm_tiles<INT8B, AMODE>(p)) {
+    case kTilesStream: launch_stream_gemm(p, s); break;
     case kTilesBig:
       if constexpr (AMODE != kAConvScalar) launch_big_gemm<INT8B, AMODE>(p, s);
       break;
@@ -899,3 +906,4 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
 }  // namespace teeny
 
 #include "gemm_dma.hpp"
+#include "gemm_stream.hpp"

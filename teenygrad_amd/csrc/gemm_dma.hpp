@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
     } else {
       const int i = d - A_LD;
       const int k = k0 + b_col;
-      const int off = live & (k < p.K) ? b_off[i] + k * (INT8B ? 1 : 2) : kOffNone;
+      const int off = (live & (k < p.K)) ? b_off[i] + k * (INT8B ? 1 : 2) : kOffNone;
       buffer_lds_dma16(b_rsrc, off, __builtin_amdgcn_readfirstlane(st_base + A_BYTES + i * 4096 + w * 1024));
     }
   };

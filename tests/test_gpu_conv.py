@@ -142,6 +142,35 @@ def test_bf16_nhwc_large_tile(dev, orc):
         check_bf16(got[i:i + 1], ref, f"image {i}")
 
 
+STREAM_CASES = [
+    # B, H, W, Cin, Cout, act: 1x1 stride-1 convs with M = B*H*W >= 16384 and
+    # C_IN, C_OUT in {64, 128, 256} take the streaming kernel
+    (8, 48, 48, 64, 256, "relu"),    # M = 18432 (whole 32-row blocks)
+    (7, 50, 50, 256, 64, None),      # M = 17500: last block has 28 rows
+    (9, 45, 45, 64, 128, "silu"),    # M = 18225: ragged, SiLU epilogue
+    (5, 61, 61, 128, 128, "gelu"),   # M = 18605: ragged, GELU epilogue
+    (4, 64, 64, 256, 128, "relu"),   # M = 16384: the smallest streamed M
+]
+
+
+@pytest.mark.parametrize("case", STREAM_CASES)
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_bf16_nhwc_stream_1x1(dev, orc, case, with_bias):
+    B, H, W, Cin, Cout, act = case
+    print(f"[conv bf16 stream 1x1] {case} bias={with_bias}", flush=True)
+    rng = np.random.default_rng(Cin + 3 * Cout + H)
+    x = rb(rng.standard_normal((B, H, W, Cin), dtype=np.float32))
+    w = rb((rng.standard_normal((Cout, 1, 1, Cin), dtype=np.float32) * np.sqrt(2.0 / Cin)).astype(np.float32))
+    b = rb(rng.normal(0, 0.1, Cout).astype(np.float32)) if with_bias else None
+    assert K.conv2d_workspace_size((B, H, W, Cin), (Cout, 1, 1, Cin), 1, 0, 1, tg.bf16, "nhwc") == 0
+    got = K.conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                   dev.upload(to_bf16(b), tg.bf16) if with_bias else None, 1, 0, 1, act, layout="nhwc").to_host()
+    ref = orc.conv2d_nhwc(x, w, b, stride=1, padding=0)
+    if act is not None:
+        ref = {"relu": orc.relu, "silu": orc.silu, "gelu": orc.gelu}[act](ref)
+    check_bf16(got, ref, str(case))
+
+
 def test_bf16_nchw_and_grouped_direct(dev, orc):
     rng = np.random.default_rng(5)
     x = rb(rng.standard_normal((2, 8, 10, 10), dtype=np.float32))

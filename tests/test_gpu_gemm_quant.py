@@ -55,6 +55,21 @@ def test_linear_bf16(dev, orc, m, n, k, scratch):
     check_bf16(got, orc.linear(x, w, b), "linear bf16")
 
 
+@pytest.mark.parametrize("m,n,k", [(16421, 64, 128), (16384, 128, 256), (20000, 256, 64)])
+def test_linear_bf16_stream(dev, orc, m, n, k):
+    # M >= 16384 with K, N in {64, 128, 256}: the streaming kernel (B staged
+    # once per workgroup, 32-row blocks per wave; 16421 and 20000 end in a
+    # partial block)
+    rng = np.random.default_rng(m + n + k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb((rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float32))
+    b = rb(rng.normal(0, 0.5, n).astype(np.float32))
+    assert K.linear_workspace_size(m, n, k, tg.bf16) == 0
+    got = K.linear(dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16),
+                   dev.upload(to_bf16(b), tg.bf16)).to_host()
+    check_bf16(got, orc.linear(x, w, b), "linear bf16 stream")
+
+
 def test_linear_bf16_large_tile(dev, orc):
     # 4096 x 512 x 4096: 256 x 256 tiles fill the chip -> large-tile kernel;
     # rows 0..31 and the last 32 rows against the oracle
