@@ -202,6 +202,64 @@ def bench_norm_act(args, tg, dev, stream):
 # ── attention ───────────────────────────────────────────────────────────────
 
 
+def bench_act_backward(args, tg, dev, stream):
+    """Activation gradients on the norm workload's shape: dy and the saved tensor in, dx out
+    (relu takes the forward output, gelu/silu the forward input); 3 x 128 MiB per op."""
+    from teenygrad_amd import kernels as K
+    from teenygrad_amd import synthetic
+    from teenygrad_amd.dtypes import round_bf16, to_bf16
+    x, _, _, _ = norm_inputs()
+    dy = round_bf16(synthetic.normal(synthetic.workload_seed(1, 4), (NORM_M, NORM_N)))
+    y = np.maximum(x, 0)
+    up = lambda a: dev.upload(to_bf16(a), tg.bf16)
+    xb, yb, dyb = up(x), up(y), up(dy)
+    shape = (NORM_M, NORM_N)
+    dr, dg, ds = (tg.Buffer(tg.bf16, shape) for _ in range(3))
+    io = 3 * NORM_M * NORM_N * 2  # read dy + saved, write dx, bf16
+    bytes_of = {"relu_backward": io, "gelu_backward": io, "silu_backward": io}
+
+    def step(t):
+        launch(t, "relu_backward", lambda: K.relu_backward(dyb, yb, dx=dr, stream=stream))
+        launch(t, "gelu_backward", lambda: K.gelu_backward(dyb, xb, dx=dg, stream=stream))
+        launch(t, "silu_backward", lambda: K.silu_backward(dyb, xb, dx=ds, stream=stream))
+
+    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 3)
+    step_bytes = sum(bytes_of.values())
+    dom = max(per, key=per.get)
+    achieved = bytes_of[dom] / (per[dom] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic("act_backward"), "algorithmic_bytes": bytes_of[dom],
+            "avg_us": round(per[dom] * 1e3, 2)}
+    ops = {k: {"us": round(v * 1e3, 2), "GB/s": round(bytes_of[k] / (v * 1e-3) / 1e9, 1),
+               "frac": round(bytes_of[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)} for k, v in per.items()}
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        th = cpu_threads()
+        oracle.set_threads(th)
+        times = []
+        for _ in range(3):
+            c0 = time.perf_counter()
+            oracle.relu_backward(dy, y)
+            oracle.gelu_backward(dy, x)
+            oracle.silu_backward(dy, x)
+            times.append(time.perf_counter() - c0)
+        cs = float(np.median(times))
+        cpu = {"value": round(step_bytes / cs / 1e9, 2), "unit": "GB/s", "cores": th, "kind": "port",
+               "seconds_per_step": round(cs, 3),
+               "sample": "the full step (3 gradients on [16384, 4096]) in fp32 on the bf16-rounded "
+                         "inputs, median of 3 runs; bytes counted as bf16 like the GPU line"}
+    return {
+        "metric": METRIC, "value": round(step_bytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+        "ms_per_step": round(ms, 4), "dtype": "bf16", "scaling": "weak",
+        "config": {"workload": "activation gradients: dy, x|y [16384,4096] bf16 -> dx for "
+                               "ReLU, GELU-tanh, SiLU (fp32 math)",
+                   "M": NORM_M, "N": NORM_N, "ops_per_step": 3, "bytes_per_step": step_bytes},
+        "roofline": roof, "cpu_baseline": cpu, "ops": ops, "wall_s": round(wall, 3),
+    }
+
+
 def bench_attention(args, tg, dev, stream, s, causal, idx):
     from teenygrad_amd import kernels as K
     from teenygrad_amd.dtypes import to_bf16
@@ -437,6 +495,7 @@ def bench_conv_f32(args, tg, dev, stream):
 
 WORKLOADS = {
     "norm_act": bench_norm_act,
+    "act_backward": bench_act_backward,
     "attention_causal_s2048": lambda a, tg, d, s: bench_attention(a, tg, d, s, 2048, True, 2),
     "attention_s4096": lambda a, tg, d, s: bench_attention(a, tg, d, s, 4096, False, 2),
     "resnet50_convs": bench_resnet,

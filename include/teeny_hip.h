@@ -196,6 +196,24 @@ teeny_status teeny_gelu_forward(const void *x, void *y, int64_t n_elements, teen
 teeny_status teeny_silu_forward(const void *x, void *y, int64_t n_elements, teeny_dtype dtype,
                                 teeny_stream stream);
 
+/* ── activation gradients ─────────────────────────────────────────────────
+ * dx[i] = dy[i] * f'(.) for i < n_elements; dx may alias dy or the saved tensor.
+ *   relu:  dx = y > 0 ? dy : 0, y = the forward OUTPUT   nn/activation/relu.rs:67-117
+ *   gelu:  inner = x + 0.044715 x^3, t = 2/(1 + exp(-2c inner)) - 1,
+ *          dx = dy (0.5 (1 + t) + x 0.5 (1 - t^2) c (1 + 3*0.044715 x^2))
+ *                                                        nn/activation/gelu.rs:81-139
+ *   silu:  s = 1/(1 + exp(-x)), y = x s, dx = dy (s + y - y s)
+ *                                                        nn/activation/sigmoid.rs:161-210
+ * Reference arguments: (dy_ptr, y_ptr | x_ptr, dx_ptr, n_elements), as the RuntimeOps'
+ * pack_backward_args visit them (relu.rs:156-172, gelu.rs:293-309, sigmoid.rs:424-440).
+ * dtype: F32 or BF16. */
+teeny_status teeny_relu_backward(const void *dy, const void *y, void *dx, int64_t n_elements,
+                                 teeny_dtype dtype, teeny_stream stream);
+teeny_status teeny_gelu_backward(const void *dy, const void *x, void *dx, int64_t n_elements,
+                                 teeny_dtype dtype, teeny_stream stream);
+teeny_status teeny_silu_backward(const void *dy, const void *x, void *dx, int64_t n_elements,
+                                 teeny_dtype dtype, teeny_stream stream);
+
 /* ── normalisation ────────────────────────────────────────────────────────
  * LayerNorm over the last dimension of a row-major [M, N] tensor:
  *   y = (x - mean) * rsqrt(var + eps) * weight + bias   (biased variance)

@@ -40,6 +40,9 @@ def _load() -> ctypes.CDLL:
         "oracle_relu_forward": [P, P, I, I, I, I],
         "oracle_gelu_forward": [P, P, I, I, I, I],
         "oracle_silu_forward": [P, P, I, I, I, I],
+        "oracle_relu_backward": [P, P, P, I, I, I, I],
+        "oracle_gelu_backward": [P, P, P, I, I, I, I],
+        "oracle_silu_backward": [P, P, P, I, I, I, I],
         "oracle_layer_norm_forward_inference": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_rms_norm_forward": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_conv2d_forward": [P, P, P, P] + [I] * 15 + [I, I],
@@ -107,6 +110,30 @@ def gelu(x, block_size=1024, pid_begin=0, pid_end=-1):
 
 def silu(x, block_size=1024, pid_begin=0, pid_end=-1):
     return _act(lib.oracle_silu_forward, x, block_size, pid_begin, pid_end)
+
+
+def _act_grad(fn, dy, v, block_size, pid_begin, pid_end):
+    dy, v = _f32(dy), _f32(v)
+    if dy.shape != v.shape:
+        raise ValueError(f"{fn.__name__}: dy {dy.shape} and saved tensor {v.shape} differ")
+    dx = np.zeros_like(dy)
+    _chk(fn(_p(dy), _p(v), _p(dx), dy.size, block_size, pid_begin, pid_end), fn.__name__)
+    return dx
+
+
+def relu_backward(dy, y, block_size=1024, pid_begin=0, pid_end=-1):
+    """relu.rs:67-117: dx = dy where the forward OUTPUT y > 0, else 0."""
+    return _act_grad(lib.oracle_relu_backward, dy, y, block_size, pid_begin, pid_end)
+
+
+def gelu_backward(dy, x, block_size=1024, pid_begin=0, pid_end=-1):
+    """gelu.rs:81-139: tanh-GELU derivative at the forward input x, times dy."""
+    return _act_grad(lib.oracle_gelu_backward, dy, x, block_size, pid_begin, pid_end)
+
+
+def silu_backward(dy, x, block_size=1024, pid_begin=0, pid_end=-1):
+    """sigmoid.rs:161-210: dy * (s + y - y s), s = sigmoid(x), y = x s."""
+    return _act_grad(lib.oracle_silu_backward, dy, x, block_size, pid_begin, pid_end)
 
 
 # ── norms (layernorm.rs:42-157, rmsnorm.rs:39-119) ──────────────────────────

@@ -157,6 +157,82 @@ int oracle_silu_forward(const float *x, float *y, int64_t n, int64_t block_size,
   return act_run(x, y, n, block_size, 2, pb, pe);
 }
 
+/* ── activation gradients ────────────────────────────────────────────────
+ * relu.rs:67-117, gelu.rs:81-139, sigmoid.rs:161-210: program pid covers the
+ * same masked BLOCK_SIZE tile as the forward kernels; v is the forward output
+ * y for relu and the forward input x for gelu and silu. */
+
+typedef struct {
+  const float *dy;
+  const float *v;
+  float *dx;
+  int64_t n;
+  int64_t block;
+  int kind;
+} act_grad_ctx;
+
+static float relu_grad_ref(float dy, float y) {
+  /* relu.rs:105-107: where(y > 0, grad_y, 0); a NaN y selects 0 */
+  return y > 0.0f ? dy : 0.0f;
+}
+
+static float gelu_grad_ref(float dy, float x) {
+  /* gelu.rs:117-130, in the reference's operation order:
+   * inner = x + coeff*x*x*x ; s = one / (one + exp(neg2c * inner)) ;
+   * t = two*s - one ; sech2 = one - t*t ; dinner = c * (one + three*coeff*x*x) ;
+   * dx = dy * (half*(one + t) + x*half*sech2*dinner) */
+  const float one = 1.0f, half = 0.5f, two = 2.0f, three = 3.0f;
+  const float c = (float)0.7978845608028654;
+  const float neg2c = (float)(-2.0 * 0.7978845608028654);
+  const float coeff = 0.044715f;
+  float inner = x + coeff * x * x * x;
+  float s = one / (one + expf(neg2c * inner));
+  float t = two * s - one;
+  float sech2 = one - t * t;
+  float dinner = c * (one + three * coeff * x * x);
+  return dy * (half * (one + t) + x * half * sech2 * dinner);
+}
+
+static float silu_grad_ref(float dy, float x) {
+  /* sigmoid.rs:196-201: s = one / (one + exp(neg1 * x)) ; y = x * s ;
+   * dx = dy * (s + y - y * s) */
+  const float one = 1.0f, neg1 = -1.0f;
+  float s = one / (one + expf(neg1 * x));
+  float y = x * s;
+  return dy * (s + y - y * s);
+}
+
+static void act_grad_program(const void *c, int64_t pid) {
+  const act_grad_ctx *a = (const act_grad_ctx *)c;
+  int64_t start = pid * a->block;
+  for (int64_t i = start; i < start + a->block && i < a->n; ++i) {
+    float d = a->dy[i], v = a->v[i];
+    a->dx[i] = a->kind == 0 ? relu_grad_ref(d, v) : a->kind == 1 ? gelu_grad_ref(d, v)
+                                                                : silu_grad_ref(d, v);
+  }
+}
+
+static int act_grad_run(const float *dy, const float *v, float *dx, int64_t n, int64_t block,
+                        int kind, int64_t pb, int64_t pe) {
+  if (n < 0 || block <= 0) return ERR_SHAPE_MISMATCH;
+  act_grad_ctx a = {dy, v, dx, n, block, kind};
+  launch(act_grad_program, &a, (n + block - 1) / block, pb, pe);
+  return OK;
+}
+
+int oracle_relu_backward(const float *dy, const float *y, float *dx, int64_t n,
+                         int64_t block_size, int64_t pb, int64_t pe) {
+  return act_grad_run(dy, y, dx, n, block_size, 0, pb, pe);
+}
+int oracle_gelu_backward(const float *dy, const float *x, float *dx, int64_t n,
+                         int64_t block_size, int64_t pb, int64_t pe) {
+  return act_grad_run(dy, x, dx, n, block_size, 1, pb, pe);
+}
+int oracle_silu_backward(const float *dy, const float *x, float *dx, int64_t n,
+                         int64_t block_size, int64_t pb, int64_t pe) {
+  return act_grad_run(dy, x, dx, n, block_size, 2, pb, pe);
+}
+
 /* ── LayerNorm / RMSNorm ─────────────────────────────────────────────────
  * layernorm.rs:42-157 and rmsnorm.rs:39-119: program = row; the row is
  * visited in BLOCK_N tiles; each tile is reduced (T::sum) and the tile sums

@@ -112,6 +112,9 @@ _SIGS = {
     "teeny_relu_forward": (S, [P, P, c_int64, c_int32, P]),
     "teeny_gelu_forward": (S, [P, P, c_int64, c_int32, P]),
     "teeny_silu_forward": (S, [P, P, c_int64, c_int32, P]),
+    "teeny_relu_backward": (S, [P, P, P, c_int64, c_int32, P]),
+    "teeny_gelu_backward": (S, [P, P, P, c_int64, c_int32, P]),
+    "teeny_silu_backward": (S, [P, P, P, c_int64, c_int32, P]),
     "teeny_layer_norm_forward_inference": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, P]),
     "teeny_rms_norm_forward": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, P]),
     "teeny_norm_act_forward": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, c_int32, c_int32, P]),

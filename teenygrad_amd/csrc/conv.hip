@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x
           const bool live = c0 + kk < ce;
           const float a = live ? wl[li] : 0.0f;
           const float bx =
-              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, live & xv ? xo : kOffNone, 0, 0));
+              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, (live & xv) ? xo : kOffNone, 0, 0));
           acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bx, acc, 0, 0, 0);
           xo += 64 * HW;
           li += 16 * KHW;

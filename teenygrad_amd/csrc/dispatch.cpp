@@ -80,6 +80,23 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
                     : teeny_silu_forward(x, y, n, dtype, stream);
   }
 
+  // relu/gelu/silu_backward<BLOCK_SIZE>(dy, y | x, dx, n_elements)
+  //   relu.rs:156-172, gelu.rs:293-309, sigmoid.rs:424-440
+  const char *grads[3] = {"relu_backward", "gelu_backward", "silu_backward"};
+  for (int a = 0; a < 3; ++a) {
+    if (!name_is(entry_point, grads[a])) continue;
+    TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT,
+                  std::string(grads[a]) + ": expects const generic BLOCK_SIZE");
+    void *dy = r.ptr("dy_ptr");
+    void *saved = r.ptr(a == 0 ? "y_ptr" : "x_ptr");
+    void *dx = r.ptr("dx_ptr");
+    int64_t n = r.i32("n_elements");
+    if (r.done() != TEENY_OK) return r.st;
+    return a == 0 ? teeny_relu_backward(dy, saved, dx, n, dtype, stream)
+           : a == 1 ? teeny_gelu_backward(dy, saved, dx, n, dtype, stream)
+                    : teeny_silu_backward(dy, saved, dx, n, dtype, stream);
+  }
+
   // layer_norm_forward_inference<BLOCK_N>(x, y, weight, bias, M, N, eps)   layernorm.rs:539-548
   if (name_is(entry_point, "layer_norm_forward_inference")) {
     TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT, "layer_norm: expects const generic BLOCK_N");

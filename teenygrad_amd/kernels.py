@@ -181,17 +181,43 @@ class _Elementwise(RuntimeOp):
         n = _prod(output_shape)
         return (-(-n // self.block_size), 1, 1)
 
+    # training hooks (core/teeny-core/src/model/mod.rs:213-280)
+    def has_backward(self) -> bool:
+        return True
+
+    def backward_entry_point_name(self) -> str:
+        return f"{self.backward_name}_entry_point"
+
+    def pack_backward_args(self, inputs, params, output, output_shape, grad_output,
+                           grad_output_row_stride, grad_inputs, grad_params, visitor):
+        """(dy_ptr, saved, dx_ptr, n_elements): saved is the forward output for relu
+        (relu.rs:156-172) and the forward input for gelu/silu (gelu.rs:293-309,
+        sigmoid.rs:424-440)."""
+        visitor.visit_ptr(grad_output)
+        visitor.visit_ptr(output if self.saves_output else inputs[0][0])
+        visitor.visit_ptr(grad_inputs[0])
+        visitor.visit_i32(_prod(output_shape))
+
+    def backward_grid(self, input_shapes, output_shape):
+        return self.grid(output_shape)
+
 
 class ReluForward(_Elementwise):
     name = "relu_forward"
+    backward_name = "relu_backward"
+    saves_output = True
 
 
 class GeluForward(_Elementwise):
     name = "gelu_forward"
+    backward_name = "gelu_backward"
+    saves_output = False
 
 
 class SiluForward(_Elementwise):
     name = "silu_forward"
+    backward_name = "silu_backward"
+    saves_output = False
 
 
 class LayerNormForwardInferenceRuntimeOp(RuntimeOp):
@@ -494,6 +520,33 @@ def silu(x: Buffer, y: Optional[Buffer] = None, stream: Optional[Stream] = None)
     y = _out(x, y)
     check(lib.teeny_silu_forward(x.ptr, y.ptr, x.numel, x.dtype.code, _h(stream)))
     return y
+
+
+def _act_grad(fn, what: str, dy: Buffer, saved: Buffer, dx: Optional[Buffer],
+              stream: Optional[Stream]) -> Buffer:
+    _need(dy.dtype == saved.dtype and dy.numel == saved.numel,
+          f"{what}: dy and the saved tensor must match in dtype and size")
+    dx = _out(dy, dx)
+    check(fn(dy.ptr, saved.ptr, dx.ptr, dy.numel, dy.dtype.code, _h(stream)))
+    return dx
+
+
+def relu_backward(dy: Buffer, y: Buffer, dx: Optional[Buffer] = None,
+                  stream: Optional[Stream] = None) -> Buffer:
+    """relu.rs:67-117: dx = dy where the forward OUTPUT y > 0, else 0."""
+    return _act_grad(lib.teeny_relu_backward, "relu_backward", dy, y, dx, stream)
+
+
+def gelu_backward(dy: Buffer, x: Buffer, dx: Optional[Buffer] = None,
+                  stream: Optional[Stream] = None) -> Buffer:
+    """gelu.rs:81-139: dy times the tanh-GELU derivative at the forward input x."""
+    return _act_grad(lib.teeny_gelu_backward, "gelu_backward", dy, x, dx, stream)
+
+
+def silu_backward(dy: Buffer, x: Buffer, dx: Optional[Buffer] = None,
+                  stream: Optional[Stream] = None) -> Buffer:
+    """sigmoid.rs:161-210: dy * (s + y - y s), s = sigmoid(x), y = x s."""
+    return _act_grad(lib.teeny_silu_backward, "silu_backward", dy, x, dx, stream)
 
 
 def layer_norm(x: Buffer, weight: Buffer, bias: Buffer, eps: float = 1e-5,

@@ -56,6 +56,17 @@ def test_activation_errors(fn):
     assert f(None, None, 0, _lib.F32, None) == _lib.OK  # empty tensor is a no-op
 
 
+@pytest.mark.parametrize("fn", ["teeny_relu_backward", "teeny_gelu_backward", "teeny_silu_backward"])
+def test_activation_backward_errors(fn):
+    f = getattr(lib, fn)
+    expect(f(None, FAKE, FAKE, 10, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(f(FAKE, None, FAKE, 10, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(f(FAKE, FAKE, None, 10, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    expect(f(FAKE, FAKE, FAKE, -1, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(f(FAKE, FAKE, FAKE, 10, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    assert f(None, None, None, 0, _lib.F32, None) == _lib.OK  # empty tensor is a no-op
+
+
 def test_norm_errors():
     ln = lib.teeny_layer_norm_forward_inference
     expect(ln(FAKE, FAKE, FAKE, None, 4, 8, 1e-5, _lib.F32, None), _lib.ERR_NULL_POINTER)
@@ -180,6 +191,24 @@ def test_dispatch_errors():
     # a rejected op through dispatch keeps the op's own status
     neg = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, -3))
     expect(d(b"relu_forward_entry_point", cg, 1, neg, 3, grid, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+
+
+@pytest.mark.parametrize("op", [b"relu_backward", b"gelu_backward", b"silu_backward"])
+def test_dispatch_backward_argument_list(op):
+    # (dy_ptr, y_ptr | x_ptr, dx_ptr, n_elements), BLOCK_SIZE: relu.rs:156-172 etc.
+    d = lib.teeny_dispatch
+    ep = op + b"_entry_point"
+    cg = (ctypes.c_int64 * 1)(1024)
+    grid = (ctypes.c_uint32 * 3)(1, 1, 1)
+    fwd_shaped = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, 8))
+    expect(d(ep, cg, 1, fwd_shaped, 3, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    null_dx = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, None), (_lib.ARG_I32, 8))
+    expect(d(ep, cg, 1, null_dx, 4, grid, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    neg = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_I32, -1))
+    expect(d(ep, cg, 1, neg, 4, grid, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(d(ep, cg, 0, neg, 4, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)  # no BLOCK_SIZE
+    empty = packed((_lib.ARG_PTR, None), (_lib.ARG_PTR, None), (_lib.ARG_PTR, None), (_lib.ARG_I32, 0))
+    assert d(ep, cg, 1, empty, 4, grid, _lib.BF16, None) == _lib.OK
 
 
 def test_no_device_paths():

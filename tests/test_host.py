@@ -71,6 +71,20 @@ def test_elementwise_runtime_ops(cls, name):
     assert op.grid([3, 1000]) == (3, 1, 1)
 
 
+@pytest.mark.parametrize("cls,bname,saved", [(kernels.ReluForward, "relu_backward", "output"),
+                                              (kernels.GeluForward, "gelu_backward", "input"),
+                                              (kernels.SiluForward, "silu_backward", "input")])
+def test_elementwise_backward_hooks(cls, bname, saved):
+    # relu.rs:148-180, gelu.rs:287-317, sigmoid.rs:418-448: (dy, y | x, dx, n)
+    op = cls(1024)
+    assert op.has_backward() and op.backward_entry_point_name() == f"{bname}_entry_point"
+    v = RecordingVisitor()
+    op.pack_backward_args([(5, [3, 1000])], [], 6, [3, 1000], 7, 1000, [8], [], v)
+    want_saved = 6 if saved == "output" else 5
+    assert v.args == [("ptr", 7), ("ptr", want_saved), ("ptr", 8), ("i32", 3000)]
+    assert op.backward_grid([[3, 1000]], [3, 1000]) == (3, 1, 1)
+
+
 def test_flash_attention_launch_contract():
     # tests/test_flash_attn2.rs:135-162: grid (N_CTX, BH, 1), args (q,k,v,o,l,nq,nk,scale,-inf)
     op = kernels.FlashAttention2Forward(64, 0.125)

@@ -21,6 +21,20 @@ def test_activations_match_fixture(orc, op, tol):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol)
 
 
+@pytest.mark.parametrize("op,tol", [("relu", 0.0), ("gelu", 2e-5), ("silu", 1e-5)])
+def test_activation_backward_matches_fixture(orc, op, tol):
+    # relu: test_relu.rs:148 (exact, on the forward OUTPUT y_backward.bin);
+    # gelu: test_gelu.rs:157 (2e-5); silu: test_sigmoid.rs:274 (1e-5)
+    if op == "relu":
+        dy, saved = load_golden("relu/dy_backward.bin"), load_golden("relu/y_backward.bin")
+    else:
+        dy, saved = load_golden(f"{op}/dy.bin"), load_golden(f"{op}/x.bin")
+    want = load_golden(f"{op}/expected_backward.bin")
+    got = getattr(orc, f"{op}_backward")(dy, saved)
+    assert dy.size == 1024
+    np.testing.assert_allclose(got, want, rtol=0, atol=tol)
+
+
 def test_layernorm_matches_fixture(orc):
     # test_layernorm.rs:159 — 16 x 128, eps 1e-5, |d| < 1e-4
     x = load_golden("layernorm/x.bin").reshape(16, 128)

@@ -46,6 +46,33 @@ def test_activation_closed_forms(orc):
         assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-30), fn.__name__
 
 
+def test_activation_gradients_vs_finite_differences(orc):
+    # d/dx of the float64 closed forms by central differences (truncation error ~h^2 = 1e-12):
+    # a dropped term, a wrong sign or a wrong constant in the restated derivative fails this
+    x = np.concatenate([RNG.normal(0, 2.5, 4000), [0.0, -0.0, 6.0, -6.0, 30.0, -30.0]])
+    x32 = x.astype(np.float32)
+    dy = RNG.normal(0, 1, x.size).astype(np.float32)
+    h = 1e-6
+    xd = x32.astype(np.float64)
+    for fn, ref in ((orc.gelu_backward, gelu_tanh64), (orc.silu_backward, silu64)):
+        want = dy.astype(np.float64) * (ref(xd + h) - ref(xd - h)) / (2 * h)
+        got = fn(dy, x32, block_size=1024).astype(np.float64)
+        assert np.all(np.abs(got - want) <= 2e-6 * np.abs(dy) + 1e-5 * np.abs(want)), fn.__name__
+
+
+def test_activation_gradients_linear_in_dy_and_relu_mask(orc):
+    x = RNG.normal(0, 2, 3000).astype(np.float32)
+    dy = RNG.normal(0, 1, 3000).astype(np.float32)
+    for fn in (orc.gelu_backward, orc.silu_backward):
+        # scaling dy by 2 scales dx by 2 exactly (one rounding of the same product)
+        np.testing.assert_array_equal(fn(2 * dy, x), 2 * fn(dy, x))
+    y = np.maximum(x, 0)
+    y[:3] = [0.0, np.nan, -0.0]
+    got = orc.relu_backward(dy, y)
+    np.testing.assert_array_equal(got[3:], np.where(y[3:] > 0, dy[3:], 0))
+    assert np.all(got[:3] == 0)  # y == 0, NaN and -0 select 0
+
+
 def test_gelu_tanh_identity():
     # the tanh statement of the same function, where 1 + tanh does not cancel
     x = np.linspace(-4, 4, 1001)
