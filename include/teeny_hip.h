@@ -290,6 +290,21 @@ teeny_status teeny_flash_attention2_forward(const void *q, const void *k, const 
                                             int32_t causal, teeny_dtype dtype,
                                             teeny_stream stream);
 
+/* Multi-head attention with grouped K/V heads: the lowering target of the
+ * reference's Op::MultiHeadAttention{q_num_heads, kv_num_heads}
+ * (core/teeny-core/src/graph/mod.rs:1240-1246), a TODO arm of its lowering
+ * (kernels/teeny-kernels/src/graph/mod.rs:2477-2481).  q/o are
+ * [batch * q_heads, n_ctx_q, head_dim], k/v [batch * kv_heads, n_ctx_k,
+ * head_dim]; query head h of a batch attends with K/V head
+ * h / (q_heads / kv_heads) (q_heads a multiple of kv_heads; equal counts are
+ * ordinary multi-head attention).  Otherwise as
+ * teeny_flash_attention2_forward, which is this function with batch = BH and
+ * q_heads = kv_heads = 1. */
+teeny_status teeny_attention_forward(const void *q, const void *k, const void *v, void *o, float *l,
+                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t n_ctx_q,
+                                     int64_t n_ctx_k, int64_t head_dim, float softmax_scale,
+                                     int32_t causal, teeny_dtype dtype, teeny_stream stream);
+
 /* ── int8 affine quantization (teeny-quant) ───────────────────────────────
  * Reference: quantize_affine(tensor, data, shape, granularity, symmetric,
  * bits) and dequantize_affine, utilities/teeny-quant/src/quant/affine.rs
@@ -382,7 +397,13 @@ teeny_status teeny_conv2d_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT,
  * contract (LoadedModel::forward, drivers/teeny-cuda/src/model/mod.rs:524-700)
  * call this library in place of cuLaunchKernel.  Entry point names are the
  * reference's "{name}_entry_point" symbols, e.g.
- * "conv2d_bias_forward_entry_point". */
+ * "conv2d_bias_forward_entry_point".  Names served (argument lists as the
+ * matching RuntimeOp packs them): relu/gelu/silu_forward and _backward,
+ * layer_norm_forward_inference, rms_norm_forward, conv2d_forward,
+ * conv2d_bias_forward, flash_attention2_forward (HEAD_DIM[, CAUSAL]),
+ * linear_forward, and for the reference's TODO lowering arms
+ * multi_head_attention_forward, w8a16_linear_forward, w8a16_conv2d_forward,
+ * quantize_affine and dequantize_affine (dims as TEENY_ARG_I64). */
 typedef enum teeny_arg_kind {
   TEENY_ARG_PTR = 0,
   TEENY_ARG_I32 = 1,

@@ -46,6 +46,7 @@ def _load() -> ctypes.CDLL:
         "oracle_layer_norm_forward_inference": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_rms_norm_forward": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_conv2d_forward": [P, P, P, P] + [I] * 15 + [I, I],
+        "oracle_conv2d_programs": [P, P, P, P] + [I] * 15 + [P, I],
         "oracle_flash_attention2_forward": [P, P, P, P, P, I, I, I, I, c_float, c_int, I, I],
         "oracle_flash_attention2_rows": [P, P, P, P, P, I, I, I, I, c_float, c_int, P, I],
         "oracle_linear_forward": [P, P, P, P] + [I] * 9 + [I, I],
@@ -186,6 +187,37 @@ def conv2d_nhwc(x, w, bias=None, stride=(1, 1), padding=(0, 0), groups=1):
     y = conv2d_nchw(np.transpose(x, (0, 3, 1, 2)), np.transpose(w, (0, 3, 1, 2)), bias, stride,
                     padding, groups)
     return np.ascontiguousarray(np.transpose(y, (0, 2, 3, 1)))
+
+
+def conv2d_nhwc_pixels(x, w, pixels, bias=None, stride=(1, 1), padding=(0, 0), groups=1):
+    """Output pixels ``pixels`` (flat indices m = (b*OH + oh)*OW + ow of the
+    NHWC output) of conv2d_nhwc, all channels: -> [len(pixels), Cout].  Runs
+    only the reference programs (b, c_out, oh, ow) those pixels need, with
+    BLOCK_OW = 1 (a tiling constant of the reference that does not change the
+    per-pixel arithmetic)."""
+    x, w = _f32(x), _f32(w)
+    bias = None if bias is None else _f32(bias)
+    xn = np.ascontiguousarray(np.transpose(x, (0, 3, 1, 2)))
+    wn = np.ascontiguousarray(np.transpose(w, (0, 3, 1, 2)))
+    sh, sw = (stride, stride) if isinstance(stride, int) else stride
+    ph, pw = (padding, padding) if isinstance(padding, int) else padding
+    B, Cin, H, W = xn.shape
+    Cout, _, KH, KW = wn.shape
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    pixels = np.asarray(pixels, dtype=np.int64).reshape(-1)
+    if pixels.size and (pixels.min() < 0 or pixels.max() >= B * OH * OW):
+        raise ValueError("conv2d_nhwc_pixels: pixel index out of range")
+    b, rest = np.divmod(pixels, OH * OW)
+    oh, ow = np.divmod(rest, OW)
+    co = np.arange(Cout, dtype=np.int64)
+    # program id ((b * Cout + co) * OH + oh) * OW + ow with BLOCK_OW = 1
+    pids = np.ascontiguousarray((((b[:, None] * Cout + co[None, :]) * OH + oh[:, None]) * OW
+                                 + ow[:, None]).reshape(-1))
+    y = np.zeros((B, Cout, OH, OW), dtype=np.float32)
+    _chk(lib.oracle_conv2d_programs(_p(xn), _p(wn), _p(bias), _p(y), B, Cin, Cout, H, W, OH, OW,
+                                    KH, KW, sh, sw, ph, pw, groups, 1, _p(pids), pids.size),
+         "conv2d_programs")
+    return np.ascontiguousarray(y[b[:, None], co[None, :], oh[:, None], ow[:, None]])
 
 
 # ── attention (flash_attn2.rs:52-158) ───────────────────────────────────────

@@ -394,6 +394,37 @@ int oracle_conv2d_forward(const float *x, const float *w, const float *bias, flo
   return OK;
 }
 
+/* The same programs as oracle_conv2d_forward, but only the program ids listed
+ * in `pids` (each in [0, B*Cout*OH*ceil(OW/block_ow))): a sampled check of a
+ * large conv touches every output tile without running the whole grid. */
+typedef struct {
+  conv_ctx conv;
+  const int64_t *pids;
+} conv_list_ctx;
+
+static void conv_list_program(const void *c, int64_t i) {
+  const conv_list_ctx *a = (const conv_list_ctx *)c;
+  conv_program(&a->conv, a->pids[i]);
+}
+
+int oracle_conv2d_programs(const float *x, const float *w, const float *bias, float *y, int64_t B,
+                           int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                           int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                           int64_t G, int64_t block_ow, const int64_t *pids, int64_t n_pids) {
+  if (G <= 0 || Cin % G != 0 || Cout % G != 0) return ERR_SHAPE_MISMATCH;
+  if (block_ow <= 0 || block_ow > 512 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0)
+    return ERR_INVALID_ARGUMENT;
+  if (OH != (H + 2 * PH - KH) / SH + 1 || OW != (W + 2 * PW - KW) / SW + 1)
+    return ERR_SHAPE_MISMATCH;
+  const int64_t total = B * Cout * OH * ((OW + block_ow - 1) / block_ow);
+  for (int64_t i = 0; i < n_pids; ++i)
+    if (pids[i] < 0 || pids[i] >= total) return ERR_SHAPE_MISMATCH;
+  conv_list_ctx a = {{x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow},
+                     pids};
+  launch(conv_list_program, &a, n_pids, 0, -1);
+  return OK;
+}
+
 /* ── flash attention 2 forward ───────────────────────────────────────────
  * flash_attn2.rs:52-158: program (pid_m, pid_bh); q row in registers;
  * sequential loop over key rows with the online-softmax recurrence

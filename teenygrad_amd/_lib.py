@@ -12,6 +12,9 @@ import os
 from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint32, c_void_p
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libteeny_hip.so")
+# A stand-alone gfx950 code object (csrc/module_example.hip, built with
+# `hipcc --genco`) that the module-load / raw-launch surface can load.
+EXAMPLE_MODULE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "teeny_example.hsaco")
 
 # status codes (include/teeny_hip.h)
 OK = 0
@@ -121,6 +124,7 @@ _SIGS = {
     "teeny_conv2d_forward": (S, [P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_conv2d_bias_forward": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_flash_attention2_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
+    "teeny_attention_forward": (S, [P, P, P, P, P] + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),
     "teeny_quant_num_groups": (S, [POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, POINTER(c_int64)]),
     "teeny_quantize_affine": (S, [P, POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, c_int32, c_int32, P, P, P, P, P]),
     "teeny_dequantize_affine": (S, [P, P, P, POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, P, P]),

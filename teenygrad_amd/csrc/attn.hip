@@ -53,7 +53,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
                                                       const bf16 *__restrict__ K,
                                                       const bf16 *__restrict__ V,
                                                       bf16 *__restrict__ O, float *__restrict__ L,
-                                                      int nq, int nk, float scale_log2, int nqb) {
+                                                      int nq, int nk, float scale_log2, int nqb,
+                                                      int kv_group) {
   constexpr int NT = 64 * WAVES;   // threads per workgroup
   constexpr int BM = 32 * WAVES;   // queries per workgroup (32 per wave)
   constexpr int BN = 64;           // keys per tile
@@ -101,8 +102,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
     const int qi = q0 + c;
 
     const bf16 *Qb = Q + static_cast<int64_t>(bh) * nq * D;
-    const bf16 *Kb = K + static_cast<int64_t>(bh) * nk * D;
-    const bf16 *Vb = V + static_cast<int64_t>(bh) * nk * D;
+    // grouped-query attention: kv_group consecutive query heads share one K/V head
+    const bf16 *Kb = K + static_cast<int64_t>(bh / kv_group) * nk * D;
+    const bf16 *Vb = V + static_cast<int64_t>(bh / kv_group) * nk * D;
 
     // A negative softmax scale is applied by negating Q (exact in bf16), so the
     // score multiplier sc is positive and the running max is a max.  It is at
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
                                                  const float *__restrict__ K,
                                                  const float *__restrict__ V,
                                                  float *__restrict__ O, float *__restrict__ L,
-                                                 int nq, int nk, float scale, int causal) {
+                                                 int nq, int nk, float scale, int causal, int kv_group) {
   constexpr int DPL = (D + 63) / 64;  // output elements per lane
   __shared__ float qs[D];
   __shared__ float ps[64];
@@ -407,8 +409,8 @@ __global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
   const int64_t bh = blockIdx.y;
   const int lane = threadIdx.x;
   const float *qrow = Q + (bh * nq + qi) * D;
-  const float *Kb = K + bh * nk * D;
-  const float *Vb = V + bh * nk * D;
+  const float *Kb = K + (bh / kv_group) * nk * D;
+  const float *Vb = V + (bh / kv_group) * nk * D;
   for (int d = lane; d < D; d += 64) qs[d] = qrow[d];
   __syncthreads();
 
@@ -457,15 +459,15 @@ __global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
 
 template <int D>
 static void launch_f32(const void *q, const void *k, const void *v, void *o, float *l, int nq,
-                       int nk, float scale, int BH, int causal, hipStream_t s) {
+                       int nk, float scale, int BH, int causal, int kv_group, hipStream_t s) {
   hipLaunchKernelGGL((fa_fwd_f32<D>), dim3(nq, BH), dim3(64), 0, s, static_cast<const float *>(q),
                      static_cast<const float *>(k), static_cast<const float *>(v),
-                     static_cast<float *>(o), l, nq, nk, scale, causal);
+                     static_cast<float *>(o), l, nq, nk, scale, causal, kv_group);
 }
 
 template <int D>
 static void launch_bf16(const void *q, const void *k, const void *v, void *o, float *l, int nq,
-                        int nk, float scale, int BH, int causal, hipStream_t s) {
+                        int nk, float scale, int BH, int causal, int kv_group, hipStream_t s) {
   constexpr int WAVES = 4;
   const int nqb = (nq + 32 * WAVES - 1) / (32 * WAVES);
   const float scale_log2 = scale * kLog2e;
@@ -474,13 +476,63 @@ static void launch_bf16(const void *q, const void *k, const void *v, void *o, fl
     hipLaunchKernelGGL((fa_fwd_bf16<D, true, WAVES>), grid, dim3(64 * WAVES), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
                        static_cast<const bf16 *>(v), static_cast<bf16 *>(o), l, nq, nk, scale_log2,
-                       nqb);
+                       nqb, kv_group);
   } else {
     hipLaunchKernelGGL((fa_fwd_bf16<D, false, WAVES>), grid, dim3(64 * WAVES), 0, s,
                        static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
                        static_cast<const bf16 *>(v), static_cast<bf16 *>(o), l, nq, nk, scale_log2,
-                       nqb);
+                       nqb, kv_group);
   }
+}
+
+// Shared by both entry points: q [batch * q_heads, nq, D], k/v
+// [batch * kv_heads, nk, D]; query head h of a batch reads K/V head
+// h / (q_heads / kv_heads).
+static teeny_status attention_entry(const void *q, const void *k, const void *v, void *o, float *l,
+                                    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t n_ctx_q,
+                                    int64_t n_ctx_k, int64_t head_dim, float softmax_scale, int32_t causal,
+                                    teeny_dtype dtype, teeny_stream stream, const char *name) {
+  const std::string nm(name);
+  TEENY_REQUIRE(n_ctx_q >= 0 && n_ctx_k >= 0 && batch >= 0 && q_heads >= 0 && kv_heads >= 0,
+                TEENY_ERR_SHAPE_MISMATCH, nm + ": negative size");
+  TEENY_REQUIRE(kv_heads > 0 ? q_heads % kv_heads == 0 : q_heads == 0, TEENY_ERR_SHAPE_MISMATCH,
+                nm + ": q_heads must be a multiple of kv_heads");
+  const int64_t BH = batch * q_heads;
+  if (n_ctx_q == 0 || BH == 0) return TEENY_OK;
+  TEENY_REQUIRE(n_ctx_k > 0, TEENY_ERR_SHAPE_MISMATCH, nm + ": n_ctx_k must be positive (softmax over no keys)");
+  TEENY_REQUIRE(n_ctx_q <= 0x7fffffff && n_ctx_k <= 0x7fffffff && BH <= 65535 &&
+                    BH * ((n_ctx_q + 127) / 128) <= 0x7fffffff,
+                TEENY_ERR_SHAPE_MISMATCH, nm + ": size out of range");
+  TEENY_REQUIRE(q != nullptr && k != nullptr && v != nullptr && o != nullptr, TEENY_ERR_NULL_POINTER,
+                nm + ": q/k/v/o");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nq = static_cast<int>(n_ctx_q), nk = static_cast<int>(n_ctx_k);
+  const int bh = static_cast<int>(BH), group = static_cast<int>(q_heads / kv_heads);
+  if (dtype == TEENY_F32) {
+    switch (head_dim) {
+      case 16: launch_f32<16>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 32: launch_f32<32>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 64: launch_f32<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 128: launch_f32<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 256: launch_f32<256>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      default: return fail(TEENY_ERR_UNSUPPORTED, nm + ": f32 head_dim must be 16, 32, 64, 128 or 256");
+    }
+    return after_launch(name, s);
+  }
+  if (dtype == TEENY_BF16) {
+    TEENY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
+                  TEENY_ERR_MISALIGNED, nm + ": bf16 q/k/v/o must be 16-byte aligned");
+    // K and V of one (batch, head) are read through 32-bit buffer offsets
+    TEENY_REQUIRE(n_ctx_k * head_dim * 2 <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                  nm + ": bf16 K/V of one head must be below 2 GiB");
+    switch (head_dim) {
+      case 64: launch_bf16<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 128: launch_bf16<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      default: return fail(TEENY_ERR_UNSUPPORTED, nm + ": bf16 head_dim must be 64 or 128");
+    }
+    return after_launch(name, s);
+  }
+  return fail(TEENY_ERR_UNSUPPORTED_DTYPE, nm + ": dtype must be F32 or BF16");
 }
 
 }  // namespace teeny
@@ -493,49 +545,15 @@ extern "C" teeny_status teeny_flash_attention2_forward(const void *q, const void
                                                        int64_t BH, int64_t head_dim,
                                                        int32_t causal, teeny_dtype dtype,
                                                        teeny_stream stream) {
-  const char *name = "flash_attention2_forward";
-  TEENY_REQUIRE(n_ctx_q >= 0 && n_ctx_k >= 0 && BH >= 0, TEENY_ERR_SHAPE_MISMATCH,
-                "flash_attention2_forward: negative size");
-  if (n_ctx_q == 0 || BH == 0) return TEENY_OK;
-  TEENY_REQUIRE(n_ctx_k > 0, TEENY_ERR_SHAPE_MISMATCH,
-                "flash_attention2_forward: n_ctx_k must be positive (softmax over no keys)");
-  TEENY_REQUIRE(n_ctx_q <= 0x7fffffff && n_ctx_k <= 0x7fffffff && BH <= 65535 &&
-                    BH * ((n_ctx_q + 127) / 128) <= 0x7fffffff,
-                TEENY_ERR_SHAPE_MISMATCH, "flash_attention2_forward: size out of range");
-  TEENY_REQUIRE(q != nullptr && k != nullptr && v != nullptr && o != nullptr,
-                TEENY_ERR_NULL_POINTER, "flash_attention2_forward: q/k/v/o");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nq = static_cast<int>(n_ctx_q), nk = static_cast<int>(n_ctx_k);
-  const int bh = static_cast<int>(BH);
-  if (dtype == TEENY_F32) {
-    TEENY_REQUIRE(n_ctx_q <= 0x7fffffff && BH <= 65535, TEENY_ERR_SHAPE_MISMATCH,
-                  "flash_attention2_forward: grid out of range");
-    switch (head_dim) {
-      case 16: launch_f32<16>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      case 32: launch_f32<32>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      case 64: launch_f32<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      case 128: launch_f32<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      case 256: launch_f32<256>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      default:
-        return fail(TEENY_ERR_UNSUPPORTED,
-                    "flash_attention2_forward: f32 head_dim must be 16, 32, 64, 128 or 256");
-    }
-    return after_launch(name, s);
-  }
-  if (dtype == TEENY_BF16) {
-    TEENY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
-                  TEENY_ERR_MISALIGNED, "flash_attention2_forward: bf16 q/k/v/o must be 16-byte aligned");
-    // K and V of one (batch, head) are read through 32-bit buffer offsets
-    TEENY_REQUIRE(n_ctx_k * head_dim * 2 <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
-                  "flash_attention2_forward: bf16 K/V of one head must be below 2 GiB");
-    switch (head_dim) {
-      case 64: launch_bf16<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      case 128: launch_bf16<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, s); break;
-      default:
-        return fail(TEENY_ERR_UNSUPPORTED,
-                    "flash_attention2_forward: bf16 head_dim must be 64 or 128");
-    }
-    return after_launch(name, s);
-  }
-  return fail(TEENY_ERR_UNSUPPORTED_DTYPE, "flash_attention2_forward: dtype must be F32 or BF16");
+  return attention_entry(q, k, v, o, l, BH, 1, 1, n_ctx_q, n_ctx_k, head_dim, softmax_scale, causal, dtype,
+                         stream, "flash_attention2_forward");
+}
+
+extern "C" teeny_status teeny_attention_forward(const void *q, const void *k, const void *v, void *o,
+                                                float *l, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                                int64_t n_ctx_q, int64_t n_ctx_k, int64_t head_dim,
+                                                float softmax_scale, int32_t causal, teeny_dtype dtype,
+                                                teeny_stream stream) {
+  return attention_entry(q, k, v, o, l, batch, q_heads, kv_heads, n_ctx_q, n_ctx_k, head_dim, softmax_scale,
+                         causal, dtype, stream, "attention_forward");
 }

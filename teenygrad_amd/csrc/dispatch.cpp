@@ -145,11 +145,26 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
     return teeny_conv2d_forward(x, w, y, B, Ci, Co, H, W, OH, OW, &p, dtype, TEENY_NCHW, stream);
   }
 
-  // flash_attention2_forward<HEAD_DIM>(q, k, v, o, l, n_ctx_q, n_ctx_k, scale, neg_inf)
+  // flash_attention2_forward<HEAD_DIM[, CAUSAL]>(q, k, v, o, l, n_ctx_q, n_ctx_k, scale, neg_inf)
   // grid (N_CTX_Q, BH, 1)                                flash_attn2.rs:48-63
-  if (name_is(entry_point, "flash_attention2_forward")) {
-    TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT, "flash_attention2: expects const generic HEAD_DIM");
-    TEENY_REQUIRE(grid != nullptr, TEENY_ERR_NULL_POINTER, "flash_attention2: grid (BH = grid[1])");
+  // The reference kernel is non-causal; an optional second const generic
+  // CAUSAL != 0 masks key j > query i.
+  // multi_head_attention_forward<HEAD_DIM, CAUSAL, Q_HEADS, KV_HEADS>(same
+  // arguments), grid (N_CTX_Q, BATCH * Q_HEADS, 1): the lowering target of
+  // Op::MultiHeadAttention{q_num_heads, kv_num_heads} (core/teeny-core/src/
+  // graph/mod.rs:1240-1246), a TODO arm of the reference's lowering
+  // (kernels/teeny-kernels/src/graph/mod.rs:2477-2481); K/V carry KV_HEADS
+  // heads per batch, shared by Q_HEADS / KV_HEADS query heads each.
+  const bool fa = name_is(entry_point, "flash_attention2_forward");
+  const bool mha = name_is(entry_point, "multi_head_attention_forward");
+  if (fa || mha) {
+    if (fa)
+      TEENY_REQUIRE(n_cg == 1 || n_cg == 2, TEENY_ERR_INVALID_ARGUMENT,
+                    "flash_attention2: expects const generics HEAD_DIM[, CAUSAL]");
+    else
+      TEENY_REQUIRE(n_cg == 4, TEENY_ERR_INVALID_ARGUMENT,
+                    "multi_head_attention: expects const generics HEAD_DIM, CAUSAL, Q_HEADS, KV_HEADS");
+    TEENY_REQUIRE(grid != nullptr, TEENY_ERR_NULL_POINTER, "attention: grid (BH = grid[1])");
     void *q = r.ptr("q_ptr"), *k = r.ptr("k_ptr"), *v = r.ptr("v_ptr"), *o = r.ptr("o_ptr"),
          *l = r.ptr("l_ptr");
     int64_t nq = r.i32("n_ctx_q"), nk = r.i32("n_ctx_k");
@@ -157,9 +172,98 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
     r.f32("neg_inf");
     if (r.done() != TEENY_OK) return r.st;
     TEENY_REQUIRE(grid[0] == static_cast<uint32_t>(nq), TEENY_ERR_SHAPE_MISMATCH,
-                  "flash_attention2: grid[0] must equal n_ctx_q");
-    return teeny_flash_attention2_forward(q, k, v, o, static_cast<float *>(l), nq, nk, scale,
-                                          grid[1], cg[0], 0, dtype, stream);
+                  "attention: grid[0] must equal n_ctx_q");
+    const int32_t causal = n_cg >= 2 && cg[1] != 0 ? 1 : 0;
+    if (fa)
+      return teeny_flash_attention2_forward(q, k, v, o, static_cast<float *>(l), nq, nk, scale,
+                                            grid[1], cg[0], causal, dtype, stream);
+    TEENY_REQUIRE(cg[2] > 0 && grid[1] % cg[2] == 0, TEENY_ERR_SHAPE_MISMATCH,
+                  "multi_head_attention: grid[1] must be BATCH * Q_HEADS");
+    return teeny_attention_forward(q, k, v, o, static_cast<float *>(l), grid[1] / cg[2], cg[2], cg[3], nq, nk,
+                                   cg[0], scale, causal, dtype, stream);
+  }
+
+  // w8a16_linear_forward<USE_BIAS, ACT>(x, qweight, scale, bias, y, M, N, K): the
+  // lowering target of Op::QLinearMatMul / Op::MatMulInteger with teeny-quant
+  // per-output-channel int8 weights (TODO arms, graph/mod.rs:2595-2601); x bf16
+  // [M, K], qweight int8 [N, K], scale / bias fp32 [N], y bf16 [M, N].
+  if (name_is(entry_point, "w8a16_linear_forward")) {
+    TEENY_REQUIRE(n_cg == 2, TEENY_ERR_INVALID_ARGUMENT, "w8a16_linear_forward: expects const generics USE_BIAS, ACT");
+    void *x = r.ptr("x_ptr"), *q = r.ptr("qweight_ptr"), *sc = r.ptr("scale_ptr"), *b = r.ptr("bias_ptr"),
+         *y = r.ptr("y_ptr");
+    int64_t M = r.i32("M"), N = r.i32("N"), K = r.i32("K");
+    if (r.done() != TEENY_OK) return r.st;
+    TEENY_REQUIRE(dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE, "w8a16_linear_forward: dtype must be BF16");
+    return teeny_w8a16_linear_forward(x, static_cast<const int8_t *>(q), static_cast<const float *>(sc),
+                                      cg[0] ? static_cast<const float *>(b) : nullptr, y, M, N, K,
+                                      static_cast<teeny_activation>(cg[1]), stream);
+  }
+
+  // w8a16_conv2d_forward<KH,KW,SH,SW,PH,PW,G,BLOCK_OW,USE_BIAS,ACT>(x, qweight,
+  // scale, bias, y, B, C_IN, C_OUT, H, W, OH, OW): Op::QLinearConv /
+  // Op::ConvInteger (TODO arms, graph/mod.rs:2595-2601) on NHWC bf16
+  // activations and int8 weights [C_OUT, KH, KW, C_IN/G].
+  if (name_is(entry_point, "w8a16_conv2d_forward")) {
+    TEENY_REQUIRE(n_cg == 10, TEENY_ERR_INVALID_ARGUMENT,
+                  "w8a16_conv2d_forward: expects const generics KH,KW,STRIDE_H,STRIDE_W,PAD_H,PAD_W,G,"
+                  "BLOCK_OW,USE_BIAS,ACT");
+    teeny_conv2d_params p;
+    p.KH = static_cast<int32_t>(cg[0]);
+    p.KW = static_cast<int32_t>(cg[1]);
+    p.stride_h = static_cast<int32_t>(cg[2]);
+    p.stride_w = static_cast<int32_t>(cg[3]);
+    p.pad_h = static_cast<int32_t>(cg[4]);
+    p.pad_w = static_cast<int32_t>(cg[5]);
+    p.groups = static_cast<int32_t>(cg[6]);
+    p.act = static_cast<int32_t>(cg[9]);
+    void *x = r.ptr("x_ptr"), *q = r.ptr("qweight_ptr"), *sc = r.ptr("scale_ptr"), *b = r.ptr("bias_ptr"),
+         *y = r.ptr("y_ptr");
+    int64_t B = r.i32("B"), Ci = r.i32("C_IN"), Co = r.i32("C_OUT"), H = r.i32("H"), W = r.i32("W"),
+            OH = r.i32("OH"), OW = r.i32("OW");
+    if (r.done() != TEENY_OK) return r.st;
+    TEENY_REQUIRE(dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE, "w8a16_conv2d_forward: dtype must be BF16");
+    return teeny_w8a16_conv2d_forward(x, static_cast<const int8_t *>(q), static_cast<const float *>(sc),
+                                      cg[8] ? static_cast<const float *>(b) : nullptr, y, B, Ci, Co, H, W, OH,
+                                      OW, &p, stream);
+  }
+
+  // quantize_affine<GRANULARITY, AXIS, GROUP_SIZE, SYMMETRIC, BITS>(data, qvalues,
+  // scales, zero_points, groups, ndim, dim_0 .. dim_{ndim-1}) and
+  // dequantize_affine<GRANULARITY, AXIS, GROUP_SIZE>(qvalues, scales,
+  // zero_points, out, ndim, dims...): teeny-quant's quantize_affine /
+  // dequantize_affine (utilities/teeny-quant/src/quant/affine.rs:55-161), the
+  // lowering targets of Op::QuantizeLinear / Op::DequantizeLinear (TODO arms,
+  // graph/mod.rs:2691-2697).  Dims are i64 arguments.
+  const bool quant = name_is(entry_point, "quantize_affine");
+  const bool dequant = name_is(entry_point, "dequantize_affine");
+  if (quant || dequant) {
+    TEENY_REQUIRE(n_cg == (quant ? 5 : 3), TEENY_ERR_INVALID_ARGUMENT,
+                  quant ? "quantize_affine: expects const generics GRANULARITY, AXIS, GROUP_SIZE, SYMMETRIC, BITS"
+                        : "dequantize_affine: expects const generics GRANULARITY, AXIS, GROUP_SIZE");
+    void *a0 = r.ptr(quant ? "data_ptr" : "qvalues_ptr");
+    void *a1 = r.ptr(quant ? "qvalues_ptr" : "scales_ptr");
+    void *a2 = r.ptr(quant ? "scales_ptr" : "zero_points_ptr");
+    void *a3 = r.ptr(quant ? "zero_points_ptr" : "out_ptr");
+    void *groups = quant ? r.ptr("groups_ptr") : nullptr;
+    const int64_t ndim = r.i32("ndim");
+    if (r.st != TEENY_OK) return r.st;
+    TEENY_REQUIRE(ndim >= 0 && ndim <= 16, TEENY_ERR_INVALID_ARGUMENT, std::string(entry_point) + ": ndim in [0, 16]");
+    int64_t shape[16];
+    for (int64_t d = 0; d < ndim; ++d) shape[d] = r.take(TEENY_ARG_I64, "dim") ? args[r.i++].v.i64 : 0;
+    if (r.done() != TEENY_OK) return r.st;
+    if (quant) {
+      TEENY_REQUIRE(dtype == TEENY_F32, TEENY_ERR_UNSUPPORTED_DTYPE, "quantize_affine: dtype is the input's, F32");
+      return teeny_quantize_affine(static_cast<const float *>(a0), shape, static_cast<int32_t>(ndim),
+                                   static_cast<teeny_granularity>(cg[0]), static_cast<int32_t>(cg[1]), cg[2],
+                                   static_cast<int32_t>(cg[3]), static_cast<int32_t>(cg[4]),
+                                   static_cast<int8_t *>(a1), static_cast<float *>(a2),
+                                   static_cast<int32_t *>(a3), static_cast<uint32_t *>(groups), stream);
+    }
+    TEENY_REQUIRE(dtype == TEENY_F32, TEENY_ERR_UNSUPPORTED_DTYPE, "dequantize_affine: dtype is the output's, F32");
+    return teeny_dequantize_affine(static_cast<const int8_t *>(a0), static_cast<const float *>(a1),
+                                   static_cast<const int32_t *>(a2), shape, static_cast<int32_t>(ndim),
+                                   static_cast<teeny_granularity>(cg[0]), static_cast<int32_t>(cg[1]), cg[2],
+                                   static_cast<float *>(a3), stream);
   }
 
   // linear_forward<USE_BIAS,BLOCK_M,BLOCK_N,BLOCK_K,GROUP_M>(x, w, b, y, M, N, K,

@@ -25,6 +25,10 @@ teeny_status fail(teeny_status code, const std::string &msg) {
 }
 
 teeny_status hip_fail(hipError_t err, const char *what) {
+  // A failed HIP call also sets the runtime's per-thread last error, which
+  // hipGetLastError would report again after the next launch: clear it, the
+  // failure is reported here.
+  (void)hipGetLastError();
   g_last_error = std::string("hip error ") + std::to_string(static_cast<int>(err)) + " (" +
                  hipGetErrorString(err) + ") in " + what;
   if (err == hipErrorNoDevice || err == hipErrorInvalidDevice) return TEENY_ERR_NO_DEVICE;
@@ -304,7 +308,10 @@ teeny_status teeny_hip_module_get_function(teeny_function *function, teeny_modul
                 TEENY_ERR_NULL_POINTER, "function/module/name");
   hipFunction_t f = nullptr;
   hipError_t e = hipModuleGetFunction(&f, static_cast<hipModule_t>(module), name);
-  if (e == hipErrorNotFound) return fail(TEENY_ERR_NOT_FOUND, std::string("kernel ") + name);
+  if (e == hipErrorNotFound) {
+    (void)hipGetLastError();  // clear the runtime's last error (see hip_fail)
+    return fail(TEENY_ERR_NOT_FOUND, std::string("kernel ") + name);
+  }
   if (e != hipSuccess) return hip_fail(e, "hipModuleGetFunction");
   *function = f;
   return TEENY_OK;
@@ -322,9 +329,13 @@ teeny_status teeny_hip_launch(teeny_function function, const uint32_t grid[3],
   TEENY_REQUIRE(function != nullptr && grid != nullptr && block != nullptr,
                 TEENY_ERR_NULL_POINTER, "function/grid/block");
   TEENY_REQUIRE(grid[0] && grid[1] && grid[2], TEENY_ERR_INVALID_ARGUMENT, "empty grid");
-  TEENY_REQUIRE(block[0] && block[1] && block[2] && block[0] * block[1] * block[2] <= 1024,
-                TEENY_ERR_INVALID_ARGUMENT, "block must have 1..1024 threads");
+  const uint64_t threads = static_cast<uint64_t>(block[0]) * block[1] * block[2];
+  TEENY_REQUIRE(threads >= 1 && threads <= 1024, TEENY_ERR_INVALID_ARGUMENT,
+                "block must have 1..1024 threads");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // the launch reports its own status: a stale last error from an earlier,
+  // unrelated HIP call must not be attributed to it
+  (void)hipGetLastError();
   TEENY_CHECK_HIP(hipModuleLaunchKernel(static_cast<hipFunction_t>(function), grid[0], grid[1],
                                         grid[2], block[0], block[1], block[2], shared_mem_bytes,
                                         s, args, nullptr));

@@ -27,6 +27,7 @@
 // their extent (zeros, no memory traffic; stores dropped).
 #pragma once
 
+#include <atomic>
 #include <type_traits>
 
 namespace teeny {
@@ -196,8 +197,10 @@ __global__ __launch_bounds__(256, 2) void gemm_stream_kernel(GemmParams p) {
 
 // Shapes the streaming kernel is instantiated for, and its preconditions:
 // plain bf16 A with 16-byte aligned rows, bf16 B with 16-byte aligned rows,
-// C rows 8-byte aligned, and enough rows that the problem is bound by HBM
-// traffic (below that the tiled kernels are as fast).
+// C rows 16-byte aligned (the epilogue writes 16-byte chunks at row offsets
+// m * ldc * 2 + 16 j, so both C and ldc * 2 must be multiples of 16), and
+// enough rows that the problem is bound by HBM traffic (below that the tiled
+// kernels are as fast).
 constexpr int kStreamMinM = 16384;
 inline bool stream_shape(int K, int N) {
   return (K == 64 || K == 128 || K == 256) && (N == 64 || N == 128 || N == 256) && N * K <= 32768;
@@ -209,19 +212,24 @@ inline bool stream_gemm_fits(const GemmParams &p) {
   } else {
     return stream_shape(p.K, p.N) && p.M >= kStreamMinM && static_cast<int64_t>(p.M) * p.ldc * 2 < 0x7fffffff &&
            p.lda % 8 == 0 && p.ldb % 8 == 0 &&
-           p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 &&
-           (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.C) & 7) == 0;
+           p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0;
   }
 }
 
 template <int K, int N>
 inline void launch_stream_kn(const GemmParams &p, hipStream_t s) {
-  static int per_cu = 0;
-  if (per_cu == 0) {
-    int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemm_stream_kernel<K, N>, 256, 0) != hipSuccess || b < 1)
-      b = 1;
-    per_cu = b;
+  // resident workgroups per CU, cached per device ordinal (relaxed atomics:
+  // racing threads compute and store the same value)
+  static std::atomic<int> occupancy[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = -1;
+  int per_cu = dev >= 0 ? occupancy[dev].load(std::memory_order_relaxed) : 0;
+  if (per_cu <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm_stream_kernel<K, N>, 256, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (dev >= 0) occupancy[dev].store(per_cu, std::memory_order_relaxed);
   }
   // Every wave walks the same number of blocks (the last round of a
   // ragged split would run a small fraction of the waves alone).

@@ -363,12 +363,14 @@ class FlashAttention2Forward(RuntimeOp):
 
     name = "flash_attention2_forward"
 
-    def __init__(self, head_dim: int, softmax_scale: Optional[float] = None):
+    def __init__(self, head_dim: int, softmax_scale: Optional[float] = None, causal: bool = False):
         self.head_dim = int(head_dim)
         self.softmax_scale = float(softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(head_dim))
+        self.causal = bool(causal)
 
     def const_generics(self):
-        return (self.head_dim,)
+        # the reference kernel has HEAD_DIM only; CAUSAL is this library's extension
+        return (self.head_dim, 1) if self.causal else (self.head_dim,)
 
     def n_activation_inputs(self):
         return 3
@@ -392,6 +394,177 @@ class FlashAttention2Forward(RuntimeOp):
 
     def grid(self, output_shape):
         return (int(output_shape[1]), int(output_shape[0]), 1)
+
+
+class MultiHeadAttentionRuntimeOp(FlashAttention2Forward):
+    """Lowering of Op::MultiHeadAttention{q_num_heads, kv_num_heads}
+    (core/teeny-core/src/graph/mod.rs:1240-1246) — a TODO arm of the
+    reference's lowering (kernels/teeny-kernels/src/graph/mod.rs:2477-2481) —
+    onto the flash kernel, with grouped K/V heads.  Inputs q [B*Q_HEADS, Nq,
+    HEAD_DIM], k and v [B*KV_HEADS, Nk, HEAD_DIM]; params[0] is l; the packed
+    arguments are flash_attention2_forward's; const generics HEAD_DIM, CAUSAL,
+    Q_HEADS, KV_HEADS; grid (Nq, B*Q_HEADS, 1)."""
+
+    name = "multi_head_attention_forward"
+
+    def __init__(self, q_num_heads: int, kv_num_heads: int, head_dim: int, causal: bool = False,
+                 softmax_scale: Optional[float] = None):
+        super().__init__(head_dim, softmax_scale, causal)
+        _need(q_num_heads > 0 and kv_num_heads > 0 and q_num_heads % kv_num_heads == 0,
+              "multi_head_attention: q_num_heads must be a positive multiple of kv_num_heads")
+        self.q_num_heads, self.kv_num_heads = int(q_num_heads), int(kv_num_heads)
+
+    def const_generics(self):
+        return (self.head_dim, int(self.causal), self.q_num_heads, self.kv_num_heads)
+
+
+class W8A16LinearRuntimeOp(RuntimeOp):
+    """Lowering of Op::QLinearMatMul / Op::MatMulInteger with teeny-quant
+    per-output-channel int8 weights — TODO arms of the reference's lowering
+    (kernels/teeny-kernels/src/graph/mod.rs:2595-2601) — as linear_forward
+    (nn/mlp/linear.rs:20-116) on dequantize_affine's weights
+    (utilities/teeny-quant/src/quant/affine.rs:151-161).  Input x bf16 [M, K];
+    params qweight int8 [N, K], scale fp32 [N] (and bias fp32 [N]); const
+    generics USE_BIAS, ACT; args (x, qweight, scale, bias, y, M, N, K)."""
+
+    name = "w8a16_linear_forward"
+
+    def __init__(self, use_bias: bool = False, act: Optional[str] = None):
+        self.use_bias = bool(use_bias)
+        self.act = ACTS[act]
+
+    def const_generics(self):
+        return (int(self.use_bias), self.act)
+
+    def param_shapes(self, input_shapes, output_shape):
+        k, n = int(input_shapes[0][1]), int(output_shape[1])
+        return [[n, k], [n], [n]] if self.use_bias else [[n, k], [n]]
+
+    def param_names(self):
+        return ("qweight", "scale", "bias") if self.use_bias else ("qweight", "scale")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        m, n = int(output_shape[0]), int(output_shape[1])
+        k = int(inputs[0][1][1])
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_ptr(params[2] if self.use_bias else None)
+        visitor.visit_ptr(output)
+        for v in (m, n, k):
+            visitor.visit_i32(v)
+
+    def grid(self, output_shape):
+        return (-(-int(output_shape[0]) // 256) * -(-int(output_shape[1]) // 256), 1, 1)
+
+
+class W8A16Conv2dRuntimeOp(RuntimeOp):
+    """Lowering of Op::QLinearConv / Op::ConvInteger with teeny-quant int8
+    weights (TODO arms, kernels/teeny-kernels/src/graph/mod.rs:2595-2601):
+    conv2d_bias_forward (nn/conv/conv2d.rs:642-764) on dequantized weights,
+    NHWC.  Input x bf16 [B, H, W, C_IN]; params qweight int8 [C_OUT, KH, KW,
+    C_IN/G], scale fp32 [C_OUT] (and bias fp32 [C_OUT]); output [B, OH, OW,
+    C_OUT]; const generics KH..BLOCK_OW of conv2d_forward plus USE_BIAS, ACT;
+    args (x, qweight, scale, bias, y, B, C_IN, C_OUT, H, W, OH, OW)."""
+
+    name = "w8a16_conv2d_forward"
+
+    def __init__(self, kh, kw, stride_h=1, stride_w=1, pad_h=0, pad_w=0, groups=1, block_ow=16,
+                 use_bias=False, act: Optional[str] = None):
+        self.conv = Conv2dForward(kh, kw, stride_h, stride_w, pad_h, pad_w, groups, block_ow)
+        self.use_bias = bool(use_bias)
+        self.act = ACTS[act]
+
+    def const_generics(self):
+        return self.conv.const_generics() + (int(self.use_bias), self.act)
+
+    def param_shapes(self, input_shapes, output_shape):
+        c = self.conv
+        cin, cout = int(input_shapes[0][3]), int(output_shape[3])
+        shapes = [[cout, c.kh, c.kw, cin // c.g], [cout]]
+        return shapes + [[cout]] if self.use_bias else shapes
+
+    def param_names(self):
+        return ("qweight", "scale", "bias") if self.use_bias else ("qweight", "scale")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        ish = inputs[0][1]
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_ptr(params[2] if self.use_bias else None)
+        visitor.visit_ptr(output)
+        for v in (ish[0], ish[3], output_shape[3], ish[1], ish[2], output_shape[1], output_shape[2]):
+            visitor.visit_i32(v)
+
+    def grid(self, output_shape):
+        b, oh, ow, cout = (int(v) for v in output_shape)
+        return (b * cout * oh * -(-ow // self.conv.block_ow), 1, 1)
+
+
+class QuantizeAffineRuntimeOp(RuntimeOp):
+    """Lowering of Op::QuantizeLinear{axis} (TODO arm, kernels/teeny-kernels/
+    src/graph/mod.rs:2691-2697) to teeny-quant's quantize_affine
+    (utilities/teeny-quant/src/quant/affine.rs:55-148).  Input fp32 data of
+    any shape; output int8 q of that shape; params scales fp32 [groups] and
+    zero_points int32 [groups]; const generics GRANULARITY, AXIS, GROUP_SIZE,
+    SYMMETRIC, BITS; args (data, q, scales, zero_points, groups = null, ndim,
+    dims as i64)."""
+
+    name = "quantize_affine"
+
+    def __init__(self, granularity="channel", axis=0, group_size=1, symmetric=True, bits=8):
+        self.gran = GRANULARITY[granularity] if isinstance(granularity, str) else int(granularity)
+        self.granularity = granularity
+        self.axis, self.group_size = int(axis), int(group_size)
+        self.symmetric, self.bits = bool(symmetric), int(bits)
+
+    def const_generics(self):
+        return (self.gran, self.axis, self.group_size, int(self.symmetric), self.bits)
+
+    def param_shapes(self, input_shapes, output_shape):
+        ng = quant_num_groups(list(input_shapes[0]), self.granularity, self.axis, self.group_size)
+        return [[max(ng, 1)], [max(ng, 1)]]
+
+    def param_names(self):
+        return ("scales", "zero_points")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        shape = list(inputs[0][1])
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(output)
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_ptr(None)
+        visitor.visit_i32(len(shape))
+        for d in shape:
+            visitor.visit_i64(d)
+
+    def grid(self, output_shape):
+        return (-(-_prod(output_shape) // 256), 1, 1)
+
+
+class DequantizeAffineRuntimeOp(QuantizeAffineRuntimeOp):
+    """Lowering of Op::DequantizeLinear{axis} (TODO arm, graph/mod.rs:2691-2697)
+    to dequantize_affine (affine.rs:151-161).  Input int8 q; output fp32 of the
+    same shape; params scales fp32 [groups] and zero_points int32 [groups];
+    const generics GRANULARITY, AXIS, GROUP_SIZE; args (q, scales,
+    zero_points, out, ndim, dims as i64)."""
+
+    name = "dequantize_affine"
+
+    def const_generics(self):
+        return (self.gran, self.axis, self.group_size)
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        shape = list(inputs[0][1])
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(params[1])
+        visitor.visit_ptr(output)
+        visitor.visit_i32(len(shape))
+        for d in shape:
+            visitor.visit_i64(d)
 
 
 class LinearForward(RuntimeOp):
@@ -642,6 +815,28 @@ def flash_attention(q: Buffer, k: Buffer, v: Buffer, softmax_scale: Optional[flo
     check(lib.teeny_flash_attention2_forward(q.ptr, k.ptr, v.ptr, o.ptr,
                                              lse.ptr if lse is not None else None, nq, nk, scale,
                                              bh, d, int(bool(causal)), q.dtype.code, _h(stream)))
+    return o
+
+
+def attention(q: Buffer, k: Buffer, v: Buffer, q_heads: int, kv_heads: int,
+              softmax_scale: Optional[float] = None, causal: bool = False, o: Optional[Buffer] = None,
+              lse: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """Multi-head attention with grouped K/V heads: q [B*q_heads, Nq, D], k/v
+    [B*kv_heads, Nk, D] -> o [B*q_heads, Nq, D]."""
+    _need(len(q.shape) == 3 and len(k.shape) == 3 and tuple(k.shape) == tuple(v.shape),
+          "attention: q [B*Hq, Nq, D], k/v [B*Hkv, Nk, D]")
+    _need(q_heads > 0 and kv_heads > 0 and q_heads % kv_heads == 0, "attention: q_heads % kv_heads != 0")
+    bhq, nq, d = q.shape
+    _need(bhq % q_heads == 0, "attention: q's first dim must be B * q_heads")
+    batch = bhq // q_heads
+    _need(k.shape[0] == batch * kv_heads and k.shape[2] == d, "attention: k/v must be [B*kv_heads, Nk, D]")
+    _need(lse is None or (lse.numel == bhq * nq and lse.dtype == f32), "attention: lse fp32 [B*q_heads, Nq]")
+    _need(k.dtype == q.dtype and v.dtype == q.dtype, "attention: q/k/v dtypes differ")
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    o = _out(q, o)
+    check(lib.teeny_attention_forward(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr if lse is not None else None,
+                                      batch, q_heads, kv_heads, nq, k.shape[1], d, scale, int(bool(causal)),
+                                      q.dtype.code, _h(stream)))
     return o
 
 

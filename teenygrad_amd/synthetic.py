@@ -34,3 +34,26 @@ def normal(seed: int, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
 def workload_seed(index: int, stream: int = 0) -> int:
     """Seed for tensor `stream` of workload `index` (distinct streams per tensor)."""
     return SEED_BASE + index + (stream << 20)
+
+
+def resnet50_convs():
+    """The 53 convolutions of ResNet-50 (torchvision v1.5: stride on the 3x3 of
+    a bottleneck) at 224x224 input, as (name, C_IN, C_OUT, H_IN, K, stride,
+    pad, relu).  BN is folded into a bias; ReLU follows the stem, c1 and c2,
+    while c3 and the downsample conv end with the residual add (not a conv),
+    so they carry no fused activation."""
+    layers = [("stem", 3, 64, 224, 7, 2, 3, True)]
+    stages = [(64, 256, 3, 56), (128, 512, 4, 56), (256, 1024, 6, 28), (512, 2048, 3, 14)]
+    cin = 64
+    for si, (width, out, blocks, hin) in enumerate(stages):
+        s = 1 if si == 0 else 2
+        for bi in range(blocks):
+            h = hin if bi == 0 else hin // s
+            stride = s if bi == 0 else 1
+            layers.append((f"l{si + 1}b{bi}c1", cin, width, h, 1, 1, 0, True))
+            layers.append((f"l{si + 1}b{bi}c2", width, width, h, 3, stride, 1, True))
+            layers.append((f"l{si + 1}b{bi}c3", width, out, h // stride, 1, 1, 0, False))
+            if bi == 0:
+                layers.append((f"l{si + 1}b{bi}ds", cin, out, h, 1, stride, 0, False))
+            cin = out
+    return layers

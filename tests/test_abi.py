@@ -246,3 +246,79 @@ def test_workspace_registry_and_sizes():
         # fp32 and NCHW convs never use scratch
         assert tg.kernels.conv2d_workspace_size((1, 20, 20, 3), (16, 3, 3, 3), 2, 1, 1, tg.f32) == 0
         assert tg.kernels.conv2d_workspace_size((1, 3, 20, 20), (16, 3, 3, 3), 2, 1, 1, tg.bf16, "nchw") == 0
+
+
+def test_module_and_launch_errors():
+    # validation before any HIP call (drivers/teeny-cuda/src/device/mod.rs:430-490 is the
+    # reference's launch; here the checks are the C ABI's own)
+    h = ctypes.c_void_p()
+    expect(lib.teeny_hip_module_load(None, b"x.hsaco"), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_module_load(ctypes.byref(h), None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_module_load_data(ctypes.byref(h), None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_module_get_function(ctypes.byref(h), None, b"k"), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_module_get_function(ctypes.byref(h), FAKE, None), _lib.ERR_NULL_POINTER)
+    assert lib.teeny_hip_module_unload(None) == _lib.OK
+    g = (ctypes.c_uint32 * 3)(1, 1, 1)
+    b = (ctypes.c_uint32 * 3)(64, 1, 1)
+    expect(lib.teeny_hip_launch(None, g, b, 0, None, None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_launch(FAKE, None, b, 0, None, None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_launch(FAKE, (ctypes.c_uint32 * 3)(0, 1, 1), b, 0, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_hip_launch(FAKE, g, (ctypes.c_uint32 * 3)(0, 1, 1), 0, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_hip_launch(FAKE, g, (ctypes.c_uint32 * 3)(1025, 1, 1), 0, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    # 65536 * 65536 wraps to 0 in 32 bits: must still be rejected as too many threads
+    expect(lib.teeny_hip_launch(FAKE, g, (ctypes.c_uint32 * 3)(65536, 65536, 1), 0, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_hip_launch(FAKE, g, (ctypes.c_uint32 * 3)(1024, 1024, 4096), 0, None, None),
+           _lib.ERR_INVALID_ARGUMENT)
+
+
+def test_example_code_object_built():
+    # the stand-alone gfx950 code object the module surface loads (hipcc --genco)
+    assert os.path.exists(_lib.EXAMPLE_MODULE_PATH)
+    with open(_lib.EXAMPLE_MODULE_PATH, "rb") as f:
+        assert f.read(4) == b"\x7fELF"
+
+
+def test_dispatch_new_names_errors():
+    d = lib.teeny_dispatch
+    grid = (ctypes.c_uint32 * 3)(8, 4, 1)
+    attn = packed(*([(_lib.ARG_PTR, FAKE)] * 5 + [(_lib.ARG_I32, 8), (_lib.ARG_I32, 8), (_lib.ARG_F32, 0.125),
+                                                  (_lib.ARG_F32, float("-inf"))]))
+    # multi_head_attention: four const generics; grid[1] a multiple of Q_HEADS; heads divide
+    expect(d(b"multi_head_attention_forward_entry_point", (ctypes.c_int64 * 2)(64, 1), 2, attn, 9, grid,
+             _lib.BF16, None), _lib.ERR_INVALID_ARGUMENT)
+    expect(d(b"multi_head_attention_forward_entry_point", (ctypes.c_int64 * 4)(64, 1, 3, 1), 4, attn, 9, grid,
+             _lib.BF16, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(d(b"multi_head_attention_forward_entry_point", (ctypes.c_int64 * 4)(64, 1, 4, 3), 4, attn, 9, grid,
+             _lib.BF16, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(d(b"flash_attention2_forward_entry_point", (ctypes.c_int64 * 3)(64, 1, 0), 3, attn, 9, grid,
+             _lib.BF16, None), _lib.ERR_INVALID_ARGUMENT)
+    # w8a16: bf16 only, USE_BIAS/ACT const generics
+    lin = packed(*([(_lib.ARG_PTR, FAKE)] * 5 + [(_lib.ARG_I32, 16)] * 3))
+    expect(d(b"w8a16_linear_forward_entry_point", (ctypes.c_int64 * 2)(0, 0), 2, lin, 8, grid, _lib.F32, None),
+           _lib.ERR_UNSUPPORTED_DTYPE)
+    expect(d(b"w8a16_linear_forward_entry_point", (ctypes.c_int64 * 1)(0), 1, lin, 8, grid, _lib.BF16, None),
+           _lib.ERR_INVALID_ARGUMENT)
+    # quantize: dims must be i64 arguments, as many as ndim says
+    q = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE),
+               (_lib.ARG_PTR, None), (_lib.ARG_I32, 2), (_lib.ARG_I32, 4), (_lib.ARG_I32, 4))
+    cg = (ctypes.c_int64 * 5)(1, 0, 1, 1, 8)
+    expect(d(b"quantize_affine_entry_point", cg, 5, q, 8, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    q_short = packed((_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE), (_lib.ARG_PTR, FAKE),
+                     (_lib.ARG_PTR, None), (_lib.ARG_I32, 2))
+    expect(d(b"quantize_affine_entry_point", cg, 5, q_short, 6, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+    expect(d(b"dequantize_affine_entry_point", cg, 5, q, 8, grid, _lib.F32, None), _lib.ERR_INVALID_ARGUMENT)
+
+
+def test_attention_forward_errors():
+    f = lib.teeny_attention_forward
+    # q_heads must be a multiple of kv_heads; sizes non-negative
+    expect(f(FAKE, FAKE, FAKE, FAKE, None, 2, 6, 4, 16, 16, 64, 0.125, 0, _lib.BF16, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(f(FAKE, FAKE, FAKE, FAKE, None, -1, 4, 4, 16, 16, 64, 0.125, 0, _lib.BF16, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(f(FAKE, None, FAKE, FAKE, None, 2, 4, 2, 16, 16, 64, 0.125, 1, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    expect(f(FAKE, FAKE, FAKE, FAKE, None, 2, 4, 2, 16, 16, 96, 0.125, 1, _lib.BF16, None), _lib.ERR_UNSUPPORTED)
+    expect(f(FAKE_ODD, FAKE, FAKE, FAKE, None, 2, 4, 2, 16, 16, 64, 0.125, 1, _lib.BF16, None), _lib.ERR_MISALIGNED)
+    assert f(None, None, None, None, None, 0, 4, 2, 16, 16, 64, 0.125, 1, _lib.BF16, None) == _lib.OK

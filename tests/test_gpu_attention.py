@@ -89,9 +89,19 @@ def test_bf16_scale(dev, orc, scale, causal):
 
 
 def sample_rows(bh, nq, n=48, seed=0):
+    """Fixed tile-border rows, random rows, and two rows of every (b, h): one
+    in query block p and one in block nqb-1-p (128-query blocks; the causal
+    kernel pairs exactly those two in one workgroup), at the 32-query slice
+    of wave h % 4, so every head and, over the heads, every wave is covered."""
     rng = np.random.default_rng(seed)
     fixed = [0, 1, 63, 64, 127, 128, nq - 1, (bh - 1) * nq, bh * nq - 1, (bh // 2) * nq + nq // 2]
-    return np.unique(np.concatenate([fixed, rng.integers(0, bh * nq, n)])).astype(np.int64)
+    nqb = max(1, nq // 128)
+    heads = np.arange(bh)
+    p = (heads * 5) % nqb
+    within = (heads % 4) * 32 + rng.integers(0, 32, bh)
+    per_head = [heads * nq + p * 128 + within, heads * nq + (nqb - 1 - p) * 128 + within]
+    rows = np.concatenate([fixed, rng.integers(0, bh * nq, n)] + per_head)
+    return np.unique(rows[(rows >= 0) & (rows < bh * nq)]).astype(np.int64)
 
 
 @pytest.mark.parametrize("s,causal", [(2048, True), (4096, False)])

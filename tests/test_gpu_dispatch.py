@@ -78,3 +78,136 @@ def test_linear(dev, use_bias):
     K.LinearForward(use_bias).launch([(dev.upload(x), [64, 64])], params, y, [64, 48], tg.f32)
     want = load_golden(f"linear/expected_{'with' if use_bias else 'no'}_bias.bin").reshape(64, 48)
     np.testing.assert_allclose(y.to_host(), want, rtol=0.02, atol=0.1)
+
+
+@pytest.mark.parametrize("cls,op,tol", [(K.ReluForward, "relu", 0.0), (K.GeluForward, "gelu", 2e-5),
+                                        (K.SiluForward, "silu", 1e-5)])
+def test_elementwise_backward(dev, cls, op, tol):
+    # RuntimeOp.pack_backward_args + backward_grid through "<op>_backward_entry_point"
+    # (relu.rs:148-180, gelu.rs:287-317, sigmoid.rs:418-448), against the reference's
+    # backward fixtures (test_relu.rs:148, test_gelu.rs:157, test_sigmoid.rs:274)
+    import ctypes
+    from teenygrad_amd._lib import check, lib
+    if op == "relu":
+        saved, dy = load_golden("relu/y_backward.bin"), load_golden("relu/dy_backward.bin")
+    else:
+        saved, dy = load_golden(f"{op}/x.bin"), load_golden(f"{op}/dy.bin")
+    shape = list(saved.shape)
+    sb, dyb, dxb = dev.upload(saved), dev.upload(dy), tg.Buffer(tg.f32, saved.shape)
+    rop = cls(1024)
+    packer = K.DispatchPacker()
+    # forward output (relu) or forward input (gelu/silu) as the saved tensor
+    rop.pack_backward_args([(sb, shape)], [], sb, shape, dyb, shape[-1], [dxb], [], packer)
+    args, n = packer.array()
+    cg = (ctypes.c_int64 * 1)(*rop.const_generics())
+    grid = (ctypes.c_uint32 * 3)(*rop.backward_grid([shape], shape))
+    check(lib.teeny_dispatch(rop.backward_entry_point_name().encode(), cg, 1, args, n, grid, tg.f32.code, None))
+    assert np.max(np.abs(dxb.to_host() - load_golden(f"{op}/expected_backward.bin"))) <= tol
+
+
+def _rb(a):
+    from teenygrad_amd.dtypes import from_bf16, to_bf16
+    return from_bf16(to_bf16(a))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_attention_causal_const_generic(dev, orc, causal):
+    # flash_attention2_forward<HEAD_DIM, CAUSAL>: the optional CAUSAL const generic
+    from gpu_util import check_bf16
+    from teenygrad_amd.dtypes import to_bf16
+    rng = np.random.default_rng(21)
+    shape = [3, 150, 128]
+    q, k, v = (_rb(rng.standard_normal(shape, dtype=np.float32)) for _ in range(3))
+    qb, kb, vb = (dev.upload(to_bf16(t), tg.bf16) for t in (q, k, v))
+    o, l = tg.Buffer(tg.bf16, shape), tg.Buffer(tg.f32, (3, 150))
+    op = K.FlashAttention2Forward(128, None, causal)
+    assert op.const_generics() == ((128, 1) if causal else (128,))
+    op.launch([(qb, shape), (kb, shape), (vb, shape)], [l], o, shape, tg.bf16)
+    oo, ol = orc.flash_attention(q, k, v, causal=causal)
+    check_bf16(o.to_host(), oo, "o")
+    assert np.max(np.abs(l.to_host() - ol)) < 1e-3
+
+
+@pytest.mark.parametrize("hq,hkv,causal,dt", [(8, 2, True, "bf16"), (4, 4, False, "bf16"), (6, 3, True, "f32"),
+                                              (4, 1, False, "f32")])
+def test_multi_head_attention(dev, orc, hq, hkv, causal, dt):
+    # Op::MultiHeadAttention{q_num_heads, kv_num_heads} lowered onto the flash kernel:
+    # grouped K/V heads equal ordinary attention on K/V heads repeated per group
+    from gpu_util import check_bf16, check_f32
+    from teenygrad_amd.dtypes import to_bf16
+    B, nq, nk, d = 2, 130, 97, 64
+    rng = np.random.default_rng(hq * 10 + hkv)
+    q = _rb(rng.standard_normal((B * hq, nq, d), dtype=np.float32))
+    k = _rb(rng.standard_normal((B * hkv, nk, d), dtype=np.float32))
+    v = _rb(rng.standard_normal((B * hkv, nk, d), dtype=np.float32))
+    up = (lambda a: dev.upload(to_bf16(a), tg.bf16)) if dt == "bf16" else dev.upload
+    dtype = tg.bf16 if dt == "bf16" else tg.f32
+    o, l = tg.Buffer(dtype, (B * hq, nq, d)), tg.Buffer(tg.f32, (B * hq, nq))
+    op = K.MultiHeadAttentionRuntimeOp(hq, hkv, d, causal)
+    assert op.grid([B * hq, nq, d]) == (nq, B * hq, 1)
+    op.launch([(up(q), list(q.shape)), (up(k), list(k.shape)), (up(v), list(v.shape))], [l], o,
+              [B * hq, nq, d], dtype)
+    g = hq // hkv
+    kr = np.repeat(k.reshape(B, hkv, nk, d), g, axis=1).reshape(B * hq, nk, d)
+    vr = np.repeat(v.reshape(B, hkv, nk, d), g, axis=1).reshape(B * hq, nk, d)
+    oo, ol = orc.flash_attention(q, kr, vr, causal=causal)
+    if dt == "bf16":
+        check_bf16(o.to_host(), oo, "mha o")
+        assert np.max(np.abs(l.to_host() - ol)) < 1e-3
+    else:
+        check_f32(o.to_host(), oo, "mha o")
+        check_f32(l.to_host(), ol, "mha l")
+
+
+@pytest.mark.parametrize("use_bias,act", [(False, None), (True, "silu")])
+def test_w8a16_linear_dispatch(dev, orc, use_bias, act):
+    from gpu_util import check_bf16
+    from teenygrad_amd.dtypes import to_bf16
+    m, n, k = 200, 320, 256
+    rng = np.random.default_rng(5)
+    x = _rb(rng.standard_normal((m, k), dtype=np.float32))
+    wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    q, s, _, _ = orc.quantize_affine(wf, [n, k], "channel", 0)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    y = tg.Buffer(tg.bf16, (m, n))
+    params = [dev.upload(q.reshape(n, k)), dev.upload(s)] + ([dev.upload(bias)] if use_bias else [])
+    K.W8A16LinearRuntimeOp(use_bias, act).launch([(dev.upload(to_bf16(x), tg.bf16), [m, k])], params, y,
+                                                 [m, n], tg.bf16)
+    ref = orc.w8a16_linear(x, q.reshape(n, k), s, bias if use_bias else None)
+    if act:
+        ref = orc.silu(ref)
+    check_bf16(y.to_host(), ref, "w8a16 dispatch")
+
+
+def test_w8a16_conv_dispatch(dev, orc):
+    from gpu_util import check_bf16
+    from teenygrad_amd.dtypes import to_bf16
+    B, H, cin, cout = 2, 14, 64, 96
+    rng = np.random.default_rng(6)
+    x = _rb(rng.standard_normal((B, H, H, cin), dtype=np.float32))
+    wf = rng.normal(0, 0.02, (cout, 3, 3, cin)).astype(np.float32)
+    q, s, _, _ = orc.quantize_affine(wf, list(wf.shape), "channel", 0)
+    bias = rng.normal(0, 0.1, cout).astype(np.float32)
+    y = tg.Buffer(tg.bf16, (B, 7, 7, cout))
+    op = K.W8A16Conv2dRuntimeOp(3, 3, 2, 2, 1, 1, 1, 16, True, "relu")
+    op.launch([(dev.upload(to_bf16(x), tg.bf16), [B, H, H, cin])],
+              [dev.upload(q.reshape(wf.shape)), dev.upload(s), dev.upload(bias)], y, [B, 7, 7, cout], tg.bf16)
+    wdeq = orc.dequantize_affine(q, s, None, list(wf.shape), "channel", 0)
+    ref = orc.relu(orc.conv2d_nhwc(x, wdeq, bias, stride=2, padding=1))
+    check_bf16(y.to_host(), ref, "w8a16 conv dispatch")
+
+
+@pytest.mark.parametrize("gran,axis,gs,sym", [("channel", 0, 1, True), ("group", 1, 8, False), ("tensor", 0, 1, True)])
+def test_quantize_dequantize_dispatch(dev, orc, gran, axis, gs, sym):
+    shape = [12, 40]
+    x = np.random.default_rng(7).normal(0, 0.05, shape).astype(np.float32)
+    ng = K.quant_num_groups(shape, gran, axis, gs)
+    qb, sb, zb = tg.Buffer(tg.i8, shape), tg.Buffer(tg.f32, (ng,)), tg.Buffer("i32", (ng,))
+    K.QuantizeAffineRuntimeOp(gran, axis, gs, sym, 8).launch([(dev.upload(x), shape)], [sb, zb], qb, shape, tg.f32)
+    oq, os_, oz, _ = orc.quantize_affine(x, shape, gran, axis, gs, sym, 8)
+    np.testing.assert_array_equal(qb.to_host().reshape(-1), oq)
+    np.testing.assert_array_equal(sb.to_host(), os_)
+    np.testing.assert_array_equal(zb.to_host(), oz)
+    out = tg.Buffer(tg.f32, shape)
+    K.DequantizeAffineRuntimeOp(gran, axis, gs).launch([(qb, shape)], [sb, zb], out, shape, tg.f32)
+    np.testing.assert_array_equal(out.to_host(), orc.dequantize_affine(oq, os_, oz, shape, gran, axis, gs))

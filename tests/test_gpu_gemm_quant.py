@@ -70,6 +70,32 @@ def test_linear_bf16_stream(dev, orc, m, n, k):
     check_bf16(got, orc.linear(x, w, b), "linear bf16 stream")
 
 
+@pytest.mark.parametrize("pad,offset", [(8, 0), (4, 0), (0, 8), (8, 16)])
+def test_linear_bf16_stream_padded_rows(dev, orc, pad, offset):
+    # the reference's LinearForward passes output_row_stride as stride_ym
+    # (linear.rs:297-311), which may be padded; M = 16421 with K = 128, N = 64 is
+    # a streaming shape.  Row pitch N + pad and y offset by `offset` bytes: the
+    # streaming kernel takes 16-byte aligned rows (pad 8, offset 0 or 16), the
+    # tiled kernels the rest; padding columns and the bytes before y stay untouched
+    m, n, k = 16421, 64, 128
+    print(f"[linear stream padded] ldy={n + pad} offset={offset}", flush=True)
+    rng = np.random.default_rng(pad + offset)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb((rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float32))
+    xb, wb = dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16)
+    ldy = n + pad
+    sentinel = np.uint16(0x7FC1)  # a NaN pattern no result has
+    ybuf = dev.upload(np.full(offset // 2 + m * ldy, sentinel, np.uint16), tg.bf16)
+    tg.check(_lib.lib.teeny_linear_forward(xb.ptr, wb.ptr, None, ybuf.ptr + offset, m, n, k, k, 1, k, 1,
+                                           ldy, 1, _lib.BF16, None))
+    host = ybuf.to_host()
+    assert np.all(host[:offset // 2] == sentinel)
+    y = host[offset // 2:].reshape(m, ldy)
+    assert np.all(y[:, n:] == sentinel)
+    rows = np.concatenate([np.arange(0, 64), np.arange(0, m, 97), np.arange(m - 64, m)])
+    check_bf16(y[rows, :n], orc.linear(x[rows], w), f"ldy={ldy} offset={offset}")
+
+
 def test_linear_bf16_large_tile(dev, orc):
     # 4096 x 512 x 4096: 256 x 256 tiles fill the chip -> large-tile kernel;
     # rows 0..31 and the last 32 rows against the oracle
@@ -147,6 +173,10 @@ def test_w8a16_config(dev, orc, k, n, scratch):
     for lo, hi in ((0, 32), (m - 32, m)):
         ref = orc.linear(x[lo:hi], wdeq)
         check_bf16(y[lo:hi], ref, f"rows {lo}..{hi}")
+    # one row from every 64-row block (each 256 x 256 and 128 x 128 row tile,
+    # and every wave's 64-row slice of one over the blocks), all N columns
+    rows = np.arange(0, m, 64) + (np.arange(m // 64) * 13) % 64
+    check_bf16(y[rows], orc.linear(x[rows], wdeq), f"{rows.size} rows, one per 64-row block")
 
 
 # ── teeny-quant on the GPU: bit-exact with the oracle ──────────────────────

@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from teenygrad_amd import dtypes, kernels, synthetic
+from teenygrad_amd import kernels as K
 from teenygrad_amd.kernels import RecordingVisitor
 
 
@@ -183,3 +184,36 @@ def test_runtime_op_buffer_check_uses_param_shapes():
     with pytest.raises(ValueError):
         op.check_buffers(inputs=[(FakeBuf(10), [2, 4, 9, 9])], params=[FakeBuf(216), FakeBuf(6)],
                          output=ok["output"], output_shape=ok["output_shape"])
+
+
+def test_lowering_runtime_ops_for_reference_todo_arms():
+    # argument lists the new dispatch names read (dispatch.cpp), packed by the mirrors
+    rv = K.RecordingVisitor()
+    mha = K.MultiHeadAttentionRuntimeOp(8, 2, 128, causal=True)
+    mha.pack_args([(1, [16, 64, 128]), (2, [4, 64, 128]), (3, [4, 64, 128])], [4], 5, [16, 64, 128], 128, rv)
+    assert [k for k, _ in rv.args] == ["ptr"] * 5 + ["i32", "i32", "f32", "f32"]
+    assert mha.const_generics() == (128, 1, 8, 2) and mha.grid([16, 64, 128]) == (64, 16, 1)
+    assert mha.entry_point_name() == "multi_head_attention_forward_entry_point"
+    with pytest.raises(ValueError):
+        K.MultiHeadAttentionRuntimeOp(6, 4, 64)
+    rv = K.RecordingVisitor()
+    lin = K.W8A16LinearRuntimeOp(False, "gelu")
+    lin.pack_args([(1, [10, 32])], [2, 3], 4, [10, 48], 48, rv)
+    assert rv.args == [("ptr", 1), ("ptr", 2), ("ptr", 3), ("ptr", None), ("ptr", 4), ("i32", 10), ("i32", 48),
+                       ("i32", 32)]
+    assert lin.param_shapes([[10, 32]], [10, 48]) == [[48, 32], [48]]
+    rv = K.RecordingVisitor()
+    cv = K.W8A16Conv2dRuntimeOp(3, 3, 1, 1, 1, 1, 1, 16, True, "relu")
+    cv.pack_args([(1, [2, 8, 9, 16])], [2, 3, 5], 4, [2, 8, 9, 24], 24, rv)
+    assert [v for _, v in rv.args] == [1, 2, 3, 5, 4, 2, 16, 24, 8, 9, 8, 9]
+    assert cv.const_generics() == (3, 3, 1, 1, 1, 1, 1, 16, 1, 1)
+    assert cv.param_shapes([[2, 8, 9, 16]], [2, 8, 9, 24]) == [[24, 3, 3, 16], [24], [24]]
+    rv = K.RecordingVisitor()
+    qop = K.QuantizeAffineRuntimeOp("group", 1, 8, False, 4)
+    qop.pack_args([(1, [3, 16])], [2, 3], 4, [3, 16], 16, rv)
+    assert rv.args == [("ptr", 1), ("ptr", 4), ("ptr", 2), ("ptr", 3), ("ptr", None), ("i32", 2), ("i64", 3),
+                       ("i64", 16)]
+    assert qop.const_generics() == (2, 1, 8, 0, 4)
+    rv = K.RecordingVisitor()
+    K.DequantizeAffineRuntimeOp("channel", 0).pack_args([(1, [5, 7])], [2, 3], 4, [5, 7], 7, rv)
+    assert [k for k, _ in rv.args] == ["ptr"] * 4 + ["i32", "i64", "i64"]

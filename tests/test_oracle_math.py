@@ -195,6 +195,23 @@ def test_conv2d_nhwc_is_transpose(orc):
     assert rel_inf(got, want.transpose(0, 2, 3, 1)) < 1e-6
 
 
+@pytest.mark.parametrize("case", [(3, 9, 7, 5, 4, 3, 3, 1, 1), (2, 11, 11, 3, 6, 7, 7, 2, 3),
+                                  (2, 6, 6, 8, 16, 1, 1, 2, 0)])
+def test_conv2d_pixel_subset(orc, case):
+    # the sampled-pixel API runs the same programs: bit-identical to the full run
+    B, H, W, Cin, Cout, KH, KW, s, p = case
+    x = RNG.normal(0, 1, (B, H, W, Cin)).astype(np.float32)
+    w = RNG.normal(0, 0.3, (Cout, KH, KW, Cin)).astype(np.float32)
+    b = RNG.normal(0, 0.1, Cout).astype(np.float32)
+    full = orc.conv2d_nhwc(x, w, b, stride=s, padding=p)
+    m = full.shape[0] * full.shape[1] * full.shape[2]
+    pix = np.unique(np.concatenate([[0, m - 1], RNG.integers(0, m, 9)]))
+    got = orc.conv2d_nhwc_pixels(x, w, pix, b, stride=s, padding=p)
+    np.testing.assert_array_equal(got, full.reshape(m, Cout)[pix])
+    with pytest.raises(ValueError):
+        orc.conv2d_nhwc_pixels(x, w, [m], b, stride=s, padding=p)
+
+
 def test_conv2d_sensitivity(orc):
     # a spatially flipped kernel (cross-correlation vs convolution) must fail
     x = RNG.normal(0, 1, (1, 2, 8, 8)).astype(np.float32)
