@@ -272,6 +272,25 @@ teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void 
                                        const teeny_conv2d_params *params, teeny_dtype dtype,
                                        teeny_layout layout, teeny_stream stream);
 
+/* conv2d_bias_forward with no allocation and no stream workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, results and plans as
+ * teeny_conv2d_bias_forward given a large enough stream workspace, except
+ * that the scratch of those plans (split-K partial sums, the space-to-depth
+ * copy of stride-2 convs over few channels) is a fixed 32 MiB device array
+ * inside the library, one per GPU, held until the process ends.  A shape
+ * whose plan needs more than 32 MiB of scratch is rejected with
+ * TEENY_ERR_UNSUPPORTED before anything is enqueued (every ResNet-50 layer at
+ * batch 64 needs at most 26 MiB).  Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (different streams, or other
+ * host threads) race on it, so serialize them.  Calls no hipMalloc/hipFree. */
+teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, const void *bias, void *y,
+                                               int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H,
+                                               int64_t W, int64_t OH, int64_t OW,
+                                               const teeny_conv2d_params *params, teeny_dtype dtype,
+                                               teeny_layout layout, teeny_stream stream);
+
 /* ── attention ────────────────────────────────────────────────────────────
  * O = softmax(Q K^T * softmax_scale) V per (batch*head), L = logsumexp of the
  * scaled scores (natural log).  Layout [BH, n_ctx, head_dim] row-major.

@@ -123,6 +123,7 @@ _SIGS = {
     "teeny_norm_act_forward": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, c_int32, c_int32, P]),
     "teeny_conv2d_forward": (S, [P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_conv2d_bias_forward": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
+    "teeny_conv2d_bias_forward_noalloc": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_flash_attention2_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
     "teeny_attention_forward": (S, [P, P, P, P, P] + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),
     "teeny_quant_num_groups": (S, [POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, POINTER(c_int64)]),

@@ -22,6 +22,8 @@
 //   (e.g. the 3-channel stem).  1x1 stride-1 unpadded convs are plain GEMMs.
 //   int8 weights (W8A16) are converted to bf16 while staging into LDS and
 //   the per-channel scale is applied to the fp32 accumulator.
+#include <mutex>
+
 #include "gemm_core.hpp"
 
 namespace teeny {
@@ -509,11 +511,10 @@ static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, v
 template <bool INT8B>
 static bool try_conv_mfma(const void *x, const void *w, const float *scale, const float *bias,
                           const bf16 *bias_bf16, void *y, const ConvGeo &q, int act,
-                          hipStream_t s) {
+                          hipStream_t s, const Scratch scr) {
   if (!aligned(x, 16) || !aligned(w, 16)) return false;
   const ConvPath path = conv_path<INT8B>(q);
   if (path == kConvNoMfma) return false;
-  const Scratch scr = stream_scratch(s);
   if (path == kConvS2D && conv_s2d_mfma(x, w, bias_bf16, y, q, act, s, scr)) return true;
   GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
   if (INT8B && (path == kConvPlain ? w8_dequant_pays<kAPlain>(p) : w8_dequant_pays<kAConvVec>(p)) &&
@@ -531,10 +532,13 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
   }
 }
 
+// `scratch_override` (non-null) replaces the stream's workspace as the
+// scratch the fast plans may use.
 static teeny_status conv_entry(const void *x, const void *w, const void *bias, void *y, int64_t B,
                                int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH,
                                int64_t OW, const teeny_conv2d_params *prm, teeny_dtype dtype,
-                               teeny_layout layout, teeny_stream stream, const char *name) {
+                               teeny_layout layout, teeny_stream stream, const char *name,
+                               const Scratch *scratch_override = nullptr) {
   ConvGeo q;
   teeny_status st = make_geo(B, Cin, Cout, H, W, OH, OW, prm, layout, &q, name);
   if (st != TEENY_OK) return st;
@@ -542,6 +546,7 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
   TEENY_REQUIRE(x != nullptr && w != nullptr && y != nullptr, TEENY_ERR_NULL_POINTER,
                 std::string(name) + ": x/w/y");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const Scratch scr = scratch_override != nullptr ? *scratch_override : stream_scratch(s);
   if (dtype == TEENY_F32) {
     if (!(layout == TEENY_NCHW &&
           try_conv_f32_mfma(static_cast<const float *>(x), static_cast<const float *>(w),
@@ -555,7 +560,7 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
   if (dtype == TEENY_BF16) {
     if (!(layout == TEENY_NHWC &&
           try_conv_mfma<false>(x, w, nullptr, nullptr, static_cast<const bf16 *>(bias), y, q,
-                               prm->act, s))) {
+                               prm->act, s, scr))) {
       launch_direct<bf16, bf16>(static_cast<const bf16 *>(x), static_cast<const bf16 *>(w),
                                 nullptr, static_cast<const bf16 *>(bias), nullptr,
                                 static_cast<bf16 *>(y), q, prm->act, s);
@@ -563,6 +568,33 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
     return after_launch(name, s);
   }
   return fail(TEENY_ERR_UNSUPPORTED_DTYPE, std::string(name) + ": dtype must be F32 or BF16");
+}
+
+// ── the no-allocation variant's scratch ─────────────────────────────────
+// A file-scope device array serves as the scratch of
+// teeny_conv2d_bias_forward_noalloc.  Each GPU that loads this library holds
+// its own copy (at its own address) until the process ends.  Its host-side
+// name is not a device address: the device address comes from
+// hipGetSymbolAddress, once per device on the entry point's first call there.
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+static std::mutex g_scratch_addr_mu;
+static void *g_scratch_addr[64];
+
+static teeny_status static_scratch(Scratch *out, const char *name) {
+  int dev = 0;
+  TEENY_CHECK_HIP(hipGetDevice(&dev));
+  TEENY_REQUIRE(dev >= 0 && dev < 64, TEENY_ERR_UNSUPPORTED, std::string(name) + ": device ordinal >= 64");
+  std::lock_guard<std::mutex> lock(g_scratch_addr_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void *ptr = nullptr;
+    TEENY_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    TEENY_REQUIRE(ptr != nullptr && aligned(ptr, 256), TEENY_ERR_HIP,
+                  std::string(name) + ": static scratch has no usable device address");
+    g_scratch_addr[dev] = ptr;
+  }
+  *out = Scratch{g_scratch_addr[dev], kStaticScratchBytes};
+  return TEENY_OK;
 }
 
 }  // namespace teeny
@@ -589,6 +621,31 @@ teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void 
                     "conv2d_bias_forward");
 }
 
+teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, const void *bias, void *y,
+                                               int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H,
+                                               int64_t W, int64_t OH, int64_t OW,
+                                               const teeny_conv2d_params *params, teeny_dtype dtype,
+                                               teeny_layout layout, teeny_stream stream) {
+  const char *name = "conv2d_bias_forward_noalloc";
+  ConvGeo q;
+  teeny_status st = make_geo(B, C_IN, C_OUT, H, W, OH, OW, params, layout, &q, name);
+  if (st != TEENY_OK) return st;
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                std::string(name) + ": dtype must be F32 or BF16");
+  if (B == 0) return TEENY_OK;
+  TEENY_REQUIRE(x != nullptr && w != nullptr && bias != nullptr && y != nullptr, TEENY_ERR_NULL_POINTER,
+                std::string(name) + ": x/w/bias/y");
+  const size_t need = (dtype == TEENY_BF16 && layout == TEENY_NHWC) ? conv_scratch_bytes<false>(q) : 0;
+  TEENY_REQUIRE(need <= kStaticScratchBytes, TEENY_ERR_UNSUPPORTED,
+                std::string(name) + ": this shape's plan needs " + std::to_string(need) +
+                    " bytes of scratch, more than the " + std::to_string(kStaticScratchBytes) +
+                    " bytes of static scratch; use conv2d_bias_forward with a stream workspace");
+  Scratch scr;
+  st = static_scratch(&scr, name);
+  if (st != TEENY_OK) return st;
+  return conv_entry(x, w, bias, y, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream, name, &scr);
+}
+
 teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, const float *scale,
                                         const float *bias, void *y, int64_t B, int64_t C_IN,
                                         int64_t C_OUT, int64_t H, int64_t W, int64_t OH,
@@ -602,7 +659,7 @@ teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, co
   TEENY_REQUIRE(x != nullptr && qweight != nullptr && scale != nullptr && y != nullptr,
                 TEENY_ERR_NULL_POINTER, "w8a16_conv2d_forward: x/qweight/scale/y");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (!try_conv_mfma<true>(x, qweight, scale, bias, nullptr, y, q, params->act, s)) {
+  if (!try_conv_mfma<true>(x, qweight, scale, bias, nullptr, y, q, params->act, s, stream_scratch(s))) {
     launch_direct<bf16, int8_t>(static_cast<const bf16 *>(x), qweight, scale, nullptr, bias,
                                 static_cast<bf16 *>(y), q, params->act, s);
   }
