@@ -1,24 +1,38 @@
 #!/usr/bin/env python3
 """Benchmark of the teeny-kernels hot path on one MI355X.
 
-Default workload (the norm + activation chain, bf16 in/out, fp32 stats):
-X[16384, 4096] ~ N(0,1); one step is
+The default run measures all five configurations and prints one JSON line.
+Its headline `value` is configuration 2, the norm + activation chain (bf16
+in/out, fp32 stats): X[16384, 4096] ~ N(0,1); one step is
     Y1 = LayerNorm(X)  (eps 1e-5, gamma ~ N(1, .02), beta ~ N(0, .02))
     G1 = GELU-tanh(Y1);  S1 = SiLU(Y1)
     Y2 = RMSNorm(X)    (eps 1e-8, gamma ~ N(1, .02))
     G2 = GELU-tanh(Y2);  S2 = SiLU(Y2)
-six HBM-bound kernels, each moving 2 x 128 MiB.  `value` is the step's
-algorithmic bytes / step time in GB/s.  Inputs are resident in HBM before
-the timed region; every kernel of the timed steps is bracketed by HIP events
-on the launch stream, which gives each kernel's average duration for the
-roofline object.
+six HBM-bound kernels, each moving 2 x 128 MiB; `value` is the step's
+algorithmic bytes / step time in GB/s.  The `configs` object carries one
+entry per configuration (1: conv2d+bias+ReLU fp32 NCHW; 2: the chain above;
+3: causal SDPA S=2048 and non-causal S=4096; 4: the 53 ResNet-50 convs at
+batch 64; 5: the two W8A16 GEMMs and the int8 3x3 conv), each with its own
+roofline object (dominant kernel) and CPU baseline.
 
-Other workloads (--workload): attention_causal_s2048, attention_s4096,
-resnet50_convs, w8a16_gemm, w8a16_conv, conv2d_f32 — TFLOP/s lines.
+Inputs are resident in HBM before any timed region.  Each workload runs W
+warmup steps eagerly, then K steps captured into one HIP graph, replayed once
+untimed and once between two HIP events on the launch stream (the step time).
+Then every op of the step is captured K times over into a graph of its own
+and timed the same way (its average launch duration, used by the roofline
+objects).  Graph replay keeps Python's launch overhead out of the GPU's
+timeline, as an executor's captured graph would.  Ops whose buffers would fit the 256 MB Infinity Cache
+cycle through 2-4 device copies of their operands, so that repeated launches
+read HBM rather than the previous launch's cached bytes.
 
-The cpu_baseline object times the CPU oracle (a C restatement of the
-reference kernels, oracle/) on the host, on the workload stated in its
-`sample` field.
+The CPU baselines time the oracle (oracle/, a C restatement of the reference
+kernels' program grids and loops, rebuilt here with -march=native) on this
+host's cores: median of 3 runs after one warm-up, on the full workload or on
+a stated prefix (>= 5 %) of its program ids, scaled linearly.
+
+--workload NAME runs one workload (for profiling); --op-markers launches an
+empty marker kernel before each op's own timed block, so that a rocprofv3
+run can be split per op.
 """
 from __future__ import annotations
 
@@ -37,7 +51,8 @@ sys.path.insert(0, ROOT)
 METRIC = "GB/s or TFLOP/s per op vs MI355X roofline; speedup vs host-CPU teenygrad path"
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
-FP32_PEAK_TFLOPS = 157.3     # fp32 vector
+FP32_PEAK_TFLOPS = 157.3     # fp32 (vector and matrix)
+CPU_PREFIX = 0.05            # minimum fraction of program ids in a sampled CPU baseline
 
 
 def log(msg):
@@ -55,72 +70,153 @@ def cpu_threads():
     return max(1, min(16, n))  # the GPU box's CPU share is 16 threads
 
 
-class Timer:
-    """Per-kernel HIP events on the launch stream.  Events are created before
-    the timed pass so that recording one costs only the enqueue."""
-
-    def __init__(self, tg, stream, kernels_per_step, steps):
-        self.stream = stream
-        self.pool = [tg.Event() for _ in range(2 * kernels_per_step * steps)]
-        self.used = 0
-        self.pairs = {}
-
-    def run(self, name, fn):
-        a, b = self.pool[self.used], self.pool[self.used + 1]
-        self.used += 2
-        a.record(self.stream)
-        fn()
-        b.record(self.stream)
-        self.pairs.setdefault(name, []).append((a, b))
-
-    def avg_ms(self):
-        return {k: float(np.mean([a.elapsed_ms(b) for a, b in v])) for k, v in self.pairs.items()}
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
-def timed_steps(tg, dev, stream, step, steps, warmup, kernels_per_step):
-    """Warmup, then two timed passes of `steps` steps each:
-    pass 1 (the reported step time) launches the kernels back to back between
-    two events; pass 2 brackets every kernel with its own event pair for the
-    per-kernel durations (the event markers add small gaps between kernels,
-    which is why pass 1 alone gives the step time)."""
-    for _ in range(warmup):
-        step(None)
-    dev.synchronize()
-    t0, t1 = tg.Event(), tg.Event()
-    t0.record(stream)
-    wall0 = time.perf_counter()
-    for _ in range(steps):
-        step(None)
-    t1.record(stream)
-    t1.synchronize()
-    wall = time.perf_counter() - wall0
-    ms = t0.elapsed_ms(t1) / steps
-    timer = Timer(tg, stream, kernels_per_step, steps)
-    dev.synchronize()
-    for _ in range(steps):
-        step(timer)
-    dev.synchronize()
-    return ms, wall, timer.avg_ms()
+class Ctx:
+    """What every workload needs: the package, device, stream and options."""
+
+    def __init__(self, args, tg, dev, stream):
+        self.args, self.tg, self.dev, self.stream = args, tg, dev, stream
+        self.marker = self._marker_kernel() if args.op_markers else None
+
+    def _marker_kernel(self):
+        """Marks op boundaries in a profiler's dispatch list with an empty
+        launch (n = 0) of the stand-alone example kernel, whose name no op
+        uses: one workgroup before each op's own block (its warm and timed
+        graph replays, 2 K launches), two after a workload's last block."""
+        import ctypes
+        lib = self.tg._lib.lib
+        mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+        self.tg.check(lib.teeny_hip_module_load(ctypes.byref(mod), self.tg._lib.EXAMPLE_MODULE_PATH.encode()))
+        self.tg.check(lib.teeny_hip_module_get_function(ctypes.byref(fn), mod, b"teeny_example_axpy"))
+        vals = (ctypes.c_float(0.0), ctypes.c_void_p(0), ctypes.c_void_p(0), ctypes.c_int32(0))
+        argv = (ctypes.c_void_p * 4)(*(ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in vals))
+        block = (ctypes.c_uint32 * 3)(64, 1, 1)
+        keep = (mod, fn, vals, argv, block)
+
+        def mark(blocks):
+            grid = (ctypes.c_uint32 * 3)(blocks, 1, 1)
+            self.tg.check(lib.teeny_hip_launch(keep[1], grid, block, 0, self.stream.handle, argv))
+        return mark
+
+    def copies(self, buf, n):
+        """`buf` and n-1 device copies of it (rotating operands)."""
+        out = [buf]
+        for _ in range(n - 1):
+            b = self.tg.Buffer(buf.dtype, buf.shape)
+            self.tg.check(self.tg._lib.lib.teeny_hip_memcpy_d2d(b.ptr, buf.ptr, buf.nbytes, self.stream.handle))
+            out.append(b)
+        self.stream.synchronize()
+        return out
+
+    def measure(self, ops):
+        """ops: [(name, [launch_0, launch_1, ...])], launch_r running the op on
+        rotation r.  Returns (step ms, {name: ms per launch of the op alone})."""
+        tg, dev, stream = self.tg, self.dev, self.stream
+        steps, warmup = self.args.steps, self.args.warmup
+        if self.marker is not None:
+            log(f"[bench] ops per step: {json.dumps([n for n, _ in ops])} steps={steps}")
+
+        def step(i):
+            for _, fns in ops:
+                fns[i % len(fns)]()
+
+        def replay_ms(enqueue, count):
+            """Captures `count` launches into one HIP graph, replays it once to
+            warm up, then times one replay: ms per launch, free of host
+            launch overhead (a 10-20 us kernel issued from Python otherwise
+            leaves the GPU idle between launches)."""
+            stream.begin_capture()
+            for i in range(count):
+                enqueue(i)
+            g = stream.end_capture()
+            g.launch(stream)
+            stream.synchronize()
+            t0.record(stream)
+            g.launch(stream)
+            t1.record(stream)
+            t1.synchronize()
+            g.destroy()
+            return t0.elapsed_ms(t1) / count
+
+        t0, t1 = tg.Event(), tg.Event()
+        for i in range(warmup):
+            step(i)
+        dev.synchronize()
+        ms = replay_ms(step, steps)
+        per = {}
+        for name, fns in ops:
+            if self.marker is not None:
+                self.marker(1)
+            per[name] = replay_ms(lambda i, fns=fns: fns[i % len(fns)](), steps)
+        if self.marker is not None:
+            self.marker(2)
+        dev.synchronize()
+        return ms, per
 
 
-def launch(timer, name, fn):
-    if timer is None:
-        fn()
-    else:
-        timer.run(name, fn)
-
-
-def load_traffic(workload):
-    """HBM bytes per launch of the dominant kernel from the committed rocprof
-    counter summary (profiles/<workload>_traffic.json), or None."""
+def load_traffic(workload, op):
+    """HBM bytes per launch of `op` (all its kernels) from the committed
+    rocprofv3 counter summary profiles/<workload>_traffic.json, or None."""
     p = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        ops = json.load(f).get("ops", {})
+    entry = ops.get(op)
+    return None if entry is None else entry.get("traffic_bytes_per_launch")
 
 
-# ── default: norm + activation chain ────────────────────────────────────────
+def roofline_bytes(workload, op, nbytes, avg_ms, per_op_bytes=None):
+    ach = nbytes / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": op, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload, op),
+            "algorithmic_bytes": nbytes, "avg_us": round(avg_ms * 1e3, 2)}
+
+
+def roofline_flops(workload, op, flops, avg_ms, peak, nbytes=None):
+    ach = flops / (avg_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": op, "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(ach / peak, 4), "traffic": load_traffic(workload, op), "algorithmic_bytes": nbytes,
+            "algorithmic_flop": flops, "avg_us": round(avg_ms * 1e3, 2)}
+
+
+def cpu_time(fn, runs=3):
+    """Median wall time of `runs` calls after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(runs):
+        c0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - c0)
+    return float(np.median(times))
+
+
+def cpu_entry(value, unit, seconds, sample, gpu_value, extra=None):
+    import oracle
+    d = {"value": value, "unit": unit, "cores": oracle.threads(), "kind": "port", "cpu": cpu_model(),
+         "build": oracle.BUILD_FLAGS, "seconds": round(seconds, 4), "sample": sample,
+         "speedup": round(gpu_value / value, 1) if value else None}
+    if extra:
+        d.update(extra)
+    return d
+
+
+def upload_bf16(ctx, a):
+    from teenygrad_amd.dtypes import to_bf16
+    return ctx.dev.upload(to_bf16(a), ctx.tg.bf16)
+
+
+# ── configuration 2: norm + activation chain ───────────────────────────────
 
 NORM_M, NORM_N = 16384, 4096
 
@@ -135,374 +231,370 @@ def norm_inputs():
     return x, g1, b1, g2
 
 
-def bench_norm_act(args, tg, dev, stream):
+def bench_norm_act(ctx):
     from teenygrad_amd import kernels as K
-    from teenygrad_amd.dtypes import to_bf16
+    tg, stream = ctx.tg, ctx.stream
     x, g1, b1, g2 = norm_inputs()
-    up = lambda a: dev.upload(to_bf16(a), tg.bf16)
-    xb, g1b, b1b, g2b = up(x), up(g1), up(b1), up(g2)
+    g1b, b1b, g2b = (upload_bf16(ctx, a) for a in (g1, b1, g2))
     shape = (NORM_M, NORM_N)
-    y1, gl, sl, y2, gr, sr = (tg.Buffer(tg.bf16, shape) for _ in range(6))
+    R = 4  # 4 x 128 MiB of X: a launch never finds its input in the Infinity Cache
+    xs = ctx.copies(upload_bf16(ctx, x), R)
+    y1, gl, sl, y2, gr, sr = ([tg.Buffer(tg.bf16, shape) for _ in range(R)] for _ in range(6))
     rrms = tg.Buffer(tg.f32, (NORM_M,))
-    elem = NORM_M * NORM_N
-    io = 2 * elem * 2  # read X + write Y, bf16
+    io = 2 * NORM_M * NORM_N * 2  # read X + write Y, bf16
     bytes_of = {"layer_norm": io + 2 * NORM_N * 2, "gelu(ln)": io, "silu(ln)": io,
                 "rms_norm": io + NORM_N * 2 + NORM_M * 4, "gelu(rms)": io, "silu(rms)": io}
-
-    def step(t):
-        launch(t, "layer_norm", lambda: K.layer_norm(xb, g1b, b1b, 1e-5, y=y1, stream=stream))
-        launch(t, "gelu(ln)", lambda: K.gelu(y1, y=gl, stream=stream))
-        launch(t, "silu(ln)", lambda: K.silu(y1, y=sl, stream=stream))
-        launch(t, "rms_norm", lambda: K.rms_norm(xb, g2b, 1e-8, y=y2, rrms=rrms, stream=stream))
-        launch(t, "gelu(rms)", lambda: K.gelu(y2, y=gr, stream=stream))
-        launch(t, "silu(rms)", lambda: K.silu(y2, y=sr, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 6)
+    ops = [("layer_norm", [lambda r=r: K.layer_norm(xs[r], g1b, b1b, 1e-5, y=y1[r], stream=stream) for r in range(R)]),
+           ("gelu(ln)", [lambda r=r: K.gelu(y1[r], y=gl[r], stream=stream) for r in range(R)]),
+           ("silu(ln)", [lambda r=r: K.silu(y1[r], y=sl[r], stream=stream) for r in range(R)]),
+           ("rms_norm", [lambda r=r: K.rms_norm(xs[r], g2b, 1e-8, y=y2[r], rrms=rrms, stream=stream)
+                         for r in range(R)]),
+           ("gelu(rms)", [lambda r=r: K.gelu(y2[r], y=gr[r], stream=stream) for r in range(R)]),
+           ("silu(rms)", [lambda r=r: K.silu(y2[r], y=sr[r], stream=stream) for r in range(R)])]
+    ms, per = ctx.measure(ops)
     step_bytes = sum(bytes_of.values())
     value = step_bytes / (ms * 1e-3) / 1e9
-    dom = max(per, key=per.get)
-    achieved = bytes_of[dom] / (per[dom] * 1e-3) / 1e9
-    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic("norm_act"), "algorithmic_bytes": bytes_of[dom],
-            "avg_us": round(per[dom] * 1e3, 2)}
-    ops = {k: {"us": round(v * 1e3, 2), "GB/s": round(bytes_of[k] / (v * 1e-3) / 1e9, 1),
-               "frac": round(bytes_of[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)} for k, v in per.items()}
-
+    # the roofline unit: LayerNorm, the op with the least headroom (two
+    # dependent reductions per row); the other five are in `ops`
+    roof = roofline_bytes("norm_act", "layer_norm", bytes_of["layer_norm"], per["layer_norm"])
+    opsd = {k: {"us": round(v * 1e3, 2), "GB/s": round(bytes_of[k] / (v * 1e-3) / 1e9, 1),
+                "frac": round(bytes_of[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "traffic": load_traffic("norm_act", k)} for k, v in per.items()}
     cpu = None
-    if not args.no_cpu:
+    if not ctx.args.no_cpu:
         import oracle
-        th = cpu_threads()
-        oracle.set_threads(th)
-        times = []
-        for _ in range(3):
-            c0 = time.perf_counter()
+
+        def run():
             ln = oracle.layer_norm(x, g1, b1, 1e-5)
             oracle.gelu(ln)
             oracle.silu(ln)
             rm, _ = oracle.rms_norm(x, g2, 1e-8)
             oracle.gelu(rm)
             oracle.silu(rm)
-            times.append(time.perf_counter() - c0)
-        cs = float(np.median(times))
-        cpu = {"value": round(step_bytes / cs / 1e9, 2), "unit": "GB/s", "cores": th, "kind": "port",
-               "seconds_per_step": round(cs, 3),
-               "sample": "the full step (6 ops on [16384, 4096]) in fp32 on the bf16-rounded "
-                         "inputs, median of 3 runs; bytes counted as bf16 like the GPU line"}
-    return {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4),
-        "dtype": "bf16", "scaling": "weak",
-        "config": {"workload": "norm_act_chain: X[16384,4096] bf16 -> LayerNorm -> GELU-tanh, SiLU; "
-                               "RMSNorm -> GELU-tanh, SiLU (fp32 stats)",
-                   "M": NORM_M, "N": NORM_N, "ops_per_step": 6, "bytes_per_step": step_bytes},
-        "roofline": roof, "cpu_baseline": cpu, "ops": ops, "wall_s": round(wall, 3),
-    }
+
+        cs = cpu_time(run)
+        cpu = cpu_entry(round(step_bytes / cs / 1e9, 2), "GB/s", cs,
+                        "the full step (6 ops on [16384, 4096]) in fp32 on the bf16-rounded inputs; bytes "
+                        "counted as bf16 like the GPU line", value)
+    return {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "norm_act_chain: X[16384,4096] bf16 -> LayerNorm -> GELU-tanh, SiLU; "
+                                   "RMSNorm -> GELU-tanh, SiLU (fp32 stats)",
+                       "M": NORM_M, "N": NORM_N, "ops_per_step": 6, "bytes_per_step": step_bytes},
+            "roofline": roof, "cpu_baseline": cpu, "ops": opsd}
 
 
-# ── attention ───────────────────────────────────────────────────────────────
-
-
-def bench_act_backward(args, tg, dev, stream):
+def bench_act_backward(ctx):
     """Activation gradients on the norm workload's shape: dy and the saved tensor in, dx out
     (relu takes the forward output, gelu/silu the forward input); 3 x 128 MiB per op."""
     from teenygrad_amd import kernels as K
     from teenygrad_amd import synthetic
-    from teenygrad_amd.dtypes import round_bf16, to_bf16
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
     x, _, _, _ = norm_inputs()
     dy = round_bf16(synthetic.normal(synthetic.workload_seed(1, 4), (NORM_M, NORM_N)))
     y = np.maximum(x, 0)
-    up = lambda a: dev.upload(to_bf16(a), tg.bf16)
-    xb, yb, dyb = up(x), up(y), up(dy)
+    R = 4
+    xb, yb, dyb = (ctx.copies(upload_bf16(ctx, a), R) for a in (x, y, dy))
     shape = (NORM_M, NORM_N)
-    dr, dg, ds = (tg.Buffer(tg.bf16, shape) for _ in range(3))
-    io = 3 * NORM_M * NORM_N * 2  # read dy + saved, write dx, bf16
+    dr, dg, ds = ([tg.Buffer(tg.bf16, shape) for _ in range(R)] for _ in range(3))
+    io = 3 * NORM_M * NORM_N * 2
     bytes_of = {"relu_backward": io, "gelu_backward": io, "silu_backward": io}
-
-    def step(t):
-        launch(t, "relu_backward", lambda: K.relu_backward(dyb, yb, dx=dr, stream=stream))
-        launch(t, "gelu_backward", lambda: K.gelu_backward(dyb, xb, dx=dg, stream=stream))
-        launch(t, "silu_backward", lambda: K.silu_backward(dyb, xb, dx=ds, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 3)
+    ops = [("relu_backward", [lambda r=r: K.relu_backward(dyb[r], yb[r], dx=dr[r], stream=stream) for r in range(R)]),
+           ("gelu_backward", [lambda r=r: K.gelu_backward(dyb[r], xb[r], dx=dg[r], stream=stream) for r in range(R)]),
+           ("silu_backward", [lambda r=r: K.silu_backward(dyb[r], xb[r], dx=ds[r], stream=stream) for r in range(R)])]
+    ms, per = ctx.measure(ops)
     step_bytes = sum(bytes_of.values())
-    dom = max(per, key=per.get)
-    achieved = bytes_of[dom] / (per[dom] * 1e-3) / 1e9
-    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic("act_backward"), "algorithmic_bytes": bytes_of[dom],
-            "avg_us": round(per[dom] * 1e3, 2)}
+    value = step_bytes / (ms * 1e-3) / 1e9
+    roof = roofline_bytes("act_backward", "gelu_backward", io, per["gelu_backward"])
     ops = {k: {"us": round(v * 1e3, 2), "GB/s": round(bytes_of[k] / (v * 1e-3) / 1e9, 1),
                "frac": round(bytes_of[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)} for k, v in per.items()}
     cpu = None
-    if not args.no_cpu:
+    if not ctx.args.no_cpu:
         import oracle
-        th = cpu_threads()
-        oracle.set_threads(th)
-        times = []
-        for _ in range(3):
-            c0 = time.perf_counter()
+
+        def run():
             oracle.relu_backward(dy, y)
             oracle.gelu_backward(dy, x)
             oracle.silu_backward(dy, x)
-            times.append(time.perf_counter() - c0)
-        cs = float(np.median(times))
-        cpu = {"value": round(step_bytes / cs / 1e9, 2), "unit": "GB/s", "cores": th, "kind": "port",
-               "seconds_per_step": round(cs, 3),
-               "sample": "the full step (3 gradients on [16384, 4096]) in fp32 on the bf16-rounded "
-                         "inputs, median of 3 runs; bytes counted as bf16 like the GPU line"}
-    return {
-        "metric": METRIC, "value": round(step_bytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
-        "ms_per_step": round(ms, 4), "dtype": "bf16", "scaling": "weak",
-        "config": {"workload": "activation gradients: dy, x|y [16384,4096] bf16 -> dx for "
-                               "ReLU, GELU-tanh, SiLU (fp32 math)",
-                   "M": NORM_M, "N": NORM_N, "ops_per_step": 3, "bytes_per_step": step_bytes},
-        "roofline": roof, "cpu_baseline": cpu, "ops": ops, "wall_s": round(wall, 3),
-    }
+
+        cs = cpu_time(run)
+        cpu = cpu_entry(round(step_bytes / cs / 1e9, 2), "GB/s", cs,
+                        "the full step (3 gradients on [16384, 4096]) in fp32 on the bf16-rounded inputs",
+                        value)
+    return {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "activation gradients: dy, x|y [16384,4096] bf16 -> dx for ReLU, GELU-tanh, "
+                                   "SiLU (fp32 math)", "bytes_per_step": step_bytes},
+            "roofline": roof, "cpu_baseline": cpu, "ops": ops}
 
 
-def bench_attention(args, tg, dev, stream, s, causal, idx):
+# ── configuration 3: attention ──────────────────────────────────────────────
+
+
+def bench_attention(ctx, s, causal):
     from teenygrad_amd import kernels as K
-    from teenygrad_amd.dtypes import to_bf16
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
     bh, d = 256, 128
-    rng = np.random.default_rng(0x7EE70000 + idx)
-    q, k, v = (dev.upload(to_bf16(rng.standard_normal((bh, s, d), dtype=np.float32)), tg.bf16)
-               for _ in range(3))
+    rng = np.random.default_rng(0x7EE70002)
+    host = [round_bf16(rng.standard_normal((bh, s, d), dtype=np.float32)) for _ in range(3)]
+    q, k, v = (upload_bf16(ctx, a) for a in host)
+    nh = math.ceil(CPU_PREFIX * bh)  # heads in the CPU baseline's prefix
+    host = [np.ascontiguousarray(a[:nh]) for a in host]
     o = tg.Buffer(tg.bf16, (bh, s, d))
     lse = tg.Buffer(tg.f32, (bh, s))
     flops = 4.0 * bh * s * s * d * (0.5 if causal else 1.0)
-    name = "flash_attention_bf16"
-
-    def step(t):
-        launch(t, name, lambda: K.flash_attention(q, k, v, None, causal, o=o, lse=lse, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 1)
-    tf = flops / (ms * 1e-3) / 1e12
-    ach = flops / (per[name] * 1e-3) / 1e12
+    name = f"flash_attention_bf16_{'causal_' if causal else ''}s{s}"
+    workload = f"attention_{'causal_' if causal else ''}s{s}"
+    # Q/K/V/O of 512 MiB (causal S=2048) or 1 GiB exceed the Infinity Cache: no rotation
+    ms, per = ctx.measure([(name, [lambda: K.flash_attention(q, k, v, None, causal, o=o, lse=lse, stream=stream)])])
+    value = flops / (ms * 1e-3) / 1e12
+    nbytes = 4 * bh * s * d * 2 + bh * s * 4
     cpu = None
-    if not args.no_cpu:
+    if not ctx.args.no_cpu:
         import oracle
-        th = cpu_threads()
-        oracle.set_threads(th)
-        # sample: every query row of the first (batch, head) pair — programs
-        # [0, S) of the oracle's (bh, row) grid; all heads cost the same, so the
-        # full workload is BH times the sample
-        qh = np.random.default_rng(1).standard_normal((1, s, d), dtype=np.float32)
-        c0 = time.perf_counter()
-        oracle.flash_attention(qh, qh, qh, None, causal)
-        cs = time.perf_counter() - c0
-        full = cs * bh
-        cpu = {"value": round(flops / full / 1e12, 5), "unit": "TFLOP/s", "cores": th, "kind": "port",
-               "sample": f"one (batch, head) of {bh}: all {s} query rows in the fp32 oracle, "
-                         f"{cs:.2f} s, scaled x{bh}", "extrapolated_seconds": round(full, 1)}
-    return {"metric": METRIC, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-            "dtype": "bf16", "scaling": "weak",
-            "config": {"workload": f"sdpa {'causal' if causal else 'non-causal'} bf16 B*H=256 S={s} D=128",
+        # prefix of the oracle's program grid (pid = bh * S + q_row): the first
+        # ceil(5% of BH) heads, all rows; every head costs the same
+        qh, kh, vh = host
+        cs = cpu_time(lambda: oracle.flash_attention(qh, kh, vh, None, causal))
+        frac = nh / bh
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: {nh} of {bh} (batch, head) pairs, all {s} query rows "
+                        f"({frac:.2%} of the grid), fp32; scaled x{bh / nh:.2f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": f"sdpa {'causal' if causal else 'non-causal'} bf16 B=8 H=32 S={s} D=128",
                        "flop_per_step": flops},
-            "roofline": {"bound": "mfma", "kernel": name, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
-                         "traffic": load_traffic(args.workload),
-                         "algorithmic_bytes": 4 * bh * s * d * 2 + bh * s * 4,
-                         "avg_us": round(per[name] * 1e3, 2)},
-            "cpu_baseline": cpu, "wall_s": round(wall, 3)}
+            "roofline": roofline_flops(workload, name, flops, per[name], BF16_PEAK_TFLOPS, nbytes),
+            "cpu_baseline": cpu}
 
 
-# ── ResNet-50 conv stack ────────────────────────────────────────────────────
+# ── configuration 4: ResNet-50 conv stack ───────────────────────────────────
 
 
-def resnet50_convs():
-    """(name, Cin, Cout, H_in, K, stride, pad, relu) for the 53 convs, batch 64, 224x224."""
-    layers = [("stem", 3, 64, 224, 7, 2, 3, True)]
-    cfg = [(64, 256, 3, 56), (128, 512, 4, 56), (256, 1024, 6, 28), (512, 2048, 3, 14)]
-    cin = 64
-    for li, (w, out, blocks, hin) in enumerate(cfg):
-        s = 1 if li == 0 else 2
-        for bi in range(blocks):
-            h = hin if bi == 0 else (hin // s)
-            stride = s if bi == 0 else 1
-            layers.append((f"l{li + 1}b{bi}c1", cin, w, h, 1, 1, 0, True))
-            layers.append((f"l{li + 1}b{bi}c2", w, w, h, 3, stride, 1, True))
-            h2 = h // stride
-            layers.append((f"l{li + 1}b{bi}c3", w, out, h2, 1, 1, 0, False))
-            if bi == 0:
-                layers.append((f"l{li + 1}b{bi}ds", cin, out, h, 1, stride, 0, False))
-            cin = out
-    return layers
-
-
-def attach_workspace(tg, dev, stream, sizes):
+def attach_workspace(ctx, sizes):
     """Gives the stream one caller-owned scratch buffer big enough for every
-    op of the workload (split-K partials, space-to-depth copies); returns
-    its size.  Allocated before timing, as an executor would."""
+    op of the workload (split-K partials, space-to-depth copies, dequantized
+    weights); returns its size.  Allocated before timing, as an executor
+    would."""
     need = max(list(sizes) + [0])
     if need > 0:
-        stream.set_workspace(dev.buffer(tg.i8, (need,)))
+        ctx.stream.set_workspace(ctx.dev.buffer(ctx.tg.i8, (need,)))
     return need
 
 
-def bench_resnet(args, tg, dev, stream):
+def bench_resnet(ctx):
     from teenygrad_amd import kernels as K
-    from teenygrad_amd.dtypes import to_bf16
+    from teenygrad_amd import synthetic
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
     B = 64
     rng = np.random.default_rng(0x7EE70003)
-    layers = resnet50_convs()
+    layers = synthetic.resnet50_convs()
     assert len(layers) == 53
-    bufs = []
+    bufs, host = [], []
     flops = 0.0
     total_bytes = 0
     for name, cin, cout, h, k, s, p, relu in layers:
         oh = (h + 2 * p - k) // s + 1
-        x = dev.upload(to_bf16(rng.random((B, h, h, cin), dtype=np.float32)), tg.bf16)
-        w = dev.upload(to_bf16((rng.standard_normal((cout, k, k, cin), dtype=np.float32)
-                                * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)), tg.bf16)
-        b = dev.upload(to_bf16(rng.normal(0, 0.01, cout).astype(np.float32)), tg.bf16)
+        x = round_bf16(rng.random((B, h, h, cin), dtype=np.float32))
+        w = round_bf16((rng.standard_normal((cout, k, k, cin), dtype=np.float32)
+                        * np.float32(np.sqrt(2.0 / (cin * k * k)))))
+        b = round_bf16(rng.normal(0, 0.01, cout).astype(np.float32))
         y = tg.Buffer(tg.bf16, (B, oh, oh, cout))
         f = 2.0 * B * oh * oh * cout * cin * k * k
+        nb = 2 * (B * h * h * cin + cout * k * k * cin + cout + B * oh * oh * cout)
         flops += f
-        total_bytes += 2 * (B * h * h * cin + cout * k * k * cin + cout + B * oh * oh * cout)
-        bufs.append((name, x, w, b, y, s, p, relu, f))
-    ws = attach_workspace(tg, dev, stream, (
+        total_bytes += nb
+        # two operand sets per layer, so the layer's own timed block reads HBM
+        xr, wr = ctx.copies(upload_bf16(ctx, x), 2), ctx.copies(upload_bf16(ctx, w), 2)
+        ys = [y, tg.Buffer(tg.bf16, (B, oh, oh, cout))]
+        bufs.append((name, xr, wr, upload_bf16(ctx, b), ys, s, p, relu, f, nb))
+        if not ctx.args.no_cpu:  # NCHW copies of the first images, for the oracle
+            xs = np.ascontiguousarray(np.transpose(x[:math.ceil(CPU_PREFIX * B)], (0, 3, 1, 2)))
+            host.append((xs, np.ascontiguousarray(np.transpose(w, (0, 3, 1, 2))), b, s, p, relu))
+        del x
+    ws = attach_workspace(ctx, (
         K.conv2d_workspace_size((B, h, h, cin), (cout, k, k, cin), s, p, 1, tg.bf16, "nhwc")
         for name, cin, cout, h, k, s, p, relu in layers))
-    log(f"[bench] stream workspace {ws / 2**20:.1f} MiB")
+    log(f"[bench] resnet50 stream workspace {ws / 2**20:.1f} MiB")
 
-    def step(t):
-        for name, x, w, b, y, s, p, relu, _ in bufs:
-            launch(t, name, lambda: K.conv2d(x, w, b, s, p, 1, "relu" if relu else None, "nhwc", y=y,
-                                             stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, len(bufs))
-    tf = flops / (ms * 1e-3) / 1e12
+    ops = [(name, [lambda r=r, x=x, w=w, b=b, y=y, s=s, p=p, relu=relu:
+                   K.conv2d(x[r], w[r], b, s, p, 1, "relu" if relu else None, "nhwc", y=y[r], stream=stream)
+                   for r in range(2)])
+           for name, x, w, b, y, s, p, relu, _, _ in bufs]
+    ms, per = ctx.measure(ops)
+    value = flops / (ms * 1e-3) / 1e12
     by_layer = {}
     for bb in bufs:
-        n, f = bb[0], bb[-1]
+        n, f = bb[0], bb[8]
         by_layer[n] = {"us": round(per[n] * 1e3, 1), "TFLOP/s": round(f / (per[n] * 1e-3) / 1e12, 1)}
     dom = max(per, key=per.get)
-    fdom = [bb[-1] for bb in bufs if bb[0] == dom][0]
-    ach = fdom / (per[dom] * 1e-3) / 1e12
-    return {"metric": METRIC, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-            "dtype": "bf16", "scaling": "weak",
+    fdom, bdom = [(bb[8], bb[9]) for bb in bufs if bb[0] == dom][0]
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        nimg = host[0][0].shape[0]
+
+        def run():
+            for x, w, b, s, p, relu in host:
+                y = oracle.conv2d_nchw(x, w, b, s, p)
+                if relu:
+                    oracle.relu(y)
+
+        cs = cpu_time(run)
+        frac = nimg / B
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: the first {nimg} of {B} images of every layer ({frac:.2%} of each "
+                        f"conv grid; programs are image-major), conv+bias and ReLU in fp32 NCHW; scaled "
+                        f"x{B / nimg:.0f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
             "config": {"workload": "resnet50 53 convs bf16 NHWC batch 64 224x224, BN folded to bias, ReLU fused",
-                       "flop_per_step": flops, "bytes_per_step": total_bytes},
-            "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None},
-            "layers": by_layer, "cpu_baseline": None, "wall_s": round(wall, 3)}
+                       "flop_per_step": flops, "bytes_per_step": total_bytes, "workspace_bytes": ws},
+            "roofline": roofline_flops("resnet50_convs", dom, fdom, per[dom], BF16_PEAK_TFLOPS, bdom),
+            "layers": by_layer, "cpu_baseline": cpu}
 
 
-# ── W8A16 ───────────────────────────────────────────────────────────────────
+# ── configuration 5: W8A16 ──────────────────────────────────────────────────
 
 
-def bench_w8a16(args, tg, dev, stream):
+def bench_w8a16(ctx):
     from teenygrad_amd import kernels as K
-    from teenygrad_amd.dtypes import to_bf16
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
     m = 4096
     rng = np.random.default_rng(0x7EE70005)
-    problems = []
+    problems, host = [], []
     for k, n in ((4096, 11008), (11008, 4096)):
-        x = dev.upload(to_bf16(rng.standard_normal((m, k), dtype=np.float32)), tg.bf16)
-        wf = dev.upload(rng.normal(0, 0.02, (n, k)).astype(np.float32))
-        q, s, _, _ = K.quantize_affine(wf, [n, k], "channel", 0)
-        del wf
+        x = round_bf16(rng.standard_normal((m, k), dtype=np.float32))
+        wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+        q, s, _, _ = K.quantize_affine(ctx.dev.upload(wf), [n, k], "channel", 0)
         y = tg.Buffer(tg.bf16, (m, n))
-        problems.append((f"w8a16 {m}x{k}->{n}", x, q, s, y, 2 * m * k + n * k + 4 * n + 2 * m * n, 2.0 * m * n * k))
-    attach_workspace(tg, dev, stream, (K.linear_workspace_size(m, n, k, tg.i8)
-                                       for k, n in ((4096, 11008), (11008, 4096))))
+        name = f"w8a16 {m}x{k}->{n}"
+        problems.append((name, ctx.copies(upload_bf16(ctx, x), 2), ctx.copies(q, 2), s, [y, tg.Buffer(tg.bf16, (m, n))],
+                         2 * m * k + n * k + 4 * n + 2 * m * n, 2.0 * m * n * k))
+        if not ctx.args.no_cpu:
+            host.append((x[:math.ceil(CPU_PREFIX * m)].copy(), q.to_host().reshape(n, k), s.to_host()))
+    attach_workspace(ctx, (K.linear_workspace_size(m, n, k, tg.i8) for k, n in ((4096, 11008), (11008, 4096))))
 
-    def step(t):
-        for name, x, q, s, y, _, _ in problems:
-            launch(t, name, lambda: K.w8a16_linear(x, q, s, y=y, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, len(problems))
+    ops = [(name, [lambda r=r, x=x, q=q, s=s, y=y: K.w8a16_linear(x[r], q[r], s, y=y[r], stream=stream)
+                   for r in range(2)])
+           for name, x, q, s, y, _, _ in problems]
+    ms, per = ctx.measure(ops)
     flops = sum(p[-1] for p in problems)
-    tf = flops / (ms * 1e-3) / 1e12
-    ops = {p[0]: {"us": round(per[p[0]] * 1e3, 1), "TFLOP/s": round(p[-1] / (per[p[0]] * 1e-3) / 1e12, 1)}
-           for p in problems}
+    value = flops / (ms * 1e-3) / 1e12
+    ops = {p[0]: {"us": round(per[p[0]] * 1e3, 1), "TFLOP/s": round(p[-1] / (per[p[0]] * 1e-3) / 1e12, 1),
+                  "traffic": load_traffic("w8a16_gemm", p[0]), "algorithmic_bytes": p[-2]} for p in problems}
     dom = max(per, key=per.get)
-    fdom = [p[-1] for p in problems if p[0] == dom][0]
-    dom_bytes = [p[-2] for p in problems if p[0] == dom][0]  # x bf16 + int8 q + fp32 scales + y bf16
-    ach = fdom / (per[dom] * 1e-3) / 1e12
-    return {"metric": METRIC, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-            "dtype": "bf16", "scaling": "weak",
-            "config": {"workload": "w8a16 GEMMs M=4096: K=4096->N=11008 and K=11008->N=4096, int8 per-channel weights",
-                       "flop_per_step": flops},
-            "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
-                         "traffic": load_traffic(args.workload), "algorithmic_bytes": dom_bytes},
-            "ops": ops, "cpu_baseline": None, "wall_s": round(wall, 3)}
+    fdom, bdom = [(p[-1], p[-2]) for p in problems if p[0] == dom][0]
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        rows = math.ceil(CPU_PREFIX * m)
+        deq = [(x, oracle.dequantize_affine(q, s, None, q.shape, "channel", 0)) for x, q, s in host]
+        cs = cpu_time(lambda: [oracle.linear(x, w) for x, w in deq])
+        frac = rows / m
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: output rows 0..{rows - 1} of {m} of both GEMMs ({frac:.2%}; one "
+                        f"program per row), fp32 on dequantize_affine's weights; scaled x{m / rows:.2f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "w8a16 GEMMs M=4096: K=4096->N=11008 and K=11008->N=4096, int8 per-channel "
+                                   "weights", "flop_per_step": flops},
+            "roofline": roofline_flops("w8a16_gemm", dom, fdom, per[dom], BF16_PEAK_TFLOPS, bdom),
+            "ops": ops, "cpu_baseline": cpu}
 
 
-def bench_w8a16_conv(args, tg, dev, stream):
+def bench_w8a16_conv(ctx):
     from teenygrad_amd import kernels as K
-    from teenygrad_amd.dtypes import to_bf16
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
     B, C, H = 32, 256, 28
     rng = np.random.default_rng(0x7EE70006)
-    x = dev.upload(to_bf16(rng.standard_normal((B, H, H, C), dtype=np.float32)), tg.bf16)
-    wf = dev.upload(rng.normal(0, 0.02, (C, 3, 3, C)).astype(np.float32))
-    q, s, _, _ = K.quantize_affine(wf, [C, 3, 3, C], "channel", 0)
-    y = tg.Buffer(tg.bf16, (B, H, H, C))
+    xh = round_bf16(rng.standard_normal((B, H, H, C), dtype=np.float32))
+    R = 4  # 4 x 26 MB of operands per launch set
+    x = ctx.copies(upload_bf16(ctx, xh), R)
+    wf = rng.normal(0, 0.02, (C, 3, 3, C)).astype(np.float32)
+    q, s, _, _ = K.quantize_affine(ctx.dev.upload(wf), [C, 3, 3, C], "channel", 0)
+    qs = ctx.copies(q, R)
+    y = [tg.Buffer(tg.bf16, (B, H, H, C)) for _ in range(R)]
     flops = 2.0 * B * H * H * C * C * 9
+    nbytes = 2 * B * H * H * C * 2 + C * 9 * C + 4 * C
     name = "w8a16_conv3x3"
-    attach_workspace(tg, dev, stream, [K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)])
-
-    def step(t):
-        launch(t, name, lambda: K.w8a16_conv2d(x, q, s, None, 1, 1, y=y, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 1)
-    ach = flops / (per[name] * 1e-3) / 1e12
-    return {"metric": METRIC, "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
-            "ms_per_step": round(ms, 4), "dtype": "bf16", "scaling": "weak",
+    attach_workspace(ctx, [K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)])
+    ms, per = ctx.measure([(name, [lambda r=r: K.w8a16_conv2d(x[r], qs[r], s, None, 1, 1, y=y[r], stream=stream)
+                                   for r in range(R)])])
+    value = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        nimg = math.ceil(CPU_PREFIX * B)
+        wd = oracle.dequantize_affine(q.to_host().reshape(-1), s.to_host(), None, [C, 3, 3, C], "channel", 0)
+        xs, ws = np.transpose(xh[:nimg], (0, 3, 1, 2)), np.transpose(wd, (0, 3, 1, 2))
+        cs = cpu_time(lambda: oracle.conv2d_nchw(xs, ws, None, 1, 1))
+        frac = nimg / B
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: the first {nimg} of {B} images ({frac:.2%}), fp32 on "
+                        f"dequantize_affine's weights; scaled x{B / nimg:.0f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
             "config": {"workload": "w8a16 conv3x3 NHWC 32x256x28x28 -> 256, p1", "flop_per_step": flops},
-            "roofline": {"bound": "mfma", "kernel": name, "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None},
-            "cpu_baseline": None, "wall_s": round(wall, 3)}
+            "roofline": roofline_flops("w8a16_conv", name, flops, per[name], BF16_PEAK_TFLOPS, nbytes),
+            "cpu_baseline": cpu}
 
 
-def bench_conv_f32(args, tg, dev, stream):
+# ── configuration 1: the reference's own fp32 conv ──────────────────────────
+
+
+def bench_conv_f32(ctx):
     from teenygrad_amd import kernels as K
+    tg, stream = ctx.tg, ctx.stream
     rng = np.random.default_rng(0x7EE70000)
     x = rng.standard_normal((1, 64, 56, 56), dtype=np.float32)
     w = (rng.standard_normal((64, 64, 3, 3), dtype=np.float32) * np.sqrt(2.0 / 576)).astype(np.float32)
     b = (rng.standard_normal(64, dtype=np.float32) * 0.01).astype(np.float32)
-    xb, wb, bb = dev.upload(x), dev.upload(w), dev.upload(b)
+    xb, wb, bb = ctx.dev.upload(x), ctx.dev.upload(w), ctx.dev.upload(b)
     y = tg.Buffer(tg.f32, (1, 64, 56, 56))
     flops = 2.0 * 64 * 56 * 56 * 64 * 9
+    nbytes = 4 * (64 * 56 * 56 * 2 + 64 * 64 * 9 + 64)
     name = "conv2d_bias_relu_f32"
 
-    def step(t):
-        launch(t, name, lambda: K.conv2d(xb, wb, bb, 1, 1, 1, "relu", y=y, stream=stream))
-
-    ms, wall, per = timed_steps(tg, dev, stream, step, args.steps, args.warmup, 1)
-    ach = flops / (per[name] * 1e-3) / 1e12
+    # 1.75 MB of operands: L2-resident whatever the rotation (a latency-bound op)
+    ms, per = ctx.measure([(name, [lambda: K.conv2d(xb, wb, bb, 1, 1, 1, "relu", y=y, stream=stream)])])
+    value = flops / (ms * 1e-3) / 1e12
     cpu = None
-    if not args.no_cpu:
+    if not ctx.args.no_cpu:
         import oracle
-        th = cpu_threads()
-        oracle.set_threads(th)
-        times = []
-        for _ in range(3):
-            c0 = time.perf_counter()
-            oracle.relu(oracle.conv2d_nchw(x, w, b, padding=1))
-            times.append(time.perf_counter() - c0)
-        cs = float(np.median(times))
-        cpu = {"value": round(flops / cs / 1e12, 4), "unit": "TFLOP/s", "cores": th, "kind": "port",
-               "sample": "the full conv (+bias) and ReLU, median of 3"}
-    return {"metric": METRIC, "value": round(flops / (ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-            "ms_per_step": round(ms, 4), "dtype": "f32", "scaling": "weak",
+        cs = cpu_time(lambda: oracle.relu(oracle.conv2d_nchw(x, w, b, padding=1)))
+        cpu = cpu_entry(round(flops / cs / 1e12, 5), "TFLOP/s", cs,
+                        "the full conv (+bias) and ReLU, the reference's two kernels", value)
+    return {"value": round(value, 3), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "f32",
             "config": {"workload": "conv2d+bias+relu fp32 NCHW 1x64x56x56 -> 64, 3x3 s1 p1", "flop_per_step": flops},
-            "roofline": {"bound": "mfma", "kernel": name, "achieved": round(ach, 3), "peak": FP32_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ach / FP32_PEAK_TFLOPS, 4), "traffic": None},
-            "cpu_baseline": cpu, "wall_s": round(wall, 3)}
+            "roofline": roofline_flops("conv2d_f32", name, flops, per[name], FP32_PEAK_TFLOPS, nbytes),
+            "cpu_baseline": cpu}
 
 
 WORKLOADS = {
+    "conv2d_f32": bench_conv_f32,
     "norm_act": bench_norm_act,
-    "act_backward": bench_act_backward,
-    "attention_causal_s2048": lambda a, tg, d, s: bench_attention(a, tg, d, s, 2048, True, 2),
-    "attention_s4096": lambda a, tg, d, s: bench_attention(a, tg, d, s, 4096, False, 2),
+    "attention_causal_s2048": lambda c: bench_attention(c, 2048, True),
+    "attention_s4096": lambda c: bench_attention(c, 4096, False),
     "resnet50_convs": bench_resnet,
     "w8a16_gemm": bench_w8a16,
     "w8a16_conv": bench_w8a16_conv,
-    "conv2d_f32": bench_conv_f32,
+    "act_backward": bench_act_backward,
 }
+# the default run: every configuration, in configuration order
+CONFIGS = [("cfg1", "conv2d_f32"), ("cfg2", "norm_act"), ("cfg3a", "attention_causal_s2048"),
+           ("cfg3b", "attention_s4096"), ("cfg4", "resnet50_convs"), ("cfg5a", "w8a16_gemm"),
+           ("cfg5b", "w8a16_conv")]
 
 
 def main():
@@ -510,33 +602,55 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="norm_act", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
+    ap.add_argument("--op-markers", action="store_true",
+                    help="an empty marker launch after every op (splits a rocprofv3 run per op)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="first run one device-to-device copy of BYTES (a reference kernel of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: the hot path has no multi-GPU component in this build "
-              f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested); "
+              f"run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import teenygrad_amd as tg
 
     dev = tg.open(int(os.environ.get("LOCAL_RANK", "0")))
     stream = tg.Stream.create()
+    ctx = Ctx(args, tg, dev, stream)
     log(f"[bench] {args.workload} steps={args.steps} warmup={args.warmup} on {dev.info()['arch']}")
+    if not args.no_cpu:
+        import oracle
+        flags = oracle.use_native_build()
+        oracle.set_threads(cpu_threads())
+        log(f"[bench] cpu baseline: oracle {flags}, {oracle.threads()} threads, {cpu_model()}")
     if args.copy_calibration:
         src, dst = tg.Buffer(tg.i8, (args.copy_calibration,)), tg.Buffer(tg.i8, (args.copy_calibration,))
         src.zero_(stream)
         tg.check(tg._lib.lib.teeny_hip_memcpy_d2d(dst.ptr, src.ptr, args.copy_calibration, stream.handle))
         stream.synchronize()
         del src, dst
-    res = WORKLOADS[args.workload](args, tg, dev, stream)
-    line = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
+    t_start = time.perf_counter()
+    if args.workload == "all":
+        configs = {}
+        for key, name in CONFIGS:
+            c0 = time.perf_counter()
+            r = WORKLOADS[name](ctx)
+            r["workload_name"] = name
+            configs[key] = r
+            log(f"[bench] {key} {name}: {r['value']} {r['unit']} (frac {r['roofline']['frac']}) "
+                f"in {time.perf_counter() - c0:.1f} s")
+        res = dict(configs["cfg2"])
+        res["configs"] = configs
+    else:
+        res = WORKLOADS[args.workload](ctx)
+    line = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": res.pop("ms_per_step"),
-            "higher_is_better": True, "scaling": res.pop("scaling"), "vs_baseline": None,
-            "dtype": res.pop("dtype"), "data": "synthetic (seeded N(0,1) inputs, random-init params)"}
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res.pop("dtype"),
+            "data": "synthetic (seeded N(0,1) / U(0,1) inputs, random-init params)"}
     line.update(res)
+    line["wall_s"] = round(time.perf_counter() - t_start, 1)
     print(json.dumps(line), flush=True)
 
 

@@ -97,6 +97,7 @@ typedef void *teeny_stream;   /* hipStream_t */
 typedef void *teeny_event;    /* hipEvent_t */
 typedef void *teeny_module;   /* hipModule_t */
 typedef void *teeny_function; /* hipFunction_t */
+typedef void *teeny_graph;    /* hipGraphExec_t */
 
 /* Message for the last failure on the calling thread ("" if none). */
 const char *teeny_hip_last_error(void);
@@ -166,6 +167,20 @@ teeny_status teeny_hip_event_destroy(teeny_event event);
 teeny_status teeny_hip_event_record(teeny_event event, teeny_stream stream);
 teeny_status teeny_hip_event_sync(teeny_event event);
 teeny_status teeny_hip_event_elapsed_ms(float *ms, teeny_event start, teeny_event stop);
+
+/* Graph capture of a stream's work: everything enqueued on `stream` between
+ * begin and end (operators, raw launches, device-to-device copies) is
+ * recorded instead of run, and end instantiates it as one executable graph
+ * that teeny_hip_graph_launch replays with a single submission.  Operators
+ * keep their buffers and plans from capture time.  Reference: the CUDA-graph
+ * executor, cuStreamBeginCapture_v2 / cuStreamEndCapture /
+ * cuGraphInstantiateWithFlags / cuGraphLaunch in LoadedModel::capture_graph
+ * and CudaGraphModel::run (drivers/teeny-cuda/src/model/mod.rs:1245-1640,
+ * :1693-1797).  The null stream cannot be captured. */
+teeny_status teeny_hip_stream_begin_capture(teeny_stream stream);
+teeny_status teeny_hip_stream_end_capture(teeny_stream stream, teeny_graph *graph);
+teeny_status teeny_hip_graph_launch(teeny_graph graph, teeny_stream stream);
+teeny_status teeny_hip_graph_destroy(teeny_graph graph);
 
 /* ── code objects and raw launch ──────────────────────────────────────────
  * Reference: CudaProgram::try_from_ptx (cuModuleLoadDataEx) and
@@ -406,6 +421,67 @@ teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, co
 teeny_status teeny_conv2d_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
                                          int64_t OH, int64_t OW, const teeny_conv2d_params *params,
                                          teeny_dtype dtype, teeny_layout layout, size_t *bytes);
+
+/* ── compressed-tensors int8 checkpoints ──────────────────────────────────
+ * Reference: teeny-quant's checkpoint convention, utilities/teeny-quant/src/
+ * format.rs:16-35 (foo.weight I8 in the tensor's shape, foo.weight_scale F32
+ * per group, foo.weight_zero_point I32 for asymmetric schemes), the
+ * quantization_config JSON in the safetensors __metadata__ (:52-126) and
+ * its reader dequantize_tensor (:249-289).  A checkpoint is opened read-only
+ * (memory-mapped) and its whole header is validated on open: every offset,
+ * shape and dtype is checked against the file before any tensor is touched,
+ * so a malformed file fails with TEENY_ERR_INVALID_ARGUMENT.  Handles are
+ * not thread-safe for concurrent close. */
+typedef void *teeny_checkpoint;
+
+typedef struct teeny_tensor_info {
+  char name[256];
+  char dtype[16];       /* safetensors dtype name: "I8", "F32", "BF16", ... */
+  int32_t ndim;
+  int32_t pad_;
+  int64_t shape[8];
+  uint64_t nbytes;
+} teeny_tensor_info;
+
+typedef struct teeny_quant_scheme {
+  int32_t present;      /* 0: the file has no quantization_config */
+  int32_t num_bits;
+  int32_t symmetric;
+  int32_t granularity;  /* teeny_granularity of "strategy", -1 if unknown */
+  int64_t axis;         /* -1 when absent */
+  int64_t group_size;   /* 0 when absent */
+  int32_t n_config_groups;
+  char quant_method[64];
+  char format[64];      /* "int-quantized", "pack-quantized", "float-quantized" */
+  char type[16];        /* "int" or "float" */
+} teeny_quant_scheme;
+
+teeny_status teeny_checkpoint_open(const char *path, teeny_checkpoint *ckpt);
+/* The same over a caller-owned in-memory image, which must outlive the handle. */
+teeny_status teeny_checkpoint_open_image(const void *data, size_t size, teeny_checkpoint *ckpt);
+teeny_status teeny_checkpoint_close(teeny_checkpoint ckpt);
+teeny_status teeny_checkpoint_num_tensors(teeny_checkpoint ckpt, int64_t *n);
+teeny_status teeny_checkpoint_tensor_info(teeny_checkpoint ckpt, int64_t index, teeny_tensor_info *info);
+/* Index of tensor `name`; TEENY_ERR_NOT_FOUND if absent. */
+teeny_status teeny_checkpoint_find(teeny_checkpoint ckpt, const char *name, int64_t *index);
+teeny_status teeny_checkpoint_quant_scheme(teeny_checkpoint ckpt, teeny_quant_scheme *scheme);
+/* Copies tensor `index`'s raw little-endian bytes (exactly its nbytes) to
+ * host memory (to_device = 0) or device memory (1, completed before return). */
+teeny_status teeny_checkpoint_read(teeny_checkpoint ckpt, int64_t index, void *dst, size_t bytes,
+                                   int32_t to_device, teeny_stream stream);
+/* W8A16 operands of layer `weight_name` ("foo.weight"): requires an 8-bit
+ * symmetric int-quantized compressed-tensors scheme with per-output-channel
+ * (axis 0) or per-tensor scales, foo.weight I8 of rank >= 2 (flattened to
+ * [N, K] with N its first dimension) and foo.weight_scale F32 with N (or 1)
+ * entries.  Other schemes are TEENY_ERR_UNSUPPORTED (read the tensors and use
+ * teeny_dequantize_affine).  _shape reports N and K; _load copies the int8
+ * weights to qweight [N, K] and N fp32 scales (a per-tensor scale repeated)
+ * to scale, both device buffers, ready for teeny_w8a16_linear_forward
+ * (conv weights [C_OUT, KH, KW, C_IN] for teeny_w8a16_conv2d_forward). */
+teeny_status teeny_checkpoint_w8a16_shape(teeny_checkpoint ckpt, const char *weight_name, int64_t *N,
+                                          int64_t *K);
+teeny_status teeny_checkpoint_load_w8a16(teeny_checkpoint ckpt, const char *weight_name, int8_t *qweight,
+                                         float *scale, int64_t N, int64_t K, teeny_stream stream);
 
 /* ── reference-shaped dispatch ────────────────────────────────────────────
  * Runs an operator from exactly the argument list that the reference's

@@ -28,10 +28,10 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
-def _load() -> ctypes.CDLL:
-    if not os.path.exists(LIB_PATH):
+def _load(path: str = LIB_PATH) -> ctypes.CDLL:
+    if path == LIB_PATH and not os.path.exists(LIB_PATH):
         build()
-    lib = ctypes.CDLL(LIB_PATH)
+    lib = ctypes.CDLL(path)
     P = c_void_p
     I = c_int64
     sigs = {
@@ -62,6 +62,27 @@ def _load() -> ctypes.CDLL:
 
 
 lib = _load()
+BUILD_FLAGS = "-O3 -march=x86-64-v3 -ffp-contract=off (prebuilt)"
+
+
+def use_native_build() -> str:
+    """Recompiles the oracle for this host (-O3 -march=native, otherwise the
+    same flags as oracle/Makefile) in a temporary directory and routes every
+    function of this module to it; returns the flags in use.  For timing the
+    CPU baseline on the host that runs it; if the compiler is missing or fails,
+    the prebuilt library stays in use."""
+    global lib, BUILD_FLAGS
+    import tempfile
+    out = os.path.join(tempfile.mkdtemp(prefix="teeny_oracle_"), "libteeny_oracle_native.so")
+    cmd = ["gcc", "-O3", "-std=c11", "-fPIC", "-march=native", "-ffp-contract=off", "-pthread", "-shared",
+           os.path.join(HERE, "teeny_oracle.c"), "-o", out, "-lm"]
+    try:
+        subprocess.run(cmd, check=True, capture_output=True, timeout=120)
+        lib = _load(out)
+        BUILD_FLAGS = "-O3 -march=native -ffp-contract=off"
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return BUILD_FLAGS
 
 
 class OracleError(RuntimeError):

@@ -9,10 +9,10 @@ contract.  Importing it without the built library raises ImportError.
 from . import _lib, dtypes, kernels, runtime, synthetic
 from ._lib import TeenyError, check
 from .dtypes import bf16, f32, from_bf16, i8, round_bf16, to_bf16
-from .runtime import Buffer, Device, Event, Stream, device_count, open
+from .runtime import Buffer, Device, Event, Graph, Stream, device_count, open
 
 __all__ = [
-    "Buffer", "Device", "Event", "Stream", "TeenyError", "bf16", "check", "device_count",
+    "Buffer", "Device", "Event", "Graph", "Stream", "TeenyError", "bf16", "check", "device_count",
     "dtypes", "f32", "from_bf16", "i8", "kernels", "open", "round_bf16", "runtime",
     "synthetic", "to_bf16",
 ]

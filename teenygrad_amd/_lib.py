@@ -71,6 +71,18 @@ class Conv2dParams(ctypes.Structure):
     ]
 
 
+class TensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("dtype", ctypes.c_char * 16), ("ndim", c_int32),
+                ("pad_", c_int32), ("shape", c_int64 * 8), ("nbytes", ctypes.c_uint64)]
+
+
+class QuantScheme(ctypes.Structure):
+    _fields_ = [("present", c_int32), ("num_bits", c_int32), ("symmetric", c_int32),
+                ("granularity", c_int32), ("axis", c_int64), ("group_size", c_int64),
+                ("n_config_groups", c_int32), ("quant_method", ctypes.c_char * 64),
+                ("format", ctypes.c_char * 64), ("type", ctypes.c_char * 16)]
+
+
 class _ArgValue(ctypes.Union):
     _fields_ = [("ptr", c_void_p), ("i32", c_int32), ("i64", c_int64), ("f32", c_float),
                 ("f64", ctypes.c_double), ("u32", c_uint32), ("b", c_int32)]
@@ -102,6 +114,10 @@ _SIGS = {
     "teeny_hip_stream_destroy": (S, [P]),
     "teeny_hip_stream_sync": (S, [P]),
     "teeny_hip_stream_set_workspace": (S, [P, P, c_size_t]),
+    "teeny_hip_stream_begin_capture": (S, [P]),
+    "teeny_hip_stream_end_capture": (S, [P, POINTER(c_void_p)]),
+    "teeny_hip_graph_launch": (S, [P, P]),
+    "teeny_hip_graph_destroy": (S, [P]),
     "teeny_hip_event_create": (S, [POINTER(c_void_p)]),
     "teeny_hip_event_destroy": (S, [P]),
     "teeny_hip_event_record": (S, [P, P]),
@@ -134,6 +150,16 @@ _SIGS = {
     "teeny_linear_workspace_size": (S, [c_int64, c_int64, c_int64, c_int32, POINTER(c_size_t)]),
     "teeny_conv2d_workspace_size": (S, [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, POINTER(c_size_t)]),
     "teeny_w8a16_conv2d_forward": (S, [P, P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), P]),
+    "teeny_checkpoint_open": (S, [c_char_p, POINTER(c_void_p)]),
+    "teeny_checkpoint_open_image": (S, [P, c_size_t, POINTER(c_void_p)]),
+    "teeny_checkpoint_close": (S, [P]),
+    "teeny_checkpoint_num_tensors": (S, [P, POINTER(c_int64)]),
+    "teeny_checkpoint_tensor_info": (S, [P, c_int64, POINTER(TensorInfo)]),
+    "teeny_checkpoint_find": (S, [P, c_char_p, POINTER(c_int64)]),
+    "teeny_checkpoint_quant_scheme": (S, [P, POINTER(QuantScheme)]),
+    "teeny_checkpoint_read": (S, [P, c_int64, P, c_size_t, c_int32, P]),
+    "teeny_checkpoint_w8a16_shape": (S, [P, c_char_p, POINTER(c_int64), POINTER(c_int64)]),
+    "teeny_checkpoint_load_w8a16": (S, [P, c_char_p, P, P, c_int64, c_int64, P]),
     "teeny_dispatch": (S, [c_char_p, POINTER(c_int64), c_int32, POINTER(TeenyArg), c_int32, POINTER(c_uint32), c_int32, P]),
 }
 

@@ -78,10 +78,13 @@ __device__ __forceinline__ float act_relu(float x) { return x < 0.0f ? 0.0f : x;
 template <bool FAST> __device__ __forceinline__ float act_gelu(float x) {
   const float neg2c = -1.5957691216057308f;  // -2 * sqrt(2/pi)
   const float coeff = 0.044715f;
-  float inner = x + coeff * x * x * x;
   if constexpr (FAST) {
-    return x * __builtin_amdgcn_rcpf(1.0f + __expf(neg2c * inner));
+    // exp(-2c (x + a x^3)) = exp2(x (k1 + k3 x^2)) with the constants folded:
+    // k1 = -2c log2(e), k3 = a k1 (one v_exp_f32, no separate cube or scaling)
+    const float k1 = -2.302208198144325f, k3 = -0.1029432395800235f;
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * __builtin_fmaf(k3, x * x, k1)));
   } else {
+    float inner = x + coeff * x * x * x;
     return x / (1.0f + expf(neg2c * inner));
   }
 }

@@ -47,6 +47,10 @@ teeny_status after_launch(const char *what, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, what);
   if (sync_after_launch()) {
+    // a stream being captured into a graph records work instead of running it
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream != nullptr && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return TEENY_OK;
     e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return hip_fail(e, what);
   }
@@ -283,6 +287,40 @@ teeny_status teeny_hip_event_elapsed_ms(float *ms, teeny_event start, teeny_even
                 "ms/start/stop");
   TEENY_CHECK_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
                                       static_cast<hipEvent_t>(stop)));
+  return TEENY_OK;
+}
+
+teeny_status teeny_hip_stream_begin_capture(teeny_stream stream) {
+  TEENY_REQUIRE(stream != nullptr, TEENY_ERR_INVALID_ARGUMENT,
+                "stream_begin_capture: the null stream cannot be captured");
+  TEENY_CHECK_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+  return TEENY_OK;
+}
+
+teeny_status teeny_hip_stream_end_capture(teeny_stream stream, teeny_graph *graph) {
+  TEENY_REQUIRE(stream != nullptr && graph != nullptr, TEENY_ERR_NULL_POINTER, "stream_end_capture: stream/graph");
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  TEENY_CHECK_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph = exec;
+  return TEENY_OK;
+}
+
+teeny_status teeny_hip_graph_launch(teeny_graph graph, teeny_stream stream) {
+  TEENY_REQUIRE(graph != nullptr, TEENY_ERR_NULL_POINTER, "graph_launch: graph");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TEENY_CHECK_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), s));
+  if (sync_after_launch()) TEENY_CHECK_HIP(hipStreamSynchronize(s));
+  return TEENY_OK;
+}
+
+teeny_status teeny_hip_graph_destroy(teeny_graph graph) {
+  if (graph == nullptr) return TEENY_OK;
+  TEENY_CHECK_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
   return TEENY_OK;
 }
 

@@ -17,8 +17,9 @@
 // ((p*VPL + j)*64 + l)*VEC, so each load instruction is one contiguous 1 KiB
 // request.  For N = 4096 bf16 this is 4 waves per row and 2 vectors per lane:
 // about 40 VGPRs, 8 waves per SIMD, which keeps enough 16-byte loads in
-// flight to stream at the chip's copy rate; gamma/beta are read after the
-// reduction (L2-resident, 8 KiB).  Outputs use non-temporal stores.  Longer
+// flight to stream at the chip's copy rate; gamma/beta (L2-resident, 8 KiB)
+// are loaded right after x, ahead of the reductions.  Outputs use
+// non-temporal stores.  Longer
 // rows, unaligned pointers or N % VEC != 0 take a multi-pass kernel with the
 // reference's pass structure.
 #include "common.hpp"
@@ -52,6 +53,15 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     const int col = ((part * VPL + j) * 64 + lane) * VEC;
     valid[j] = row_ok && col < N;
     raw[j] = valid[j] ? *reinterpret_cast<const u32x4 *>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // gamma / beta are issued right behind x, so their (L2) latency overlaps
+  // the row's reductions instead of following them
+  u32x4 rg[VPL], rbt[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int col = ((part * VPL + j) * 64 + lane) * VEC;
+    rg[j] = valid[j] ? *reinterpret_cast<const u32x4 *>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (!RMS) rbt[j] = valid[j] ? *reinterpret_cast<const u32x4 *>(beta + col) : u32x4{0u, 0u, 0u, 0u};
   }
   float v[VPL][VEC];
 #pragma unroll
@@ -110,12 +120,8 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     if (!valid[j]) continue;
     const int col = ((part * VPL + j) * 64 + lane) * VEC;
     T ge[VEC], be[VEC];
-    u32x4 rg = *reinterpret_cast<const u32x4 *>(gamma + col);
-    __builtin_memcpy(ge, &rg, 16);
-    if constexpr (!RMS) {
-      u32x4 rb = *reinterpret_cast<const u32x4 *>(beta + col);
-      __builtin_memcpy(be, &rb, 16);
-    }
+    __builtin_memcpy(ge, &rg[j], 16);
+    if constexpr (!RMS) __builtin_memcpy(be, &rbt[j], 16);
     T e[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {

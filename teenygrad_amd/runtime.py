@@ -18,7 +18,7 @@ from . import _lib
 from ._lib import check, lib
 from .dtypes import DType, from_any
 
-__all__ = ["open", "Device", "Buffer", "Stream", "Event", "device_count"]
+__all__ = ["open", "Device", "Buffer", "Stream", "Event", "Graph", "device_count"]
 
 
 def device_count() -> int:
@@ -53,6 +53,15 @@ class Stream:
             check(lib.teeny_hip_stream_set_workspace(self.handle, buf.ptr, buf.nbytes))
         self._workspace = buf
 
+    def begin_capture(self) -> None:
+        """Record the work enqueued on this stream until end_capture()."""
+        check(lib.teeny_hip_stream_begin_capture(self.handle))
+
+    def end_capture(self) -> "Graph":
+        g = ctypes.c_void_p()
+        check(lib.teeny_hip_stream_end_capture(self.handle, ctypes.byref(g)))
+        return Graph(g.value)
+
     def destroy(self) -> None:
         if self._owned and self.handle:
             check(lib.teeny_hip_stream_destroy(self.handle))
@@ -71,6 +80,27 @@ NULL_STREAM = Stream(None)
 
 def _h(stream: Optional[Stream]):
     return None if stream is None else stream.handle
+
+
+class Graph:
+    """An instantiated HIP graph from Stream.begin_capture()/end_capture()."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    def launch(self, stream: Optional["Stream"] = None) -> None:
+        check(lib.teeny_hip_graph_launch(self.handle, _h(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(lib.teeny_hip_graph_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class Event:

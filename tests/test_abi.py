@@ -322,3 +322,12 @@ def test_attention_forward_errors():
     expect(f(FAKE, FAKE, FAKE, FAKE, None, 2, 4, 2, 16, 16, 96, 0.125, 1, _lib.BF16, None), _lib.ERR_UNSUPPORTED)
     expect(f(FAKE_ODD, FAKE, FAKE, FAKE, None, 2, 4, 2, 16, 16, 64, 0.125, 1, _lib.BF16, None), _lib.ERR_MISALIGNED)
     assert f(None, None, None, None, None, 0, 4, 2, 16, 16, 64, 0.125, 1, _lib.BF16, None) == _lib.OK
+
+
+def test_graph_capture_errors():
+    g = ctypes.c_void_p()
+    expect(lib.teeny_hip_stream_begin_capture(None), _lib.ERR_INVALID_ARGUMENT)
+    expect(lib.teeny_hip_stream_end_capture(None, ctypes.byref(g)), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_stream_end_capture(FAKE, None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_hip_graph_launch(None, None), _lib.ERR_NULL_POINTER)
+    assert lib.teeny_hip_graph_destroy(None) == _lib.OK
