@@ -248,6 +248,43 @@ teeny_status teeny_rms_norm_forward(const void *x, void *y, const void *weight, 
                                     int64_t M, int64_t N, float eps, teeny_dtype dtype,
                                     teeny_stream stream);
 
+/* LayerNorm training forward: the inference result plus the per-row
+ * statistics the backward pass reads, mean[m] and rstd[m] =
+ * rsqrt(var + eps) (fp32 for every dtype).  Reference: layer_norm_forward(x,
+ * y, weight, bias, mean, rstd, M, N, eps), layernorm.rs:162-298. */
+teeny_status teeny_layer_norm_forward(const void *x, void *y, const void *weight, const void *bias,
+                                      float *mean, float *rstd, int64_t M, int64_t N, float eps,
+                                      teeny_dtype dtype, teeny_stream stream);
+
+/* LayerNorm backward.  Reference: layer_norm_backward(dy, x, dx, weight,
+ * dweight, dbias, mean, rstd, M, N), layernorm.rs:300-482:
+ *   xhat = (x - mean) * rstd, c1 = sum_n(dy * weight) / N,
+ *   c2 = sum_n(dy * weight * xhat) / N,
+ *   dx = rstd * weight * (dy - c1 - xhat * c2)       (the reference's formula,
+ *        which is the gradient of the forward when weight == 1),
+ *   dweight[n] += sum_m dy * xhat, dbias[n] += sum_m dy  (accumulated into
+ *        the existing values, deterministically).
+ * dy, x, dx, weight share `dtype` (F32 or BF16); mean, rstd, dweight, dbias
+ * are fp32; dweight and/or dbias may be NULL to skip them.  With a stream
+ * workspace of teeny_norm_backward_workspace_size bytes the parameter
+ * gradients come from per-workgroup partials; without it from a second pass
+ * over x and dy. */
+teeny_status teeny_layer_norm_backward(const void *dy, const void *x, void *dx, const void *weight,
+                                       float *dweight, float *dbias, const float *mean, const float *rstd,
+                                       int64_t M, int64_t N, teeny_dtype dtype, teeny_stream stream);
+
+/* RMSNorm backward.  Reference: rms_norm_backward(dy, x, dx, weight, dweight,
+ * rrms, M, N), rmsnorm.rs:135-277:
+ *   s = sum_n(dy * weight * x) / N, dx = rrms * weight * (dy - x * rrms^2 * s),
+ *   dweight[n] += sum_m dy * x * rrms.   Types and workspace as above. */
+teeny_status teeny_rms_norm_backward(const void *dy, const void *x, void *dx, const void *weight, float *dweight,
+                                     const float *rrms, int64_t M, int64_t N, teeny_dtype dtype,
+                                     teeny_stream stream);
+
+/* Stream workspace that lets the norm backward ops take their fastest plan. */
+teeny_status teeny_norm_backward_workspace_size(int64_t M, int64_t N, int32_t is_rms, teeny_dtype dtype,
+                                                size_t *bytes);
+
 /* Fused norm + activation: one pass computing act(norm(x)).  No reference
  * counterpart as a single kernel: it is the composition of the two kernels
  * above with the activation kernels (the Anduin pointwise-fusion idea,
@@ -305,6 +342,37 @@ teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, con
                                                int64_t W, int64_t OH, int64_t OW,
                                                const teeny_conv2d_params *params, teeny_dtype dtype,
                                                teeny_layout layout, teeny_stream stream);
+
+/* conv2d backward.  Reference: conv2d_backward_dx(dy, w, dx, B, C_IN, C_OUT,
+ * H, W, OH, OW), conv2d_backward_dw(dy, x, dw, ...) and the combined
+ * conv2d_backward(dy, x, w, dx, dw, ...) with conv2d_forward's const
+ * generics, conv2d.rs:171-521 (the Conv2d RuntimeOp's backward kernel,
+ * :575-617):
+ *   dx[b,ci,ih,iw] = sum dy[b,co,oh,ow] * w[co,ci_local,kh,kw] over the
+ *                    (co, kh, kw) with oh*SH - PH + kh = ih, ow*SW - PW + kw = iw
+ *   dw[co,ci_local,kh,kw] = sum over (b, oh, ow) of dy * x at those positions.
+ * The reference atomically adds into zero-initialised dx/dw; these write the
+ * sums (same values for zero-initialised buffers, fixed summation order).
+ * Any dtype (F32, BF16), layout, stride, padding and groups; dy has y's
+ * layout, dw the weight layout of `layout`.  bf16 NHWC dx with groups == 1
+ * runs on the MFMA implicit GEMM given a stream workspace of
+ * teeny_conv2d_backward_workspace_size bytes (flipped weights and, for a
+ * strided conv, dy spread to the stride). */
+teeny_status teeny_conv2d_backward_dx(const void *dy, const void *w, void *dx, int64_t B, int64_t C_IN,
+                                      int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                      const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                      teeny_stream stream);
+teeny_status teeny_conv2d_backward_dw(const void *dy, const void *x, void *dw, int64_t B, int64_t C_IN,
+                                      int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                      const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                      teeny_stream stream);
+teeny_status teeny_conv2d_backward(const void *dy, const void *x, const void *w, void *dx, void *dw, int64_t B,
+                                   int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                   const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                   teeny_stream stream);
+teeny_status teeny_conv2d_backward_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                                  int64_t OH, int64_t OW, const teeny_conv2d_params *params,
+                                                  teeny_dtype dtype, teeny_layout layout, size_t *bytes);
 
 /* ── attention ────────────────────────────────────────────────────────────
  * O = softmax(Q K^T * softmax_scale) V per (batch*head), L = logsumexp of the

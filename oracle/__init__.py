@@ -50,6 +50,12 @@ def _load(path: str = LIB_PATH) -> ctypes.CDLL:
         "oracle_flash_attention2_forward": [P, P, P, P, P, I, I, I, I, c_float, c_int, I, I],
         "oracle_flash_attention2_rows": [P, P, P, P, P, I, I, I, I, c_float, c_int, P, I],
         "oracle_linear_forward": [P, P, P, P] + [I] * 9 + [I, I],
+        "oracle_layer_norm_forward": [P, P, P, P, P, P, I, I, c_float, I, I, I],
+        "oracle_layer_norm_backward": [P, P, P, P, P, P, P, P, I, I, I],
+        "oracle_rms_norm_backward": [P, P, P, P, P, P, I, I, I],
+        "oracle_conv2d_backward_dx": [P, P, P] + [I] * 14,
+        "oracle_conv2d_backward_dw": [P, P, P] + [I] * 15,
+        "oracle_flash_attention2_backward": [P] * 9 + [I, I, I, I, c_float, c_int],
         "oracle_quant_num_groups": [P, c_int, c_int, c_int, I, POINTER(c_int64)],
         "oracle_quantize_affine": [P, I, P, c_int, c_int, c_int, I, c_int, c_int, P, P, P, P],
         "oracle_dequantize_affine": [P, P, P, P, c_int, c_int, c_int, I, P],
@@ -283,6 +289,90 @@ def linear(x, w, b=None, pid_begin=0, pid_end=-1):
     _chk(lib.oracle_linear_forward(_p(x), _p(w), _p(b), _p(y), M, N, K, K, 1, K, 1, N, 1, pid_begin,
                                    pid_end), "linear")
     return y
+
+
+# ── training: saved statistics and backward kernels ─────────────────────────
+
+
+def layer_norm_train(x, weight, bias, eps=1e-5, block_n=1024):
+    """layernorm.rs:162-298: (y, mean [M], rstd [M])."""
+    x = _f32(x)
+    w, b = _f32(weight), _f32(bias)
+    n = x.shape[-1]
+    m = x.size // n
+    y = np.zeros_like(x)
+    mean = np.zeros(m, np.float32)
+    rstd = np.zeros(m, np.float32)
+    _chk(lib.oracle_layer_norm_forward(_p(x), _p(y), _p(w), _p(b), _p(mean), _p(rstd), m, n, eps, block_n, 0, -1),
+         "layer_norm_train")
+    return y, mean, rstd
+
+
+def layer_norm_backward(dy, x, weight, mean, rstd, dweight=None, dbias=None, block_n=1024):
+    """layernorm.rs:300-482: (dx, dweight, dbias); dweight/dbias accumulate
+    into the given arrays (zeros when None), rows in order."""
+    dy, x, w = _f32(dy), _f32(x), _f32(weight)
+    n = x.shape[-1]
+    m = x.size // n
+    dx = np.zeros_like(x)
+    dw = np.zeros(n, np.float32) if dweight is None else _f32(dweight).copy()
+    db = np.zeros(n, np.float32) if dbias is None else _f32(dbias).copy()
+    _chk(lib.oracle_layer_norm_backward(_p(dy), _p(x), _p(dx), _p(w), _p(dw), _p(db), _p(_f32(mean)),
+                                        _p(_f32(rstd)), m, n, block_n), "layer_norm_backward")
+    return dx, dw, db
+
+
+def rms_norm_backward(dy, x, weight, rrms, dweight=None, block_n=1024):
+    """rmsnorm.rs:135-277: (dx, dweight), dweight accumulated as above."""
+    dy, x, w = _f32(dy), _f32(x), _f32(weight)
+    n = x.shape[-1]
+    m = x.size // n
+    dx = np.zeros_like(x)
+    dw = np.zeros(n, np.float32) if dweight is None else _f32(dweight).copy()
+    _chk(lib.oracle_rms_norm_backward(_p(dy), _p(x), _p(dx), _p(w), _p(dw), _p(_f32(rrms)), m, n, block_n),
+         "rms_norm_backward")
+    return dx, dw
+
+
+def _conv_geo(x_shape, w_shape, stride, padding):
+    sh, sw = (stride, stride) if isinstance(stride, int) else stride
+    ph, pw = (padding, padding) if isinstance(padding, int) else padding
+    B, Cin, H, W = x_shape
+    Cout, _, KH, KW = w_shape
+    return B, Cin, Cout, H, W, (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1, KH, KW, sh, sw, ph, pw
+
+
+def conv2d_backward_dx(dy, w, x_shape, stride=(1, 1), padding=(0, 0), groups=1):
+    """conv2d.rs:171-284, NCHW: dx [B, Cin, H, W]."""
+    dy, w = _f32(dy), _f32(w)
+    B, Cin, Cout, H, W, OH, OW, KH, KW, sh, sw, ph, pw = _conv_geo(x_shape, w.shape, stride, padding)
+    dx = np.zeros(tuple(x_shape), np.float32)
+    _chk(lib.oracle_conv2d_backward_dx(_p(dy), _p(w), _p(dx), B, Cin, Cout, H, W, OH, OW, KH, KW, sh, sw, ph, pw,
+                                       groups), "conv2d_backward_dx")
+    return dx
+
+
+def conv2d_backward_dw(dy, x, w_shape, stride=(1, 1), padding=(0, 0), groups=1, block_ow=16):
+    """conv2d.rs:286-397, NCHW: dw [Cout, Cin/G, KH, KW]."""
+    dy, x = _f32(dy), _f32(x)
+    B, Cin, Cout, H, W, OH, OW, KH, KW, sh, sw, ph, pw = _conv_geo(x.shape, w_shape, stride, padding)
+    dw = np.zeros(tuple(w_shape), np.float32)
+    _chk(lib.oracle_conv2d_backward_dw(_p(dy), _p(x), _p(dw), B, Cin, Cout, H, W, OH, OW, KH, KW, sh, sw, ph, pw,
+                                       groups, block_ow), "conv2d_backward_dw")
+    return dw
+
+
+def flash_attention_backward(q, k, v, o, do, l, softmax_scale=None, causal=False):
+    """flash_attn2.rs:173-447: (dq, dk, dv) for [BH, N, D] tensors, L the
+    forward's logsumexp [BH, Nq]."""
+    q, k, v, o, do, l = (_f32(a) for a in (q, k, v, o, do, l))
+    BH, nq, D = q.shape
+    nk = k.shape[1]
+    scale = 1.0 / np.sqrt(D) if softmax_scale is None else softmax_scale
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    _chk(lib.oracle_flash_attention2_backward(_p(q), _p(k), _p(v), _p(o), _p(do), _p(l), _p(dq), _p(dk), _p(dv),
+                                              BH, nq, nk, D, scale, int(causal)), "flash_attention_backward")
+    return dq, dk, dv
 
 
 # ── teeny-quant (affine.rs:47-161, groups.rs:20-100) ───────────────────────

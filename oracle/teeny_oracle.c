@@ -675,3 +675,327 @@ int oracle_dequantize_affine(const int8_t *q, const float *scales, const int32_t
   }
   return OK;
 }
+
+/* ══ training: norm forward with saved statistics, and the backward kernels ══ */
+
+/* ── LayerNorm training forward ──────────────────────────────────────────
+ * layernorm.rs:162-298 (layer_norm_forward): the inference kernel's three
+ * passes, plus mean[row] and rstd[row] stored for the backward pass. */
+
+typedef struct {
+  const float *x, *w, *b;
+  float *y, *mean, *rstd;
+  int64_t N, block;
+  float eps;
+} lnf_ctx;
+
+static void layernorm_train_program(const void *c, int64_t row) {
+  const lnf_ctx *a = (const lnf_ctx *)c;
+  const float *x = a->x + row * a->N;
+  float *y = a->y + row * a->N;
+  const int64_t N = a->N, B = a->block;
+  float *tile = (float *)malloc(sizeof(float) * (size_t)B);
+  float sum = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    sum = sum + tile_sum(x + s, m);
+  }
+  const float n_inv = 1.0f / (float)N;
+  const float mean = sum * n_inv;
+  float var_sum = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    for (int64_t i = 0; i < m; ++i) {
+      float d = x[s + i] - mean;
+      tile[i] = d * d;
+    }
+    var_sum = var_sum + tile_sum(tile, m);
+  }
+  const float rstd = 1.0f / sqrtf(var_sum * n_inv + a->eps);
+  a->mean[row] = mean; /* layernorm.rs:229-230 */
+  a->rstd[row] = rstd;
+  for (int64_t i = 0; i < N; ++i) y[i] = (x[i] - mean) * rstd * a->w[i] + a->b[i];
+  free(tile);
+}
+
+int oracle_layer_norm_forward(const float *x, float *y, const float *w, const float *b, float *mean,
+                              float *rstd, int64_t M, int64_t N, float eps, int64_t block_n, int64_t pb,
+                              int64_t pe) {
+  if (M < 0 || N <= 0 || block_n <= 0) return ERR_SHAPE_MISMATCH;
+  lnf_ctx a = {x, w, b, y, mean, rstd, N, block_n, eps};
+  launch(layernorm_train_program, &a, M, pb, pe);
+  return OK;
+}
+
+/* ── LayerNorm backward ──────────────────────────────────────────────────
+ * layernorm.rs:300-482 (layer_norm_backward): program = row.
+ *   pass 1: sum_dy_gamma = sum dy*gamma, sum_dy_gamma_xhat = sum dy*gamma*xhat
+ *           (BLOCK_N tiles, tile sums accumulated), c1 = sum_dy_gamma / N,
+ *           c2 = sum_dy_gamma_xhat / N, xhat = (x - mean) * rstd;
+ *   pass 2: dx = rstd * gamma * (dy - c1 - xhat * c2),
+ *           dweight[n] = dweight[n] + dy * xhat, dbias[n] = dbias[n] + dy.
+ * The reference updates dweight/dbias by a load-add-store per program; here
+ * the programs compute dx in parallel and the parameter gradients are then
+ * accumulated in program (row) order, the order a one-program-at-a-time
+ * launch gives. */
+
+typedef struct {
+  const float *dy, *x, *w, *mean, *rstd;
+  float *dx;
+  int64_t N, block;
+} lnb_ctx;
+
+static void layernorm_bwd_program(const void *c, int64_t row) {
+  const lnb_ctx *a = (const lnb_ctx *)c;
+  const int64_t N = a->N, B = a->block;
+  const float *x = a->x + row * N, *dy = a->dy + row * N;
+  float *dx = a->dx + row * N;
+  const float mean = a->mean[row], rstd = a->rstd[row];
+  const float n_inv = 1.0f / (float)N;
+  float *t1 = (float *)malloc(sizeof(float) * (size_t)B);
+  float *t2 = (float *)malloc(sizeof(float) * (size_t)B);
+  float s1 = 0.0f, s2 = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    for (int64_t i = 0; i < m; ++i) {
+      const float xhat = (x[s + i] - mean) * rstd;
+      t1[i] = dy[s + i] * a->w[s + i];
+      t2[i] = dy[s + i] * a->w[s + i] * xhat;
+    }
+    s1 = s1 + tile_sum(t1, m);
+    s2 = s2 + tile_sum(t2, m);
+  }
+  const float c1 = s1 * n_inv, c2 = s2 * n_inv;
+  for (int64_t i = 0; i < N; ++i) {
+    const float xhat = (x[i] - mean) * rstd;
+    dx[i] = rstd * a->w[i] * (dy[i] - c1 - xhat * c2);
+  }
+  free(t1);
+  free(t2);
+}
+
+int oracle_layer_norm_backward(const float *dy, const float *x, float *dx, const float *w, float *dweight,
+                               float *dbias, const float *mean, const float *rstd, int64_t M, int64_t N,
+                               int64_t block_n) {
+  if (M < 0 || N <= 0 || block_n <= 0) return ERR_SHAPE_MISMATCH;
+  lnb_ctx a = {dy, x, w, mean, rstd, dx, N, block_n};
+  launch(layernorm_bwd_program, &a, M, 0, -1);
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      const float xhat = (x[m * N + n] - mean[m]) * rstd[m];
+      if (dweight != NULL) dweight[n] = dweight[n] + dy[m * N + n] * xhat;
+      if (dbias != NULL) dbias[n] = dbias[n] + dy[m * N + n];
+    }
+  return OK;
+}
+
+/* ── RMSNorm backward ────────────────────────────────────────────────────
+ * rmsnorm.rs:135-277 (rms_norm_backward): program = row.
+ *   pass 1: dot = sum dy*gamma*x; scale = dot / N;
+ *   pass 2: dx = rrms * gamma * (dy - x * rrms^2 * scale),
+ *           dweight[n] = dweight[n] + dy * x * rrms  (row order, as above). */
+
+typedef struct {
+  const float *dy, *x, *w, *rrms;
+  float *dx;
+  int64_t N, block;
+} rmsb_ctx;
+
+static void rmsnorm_bwd_program(const void *c, int64_t row) {
+  const rmsb_ctx *a = (const rmsb_ctx *)c;
+  const int64_t N = a->N, B = a->block;
+  const float *x = a->x + row * N, *dy = a->dy + row * N;
+  float *dx = a->dx + row * N;
+  const float r = a->rrms[row];
+  float *t = (float *)malloc(sizeof(float) * (size_t)B);
+  float dot = 0.0f;
+  for (int64_t s = 0; s < N; s += B) {
+    int64_t m = N - s < B ? N - s : B;
+    for (int64_t i = 0; i < m; ++i) t[i] = dy[s + i] * a->w[s + i] * x[s + i];
+    dot = dot + tile_sum(t, m);
+  }
+  const float rsq = r * r;
+  const float scale = dot * (1.0f / (float)N);
+  for (int64_t i = 0; i < N; ++i) dx[i] = r * a->w[i] * (dy[i] - x[i] * rsq * scale);
+  free(t);
+}
+
+int oracle_rms_norm_backward(const float *dy, const float *x, float *dx, const float *w, float *dweight,
+                             const float *rrms, int64_t M, int64_t N, int64_t block_n) {
+  if (M < 0 || N <= 0 || block_n <= 0) return ERR_SHAPE_MISMATCH;
+  rmsb_ctx a = {dy, x, w, rrms, dx, N, block_n};
+  launch(rmsnorm_bwd_program, &a, M, 0, -1);
+  if (dweight != NULL)
+    for (int64_t m = 0; m < M; ++m)
+      for (int64_t n = 0; n < N; ++n) dweight[n] = dweight[n] + dy[m * N + n] * x[m * N + n] * rrms[m];
+  return OK;
+}
+
+/* ── conv2d backward ─────────────────────────────────────────────────────
+ * conv2d.rs:171-284 (conv2d_backward_dx) scatters dy[b,co,oh,ow] * w into
+ * dx[b, ci, oh*SH - PH + kh, ow*SW - PW + kw] with atomic adds (summation
+ * order set by the atomics); :286-397 (conv2d_backward_dw) adds, per
+ * program (b, co, oh, ow-tile) and tap, the tile sum of dy * x into
+ * dw[co, ci_local, kh, kw].  Restated deterministically: dx as a gather per
+ * input element, taps in (co, kh, kw) order; dw as the reference's
+ * per-program tile sums added in program order (b, oh, ow-tile).  Both
+ * compute exactly the reference's sums of products, in a fixed order. */
+
+typedef struct {
+  const float *dy, *w, *x;
+  float *out;
+  int64_t B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow;
+} convb_ctx;
+
+static void conv_dx_program(const void *c, int64_t pid) {
+  /* pid = (b * Cin + ci) * H + ih: one input row */
+  const convb_ctx *a = (const convb_ctx *)c;
+  const int64_t ih = pid % a->H, bc = pid / a->H, ci = bc % a->Cin, b = bc / a->Cin;
+  const int64_t cin_g = a->Cin / a->G, cout_g = a->Cout / a->G;
+  const int64_t g = ci / cin_g, cl = ci % cin_g;
+  for (int64_t iw = 0; iw < a->W; ++iw) {
+    float acc = 0.0f;
+    for (int64_t co = g * cout_g; co < (g + 1) * cout_g; ++co)
+      for (int64_t kh = 0; kh < a->KH; ++kh) {
+        const int64_t th = ih + a->PH - kh;
+        if (th < 0 || th % a->SH != 0 || th / a->SH >= a->OH) continue;
+        const int64_t oh = th / a->SH;
+        for (int64_t kw = 0; kw < a->KW; ++kw) {
+          const int64_t tw = iw + a->PW - kw;
+          if (tw < 0 || tw % a->SW != 0 || tw / a->SW >= a->OW) continue;
+          const int64_t ow = tw / a->SW;
+          acc += a->dy[((b * a->Cout + co) * a->OH + oh) * a->OW + ow] *
+                 a->w[((co * cin_g + cl) * a->KH + kh) * a->KW + kw];
+        }
+      }
+    a->out[((b * a->Cin + ci) * a->H + ih) * a->W + iw] = acc;
+  }
+}
+
+static void conv_dw_program(const void *c, int64_t pid) {
+  /* pid = co * (Cin/G) * KH * KW + tap: one weight element */
+  const convb_ctx *a = (const convb_ctx *)c;
+  const int64_t cin_g = a->Cin / a->G, cout_g = a->Cout / a->G;
+  const int64_t kw = pid % a->KW, t1 = pid / a->KW, kh = t1 % a->KH, t2 = t1 / a->KH, cl = t2 % cin_g,
+                co = t2 / cin_g;
+  const int64_t ci = (co / cout_g) * cin_g + cl;
+  const int64_t tiles = (a->OW + a->block_ow - 1) / a->block_ow;
+  float acc = 0.0f;
+  for (int64_t b = 0; b < a->B; ++b)
+    for (int64_t oh = 0; oh < a->OH; ++oh) {
+      const int64_t ih = oh * a->SH - a->PH + kh;
+      for (int64_t t = 0; t < tiles; ++t) {
+        float part = 0.0f; /* T::sum over the ow tile (conv2d.rs:384-386) */
+        for (int64_t j = 0; j < a->block_ow; ++j) {
+          const int64_t ow = t * a->block_ow + j, iw = ow * a->SW - a->PW + kw;
+          if (ow >= a->OW || ih < 0 || ih >= a->H || iw < 0 || iw >= a->W) continue;
+          part += a->dy[((b * a->Cout + co) * a->OH + oh) * a->OW + ow] *
+                  a->x[((b * a->Cin + ci) * a->H + ih) * a->W + iw];
+        }
+        acc += part;
+      }
+    }
+  a->out[pid] = acc;
+}
+
+static int convb_check(int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t KH,
+                       int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW, int64_t G) {
+  if (G <= 0 || Cin % G != 0 || Cout % G != 0 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0) return ERR_SHAPE_MISMATCH;
+  if (OH != (H + 2 * PH - KH) / SH + 1 || OW != (W + 2 * PW - KW) / SW + 1) return ERR_SHAPE_MISMATCH;
+  return OK;
+}
+
+int oracle_conv2d_backward_dx(const float *dy, const float *w, float *dx, int64_t B, int64_t Cin, int64_t Cout,
+                              int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t KH, int64_t KW, int64_t SH,
+                              int64_t SW, int64_t PH, int64_t PW, int64_t G) {
+  int rc = convb_check(Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G);
+  if (rc != OK) return rc;
+  convb_ctx a = {dy, w, NULL, dx, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, 16};
+  launch(conv_dx_program, &a, B * Cin * H, 0, -1);
+  return OK;
+}
+
+int oracle_conv2d_backward_dw(const float *dy, const float *x, float *dw, int64_t B, int64_t Cin, int64_t Cout,
+                              int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t KH, int64_t KW, int64_t SH,
+                              int64_t SW, int64_t PH, int64_t PW, int64_t G, int64_t block_ow) {
+  int rc = convb_check(Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G);
+  if (rc != OK) return rc;
+  if (block_ow <= 0) return ERR_INVALID_ARGUMENT;
+  convb_ctx a = {dy, NULL, x, dw, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow};
+  launch(conv_dw_program, &a, Cout * (Cin / G) * KH * KW, 0, -1);
+  return OK;
+}
+
+/* ── flash attention 2 backward ──────────────────────────────────────────
+ * flash_attn2.rs:173-309 (backward_dq): program (q_row, bh):
+ *   D_q = sum(O_q * dO_q); for each key row k: p = exp(Q_q.K_k * scale - L_q),
+ *   dS = p * (dO_q.V_k - D_q), dQ += dS * K_k * scale.
+ * flash_attn2.rs:311-447 (backward_dkv): program (k_row, bh): for each query
+ *   row m: p = exp(Q_m.K_n * scale - L_m), dV += p * dO_m,
+ *   dS = p * (dO_m.V_n - D_m), dK += dS * Q_m * scale.
+ * Causal (an extension, as in the forward): only pairs with k_row <= q_row. */
+
+typedef struct {
+  const float *q, *k, *v, *o, *dO, *l;
+  float *d1, *d2;
+  int64_t nq, nk, D;
+  float scale;
+  int causal;
+} fab_ctx;
+
+static float dotf(const float *a, const float *b, int64_t n) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) s += a[i] * b[i];
+  return s;
+}
+
+static void fa_dq_program(const void *c, int64_t id) {
+  const fab_ctx *a = (const fab_ctx *)c;
+  const int64_t bh = id / a->nq, qr = id % a->nq, D = a->D;
+  const float *q = a->q + (bh * a->nq + qr) * D, *o = a->o + (bh * a->nq + qr) * D, *dO = a->dO + (bh * a->nq + qr) * D;
+  const float dq_ = dotf(o, dO, D), lq = a->l[bh * a->nq + qr];
+  float acc[1024];
+  for (int64_t d = 0; d < D; ++d) acc[d] = 0.0f;
+  const int64_t kend = a->causal && qr + 1 < a->nk ? qr + 1 : a->nk;
+  for (int64_t kr = 0; kr < kend; ++kr) {
+    const float *k = a->k + (bh * a->nk + kr) * D, *v = a->v + (bh * a->nk + kr) * D;
+    const float p = expf(dotf(q, k, D) * a->scale - lq);
+    const float ds = p * (dotf(dO, v, D) - dq_);
+    for (int64_t d = 0; d < D; ++d) acc[d] = acc[d] + ds * k[d] * a->scale;
+  }
+  float *dq = a->d1 + (bh * a->nq + qr) * D;
+  for (int64_t d = 0; d < D; ++d) dq[d] = acc[d];
+}
+
+static void fa_dkv_program(const void *c, int64_t id) {
+  const fab_ctx *a = (const fab_ctx *)c;
+  const int64_t bh = id / a->nk, kr = id % a->nk, D = a->D;
+  const float *k = a->k + (bh * a->nk + kr) * D, *v = a->v + (bh * a->nk + kr) * D;
+  float dk[1024], dv[1024];
+  for (int64_t d = 0; d < D; ++d) dk[d] = dv[d] = 0.0f;
+  for (int64_t qr = a->causal ? kr : 0; qr < a->nq; ++qr) {
+    const float *q = a->q + (bh * a->nq + qr) * D, *o = a->o + (bh * a->nq + qr) * D,
+                *dO = a->dO + (bh * a->nq + qr) * D;
+    const float lm = a->l[bh * a->nq + qr], dm = dotf(o, dO, D);
+    const float p = expf(dotf(q, k, D) * a->scale - lm);
+    for (int64_t d = 0; d < D; ++d) dv[d] = dv[d] + p * dO[d];
+    const float ds = p * (dotf(dO, v, D) - dm);
+    for (int64_t d = 0; d < D; ++d) dk[d] = dk[d] + ds * q[d] * a->scale;
+  }
+  float *dko = a->d1 + (bh * a->nk + kr) * D, *dvo = a->d2 + (bh * a->nk + kr) * D;
+  for (int64_t d = 0; d < D; ++d) {
+    dko[d] = dk[d];
+    dvo[d] = dv[d];
+  }
+}
+
+int oracle_flash_attention2_backward(const float *q, const float *k, const float *v, const float *o,
+                                     const float *dO, const float *l, float *dq, float *dk, float *dv, int64_t BH,
+                                     int64_t nq, int64_t nk, int64_t D, float scale, int causal) {
+  if (D <= 0 || D > 1024 || nq < 0 || nk <= 0 || BH < 0) return ERR_SHAPE_MISMATCH;
+  fab_ctx a = {q, k, v, o, dO, l, dq, NULL, nq, nk, D, scale, causal};
+  launch(fa_dq_program, &a, BH * nq, 0, -1);
+  fab_ctx b = {q, k, v, o, dO, l, dk, dv, nq, nk, D, scale, causal};
+  launch(fa_dkv_program, &b, BH * nk, 0, -1);
+  return OK;
+}

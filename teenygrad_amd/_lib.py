@@ -136,6 +136,14 @@ _SIGS = {
     "teeny_silu_backward": (S, [P, P, P, c_int64, c_int32, P]),
     "teeny_layer_norm_forward_inference": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, P]),
     "teeny_rms_norm_forward": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, P]),
+    "teeny_layer_norm_forward": (S, [P, P, P, P, P, P, c_int64, c_int64, c_float, c_int32, P]),
+    "teeny_layer_norm_backward": (S, [P, P, P, P, P, P, P, P, c_int64, c_int64, c_int32, P]),
+    "teeny_rms_norm_backward": (S, [P, P, P, P, P, P, c_int64, c_int64, c_int32, P]),
+    "teeny_norm_backward_workspace_size": (S, [c_int64, c_int64, c_int32, c_int32, POINTER(c_size_t)]),
+    "teeny_conv2d_backward_dx": (S, [P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
+    "teeny_conv2d_backward_dw": (S, [P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
+    "teeny_conv2d_backward": (S, [P, P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
+    "teeny_conv2d_backward_workspace_size": (S, [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, POINTER(c_size_t)]),
     "teeny_norm_act_forward": (S, [P, P, P, P, c_int64, c_int64, c_float, c_int32, c_int32, c_int32, P]),
     "teeny_conv2d_forward": (S, [P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_conv2d_bias_forward": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),

@@ -570,6 +570,220 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
   return fail(TEENY_ERR_UNSUPPORTED_DTYPE, std::string(name) + ": dtype must be F32 or BF16");
 }
 
+// ── backward ────────────────────────────────────────────────────────────
+// Reference: conv2d_backward_dx (conv2d.rs:171-284), conv2d_backward_dw
+// (:286-397) and the combined conv2d_backward (:399-521), the RuntimeOp's
+// backward kernel (:575-617).  The reference scatters with atomic adds into
+// zero-initialised dx / dw; these kernels write the same sums directly (a
+// gather per element), so a zero-initialised buffer ends with the same
+// values and the summation order is fixed.
+//
+// Direct kernels (any dtype, layout, stride, padding, groups): one thread per
+// dx element, taps in (co, kh, kw) order; one workgroup per dw element,
+// reducing over (b, oh, ow) with a fixed tree.  bf16 NHWC dx with groups == 1
+// runs on the MFMA implicit GEMM: dx is the stride-1 convolution of dy (for a
+// strided conv, dy spread out with zeros to the stride) with the weights
+// flipped in (kh, kw) and transposed to [C_IN, KH, KW, C_OUT], padded by
+// K - 1 - pad; the flipped weights and the spread dy live in the stream
+// workspace.
+
+template <typename T>
+__global__ __launch_bounds__(256) void conv_bwd_dx_direct(const T *__restrict__ dy, const T *__restrict__ w,
+                                                          T *__restrict__ dx, ConvGeo q, int nhwc) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(q.B) * q.Cin * q.H * q.W;
+  if (e >= total) return;
+  int b, ci, ih, iw;
+  if (nhwc) {
+    ci = static_cast<int>(e % q.Cin);
+    iw = static_cast<int>((e / q.Cin) % q.W);
+    ih = static_cast<int>((e / (static_cast<int64_t>(q.Cin) * q.W)) % q.H);
+    b = static_cast<int>(e / (static_cast<int64_t>(q.Cin) * q.W * q.H));
+  } else {
+    iw = static_cast<int>(e % q.W);
+    ih = static_cast<int>((e / q.W) % q.H);
+    ci = static_cast<int>((e / (static_cast<int64_t>(q.W) * q.H)) % q.Cin);
+    b = static_cast<int>(e / (static_cast<int64_t>(q.W) * q.H * q.Cin));
+  }
+  const int cin_g = q.Cin / q.G, cout_g = q.Cout / q.G;
+  const int g = ci / cin_g, cl = ci % cin_g;
+  float acc = 0.0f;
+  for (int co = g * cout_g; co < (g + 1) * cout_g; ++co) {
+    for (int kh = 0; kh < q.KH; ++kh) {
+      const int th = ih + q.PH - kh;
+      if (th < 0 || th % q.SH != 0 || th / q.SH >= q.OH) continue;
+      const int oh = th / q.SH;
+      for (int kw = 0; kw < q.KW; ++kw) {
+        const int tw = iw + q.PW - kw;
+        if (tw < 0 || tw % q.SW != 0 || tw / q.SW >= q.OW) continue;
+        const int ow = tw / q.SW;
+        acc += to_f32(dy[b * q.ys[0] + co * q.ys[1] + oh * q.ys[2] + ow * q.ys[3]]) *
+               to_f32(w[co * q.ws[0] + cl * q.ws[1] + kh * q.ws[2] + kw * q.ws[3]]);
+      }
+    }
+  }
+  dx[b * q.xs[0] + ci * q.xs[1] + ih * q.xs[2] + iw * q.xs[3]] = from_f32<T>(acc);
+}
+
+// dw[co, cl, kh, kw] = sum over (b, oh, ow) of dy[b, co, oh, ow] * x[b, ci, ih, iw]:
+// one workgroup per weight element, a strided per-thread sum, then a fixed tree.
+template <typename T>
+__global__ __launch_bounds__(256) void conv_bwd_dw_direct(const T *__restrict__ dy, const T *__restrict__ x,
+                                                          T *__restrict__ dw, ConvGeo q) {
+  __shared__ float red[4];
+  const int cin_g = q.Cin / q.G, cout_g = q.Cout / q.G;
+  const int64_t id = blockIdx.x;
+  const int kw = static_cast<int>(id % q.KW), kh = static_cast<int>((id / q.KW) % q.KH);
+  const int cl = static_cast<int>((id / (static_cast<int64_t>(q.KW) * q.KH)) % cin_g);
+  const int co = static_cast<int>(id / (static_cast<int64_t>(q.KW) * q.KH * cin_g));
+  const int ci = (co / cout_g) * cin_g + cl;
+  const int64_t npix = static_cast<int64_t>(q.B) * q.OH * q.OW;
+  float acc = 0.0f;
+  for (int64_t p = threadIdx.x; p < npix; p += 256) {
+    const int ow = static_cast<int>(p % q.OW), oh = static_cast<int>((p / q.OW) % q.OH);
+    const int b = static_cast<int>(p / (static_cast<int64_t>(q.OW) * q.OH));
+    const int ih = oh * q.SH - q.PH + kh, iw = ow * q.SW - q.PW + kw;
+    if (ih < 0 || ih >= q.H || iw < 0 || iw >= q.W) continue;
+    acc += to_f32(dy[b * q.ys[0] + co * q.ys[1] + oh * q.ys[2] + ow * q.ys[3]]) *
+           to_f32(x[b * q.xs[0] + ci * q.xs[1] + ih * q.xs[2] + iw * q.xs[3]]);
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    dw[co * q.ws[0] + cl * q.ws[1] + kh * q.ws[2] + kw * q.ws[3]] = from_f32<T>(((red[0] + red[1]) + red[2]) + red[3]);
+}
+
+// w [C_OUT, KH, KW, C_IN] -> wt [C_IN, KH, KW, C_OUT], flipped in (kh, kw).
+__global__ __launch_bounds__(256) void conv_bwd_flip_weights(const bf16 *__restrict__ w, bf16 *__restrict__ wt,
+                                                             int Cout, int KH, int KW, int Cin) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(Cout) * KH * KW * Cin;
+  if (t >= total) return;
+  const int co = static_cast<int>(t % Cout);
+  const int kw = static_cast<int>((t / Cout) % KW);
+  const int kh = static_cast<int>((t / (static_cast<int64_t>(Cout) * KW)) % KH);
+  const int ci = static_cast<int>(t / (static_cast<int64_t>(Cout) * KW * KH));
+  wt[t] = w[((static_cast<int64_t>(co) * KH + (KH - 1 - kh)) * KW + (KW - 1 - kw)) * Cin + ci];
+}
+
+// dy [B, OH, OW, C] spread to [B, HD, WD, C] with zeros between (stride SH, SW).
+__global__ __launch_bounds__(256) void conv_bwd_spread(const bf16 *__restrict__ dy, bf16 *__restrict__ dyd, int B,
+                                                       int OH, int OW, int C, int HD, int WD, int SH, int SW) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // one 16-byte chunk (8 channels)
+  const int cv = C / 8;
+  const int64_t total = static_cast<int64_t>(B) * HD * WD * cv;
+  if (t >= total) return;
+  const int c8 = static_cast<int>(t % cv);
+  const int wd = static_cast<int>((t / cv) % WD);
+  const int hd = static_cast<int>((t / (static_cast<int64_t>(cv) * WD)) % HD);
+  const int b = static_cast<int>(t / (static_cast<int64_t>(cv) * WD * HD));
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (hd % SH == 0 && wd % SW == 0 && hd / SH < OH && wd / SW < OW)
+    v = *reinterpret_cast<const u32x4 *>(dy + ((static_cast<int64_t>(b) * OH + hd / SH) * OW + wd / SW) * C + 8 * c8);
+  reinterpret_cast<u32x4 *>(dyd)[t] = v;
+}
+
+// The MFMA form of bf16 NHWC dx: the stride-1 conv it becomes and its scratch.
+struct DxPlan {
+  bool ok = false;
+  ConvGeo g2;            // dy (or spread dy) -> dx
+  bool spread = false;
+  int HD = 0, WD = 0;
+  size_t wt_bytes = 0, dyd_off = 0, gemm_off = 0;
+};
+
+static DxPlan dx_plan(const ConvGeo &q) {
+  DxPlan d;
+  if (q.G != 1 || q.PH > q.KH - 1 || q.PW > q.KW - 1 || q.Cout % 8 != 0) return d;
+  d.spread = q.SH > 1 || q.SW > 1;
+  d.HD = d.spread ? (q.OH - 1) * q.SH + 1 + (q.H + 2 * q.PH - q.KH) % q.SH : q.OH;
+  d.WD = d.spread ? (q.OW - 1) * q.SW + 1 + (q.W + 2 * q.PW - q.KW) % q.SW : q.OW;
+  teeny_conv2d_params p2{q.KH, q.KW, 1, 1, q.KH - 1 - q.PH, q.KW - 1 - q.PW, 1, TEENY_ACT_NONE};
+  if (make_geo(q.B, q.Cout, q.Cin, d.HD, d.WD, q.H, q.W, &p2, TEENY_NHWC, &d.g2, "conv2d_backward_dx") != TEENY_OK)
+    return d;
+  if (conv_path<false>(d.g2) == kConvNoMfma) return d;
+  d.ok = true;
+  d.wt_bytes = static_cast<size_t>(q.Cout) * q.KH * q.KW * q.Cin * sizeof(bf16);
+  d.dyd_off = round256(d.wt_bytes);
+  d.gemm_off = d.dyd_off + (d.spread ? round256(static_cast<size_t>(q.B) * d.HD * d.WD * q.Cout * sizeof(bf16)) : 0);
+  return d;
+}
+
+static size_t dx_scratch_bytes(const ConvGeo &q) {
+  const DxPlan d = dx_plan(q);
+  return d.ok ? d.gemm_off + conv_scratch_bytes<false>(d.g2) : 0;
+}
+
+// bf16 NHWC dx on the MFMA path; false (nothing launched) if it does not apply.
+static bool conv_dx_mfma(const void *dy, const void *w, void *dx, const ConvGeo &q, hipStream_t s, Scratch scr) {
+  const DxPlan d = dx_plan(q);
+  if (!d.ok || scr.ptr == nullptr || scr.bytes < d.gemm_off || !aligned(dy, 16) || !aligned(w, 16)) return false;
+  char *base = static_cast<char *>(scr.ptr);
+  bf16 *wt = reinterpret_cast<bf16 *>(base);
+  const int64_t nw = static_cast<int64_t>(q.Cout) * q.KH * q.KW * q.Cin;
+  hipLaunchKernelGGL(conv_bwd_flip_weights, dim3(static_cast<unsigned>(cdiv(nw, 256))), dim3(256), 0, s,
+                     static_cast<const bf16 *>(w), wt, q.Cout, q.KH, q.KW, q.Cin);
+  const void *src = dy;
+  if (d.spread) {
+    bf16 *dyd = reinterpret_cast<bf16 *>(base + d.dyd_off);
+    const int64_t nc = static_cast<int64_t>(q.B) * d.HD * d.WD * (q.Cout / 8);
+    hipLaunchKernelGGL(conv_bwd_spread, dim3(static_cast<unsigned>(cdiv(nc, 256))), dim3(256), 0, s,
+                       static_cast<const bf16 *>(dy), dyd, q.B, q.OH, q.OW, q.Cout, d.HD, d.WD, q.SH, q.SW);
+    src = dyd;
+  }
+  const Scratch rest{base + d.gemm_off, scr.bytes - d.gemm_off};
+  if (try_conv_mfma<false>(src, wt, nullptr, nullptr, nullptr, dx, d.g2, TEENY_ACT_NONE, s, rest)) return true;
+  // the GEMM declined (alignment): the direct kernel reads the caller's buffers
+  return false;
+}
+
+template <typename T>
+static void launch_dx_direct(const void *dy, const void *w, void *dx, const ConvGeo &q, bool nhwc, hipStream_t s) {
+  const int64_t total = static_cast<int64_t>(q.B) * q.Cin * q.H * q.W;
+  hipLaunchKernelGGL((conv_bwd_dx_direct<T>), dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256), 0, s,
+                     static_cast<const T *>(dy), static_cast<const T *>(w), static_cast<T *>(dx), q, nhwc ? 1 : 0);
+}
+
+template <typename T>
+static void launch_dw_direct(const void *dy, const void *x, void *dw, const ConvGeo &q, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(q.Cout) * (q.Cin / q.G) * q.KH * q.KW;
+  hipLaunchKernelGGL((conv_bwd_dw_direct<T>), dim3(static_cast<unsigned>(n)), dim3(256), 0, s,
+                     static_cast<const T *>(dy), static_cast<const T *>(x), static_cast<T *>(dw), q);
+}
+
+static teeny_status conv_bwd_entry(const void *dy, const void *x, const void *w, void *dx, void *dw, int64_t B,
+                                   int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                   const teeny_conv2d_params *prm, teeny_dtype dtype, teeny_layout layout,
+                                   teeny_stream stream, const char *name) {
+  ConvGeo q;
+  teeny_status st = make_geo(B, Cin, Cout, H, W, OH, OW, prm, layout, &q, name);
+  if (st != TEENY_OK) return st;
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                std::string(name) + ": dtype must be F32 or BF16");
+  TEENY_REQUIRE(static_cast<int64_t>(Cout) * (Cin / prm->groups) * prm->KH * prm->KW <= 0x7fffffff,
+                TEENY_ERR_SHAPE_MISMATCH, std::string(name) + ": weight too large");
+  if (B == 0) return TEENY_OK;
+  TEENY_REQUIRE(dy != nullptr && (dx == nullptr || w != nullptr) && (dw == nullptr || x != nullptr),
+                TEENY_ERR_NULL_POINTER, std::string(name) + ": dy/w/x");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool nhwc = layout == TEENY_NHWC;
+  if (dx != nullptr) {
+    if (!(dtype == TEENY_BF16 && nhwc && conv_dx_mfma(dy, w, dx, q, s, stream_scratch(s)))) {
+      if (dtype == TEENY_F32) launch_dx_direct<float>(dy, w, dx, q, nhwc, s);
+      else launch_dx_direct<bf16>(dy, w, dx, q, nhwc, s);
+    }
+    st = after_launch(name, s);
+    if (st != TEENY_OK) return st;
+  }
+  if (dw != nullptr) {
+    if (dtype == TEENY_F32) launch_dw_direct<float>(dy, x, dw, q, s);
+    else launch_dw_direct<bf16>(dy, x, dw, q, s);
+    st = after_launch(name, s);
+  }
+  return st;
+}
+
 // ── the no-allocation variant's scratch ─────────────────────────────────
 // A file-scope device array serves as the scratch of
 // teeny_conv2d_bias_forward_noalloc.  Each GPU that loads this library holds
@@ -664,6 +878,47 @@ teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, co
                                 static_cast<bf16 *>(y), q, params->act, s);
   }
   return after_launch(name, s);
+}
+
+teeny_status teeny_conv2d_backward_dx(const void *dy, const void *w, void *dx, int64_t B, int64_t C_IN,
+                                      int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                      const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                      teeny_stream stream) {
+  TEENY_REQUIRE(dx != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_backward_dx: dx");
+  return conv_bwd_entry(dy, nullptr, w, dx, nullptr, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
+                        "conv2d_backward_dx");
+}
+
+teeny_status teeny_conv2d_backward_dw(const void *dy, const void *x, void *dw, int64_t B, int64_t C_IN,
+                                      int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                      const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                      teeny_stream stream) {
+  TEENY_REQUIRE(dw != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_backward_dw: dw");
+  return conv_bwd_entry(dy, x, nullptr, nullptr, dw, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
+                        "conv2d_backward_dw");
+}
+
+teeny_status teeny_conv2d_backward(const void *dy, const void *x, const void *w, void *dx, void *dw, int64_t B,
+                                   int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                                   const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                   teeny_stream stream) {
+  TEENY_REQUIRE(dx != nullptr && dw != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_backward: dx/dw");
+  return conv_bwd_entry(dy, x, w, dx, dw, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
+                        "conv2d_backward");
+}
+
+teeny_status teeny_conv2d_backward_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                                  int64_t OH, int64_t OW, const teeny_conv2d_params *params,
+                                                  teeny_dtype dtype, teeny_layout layout, size_t *bytes) {
+  TEENY_REQUIRE(bytes != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_backward_workspace_size: bytes");
+  *bytes = 0;
+  ConvGeo q;
+  teeny_status st = make_geo(B, C_IN, C_OUT, H, W, OH, OW, params, layout, &q, "conv2d_backward_workspace_size");
+  if (st != TEENY_OK) return st;
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                "conv2d_backward_workspace_size: dtype must be F32 or BF16");
+  if (B > 0 && dtype == TEENY_BF16 && layout == TEENY_NHWC) *bytes = dx_scratch_bytes(q);
+  return TEENY_OK;
 }
 
 teeny_status teeny_conv2d_workspace_size(int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,

@@ -33,7 +33,7 @@ constexpr int kNormMaxBlocks = 256 * 8;
 template <typename T, int WPR, int VPL, bool RMS, int ACT>
 __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     const T *__restrict__ x, T *__restrict__ y, const T *__restrict__ gamma,
-    const T *__restrict__ beta, float *__restrict__ rrms, int64_t M, int32_t N, float eps,
+    const T *__restrict__ beta, float *__restrict__ st0, float *__restrict__ st1, int64_t M, int32_t N, float eps,
     float inv_n) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int RPB = kNormWaves / WPR;  // rows per workgroup
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
       for (int i = 0; i < VEC; ++i) q += v[j][i] * v[j][i];
     q = row_sum(q, 0);
     rstd = rsqrtf(q * inv_n + eps);
-    if (rrms != nullptr && row_ok && part == 0 && lane == 0) rrms[row] = rstd;
+    if (st0 != nullptr && row_ok && part == 0 && lane == 0) st0[row] = rstd;  // rrms
   } else {
     float s = 0.0f;
 #pragma unroll
@@ -113,6 +113,10 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
       }
     }
     rstd = rsqrtf(row_sum(q, 1) * inv_n + eps);
+    if (row_ok && part == 0 && lane == 0) {  // training forward: saved statistics
+      if (st0 != nullptr) st0[row] = mean;
+      if (st1 != nullptr) st1[row] = rstd;
+    }
   }
 
 #pragma unroll
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
 template <typename T, bool RMS, int ACT>
 __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
     const T *__restrict__ x, T *__restrict__ y, const T *__restrict__ gamma,
-    const T *__restrict__ beta, float *__restrict__ rrms, int64_t M, int64_t N, float eps,
+    const T *__restrict__ beta, float *__restrict__ st0, float *__restrict__ st1, int64_t M, int64_t N, float eps,
     float inv_n) {
   constexpr bool fast = !std::is_same<T, float>::value;
   const int lane = threadIdx.x & 63;
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
       }
       q = wave_sum(q);
       rstd = rsqrtf(q * inv_n + eps);
-      if (rrms != nullptr && lane == 0) rrms[row] = rstd;
+      if (st0 != nullptr && lane == 0) st0[row] = rstd;  // rrms
     } else {
       float s = 0.0f;
       for (int64_t c = lane; c < N; c += 64) s += to_f32(xr[c]);
@@ -170,6 +174,10 @@ __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
       }
       q = wave_sum(q);
       rstd = rsqrtf(q * inv_n + eps);
+      if (lane == 0) {
+        if (st0 != nullptr) st0[row] = mean;
+        if (st1 != nullptr) st1[row] = rstd;
+      }
     }
     for (int64_t c = lane; c < N; c += 64) {
       float v = to_f32(xr[c]);
@@ -181,17 +189,17 @@ __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
 }
 
 template <typename T, int WPR, int VPL, bool RMS, int ACT>
-static void launch_rows(const void *x, void *y, const void *g, const void *b, float *rrms, int64_t M,
-                        int64_t N, float eps, float inv_n, hipStream_t s) {
+static void launch_rows(const void *x, void *y, const void *g, const void *b, float *st0, float *st1,
+                        int64_t M, int64_t N, float eps, float inv_n, hipStream_t s) {
   constexpr int RPB = kNormWaves / WPR;
   hipLaunchKernelGGL((norm_rows_kernel<T, WPR, VPL, RMS, ACT>), dim3(cdiv(M, RPB)),
                      dim3(kNormThreads), 0, s, static_cast<const T *>(x), static_cast<T *>(y),
-                     static_cast<const T *>(g), static_cast<const T *>(b), rrms, M,
+                     static_cast<const T *>(g), static_cast<const T *>(b), st0, st1, M,
                      static_cast<int32_t>(N), eps, inv_n);
 }
 
 template <typename T, bool RMS, int ACT>
-static teeny_status launch_norm(const void *x, void *y, const void *g, const void *b, float *rrms,
+static teeny_status launch_norm(const void *x, void *y, const void *g, const void *b, float *st0, float *st1,
                                 int64_t M, int64_t N, float eps, hipStream_t s, const char *name) {
   constexpr int VEC = 16 / sizeof(T);
   const float inv_n = 1.0f / static_cast<float>(N);
@@ -200,41 +208,41 @@ static teeny_status launch_norm(const void *x, void *y, const void *g, const voi
   const int64_t nv = N / VEC;  // 16-byte vectors per row
   TEENY_REQUIRE(cdiv(M, 4) <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, std::string(name) + ": M too large");
   if (vec_ok && nv <= 64) {
-    launch_rows<T, 1, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 1, 1, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 128) {
-    launch_rows<T, 2, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 2, 1, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 256) {
-    launch_rows<T, 4, 1, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 4, 1, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 512) {
-    launch_rows<T, 4, 2, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 4, 2, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 1024) {
-    launch_rows<T, 4, 4, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 4, 4, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 2048) {
-    launch_rows<T, 4, 8, RMS, ACT>(x, y, g, b, rrms, M, N, eps, inv_n, s);
+    launch_rows<T, 4, 8, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else {
     const int blocks = static_cast<int>(std::min<int64_t>(cdiv(M, kNormWaves), kNormMaxBlocks));
     hipLaunchKernelGGL((norm_multipass_kernel<T, RMS, ACT>), dim3(blocks), dim3(kNormThreads), 0,
                        s, static_cast<const T *>(x), static_cast<T *>(y),
-                       static_cast<const T *>(g), static_cast<const T *>(b), rrms, M, N, eps,
+                       static_cast<const T *>(g), static_cast<const T *>(b), st0, st1, M, N, eps,
                        inv_n);
   }
   return after_launch(name, s);
 }
 
 template <typename T, bool RMS>
-static teeny_status dispatch_act(const void *x, void *y, const void *g, const void *b, float *rrms,
+static teeny_status dispatch_act(const void *x, void *y, const void *g, const void *b, float *st0, float *st1,
                                  int64_t M, int64_t N, float eps, int act, hipStream_t s,
                                  const char *name) {
   switch (act) {
-    case TEENY_ACT_NONE: return launch_norm<T, RMS, TEENY_ACT_NONE>(x, y, g, b, rrms, M, N, eps, s, name);
-    case TEENY_ACT_RELU: return launch_norm<T, RMS, TEENY_ACT_RELU>(x, y, g, b, rrms, M, N, eps, s, name);
-    case TEENY_ACT_GELU_TANH: return launch_norm<T, RMS, TEENY_ACT_GELU_TANH>(x, y, g, b, rrms, M, N, eps, s, name);
-    case TEENY_ACT_SILU: return launch_norm<T, RMS, TEENY_ACT_SILU>(x, y, g, b, rrms, M, N, eps, s, name);
+    case TEENY_ACT_NONE: return launch_norm<T, RMS, TEENY_ACT_NONE>(x, y, g, b, st0, st1, M, N, eps, s, name);
+    case TEENY_ACT_RELU: return launch_norm<T, RMS, TEENY_ACT_RELU>(x, y, g, b, st0, st1, M, N, eps, s, name);
+    case TEENY_ACT_GELU_TANH: return launch_norm<T, RMS, TEENY_ACT_GELU_TANH>(x, y, g, b, st0, st1, M, N, eps, s, name);
+    case TEENY_ACT_SILU: return launch_norm<T, RMS, TEENY_ACT_SILU>(x, y, g, b, st0, st1, M, N, eps, s, name);
     default: return fail(TEENY_ERR_INVALID_ARGUMENT, std::string(name) + ": unknown activation");
   }
 }
 
-static teeny_status norm_entry(const void *x, void *y, const void *g, const void *b, float *rrms,
+static teeny_status norm_entry(const void *x, void *y, const void *g, const void *b, float *st0, float *st1,
                                int64_t M, int64_t N, float eps, bool rms, int act,
                                teeny_dtype dtype, teeny_stream stream, const char *name) {
   const std::string n(name);
@@ -249,12 +257,12 @@ static teeny_status norm_entry(const void *x, void *y, const void *g, const void
                 n + ": unknown activation");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TEENY_F32) {
-    return rms ? dispatch_act<float, true>(x, y, g, b, rrms, M, N, eps, act, s, name)
-               : dispatch_act<float, false>(x, y, g, b, rrms, M, N, eps, act, s, name);
+    return rms ? dispatch_act<float, true>(x, y, g, b, st0, st1, M, N, eps, act, s, name)
+               : dispatch_act<float, false>(x, y, g, b, st0, st1, M, N, eps, act, s, name);
   }
   if (dtype == TEENY_BF16) {
-    return rms ? dispatch_act<bf16, true>(x, y, g, b, rrms, M, N, eps, act, s, name)
-               : dispatch_act<bf16, false>(x, y, g, b, rrms, M, N, eps, act, s, name);
+    return rms ? dispatch_act<bf16, true>(x, y, g, b, st0, st1, M, N, eps, act, s, name)
+               : dispatch_act<bf16, false>(x, y, g, b, st0, st1, M, N, eps, act, s, name);
   }
   return fail(TEENY_ERR_UNSUPPORTED_DTYPE, n + ": dtype must be F32 or BF16");
 }
@@ -269,21 +277,30 @@ teeny_status teeny_layer_norm_forward_inference(const void *x, void *y, const vo
                                                 const void *bias, int64_t M, int64_t N,
                                                 float eps, teeny_dtype dtype,
                                                 teeny_stream stream) {
-  return norm_entry(x, y, weight, bias, nullptr, M, N, eps, false, TEENY_ACT_NONE, dtype, stream,
+  return norm_entry(x, y, weight, bias, nullptr, nullptr, M, N, eps, false, TEENY_ACT_NONE, dtype, stream,
                     "layer_norm_forward_inference");
 }
 
 teeny_status teeny_rms_norm_forward(const void *x, void *y, const void *weight, float *rrms,
                                     int64_t M, int64_t N, float eps, teeny_dtype dtype,
                                     teeny_stream stream) {
-  return norm_entry(x, y, weight, nullptr, rrms, M, N, eps, true, TEENY_ACT_NONE, dtype, stream,
+  return norm_entry(x, y, weight, nullptr, rrms, nullptr, M, N, eps, true, TEENY_ACT_NONE, dtype, stream,
                     "rms_norm_forward");
+}
+
+teeny_status teeny_layer_norm_forward(const void *x, void *y, const void *weight, const void *bias,
+                                      float *mean, float *rstd, int64_t M, int64_t N, float eps,
+                                      teeny_dtype dtype, teeny_stream stream) {
+  TEENY_REQUIRE(M == 0 || (mean != nullptr && rstd != nullptr), TEENY_ERR_NULL_POINTER,
+                "layer_norm_forward: mean/rstd");
+  return norm_entry(x, y, weight, bias, mean, rstd, M, N, eps, false, TEENY_ACT_NONE, dtype, stream,
+                    "layer_norm_forward");
 }
 
 teeny_status teeny_norm_act_forward(const void *x, void *y, const void *weight, const void *bias,
                                     int64_t M, int64_t N, float eps, int32_t is_rms,
                                     teeny_activation act, teeny_dtype dtype, teeny_stream stream) {
-  return norm_entry(x, y, weight, bias, nullptr, M, N, eps, is_rms != 0, act, dtype, stream,
+  return norm_entry(x, y, weight, bias, nullptr, nullptr, M, N, eps, is_rms != 0, act, dtype, stream,
                     "norm_act_forward");
 }
 

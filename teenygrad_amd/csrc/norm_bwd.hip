@@ -1,0 +1,369 @@
+// LayerNorm and RMSNorm backward.
+//
+// Reference kernels (one program per row, BLOCK_N tiles, two passes):
+//   layer_norm_backward  kernels/teeny-kernels/src/nn/norm/layernorm.rs:300-482
+//     xhat = (x - mean) * rstd, c1 = sum(dy g) / N, c2 = sum(dy g xhat) / N,
+//     dx = rstd * g * (dy - c1 - xhat * c2), dweight += dy xhat, dbias += dy
+//   rms_norm_backward    kernels/teeny-kernels/src/nn/norm/rmsnorm.rs:135-277
+//     s = sum(dy g x) / N, dx = rrms * g * (dy - x rrms^2 s), dweight += dy x rrms
+// The dx formulas are the reference's exactly (gamma outside the bracket:
+// the true gradient of the forward when gamma == 1).  The reference updates
+// dweight/dbias with an unsynchronised load-add-store in every program; here
+// the column sums are deterministic and accumulate into the existing values.
+//
+// MI355X design (HBM-bound: read x and dy, write dx).  A persistent grid of G
+// workgroups walks the rows (row r on workgroup r mod G); each thread owns
+// VPT fixed 16-byte column vectors of every row, so gamma is loaded once and
+// the per-column gradient partials stay in fp32 registers across rows.  A
+// row's one or two sums are a wave shuffle plus one LDS exchange; the LDS
+// slots alternate between rows so one barrier per row suffices.  At the end
+// each workgroup writes its column partials to the stream workspace and a
+// second kernel adds the G partials of every column, in workgroup order, to
+// dweight (and dbias).  Without a large enough workspace the parameter
+// gradients come from a column kernel that re-reads x and dy instead (no
+// scratch, two more tensor reads).  Rows that do not fit the register plan
+// (N > 8192 bf16 / 4096 fp32, N % 8 != 0, unaligned) take a multi-pass
+// wave-per-row kernel for dx and the column kernel.
+#include "common.hpp"
+
+namespace teeny {
+
+constexpr int kNbThreads = 256;
+constexpr int kNbWaves = kNbThreads / 64;
+
+template <typename T>
+__device__ __forceinline__ void load_vec(const T *p, float *out) {
+  constexpr int VEC = 16 / sizeof(T);
+  const u32x4 raw = *reinterpret_cast<const u32x4 *>(p);
+  T e[VEC];
+  __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) out[i] = to_f32(e[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_vec(T *p, const float *v) {
+  constexpr int VEC = 16 / sizeof(T);
+  T e[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) e[i] = from_f32<T>(v[i]);
+  u32x4 raw;
+  __builtin_memcpy(&raw, e, 16);
+  __builtin_nontemporal_store(raw, reinterpret_cast<u32x4 *>(p));
+}
+
+// dx for rows blockIdx.x, blockIdx.x + G, ...; with PART, per-workgroup column
+// partials of dweight (part_g) and dbias (part_b, LayerNorm) as fp32 [G, N].
+template <typename T, int VPT, bool RMS, bool PART>
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
+    const T *__restrict__ dy, const T *__restrict__ x, T *__restrict__ dx, const T *__restrict__ gamma,
+    const float *__restrict__ st0, const float *__restrict__ st1, float *__restrict__ part_g,
+    float *__restrict__ part_b, int64_t M, int32_t N, float inv_n) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NS = RMS ? 1 : 2;  // row sums
+  __shared__ float red[2][kNbWaves][NS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nv = N / VEC;
+  float g[VPT][VEC], acc_g[VPT][VEC], acc_b[VPT][VEC];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = j * kNbThreads + tid;
+    if (v < nv) load_vec(gamma + static_cast<int64_t>(v) * VEC, g[j]);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      if (v >= nv) g[j][i] = 0.0f;
+      acc_g[j][i] = 0.0f;
+      acc_b[j][i] = 0.0f;
+    }
+  }
+  int par = 0;
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x, par ^= 1) {
+    const T *xr = x + row * N, *dyr = dy + row * N;
+    T *dxr = dx + row * N;
+    float xv[VPT][VEC], dv[VPT][VEC];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = j * kNbThreads + tid;
+      if (v < nv) {
+        load_vec(xr + static_cast<int64_t>(v) * VEC, xv[j]);
+        load_vec(dyr + static_cast<int64_t>(v) * VEC, dv[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) xv[j][i] = dv[j][i] = 0.0f;
+      }
+    }
+    const float a = st0[row];                // LayerNorm: mean; RMSNorm: rrms
+    const float rstd = RMS ? a : st1[row];   // LayerNorm: rstd
+    float s[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) s[k] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float dg = dv[j][i] * g[j][i];
+        if constexpr (RMS) {
+          s[0] += dg * xv[j][i];
+        } else {
+          s[0] += dg;
+          s[1] += dg * ((xv[j][i] - a) * rstd);
+        }
+      }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) s[k] = wave_sum(s[k]);
+    if (lane == 0)
+#pragma unroll
+      for (int k = 0; k < NS; ++k) red[par][w][k] = s[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NS; ++k) s[k] = red[par][0][k] + red[par][1][k] + red[par][2][k] + red[par][3][k];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = j * kNbThreads + tid;
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        if constexpr (RMS) {
+          const float scale = s[0] * inv_n;
+          o[i] = rstd * g[j][i] * (dv[j][i] - xv[j][i] * (rstd * rstd) * scale);
+          if constexpr (PART) acc_g[j][i] += dv[j][i] * xv[j][i] * rstd;
+        } else {
+          const float xhat = (xv[j][i] - a) * rstd;
+          o[i] = rstd * g[j][i] * (dv[j][i] - s[0] * inv_n - xhat * (s[1] * inv_n));
+          if constexpr (PART) {
+            acc_g[j][i] += dv[j][i] * xhat;
+            acc_b[j][i] += dv[j][i];
+          }
+        }
+      }
+      if (v < nv) store_vec(dxr + static_cast<int64_t>(v) * VEC, o);
+    }
+  }
+  if constexpr (PART) {
+    float *pg = part_g + static_cast<int64_t>(blockIdx.x) * N;
+    float *pb = RMS ? nullptr : part_b + static_cast<int64_t>(blockIdx.x) * N;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = j * kNbThreads + tid;
+      if (v >= nv) continue;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        pg[static_cast<int64_t>(v) * VEC + i] = acc_g[j][i];
+        if constexpr (!RMS) pb[static_cast<int64_t>(v) * VEC + i] = acc_b[j][i];
+      }
+    }
+  }
+}
+
+// dweight[n] += sum_g part_g[g, n] (and dbias from part_b), g in order: a
+// workgroup owns 64 columns, its four waves take g = w, w+4, ... and the
+// wave sums are added in wave order.
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum_kernel(const float *__restrict__ part_g,
+                                                                     const float *__restrict__ part_b, int G,
+                                                                     int N, float *__restrict__ dweight,
+                                                                     float *__restrict__ dbias) {
+  __shared__ float red[kNbWaves][64][2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
+  float sg = 0.0f, sb = 0.0f;
+  if (n < N) {
+    for (int gi = w; gi < G; gi += kNbWaves) {
+      sg += part_g[static_cast<int64_t>(gi) * N + n];
+      if (part_b != nullptr) sb += part_b[static_cast<int64_t>(gi) * N + n];
+    }
+  }
+  red[w][lane][0] = sg;
+  red[w][lane][1] = sb;
+  __syncthreads();
+  if (w == 0 && n < N) {
+    const float tg = ((red[0][lane][0] + red[1][lane][0]) + red[2][lane][0]) + red[3][lane][0];
+    const float tb = ((red[0][lane][1] + red[1][lane][1]) + red[2][lane][1]) + red[3][lane][1];
+    if (dweight != nullptr) dweight[n] = dweight[n] + tg;
+    if (dbias != nullptr) dbias[n] = dbias[n] + tb;
+  }
+}
+
+// Parameter gradients without scratch: thread = column, all rows in order.
+template <typename T, bool RMS>
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_cols_kernel(const T *__restrict__ dy,
+                                                                   const T *__restrict__ x,
+                                                                   const float *__restrict__ st0,
+                                                                   const float *__restrict__ st1, int64_t M,
+                                                                   int64_t N, float *__restrict__ dweight,
+                                                                   float *__restrict__ dbias) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kNbThreads + threadIdx.x;
+  if (n >= N) return;
+  float sg = 0.0f, sb = 0.0f;
+  for (int64_t m = 0; m < M; ++m) {
+    const float d = to_f32(dy[m * N + n]), xv = to_f32(x[m * N + n]);
+    if constexpr (RMS) {
+      sg += d * xv * st0[m];
+    } else {
+      sg += d * ((xv - st0[m]) * st1[m]);
+      sb += d;
+    }
+  }
+  if (dweight != nullptr) dweight[n] = dweight[n] + sg;
+  if (!RMS && dbias != nullptr) dbias[n] = dbias[n] + sb;
+}
+
+// dx for any N and alignment: one wave per row, the reference's two passes.
+template <typename T, bool RMS>
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_multipass_kernel(
+    const T *__restrict__ dy, const T *__restrict__ x, T *__restrict__ dx, const T *__restrict__ gamma,
+    const float *__restrict__ st0, const float *__restrict__ st1, int64_t M, int64_t N, float inv_n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kNbWaves;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kNbWaves + (threadIdx.x >> 6); row < M; row += nwaves) {
+    const T *xr = x + row * N, *dyr = dy + row * N;
+    T *dxr = dx + row * N;
+    const float a = st0[row], rstd = RMS ? a : st1[row];
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int64_t c = lane; c < N; c += 64) {
+      const float dg = to_f32(dyr[c]) * to_f32(gamma[c]), xv = to_f32(xr[c]);
+      if constexpr (RMS) {
+        s0 += dg * xv;
+      } else {
+        s0 += dg;
+        s1 += dg * ((xv - a) * rstd);
+      }
+    }
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    for (int64_t c = lane; c < N; c += 64) {
+      const float d = to_f32(dyr[c]), gm = to_f32(gamma[c]), xv = to_f32(xr[c]);
+      float o;
+      if constexpr (RMS) o = rstd * gm * (d - xv * (rstd * rstd) * (s0 * inv_n));
+      else o = rstd * gm * (d - s0 * inv_n - ((xv - a) * rstd) * (s1 * inv_n));
+      dxr[c] = from_f32<T>(o);
+    }
+  }
+}
+
+// Workgroups of the row kernel: two per CU, at most one per row.
+static int bwd_groups(int64_t M) {
+  return static_cast<int>(std::min<int64_t>(M, 2 * static_cast<int64_t>(device_cu_count())));
+}
+
+template <typename T>
+static int bwd_vpt(int64_t N, bool vec_ok) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (!vec_ok || N % VEC != 0) return 0;
+  const int64_t nv = N / VEC;
+  for (int v : {1, 2, 4})
+    if (nv <= static_cast<int64_t>(v) * kNbThreads) return v;
+  return 0;
+}
+
+static size_t bwd_scratch_bytes(int64_t M, int64_t N, bool rms) {
+  return static_cast<size_t>(bwd_groups(M)) * static_cast<size_t>(N) * 4 * (rms ? 1 : 2);
+}
+
+template <typename T, int VPT, bool RMS, bool PART>
+static void launch_bwd_rows(const void *dy, const void *x, void *dx, const void *g, const float *st0,
+                            const float *st1, float *pg, float *pb, int64_t M, int64_t N, int G, hipStream_t s) {
+  hipLaunchKernelGGL((norm_bwd_rows_kernel<T, VPT, RMS, PART>), dim3(G), dim3(kNbThreads), 0, s,
+                     static_cast<const T *>(dy), static_cast<const T *>(x), static_cast<T *>(dx),
+                     static_cast<const T *>(g), st0, st1, pg, pb, M, static_cast<int32_t>(N),
+                     1.0f / static_cast<float>(N));
+}
+
+template <typename T, bool RMS>
+static teeny_status norm_bwd(const void *dy, const void *x, void *dx, const void *g, const float *st0,
+                             const float *st1, float *dweight, float *dbias, int64_t M, int64_t N, hipStream_t s,
+                             const char *name) {
+  const bool vec_ok = aligned(dy, 16) && aligned(x, 16) && aligned(dx, 16) && aligned(g, 16);
+  const int vpt = bwd_vpt<T>(N, vec_ok);
+  const bool grads = dweight != nullptr || (!RMS && dbias != nullptr);
+  const int G = bwd_groups(M);
+  const Scratch scr = stream_scratch(s);
+  const bool part = grads && vpt > 0 && scr.ptr != nullptr && scr.bytes >= bwd_scratch_bytes(M, N, RMS);
+  float *pg = part ? static_cast<float *>(scr.ptr) : nullptr;
+  float *pb = part && !RMS ? pg + static_cast<int64_t>(G) * N : nullptr;
+  if (vpt > 0) {
+#define TEENY_NB_ROWS(V)                                                                            \
+  do {                                                                                              \
+    if (part) launch_bwd_rows<T, V, RMS, true>(dy, x, dx, g, st0, st1, pg, pb, M, N, G, s);         \
+    else launch_bwd_rows<T, V, RMS, false>(dy, x, dx, g, st0, st1, nullptr, nullptr, M, N, G, s);   \
+  } while (0)
+    switch (vpt) {
+      case 1: TEENY_NB_ROWS(1); break;
+      case 2: TEENY_NB_ROWS(2); break;
+      case 4: TEENY_NB_ROWS(4); break;
+      default: TEENY_NB_ROWS(4); break;
+    }
+#undef TEENY_NB_ROWS
+  } else {
+    const int blocks = static_cast<int>(std::min<int64_t>(cdiv(M, kNbWaves), 8 * device_cu_count()));
+    hipLaunchKernelGGL((norm_bwd_multipass_kernel<T, RMS>), dim3(blocks), dim3(kNbThreads), 0, s,
+                       static_cast<const T *>(dy), static_cast<const T *>(x), static_cast<T *>(dx),
+                       static_cast<const T *>(g), st0, st1, M, N, 1.0f / static_cast<float>(N));
+  }
+  teeny_status st = after_launch(name, s);
+  if (st != TEENY_OK || !grads) return st;
+  if (part) {
+    hipLaunchKernelGGL(norm_bwd_colsum_kernel, dim3(static_cast<unsigned>(cdiv(N, 64))), dim3(kNbThreads), 0, s,
+                       pg, pb, G, static_cast<int>(N), dweight, RMS ? nullptr : dbias);
+  } else {
+    hipLaunchKernelGGL((norm_bwd_cols_kernel<T, RMS>), dim3(static_cast<unsigned>(cdiv(N, kNbThreads))),
+                       dim3(kNbThreads), 0, s, static_cast<const T *>(dy), static_cast<const T *>(x), st0, st1, M,
+                       N, dweight, RMS ? nullptr : dbias);
+  }
+  return after_launch(name, s);
+}
+
+static teeny_status norm_bwd_entry(const void *dy, const void *x, void *dx, const void *g, float *dweight,
+                                   float *dbias, const float *st0, const float *st1, int64_t M, int64_t N,
+                                   bool rms, teeny_dtype dtype, teeny_stream stream, const char *name) {
+  const std::string nm(name);
+  TEENY_REQUIRE(M >= 0 && N >= 0, TEENY_ERR_SHAPE_MISMATCH, nm + ": negative M or N");
+  if (M == 0) return TEENY_OK;
+  TEENY_REQUIRE(N > 0 && N <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH, nm + ": N must be in [1, 2^31)");
+  TEENY_REQUIRE(dy != nullptr && x != nullptr && dx != nullptr && g != nullptr && st0 != nullptr &&
+                    (rms || st1 != nullptr),
+                TEENY_ERR_NULL_POINTER, nm + (rms ? ": dy/x/dx/weight/rrms" : ": dy/x/dx/weight/mean/rstd"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TEENY_F32)
+    return rms ? norm_bwd<float, true>(dy, x, dx, g, st0, st1, dweight, dbias, M, N, s, name)
+               : norm_bwd<float, false>(dy, x, dx, g, st0, st1, dweight, dbias, M, N, s, name);
+  if (dtype == TEENY_BF16)
+    return rms ? norm_bwd<bf16, true>(dy, x, dx, g, st0, st1, dweight, dbias, M, N, s, name)
+               : norm_bwd<bf16, false>(dy, x, dx, g, st0, st1, dweight, dbias, M, N, s, name);
+  return fail(TEENY_ERR_UNSUPPORTED_DTYPE, nm + ": dtype must be F32 or BF16");
+}
+
+}  // namespace teeny
+
+using namespace teeny;
+
+extern "C" {
+
+teeny_status teeny_layer_norm_backward(const void *dy, const void *x, void *dx, const void *weight,
+                                       float *dweight, float *dbias, const float *mean, const float *rstd,
+                                       int64_t M, int64_t N, teeny_dtype dtype, teeny_stream stream) {
+  return norm_bwd_entry(dy, x, dx, weight, dweight, dbias, mean, rstd, M, N, false, dtype, stream,
+                        "layer_norm_backward");
+}
+
+teeny_status teeny_rms_norm_backward(const void *dy, const void *x, void *dx, const void *weight, float *dweight,
+                                     const float *rrms, int64_t M, int64_t N, teeny_dtype dtype,
+                                     teeny_stream stream) {
+  return norm_bwd_entry(dy, x, dx, weight, dweight, nullptr, rrms, nullptr, M, N, true, dtype, stream,
+                        "rms_norm_backward");
+}
+
+teeny_status teeny_norm_backward_workspace_size(int64_t M, int64_t N, int32_t is_rms, teeny_dtype dtype,
+                                                size_t *bytes) {
+  TEENY_REQUIRE(bytes != nullptr, TEENY_ERR_NULL_POINTER, "norm_backward_workspace_size: bytes");
+  *bytes = 0;
+  TEENY_REQUIRE(M >= 0 && N >= 0, TEENY_ERR_SHAPE_MISMATCH, "norm_backward_workspace_size: negative size");
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                "norm_backward_workspace_size: dtype must be F32 or BF16");
+  if (M == 0 || N == 0) return TEENY_OK;
+  // the row kernel's plan (aligned operands assumed); other shapes use no scratch
+  const int vpt = dtype == TEENY_F32 ? bwd_vpt<float>(N, true) : bwd_vpt<bf16>(N, true);
+  if (vpt > 0) *bytes = bwd_scratch_bytes(M, N, is_rms != 0);
+  return TEENY_OK;
+}
+
+}  // extern "C"

@@ -346,6 +346,28 @@ class Conv2dForward(RuntimeOp):
         tiles = -(-int(output_shape[3]) // self.block_ow)
         return (int(output_shape[0]) * int(output_shape[1]) * int(output_shape[2]) * tiles, 1, 1)
 
+    # training hooks (conv2d.rs:574-617): the combined conv2d_backward kernel
+    def has_backward(self) -> bool:
+        return True
+
+    def backward_entry_point_name(self) -> str:
+        return "conv2d_backward_entry_point"
+
+    def pack_backward_args(self, inputs, params, output, output_shape, grad_output,
+                           grad_output_row_stride, grad_inputs, grad_params, visitor):
+        """(dy, x, w, dx, dw, B, C_IN, C_OUT, H, W, OH, OW), conv2d.rs:581-608."""
+        ish = inputs[0][1]
+        visitor.visit_ptr(grad_output)
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(grad_inputs[0])
+        visitor.visit_ptr(grad_params[0])
+        for v in (ish[0], ish[1], output_shape[1], ish[2], ish[3], output_shape[2], output_shape[3]):
+            visitor.visit_i32(v)
+
+    def backward_grid(self, input_shapes, output_shape):
+        return self.grid(output_shape)
+
 
 class Conv2dBiasForward(Conv2dForward):
     """conv2d.rs:766-820: the conv2d_forward contract plus bias after w."""
@@ -743,6 +765,55 @@ def rms_norm(x: Buffer, weight: Buffer, eps: float = 1e-8, y: Optional[Buffer] =
     return y
 
 
+def layer_norm_train(x: Buffer, weight: Buffer, bias: Buffer, eps: float = 1e-5, y: Optional[Buffer] = None,
+                     mean: Optional[Buffer] = None, rstd: Optional[Buffer] = None,
+                     stream: Optional[Stream] = None):
+    """layernorm.rs:162-298: (y, mean fp32 [M], rstd fp32 [M])."""
+    m, n = norm_dims(x.shape, weight.shape, bias.shape)
+    y = _out(x, y)
+    mean = _out(x, mean, (m,), f32)
+    rstd = _out(x, rstd, (m,), f32)
+    check(lib.teeny_layer_norm_forward(x.ptr, y.ptr, weight.ptr, bias.ptr, mean.ptr, rstd.ptr, m, n, eps,
+                                       x.dtype.code, _h(stream)))
+    return y, mean, rstd
+
+
+def layer_norm_backward(dy: Buffer, x: Buffer, weight: Buffer, mean: Buffer, rstd: Buffer,
+                        dweight: Optional[Buffer] = None, dbias: Optional[Buffer] = None,
+                        dx: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """layernorm.rs:300-482: returns dx; dweight / dbias (fp32 [N]) accumulate in place."""
+    m, n = norm_dims(x.shape, weight.shape)
+    _need(dy.shape == x.shape and dy.dtype == x.dtype and weight.dtype == x.dtype, "layer_norm_backward: dy/x/weight")
+    _need(mean.numel == m and rstd.numel == m and mean.dtype == f32 and rstd.dtype == f32,
+          f"layer_norm_backward: mean/rstd fp32 [{m}]")
+    for g in (dweight, dbias):
+        _need(g is None or (g.numel == n and g.dtype == f32), f"layer_norm_backward: dweight/dbias fp32 [{n}]")
+    dx = _out(x, dx)
+    check(lib.teeny_layer_norm_backward(dy.ptr, x.ptr, dx.ptr, weight.ptr, dweight.ptr if dweight else None,
+                                        dbias.ptr if dbias else None, mean.ptr, rstd.ptr, m, n, x.dtype.code,
+                                        _h(stream)))
+    return dx
+
+
+def rms_norm_backward(dy: Buffer, x: Buffer, weight: Buffer, rrms: Buffer, dweight: Optional[Buffer] = None,
+                      dx: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """rmsnorm.rs:135-277: returns dx; dweight (fp32 [N]) accumulates in place."""
+    m, n = norm_dims(x.shape, weight.shape, None, rrms.shape)
+    _need(dy.shape == x.shape and dy.dtype == x.dtype and weight.dtype == x.dtype, "rms_norm_backward: dy/x/weight")
+    _need(rrms.dtype == f32 and (dweight is None or (dweight.numel == n and dweight.dtype == f32)),
+          "rms_norm_backward: rrms / dweight fp32")
+    dx = _out(x, dx)
+    check(lib.teeny_rms_norm_backward(dy.ptr, x.ptr, dx.ptr, weight.ptr, dweight.ptr if dweight else None, rrms.ptr,
+                                      m, n, x.dtype.code, _h(stream)))
+    return dx
+
+
+def norm_backward_workspace_size(m: int, n: int, rms: bool, dtype=bf16) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_norm_backward_workspace_size(m, n, int(bool(rms)), from_any(dtype).code, ctypes.byref(out)))
+    return int(out.value)
+
+
 ACTS = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "relu": _lib.ACT_RELU,
         "gelu": _lib.ACT_GELU_TANH, "gelu_tanh": _lib.ACT_GELU_TANH, "silu": _lib.ACT_SILU}
 
@@ -779,6 +850,46 @@ def conv2d(x: Buffer, w: Buffer, bias: Optional[Buffer] = None, stride=(1, 1), p
         check(lib.teeny_conv2d_bias_forward(x.ptr, w.ptr, bias.ptr, y.ptr, b, cin, cout, h, wd, oh,
                                             ow, ctypes.byref(prm), x.dtype.code, lay, _h(stream)))
     return y
+
+
+def _conv_bwd_args(x_shape, w_shape, stride, padding, groups, layout, dtype):
+    nhwc = layout.lower() == "nhwc"
+    geo = conv2d_dims(x_shape, w_shape, stride, padding, groups, "nhwc" if nhwc else "nchw")
+    b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw = geo
+    prm = _lib.Conv2dParams(kh, kw, sh, sw, ph, pw, groups, 0)
+    yshape = (b, oh, ow, cout) if nhwc else (b, cout, oh, ow)
+    return (b, cin, cout, h, wd, oh, ow), prm, _lib.NHWC if nhwc else _lib.NCHW, yshape
+
+
+def conv2d_backward_dx(dy: Buffer, w: Buffer, x_shape, stride=(1, 1), padding=(0, 0), groups: int = 1,
+                       layout: str = "nchw", dx: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """conv2d.rs:171-284: dx of x's shape from dy (y's shape) and w."""
+    dims, prm, lay, yshape = _conv_bwd_args(x_shape, w.shape, stride, padding, groups, layout, dy.dtype)
+    _need(tuple(dy.shape) == tuple(yshape) and w.dtype == dy.dtype, f"conv2d_backward_dx: dy must be {yshape}")
+    dx = _out(dy, dx, tuple(x_shape))
+    check(lib.teeny_conv2d_backward_dx(dy.ptr, w.ptr, dx.ptr, *dims, ctypes.byref(prm), dy.dtype.code, lay,
+                                       _h(stream)))
+    return dx
+
+
+def conv2d_backward_dw(dy: Buffer, x: Buffer, w_shape, stride=(1, 1), padding=(0, 0), groups: int = 1,
+                       layout: str = "nchw", dw: Optional[Buffer] = None, stream: Optional[Stream] = None) -> Buffer:
+    """conv2d.rs:286-397: dw of w's shape from dy and x."""
+    dims, prm, lay, yshape = _conv_bwd_args(x.shape, w_shape, stride, padding, groups, layout, dy.dtype)
+    _need(tuple(dy.shape) == tuple(yshape) and x.dtype == dy.dtype, f"conv2d_backward_dw: dy must be {yshape}")
+    dw = _out(dy, dw, tuple(w_shape))
+    check(lib.teeny_conv2d_backward_dw(dy.ptr, x.ptr, dw.ptr, *dims, ctypes.byref(prm), dy.dtype.code, lay,
+                                       _h(stream)))
+    return dw
+
+
+def conv2d_backward_workspace_size(x_shape, w_shape, stride=(1, 1), padding=(0, 0), groups: int = 1,
+                                   dtype=bf16, layout: str = "nhwc") -> int:
+    dims, prm, lay, _ = _conv_bwd_args(x_shape, w_shape, stride, padding, groups, layout, dtype)
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_conv2d_backward_workspace_size(*dims, ctypes.byref(prm), from_any(dtype).code, lay,
+                                                   ctypes.byref(out)))
+    return int(out.value)
 
 
 def conv2d_workspace_size(x_shape, w_shape, stride=(1, 1), padding=(0, 0), groups: int = 1,
