@@ -407,6 +407,44 @@ teeny_status teeny_attention_forward(const void *q, const void *k, const void *v
                                      int64_t n_ctx_k, int64_t head_dim, float softmax_scale,
                                      int32_t causal, teeny_dtype dtype, teeny_stream stream);
 
+/* Attention backward.  Reference: flash_attention2_backward_dq(q, k, v, o,
+ * do, l, dq, n_ctx_q, n_ctx_k, softmax_scale) with grid (n_ctx_q, BH, 1) and
+ * flash_attention2_backward_dkv(q, k, v, o, do, l, dk, dv, n_ctx_q, n_ctx_k,
+ * softmax_scale) with grid (n_ctx_k, BH, 1), kernels/teeny-kernels/src/nn/
+ * attention/flash_attn2.rs:173-447:
+ *   D_m = sum_d o[m,d] do[m,d],  p_mn = exp(scale q_m . k_n - l_m),
+ *   ds_mn = p_mn (do_m . v_n - D_m),
+ *   dq_m = scale sum_n ds_mn k_n,  dk_n = scale sum_m ds_mn q_m,
+ *   dv_n = sum_m p_mn do_m.
+ * Shapes and dtypes as the forward (l is the forward's fp32 logsumexp, `dout`
+ * the reference's do); `causal` as the forward (the reference is
+ * non-causal).  No atomics: each output row is written once.  bf16 with
+ * head_dim 64 / 128 and 16-byte aligned tensors runs on the MFMA kernels
+ * (dkv needs a stream workspace of teeny_attention_backward_workspace_size
+ * bytes for its D_m pre-pass, else it takes the per-row kernel); fp32 and
+ * any other head_dim in {16, 32, 64, 128, 256} run the reference's per-row
+ * structure. */
+teeny_status teeny_flash_attention2_backward_dq(const void *q, const void *k, const void *v, const void *o,
+                                                const void *dout, const float *l, void *dq, int64_t n_ctx_q,
+                                                int64_t n_ctx_k, float softmax_scale, int64_t BH, int64_t head_dim,
+                                                int32_t causal, teeny_dtype dtype, teeny_stream stream);
+teeny_status teeny_flash_attention2_backward_dkv(const void *q, const void *k, const void *v, const void *o,
+                                                 const void *dout, const float *l, void *dk, void *dv,
+                                                 int64_t n_ctx_q, int64_t n_ctx_k, float softmax_scale, int64_t BH,
+                                                 int64_t head_dim, int32_t causal, teeny_dtype dtype,
+                                                 teeny_stream stream);
+/* dq, dk and dv in one call, with grouped K/V heads as teeny_attention_forward
+ * (dk/dv of a K/V head sum over the query heads that share it).  It needs no
+ * workspace: without one, D_m is parked in dq's memory until the dq kernel
+ * overwrites it. */
+teeny_status teeny_attention_backward(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                                      const float *l, void *dq, void *dk, void *dv, int64_t batch, int64_t q_heads,
+                                      int64_t kv_heads, int64_t n_ctx_q, int64_t n_ctx_k, int64_t head_dim,
+                                      float softmax_scale, int32_t causal, teeny_dtype dtype, teeny_stream stream);
+/* batch * q_heads * n_ctx_q fp32 values (the D_m of every query row). */
+teeny_status teeny_attention_backward_workspace_size(int64_t batch, int64_t q_heads, int64_t n_ctx_q,
+                                                     size_t *bytes);
+
 /* ── int8 affine quantization (teeny-quant) ───────────────────────────────
  * Reference: quantize_affine(tensor, data, shape, granularity, symmetric,
  * bits) and dequantize_affine, utilities/teeny-quant/src/quant/affine.rs

@@ -150,6 +150,10 @@ _SIGS = {
     "teeny_conv2d_bias_forward_noalloc": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_flash_attention2_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
     "teeny_attention_forward": (S, [P, P, P, P, P] + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),
+    "teeny_flash_attention2_backward_dq": (S, [P] * 7 + [c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
+    "teeny_flash_attention2_backward_dkv": (S, [P] * 8 + [c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
+    "teeny_attention_backward": (S, [P] * 9 + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),
+    "teeny_attention_backward_workspace_size": (S, [c_int64, c_int64, c_int64, POINTER(c_size_t)]),
     "teeny_quant_num_groups": (S, [POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, POINTER(c_int64)]),
     "teeny_quantize_affine": (S, [P, POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, c_int32, c_int32, P, P, P, P, P]),
     "teeny_dequantize_affine": (S, [P, P, P, POINTER(c_int64), c_int32, c_int32, c_int32, c_int64, P, P]),

@@ -763,10 +763,15 @@ static teeny_status conv_bwd_entry(const void *dy, const void *x, const void *w,
                 std::string(name) + ": dtype must be F32 or BF16");
   TEENY_REQUIRE(static_cast<int64_t>(Cout) * (Cin / prm->groups) * prm->KH * prm->KW <= 0x7fffffff,
                 TEENY_ERR_SHAPE_MISMATCH, std::string(name) + ": weight too large");
-  if (B == 0) return TEENY_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0) {  // an empty batch: dx is empty, dw = 0 (a sum over no pixels)
+    if (dw == nullptr) return TEENY_OK;
+    if (dtype == TEENY_F32) launch_dw_direct<float>(dy, x, dw, q, s);
+    else launch_dw_direct<bf16>(dy, x, dw, q, s);
+    return after_launch(name, s);
+  }
   TEENY_REQUIRE(dy != nullptr && (dx == nullptr || w != nullptr) && (dw == nullptr || x != nullptr),
                 TEENY_ERR_NULL_POINTER, std::string(name) + ": dy/w/x");
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const bool nhwc = layout == TEENY_NHWC;
   if (dx != nullptr) {
     if (!(dtype == TEENY_BF16 && nhwc && conv_dx_mfma(dy, w, dx, q, s, stream_scratch(s)))) {

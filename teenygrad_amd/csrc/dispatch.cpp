@@ -280,5 +280,99 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
                                 syn, dtype, stream);
   }
 
+  // ── training kernels ──
+  // layer_norm_forward<BLOCK_N>(x, y, weight, bias, mean, rstd, M, N, eps)        layernorm.rs:163-172
+  // layer_norm_backward<BLOCK_N>(dy, x, dx, weight, dweight, dbias, mean, rstd, M, N)  :301-311
+  // rms_norm_backward<BLOCK_N>(dy, x, dx, weight, dweight, rrms, M, N)            rmsnorm.rs:136-144
+  // The statistics and parameter gradients are fp32 buffers for every dtype.
+  if (name_is(entry_point, "layer_norm_forward")) {
+    TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT, "layer_norm_forward: expects const generic BLOCK_N");
+    void *x = r.ptr("x"), *y = r.ptr("y"), *w = r.ptr("weight"), *b = r.ptr("bias"), *mean = r.ptr("mean"),
+         *rstd = r.ptr("rstd");
+    int64_t M = r.i32("M"), N = r.i32("N");
+    float eps = r.f32("eps");
+    if (r.done() != TEENY_OK) return r.st;
+    return teeny_layer_norm_forward(x, y, w, b, static_cast<float *>(mean), static_cast<float *>(rstd), M, N, eps,
+                                    dtype, stream);
+  }
+  if (name_is(entry_point, "layer_norm_backward")) {
+    TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT, "layer_norm_backward: expects const generic BLOCK_N");
+    void *dy = r.ptr("dy"), *x = r.ptr("x"), *dx = r.ptr("dx"), *w = r.ptr("weight"), *dw = r.ptr("dweight"),
+         *db = r.ptr("dbias"), *mean = r.ptr("mean"), *rstd = r.ptr("rstd");
+    int64_t M = r.i32("M"), N = r.i32("N");
+    if (r.done() != TEENY_OK) return r.st;
+    return teeny_layer_norm_backward(dy, x, dx, w, static_cast<float *>(dw), static_cast<float *>(db),
+                                     static_cast<const float *>(mean), static_cast<const float *>(rstd), M, N, dtype,
+                                     stream);
+  }
+  if (name_is(entry_point, "rms_norm_backward")) {
+    TEENY_REQUIRE(n_cg == 1, TEENY_ERR_INVALID_ARGUMENT, "rms_norm_backward: expects const generic BLOCK_N");
+    void *dy = r.ptr("dy"), *x = r.ptr("x"), *dx = r.ptr("dx"), *w = r.ptr("weight"), *dw = r.ptr("dweight"),
+         *rr = r.ptr("rrms");
+    int64_t M = r.i32("M"), N = r.i32("N");
+    if (r.done() != TEENY_OK) return r.st;
+    return teeny_rms_norm_backward(dy, x, dx, w, static_cast<float *>(dw), static_cast<const float *>(rr), M, N,
+                                   dtype, stream);
+  }
+
+  // conv2d_backward_dx<KH,KW,SH,SW,PH,PW,G,BLOCK_OW>(dy, w, dx, B, C_IN, C_OUT, H, W, OH, OW)  conv2d.rs:172-196
+  // conv2d_backward_dw<...>(dy, x, dw, B, C_IN, C_OUT, H, W, OH, OW)                         :287-311
+  // conv2d_backward<...>(dy, x, w, dx, dw, B, C_IN, C_OUT, H, W, OH, OW)  (the Conv2d RuntimeOp's
+  //   backward kernel, :400-425, :574-617); NCHW as conv2d_forward.
+  const bool cbx = name_is(entry_point, "conv2d_backward_dx");
+  const bool cbw = name_is(entry_point, "conv2d_backward_dw");
+  const bool cb = name_is(entry_point, "conv2d_backward");
+  if (cbx || cbw || cb) {
+    TEENY_REQUIRE(n_cg == 8, TEENY_ERR_INVALID_ARGUMENT,
+                  std::string(entry_point) + ": expects const generics KH,KW,STRIDE_H,STRIDE_W,PAD_H,PAD_W,G,BLOCK_OW");
+    teeny_conv2d_params p;
+    p.KH = static_cast<int32_t>(cg[0]);
+    p.KW = static_cast<int32_t>(cg[1]);
+    p.stride_h = static_cast<int32_t>(cg[2]);
+    p.stride_w = static_cast<int32_t>(cg[3]);
+    p.pad_h = static_cast<int32_t>(cg[4]);
+    p.pad_w = static_cast<int32_t>(cg[5]);
+    p.groups = static_cast<int32_t>(cg[6]);
+    p.act = TEENY_ACT_NONE;
+    void *dy = r.ptr("dy_ptr");
+    void *x = cbx ? nullptr : r.ptr("x_ptr");
+    void *w = cbw ? nullptr : r.ptr("w_ptr");
+    void *dx = cbw ? nullptr : r.ptr("dx_ptr");
+    void *dw = cbx ? nullptr : r.ptr("dw_ptr");
+    int64_t B = r.i32("B"), Ci = r.i32("C_IN"), Co = r.i32("C_OUT"), H = r.i32("H"), W = r.i32("W"),
+            OH = r.i32("OH"), OW = r.i32("OW");
+    if (r.done() != TEENY_OK) return r.st;
+    if (cbx) return teeny_conv2d_backward_dx(dy, w, dx, B, Ci, Co, H, W, OH, OW, &p, dtype, TEENY_NCHW, stream);
+    if (cbw) return teeny_conv2d_backward_dw(dy, x, dw, B, Ci, Co, H, W, OH, OW, &p, dtype, TEENY_NCHW, stream);
+    return teeny_conv2d_backward(dy, x, w, dx, dw, B, Ci, Co, H, W, OH, OW, &p, dtype, TEENY_NCHW, stream);
+  }
+
+  // flash_attention2_backward_dq<HEAD_DIM[, CAUSAL]>(q, k, v, o, do, l, dq, n_ctx_q, n_ctx_k,
+  //   softmax_scale), grid (n_ctx_q, BH, 1)                           flash_attn2.rs:174-185
+  // flash_attention2_backward_dkv<HEAD_DIM[, CAUSAL]>(q, k, v, o, do, l, dk, dv, n_ctx_q,
+  //   n_ctx_k, softmax_scale), grid (n_ctx_k, BH, 1)                   :312-324
+  const bool fdq = name_is(entry_point, "flash_attention2_backward_dq");
+  const bool fdkv = name_is(entry_point, "flash_attention2_backward_dkv");
+  if (fdq || fdkv) {
+    TEENY_REQUIRE(n_cg == 1 || n_cg == 2, TEENY_ERR_INVALID_ARGUMENT,
+                  std::string(entry_point) + ": expects const generics HEAD_DIM[, CAUSAL]");
+    TEENY_REQUIRE(grid != nullptr, TEENY_ERR_NULL_POINTER, std::string(entry_point) + ": grid (BH = grid[1])");
+    void *q = r.ptr("q_ptr"), *k = r.ptr("k_ptr"), *v = r.ptr("v_ptr"), *o = r.ptr("o_ptr"), *d_o = r.ptr("do_ptr"),
+         *l = r.ptr("l_ptr");
+    void *g0 = r.ptr(fdq ? "dq_ptr" : "dk_ptr");
+    void *g1 = fdkv ? r.ptr("dv_ptr") : nullptr;
+    int64_t nq = r.i32("n_ctx_q"), nk = r.i32("n_ctx_k");
+    float scale = r.f32("softmax_scale");
+    if (r.done() != TEENY_OK) return r.st;
+    TEENY_REQUIRE(grid[0] == static_cast<uint32_t>(fdq ? nq : nk), TEENY_ERR_SHAPE_MISMATCH,
+                  std::string(entry_point) + (fdq ? ": grid[0] must equal n_ctx_q" : ": grid[0] must equal n_ctx_k"));
+    const int32_t causal = n_cg == 2 && cg[1] != 0 ? 1 : 0;
+    if (fdq)
+      return teeny_flash_attention2_backward_dq(q, k, v, o, d_o, static_cast<const float *>(l), g0, nq, nk, scale,
+                                                grid[1], cg[0], causal, dtype, stream);
+    return teeny_flash_attention2_backward_dkv(q, k, v, o, d_o, static_cast<const float *>(l), g0, g1, nq, nk, scale,
+                                               grid[1], cg[0], causal, dtype, stream);
+  }
+
   return fail(TEENY_ERR_NOT_FOUND, std::string("dispatch: no operator for ") + entry_point);
 }

@@ -951,6 +951,57 @@ def attention(q: Buffer, k: Buffer, v: Buffer, q_heads: int, kv_heads: int,
     return o
 
 
+def attention_backward(q: Buffer, k: Buffer, v: Buffer, o: Buffer, do: Buffer, lse: Buffer,
+                       q_heads: int = 1, kv_heads: int = 1, softmax_scale: Optional[float] = None,
+                       causal: bool = False, dq: Optional[Buffer] = None, dk: Optional[Buffer] = None,
+                       dv: Optional[Buffer] = None, stream: Optional[Stream] = None):
+    """flash_attn2.rs:173-447: (dq, dk, dv) from the forward's o and lse (fp32
+    logsumexp); q/o/do [B*q_heads, Nq, D], k/v [B*kv_heads, Nk, D]."""
+    _need(len(q.shape) == 3 and len(k.shape) == 3 and tuple(k.shape) == tuple(v.shape),
+          "attention_backward: q [B*Hq, Nq, D], k/v [B*Hkv, Nk, D]")
+    _need(q_heads > 0 and kv_heads > 0 and q_heads % kv_heads == 0, "attention_backward: q_heads % kv_heads != 0")
+    bhq, nq, d = q.shape
+    _need(bhq % q_heads == 0, "attention_backward: q's first dim must be B * q_heads")
+    batch = bhq // q_heads
+    _need(k.shape[0] == batch * kv_heads and k.shape[2] == d, "attention_backward: k/v must be [B*kv_heads, Nk, D]")
+    _need(tuple(o.shape) == tuple(q.shape) and tuple(do.shape) == tuple(q.shape), "attention_backward: o/do like q")
+    _need(all(t.dtype == q.dtype for t in (k, v, o, do)), "attention_backward: dtypes differ")
+    _need(lse.numel == bhq * nq and lse.dtype == f32, "attention_backward: lse fp32 [B*q_heads, Nq]")
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    dq, dk, dv = _out(q, dq), _out(k, dk), _out(v, dv)
+    check(lib.teeny_attention_backward(q.ptr, k.ptr, v.ptr, o.ptr, do.ptr, lse.ptr, dq.ptr, dk.ptr, dv.ptr, batch,
+                                       q_heads, kv_heads, nq, k.shape[1], d, scale, int(bool(causal)),
+                                       q.dtype.code, _h(stream)))
+    return dq, dk, dv
+
+
+def flash_attention_backward_dq(q, k, v, o, do, lse, softmax_scale=None, causal=False, dq=None, stream=None):
+    """flash_attention2_backward_dq (flash_attn2.rs:173-310): [BH, N, D] tensors."""
+    bh, nq, nk, d = attention_dims(q.shape, k.shape, v.shape, lse.shape)
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    dq = _out(q, dq)
+    check(lib.teeny_flash_attention2_backward_dq(q.ptr, k.ptr, v.ptr, o.ptr, do.ptr, lse.ptr, dq.ptr, nq, nk, scale,
+                                                 bh, d, int(bool(causal)), q.dtype.code, _h(stream)))
+    return dq
+
+
+def flash_attention_backward_dkv(q, k, v, o, do, lse, softmax_scale=None, causal=False, dk=None, dv=None,
+                                 stream=None):
+    """flash_attention2_backward_dkv (flash_attn2.rs:312-447): [BH, N, D] tensors."""
+    bh, nq, nk, d = attention_dims(q.shape, k.shape, v.shape, lse.shape)
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    dk, dv = _out(k, dk), _out(v, dv)
+    check(lib.teeny_flash_attention2_backward_dkv(q.ptr, k.ptr, v.ptr, o.ptr, do.ptr, lse.ptr, dk.ptr, dv.ptr, nq,
+                                                  nk, scale, bh, d, int(bool(causal)), q.dtype.code, _h(stream)))
+    return dk, dv
+
+
+def attention_backward_workspace_size(batch: int, q_heads: int, n_ctx_q: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_attention_backward_workspace_size(batch, q_heads, n_ctx_q, ctypes.byref(out)))
+    return int(out.value)
+
+
 GRANULARITY = {"tensor": _lib.PER_TENSOR, "channel": _lib.PER_CHANNEL, "group": _lib.GROUP}
 
 

@@ -40,6 +40,18 @@ def check_bf16(got_bits, ref32, what=""):
     return float(err.max())
 
 
+def check_bf16_normwise(got_bits, ref32, what="", rel=8e-3):
+    """bf16 output against the fp32 oracle, norm-wise: ||got - ref||_inf <=
+    rel * ||ref||_inf (8e-3 is two bf16 ulps of the largest value), for
+    outputs whose values can be small next to the 2e-2 absolute bound."""
+    got = from_bf16(got_bits).astype(np.float64).reshape(-1)
+    ref = np.asarray(ref32, dtype=np.float64).reshape(-1)
+    scale = max(float(np.max(np.abs(ref))), 1e-30)
+    e = float(np.max(np.abs(got - ref))) / scale
+    assert e <= rel, f"{what}: norm-wise relative error {e:.3g} > {rel} (max |ref| {scale:.3g})"
+    return e
+
+
 def check_f32(got, ref, what="", rel=F32_REL):
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     ref = np.asarray(ref, dtype=np.float64).reshape(-1)

@@ -331,3 +331,63 @@ def test_graph_capture_errors():
     expect(lib.teeny_hip_stream_end_capture(FAKE, None), _lib.ERR_NULL_POINTER)
     expect(lib.teeny_hip_graph_launch(None, None), _lib.ERR_NULL_POINTER)
     assert lib.teeny_hip_graph_destroy(None) == _lib.OK
+
+
+def test_training_kernel_errors():
+    lf = lib.teeny_layer_norm_forward
+    expect(lf(FAKE, FAKE, FAKE, FAKE, None, FAKE, 4, 8, 1e-5, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    lb = lib.teeny_layer_norm_backward
+    expect(lb(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None, 4, 8, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 0, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, -1, 8, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 8, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    assert lb(None, None, None, None, None, None, None, None, 0, 8, _lib.F32, None) == _lib.OK
+    rb = lib.teeny_rms_norm_backward
+    expect(rb(FAKE, FAKE, FAKE, None, None, FAKE, 4, 8, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    size = ctypes.c_size_t(123)
+    assert lib.teeny_norm_backward_workspace_size(100, 4096, 0, _lib.BF16, ctypes.byref(size)) == _lib.OK
+    assert size.value > 0 and size.value % (4096 * 4) == 0
+    assert lib.teeny_norm_backward_workspace_size(100, 4095, 1, _lib.BF16, ctypes.byref(size)) == _lib.OK
+    assert size.value == 0  # no register plan for a ragged row: no scratch either
+    expect(lib.teeny_norm_backward_workspace_size(1, 8, 0, _lib.F32, None), _lib.ERR_NULL_POINTER)
+
+    cbx, cbw, cb = lib.teeny_conv2d_backward_dx, lib.teeny_conv2d_backward_dw, lib.teeny_conv2d_backward
+    expect(cbx(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 7, 8, conv_params(), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_SHAPE_MISMATCH)
+    expect(cbx(None, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_NULL_POINTER)
+    expect(cbw(FAKE, None, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, _lib.NCHW, None),
+           _lib.ERR_NULL_POINTER)
+    expect(cb(FAKE, FAKE, None, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, _lib.NHWC, None),
+           _lib.ERR_NULL_POINTER)
+    expect(cbw(FAKE, FAKE, FAKE, 1, 4, 4, 8, 8, 8, 8, conv_params(), _lib.I8, _lib.NCHW, None),
+           _lib.ERR_UNSUPPORTED_DTYPE)
+    # an empty batch: nothing to write for dx (dw would be zero-filled on a device)
+    assert cbx(None, None, FAKE, 0, 4, 4, 8, 8, 8, 8, conv_params(), _lib.F32, _lib.NCHW, None) == _lib.OK
+    assert lib.teeny_conv2d_backward_workspace_size(2, 64, 128, 14, 14, 14, 14, conv_params(), _lib.BF16,
+                                                    _lib.NHWC, ctypes.byref(size)) == _lib.OK
+    assert size.value >= 128 * 9 * 64 * 2  # the flipped weights at least
+    assert lib.teeny_conv2d_backward_workspace_size(2, 64, 128, 14, 14, 14, 14, conv_params(), _lib.F32,
+                                                    _lib.NCHW, ctypes.byref(size)) == _lib.OK
+    assert size.value == 0
+
+
+def test_attention_backward_errors():
+    dq, dkv = lib.teeny_flash_attention2_backward_dq, lib.teeny_flash_attention2_backward_dkv
+    ab = lib.teeny_attention_backward
+    args6 = (FAKE,) * 6
+    expect(dq(*args6, None, 8, 8, 0.125, 4, 64, 0, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(dq(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 8, 8, 0.125, 4, 64, 0, _lib.F32, None),
+           _lib.ERR_NULL_POINTER)
+    expect(dkv(*args6, FAKE, None, 8, 8, 0.125, 4, 64, 0, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(dq(*args6, FAKE, 8, 8, 0.125, 4, 48, 0, _lib.F32, None), _lib.ERR_UNSUPPORTED)
+    expect(dq(*args6, FAKE, 8, 8, 0.125, 4, 64, 0, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    expect(dq(*args6, FAKE, 8, 0, 0.125, 4, 64, 0, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(dq(*args6, FAKE, -1, 8, 0.125, 4, 64, 0, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(ab(*args6, FAKE, FAKE, FAKE, 2, 6, 4, 8, 8, 64, 0.125, 0, _lib.BF16, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(ab(*args6, FAKE, None, FAKE, 2, 4, 2, 8, 8, 64, 0.125, 0, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    assert ab(*args6, FAKE, FAKE, FAKE, 0, 4, 2, 8, 8, 64, 0.125, 0, _lib.BF16, None) == _lib.OK
+    size = ctypes.c_size_t(0)
+    assert lib.teeny_attention_backward_workspace_size(2, 8, 1000, ctypes.byref(size)) == _lib.OK
+    assert size.value == 2 * 8 * 1000 * 4
+    expect(lib.teeny_attention_backward_workspace_size(2, 8, 10, None), _lib.ERR_NULL_POINTER)

@@ -253,3 +253,16 @@ def test_conv_backward_combined_and_dispatch_hooks(dev, orc):
     check_f32(dw.to_host(), orc.conv2d_backward_dw(dy, x, w.shape, 1, 1), "dw")
     op = K.Conv2dForward(3, 3, 1, 1, 1, 1)
     assert op.has_backward()
+
+
+def test_conv_backward_empty_batch_zeroes_dw(dev):
+    # no images: dw is the sum over no pixels, written as zeros
+    w_shape = (8, 4, 3, 3)
+    dw = dev.upload(np.full(w_shape, 5.0, np.float32))
+    dy, x = tg.Buffer(tg.f32, (1, 8, 6, 6)), tg.Buffer(tg.f32, (1, 4, 6, 6))
+    import ctypes
+    from teenygrad_amd import _lib
+    prm = _lib.Conv2dParams(3, 3, 1, 1, 1, 1, 1, 0)
+    tg.check(_lib.lib.teeny_conv2d_backward_dw(dy.ptr, x.ptr, dw.ptr, 0, 4, 8, 6, 6, 6, 6, ctypes.byref(prm),
+                                               _lib.F32, _lib.NCHW, None))
+    np.testing.assert_array_equal(dw.to_host(), 0.0)

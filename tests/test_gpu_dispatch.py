@@ -211,3 +211,151 @@ def test_quantize_dequantize_dispatch(dev, orc, gran, axis, gs, sym):
     out = tg.Buffer(tg.f32, shape)
     K.DequantizeAffineRuntimeOp(gran, axis, gs).launch([(qb, shape)], [sb, zb], out, shape, tg.f32)
     np.testing.assert_array_equal(out.to_host(), orc.dequantize_affine(oq, os_, oz, shape, gran, axis, gs))
+
+
+# ── training kernels through teeny_dispatch ────────────────────────────────
+
+
+def _dispatch(name, cgs, fill, grid, dtype=tg.f32):
+    import ctypes
+    from teenygrad_amd._lib import check, lib
+    packer = K.DispatchPacker()
+    fill(packer)
+    args, n = packer.array()
+    cg = (ctypes.c_int64 * max(1, len(cgs)))(*cgs)
+    g = (ctypes.c_uint32 * 3)(*grid)
+    check(lib.teeny_dispatch(name.encode(), cg, len(cgs), args, n, g, dtype.code, None))
+
+
+@pytest.mark.parametrize("case,pad,oh", [("conv2d", 0, 6), ("conv2d_padded", 1, 8)])
+def test_conv2d_backward_hooks(dev, case, pad, oh):
+    # Conv2dForward's pack_backward_args + backward_grid through
+    # "conv2d_backward_entry_point" (conv2d.rs:574-617), against test_conv2d.rs's
+    # backward fixtures; then the separate dx / dw kernels (conv2d.rs:172-311)
+    x = load_golden(f"{case}/x.bin").reshape(1, 2, 8, 8)
+    w = load_golden(f"{case}/w.bin").reshape(4, 2, 3, 3)
+    dy = load_golden(f"{case}/dy.bin").reshape(1, 4, oh, oh)
+    want_dx = load_golden(f"{case}/expected_dx.bin").reshape(x.shape)
+    want_dw = load_golden(f"{case}/expected_dw.bin").reshape(w.shape)
+    xb, wb, dyb = dev.upload(x), dev.upload(w), dev.upload(dy)
+    dx, dw = tg.Buffer(tg.f32, x.shape), tg.Buffer(tg.f32, w.shape)
+    op = K.Conv2dForward(3, 3, 1, 1, pad, pad)
+    yshape = [1, 4, oh, oh]
+    _dispatch(op.backward_entry_point_name(), op.const_generics(),
+              lambda p: op.pack_backward_args([(xb, list(x.shape))], [wb], None, yshape, dyb, oh, [dx], [dw], p),
+              op.backward_grid([list(x.shape)], yshape))
+    assert np.max(np.abs(dx.to_host() - want_dx)) < 1e-4
+    assert np.max(np.abs(dw.to_host() - want_dw)) < 1e-3
+    dx2, dw2 = tg.Buffer(tg.f32, x.shape), tg.Buffer(tg.f32, w.shape)
+    dims = (1, 2, 4, 8, 8, oh, oh)
+
+    def fill_dx(p):
+        for b in (dyb, wb, dx2):
+            p.visit_ptr(b)
+        for d in dims:
+            p.visit_i32(d)
+
+    def fill_dw(p):
+        for b in (dyb, xb, dw2):
+            p.visit_ptr(b)
+        for d in dims:
+            p.visit_i32(d)
+
+    _dispatch("conv2d_backward_dx_entry_point", op.const_generics(), fill_dx, op.grid(yshape))
+    _dispatch("conv2d_backward_dw_entry_point", op.const_generics(), fill_dw, op.grid(yshape))
+    np.testing.assert_array_equal(dx2.to_host(), dx.to_host())
+    np.testing.assert_array_equal(dw2.to_host(), dw.to_host())
+
+
+def test_layer_norm_training_dispatch(dev, orc):
+    # layer_norm_forward (layernorm.rs:163-172) and layer_norm_backward (:301-311)
+    # on the reference's layernorm fixture inputs
+    from gpu_util import check_f32
+    x = load_golden("layernorm/x.bin")
+    w, b = load_golden("layernorm/weight.bin"), load_golden("layernorm/bias.bin")
+    n = w.size
+    m = x.size // n
+    dy = np.random.default_rng(5).normal(0, 1, x.size).astype(np.float32)
+    xb, wb, bb, dyb = (dev.upload(a) for a in (x, w, b, dy))
+    y, mean, rstd = tg.Buffer(tg.f32, (x.size,)), tg.Buffer(tg.f32, (m,)), tg.Buffer(tg.f32, (m,))
+
+    def fill_fwd(p):
+        for t in (xb, y, wb, bb, mean, rstd):
+            p.visit_ptr(t)
+        p.visit_i32(m)
+        p.visit_i32(n)
+        p.visit_f32(1e-5)
+
+    _dispatch("layer_norm_forward_entry_point", (1024,), fill_fwd, (m, 1, 1))
+    np.testing.assert_allclose(y.to_host(), load_golden("layernorm/expected_forward.bin"), atol=1e-4)
+    ry, rmean, rrstd = orc.layer_norm_train(x.reshape(m, n), w, b, 1e-5)
+    check_f32(mean.to_host(), rmean, "mean")
+    check_f32(rstd.to_host(), rrstd, "rstd")
+    dx, dwt, dbt = tg.Buffer(tg.f32, (x.size,)), dev.upload(np.zeros(n, np.float32)), dev.upload(
+        np.zeros(n, np.float32))
+
+    def fill_bwd(p):
+        for t in (dyb, xb, dx, wb, dwt, dbt, mean, rstd):
+            p.visit_ptr(t)
+        p.visit_i32(m)
+        p.visit_i32(n)
+
+    _dispatch("layer_norm_backward_entry_point", (1024,), fill_bwd, (m, 1, 1))
+    rdx, rdw, rdb = orc.layer_norm_backward(dy.reshape(m, n), x.reshape(m, n), w, rmean, rrstd)
+    check_f32(dx.to_host(), rdx, "dx")
+    check_f32(dwt.to_host(), rdw, "dweight")
+    check_f32(dbt.to_host(), rdb, "dbias")
+
+
+def test_rms_norm_backward_dispatch(dev, orc):
+    # rms_norm_backward (rmsnorm.rs:136-144) from the fixture's rrms
+    from gpu_util import check_f32
+    x, w = load_golden("rmsnorm/x.bin"), load_golden("rmsnorm/weight.bin")
+    rrms = load_golden("rmsnorm/expected_rrms.bin")
+    n, m = w.size, rrms.size
+    dy = np.random.default_rng(6).normal(0, 1, x.size).astype(np.float32)
+    xb, wb, rb_, dyb = (dev.upload(a) for a in (x, w, rrms, dy))
+    dx, dwt = tg.Buffer(tg.f32, (x.size,)), dev.upload(np.zeros(n, np.float32))
+
+    def fill(p):
+        for t in (dyb, xb, dx, wb, dwt, rb_):
+            p.visit_ptr(t)
+        p.visit_i32(m)
+        p.visit_i32(n)
+
+    _dispatch("rms_norm_backward_entry_point", (1024,), fill, (m, 1, 1))
+    rdx, rdw = orc.rms_norm_backward(dy.reshape(m, n), x.reshape(m, n), w, rrms)
+    check_f32(dx.to_host(), rdx, "dx")
+    check_f32(dwt.to_host(), rdw, "dweight")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_attention_backward_dispatch(dev, orc, causal):
+    # flash_attention2_backward_dq / _dkv (flash_attn2.rs:174-185, :312-324) with the
+    # reference grids (n_ctx_q, BH, 1) / (n_ctx_k, BH, 1); the reference fixture
+    # (non-causal) and the oracle
+    from gpu_util import check_f32
+    shape = (4, 8, 64)
+    q, k, v, do = (load_golden(f"flash_attn2/{n}.bin").reshape(shape) for n in ("q", "k", "v", "do"))
+    o, l = orc.flash_attention(q, k, v, 0.125, causal)
+    bufs = [dev.upload(a) for a in (q, k, v, o, do, l)]
+    dq, dk, dv = (tg.Buffer(tg.f32, shape) for _ in range(3))
+    cgs = (64, 1) if causal else (64,)
+
+    def fill(outs):
+        def f(p):
+            for t in bufs + outs:
+                p.visit_ptr(t)
+            p.visit_i32(8)
+            p.visit_i32(8)
+            p.visit_f32(0.125)
+        return f
+
+    _dispatch("flash_attention2_backward_dq_entry_point", cgs, fill([dq]), (8, 4, 1))
+    _dispatch("flash_attention2_backward_dkv_entry_point", cgs, fill([dk, dv]), (8, 4, 1))
+    rq, rk, rv = orc.flash_attention_backward(q, k, v, o, do, l, 0.125, causal)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        g = got.to_host()
+        check_f32(g, ref, name)
+        if not causal:
+            assert np.max(np.abs(g - load_golden(f"flash_attn2/expected_backward_{name}.bin").reshape(shape))) < 1e-3
