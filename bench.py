@@ -581,6 +581,178 @@ def bench_conv_f32(ctx):
             "cpu_baseline": cpu}
 
 
+# ── training kernels (backward passes) ──────────────────────────────────────
+
+
+def bench_norm_backward(ctx):
+    """LayerNorm and RMSNorm backward on the norm workload's shape: dy, x in,
+    dx out (bf16), fp32 statistics in and fp32 parameter gradients, with the
+    stream workspace (per-workgroup column partials)."""
+    from teenygrad_amd import kernels as K
+    from teenygrad_amd import synthetic
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
+    x, g1, b1, g2 = norm_inputs()
+    dy = round_bf16(synthetic.normal(synthetic.workload_seed(1, 4), (NORM_M, NORM_N)))
+    R = 3
+    xb, dyb = ctx.copies(upload_bf16(ctx, x), R), ctx.copies(upload_bf16(ctx, dy), R)
+    g1b, b1b, g2b = (upload_bf16(ctx, a) for a in (g1, b1, g2))
+    _, mean, rstd = K.layer_norm_train(xb[0], g1b, b1b, 1e-5, stream=stream)
+    rrms = tg.Buffer(tg.f32, (NORM_M,))
+    K.rms_norm(xb[0], g2b, 1e-8, rrms=rrms, stream=stream)
+    shape = (NORM_M, NORM_N)
+    dxl, dxr = ([tg.Buffer(tg.bf16, shape) for _ in range(R)] for _ in range(2))
+    dw1, db1, dw2 = (tg.Buffer(tg.f32, (NORM_N,)).zero_(stream) for _ in range(3))
+    ws = attach_workspace(ctx, [K.norm_backward_workspace_size(NORM_M, NORM_N, False)])
+    io = 3 * NORM_M * NORM_N * 2  # read dy and x, write dx (bf16)
+    bytes_of = {"layer_norm_backward": io + NORM_N * 2 + 8 * NORM_M + 16 * NORM_N,
+                "rms_norm_backward": io + NORM_N * 2 + 4 * NORM_M + 8 * NORM_N}
+    ops = [("layer_norm_backward", [lambda r=r: K.layer_norm_backward(dyb[r], xb[r], g1b, mean, rstd, dw1, db1,
+                                                                      dx=dxl[r], stream=stream) for r in range(R)]),
+           ("rms_norm_backward", [lambda r=r: K.rms_norm_backward(dyb[r], xb[r], g2b, rrms, dw2, dx=dxr[r],
+                                                                  stream=stream) for r in range(R)])]
+    ms, per = ctx.measure(ops)
+    step_bytes = sum(bytes_of.values())
+    value = step_bytes / (ms * 1e-3) / 1e9
+    roof = roofline_bytes("norm_backward", "layer_norm_backward", bytes_of["layer_norm_backward"],
+                          per["layer_norm_backward"])
+    opsd = {k: {"us": round(v * 1e3, 2), "GB/s": round(bytes_of[k] / (v * 1e-3) / 1e9, 1),
+                "frac": round(bytes_of[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "traffic": load_traffic("norm_backward", k)} for k, v in per.items()}
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        _, om, orr = oracle.layer_norm_train(x, g1, b1, 1e-5)
+        _, orrms = oracle.rms_norm(x, g2, 1e-8)
+
+        def run():
+            oracle.layer_norm_backward(dy, x, g1, om, orr)
+            oracle.rms_norm_backward(dy, x, g2, orrms)
+
+        cs = cpu_time(run)
+        cpu = cpu_entry(round(step_bytes / cs / 1e9, 2), "GB/s", cs,
+                        "both backward kernels on the full [16384, 4096] in fp32 on the bf16-rounded inputs; bytes "
+                        "counted as bf16 like the GPU line", value)
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "norm backward: dy, x [16384,4096] bf16 -> dx bf16, dweight/dbias fp32 "
+                                   "(LayerNorm, RMSNorm)", "bytes_per_step": step_bytes, "workspace_bytes": ws},
+            "roofline": roof, "cpu_baseline": cpu, "ops": opsd}
+
+
+def bench_attention_backward(ctx, s, causal):
+    """dq, dk, dv of SDPA at the attention workload's shape (B=8, H=32, D=128)
+    from the forward's o and lse.  Algorithmic flops: the five S^2 D products
+    of the flash backward (S, dP, dV, dK, dQ), 2.5x the forward's."""
+    from teenygrad_amd import kernels as K
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
+    bh, d = 256, 128
+    rng = np.random.default_rng(0x7EE70012)
+    host = [round_bf16(rng.standard_normal((bh, s, d), dtype=np.float32)) for _ in range(4)]
+    q, k, v, do = (upload_bf16(ctx, a) for a in host)
+    o = tg.Buffer(tg.bf16, (bh, s, d))
+    lse = tg.Buffer(tg.f32, (bh, s))
+    K.flash_attention(q, k, v, None, causal, o=o, lse=lse, stream=stream)
+    dq, dk, dv = (tg.Buffer(tg.bf16, (bh, s, d)) for _ in range(3))
+    ws = attach_workspace(ctx, [K.attention_backward_workspace_size(bh, 1, s)])
+    flops = 10.0 * bh * s * s * d * (0.5 if causal else 1.0)
+    name = f"attention_backward_bf16_{'causal_' if causal else ''}s{s}"
+    workload = f"attention_backward_{'causal_' if causal else ''}s{s}"
+    ms, per = ctx.measure([(name, [lambda: K.attention_backward(q, k, v, o, do, lse, causal=causal, dq=dq, dk=dk,
+                                                                dv=dv, stream=stream)])])
+    value = flops / (ms * 1e-3) / 1e12
+    nbytes = 8 * bh * s * d * 2 + bh * s * 4
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        nh = math.ceil(CPU_PREFIX * bh)
+        qh, kh, vh, doh = (np.ascontiguousarray(a[:nh]) for a in host)
+        oh, lh = oracle.flash_attention(qh, kh, vh, None, causal)
+        cs = cpu_time(lambda: oracle.flash_attention_backward(qh, kh, vh, oh, doh, lh, None, causal))
+        frac = nh / bh
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: {nh} of {bh} (batch, head) pairs, all {s} rows ({frac:.2%} of both "
+                        f"grids), fp32; scaled x{bh / nh:.2f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": f"sdpa backward {'causal' if causal else 'non-causal'} bf16 B=8 H=32 S={s} "
+                                   f"D=128 (dq, dk, dv)", "flop_per_step": flops, "workspace_bytes": ws},
+            "roofline": roofline_flops(workload, name, flops, per[name], BF16_PEAK_TFLOPS, nbytes),
+            "cpu_baseline": cpu}
+
+
+CONV_BWD_LAYERS = [  # name, Cin, Cout, H, K, stride, pad: ResNet-50 layers at batch 64
+    ("l2_3x3", 128, 128, 28, 3, 1, 1), ("l3_3x3_s2", 256, 256, 28, 3, 2, 1), ("l4_1x1", 512, 2048, 7, 1, 1, 0)]
+
+
+def bench_conv_backward(ctx):
+    """conv2d dx and dw (bf16 NHWC, batch 64) of three ResNet-50 layers, with
+    the stream workspace (flipped weights, spread dy)."""
+    from teenygrad_amd import kernels as K
+    from teenygrad_amd.dtypes import round_bf16
+    tg, stream = ctx.tg, ctx.stream
+    B = 64
+    rng = np.random.default_rng(0x7EE70013)
+    ops, facts, host, sizes = [], {}, [], []
+    for name, cin, cout, h, k, st, p in CONV_BWD_LAYERS:
+        oh = (h + 2 * p - k) // st + 1
+        x = round_bf16(rng.random((B, h, h, cin), dtype=np.float32))
+        w = round_bf16(rng.standard_normal((cout, k, k, cin), dtype=np.float32) * np.float32(0.05))
+        dy = round_bf16(rng.standard_normal((B, oh, oh, cout), dtype=np.float32))
+        xb, wb, dyb = (upload_bf16(ctx, a) for a in (x, w, dy))
+        dx, dw = tg.Buffer(tg.bf16, x.shape), tg.Buffer(tg.bf16, w.shape)
+        f = 2.0 * B * oh * oh * cout * cin * k * k
+        sizes.append(K.conv2d_backward_workspace_size(x.shape, w.shape, st, p, 1, tg.bf16, "nhwc"))
+        ops.append((f"{name}.dx", [lambda dyb=dyb, wb=wb, dx=dx, xs=x.shape, st=st, p=p:
+                                   K.conv2d_backward_dx(dyb, wb, xs, st, p, 1, "nhwc", dx=dx, stream=stream)]))
+        ops.append((f"{name}.dw", [lambda dyb=dyb, xb=xb, dw=dw, ws_=w.shape, st=st, p=p:
+                                   K.conv2d_backward_dw(dyb, xb, ws_, st, p, 1, "nhwc", dw=dw, stream=stream)]))
+        nb_dx = 2 * (B * oh * oh * cout + cout * k * k * cin + B * h * h * cin)
+        nb_dw = 2 * (B * oh * oh * cout + B * h * h * cin + cout * k * k * cin)
+        facts[f"{name}.dx"] = (f, nb_dx)
+        facts[f"{name}.dw"] = (f, nb_dw)
+        if not ctx.args.no_cpu:
+            nimg = math.ceil(CPU_PREFIX * B)
+            host.append((np.ascontiguousarray(np.transpose(dy[:nimg], (0, 3, 1, 2))),
+                         np.ascontiguousarray(np.transpose(x[:nimg], (0, 3, 1, 2))),
+                         np.ascontiguousarray(np.transpose(w, (0, 3, 1, 2))), st, p))
+    ws = attach_workspace(ctx, sizes)
+    ms, per = ctx.measure(ops)
+    flops = sum(f for f, _ in facts.values())
+    value = flops / (ms * 1e-3) / 1e12
+    dom = max(per, key=per.get)
+    opsd = {n: {"us": round(v * 1e3, 1), "TFLOP/s": round(facts[n][0] / (v * 1e-3) / 1e12, 2)}
+            for n, v in per.items()}
+    cpu = None
+    if not ctx.args.no_cpu:
+        import oracle
+        nimg = host[0][0].shape[0]
+
+        def run():
+            for dyh, xh, wh, st, p in host:
+                oracle.conv2d_backward_dx(dyh, wh, xh.shape, st, p)
+                oracle.conv2d_backward_dw(dyh, xh, wh.shape, st, p)
+
+        cs = cpu_time(run)
+        frac = nimg / B
+        full = cs / frac
+        cpu = cpu_entry(round(flops / full / 1e12, 5), "TFLOP/s", cs,
+                        f"program-id prefix: the first {nimg} of {B} images of each layer ({frac:.2%}), dx and dw "
+                        f"in fp32 NCHW; scaled x{B / nimg:.0f}", value,
+                        {"prefix_fraction": round(frac, 4), "extrapolated_seconds": round(full, 2)})
+    ctx.stream.set_workspace(None)
+    return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "conv2d backward dx + dw, bf16 NHWC batch 64: ResNet-50 3x3 128ch 28x28, "
+                                   "3x3/2 256ch 28x28, 1x1 512->2048 7x7", "flop_per_step": flops,
+                       "workspace_bytes": ws},
+            "roofline": roofline_flops("conv_backward", dom, facts[dom][0], per[dom], BF16_PEAK_TFLOPS,
+                                       facts[dom][1]),
+            "ops": opsd, "cpu_baseline": cpu}
+
+
 WORKLOADS = {
     "conv2d_f32": bench_conv_f32,
     "norm_act": bench_norm_act,
@@ -590,11 +762,17 @@ WORKLOADS = {
     "w8a16_gemm": bench_w8a16,
     "w8a16_conv": bench_w8a16_conv,
     "act_backward": bench_act_backward,
+    "norm_backward": bench_norm_backward,
+    "attention_backward_causal_s2048": lambda c: bench_attention_backward(c, 2048, True),
+    "conv_backward": bench_conv_backward,
 }
 # the default run: every configuration, in configuration order
 CONFIGS = [("cfg1", "conv2d_f32"), ("cfg2", "norm_act"), ("cfg3a", "attention_causal_s2048"),
            ("cfg3b", "attention_s4096"), ("cfg4", "resnet50_convs"), ("cfg5a", "w8a16_gemm"),
-           ("cfg5b", "w8a16_conv")]
+           ("cfg5b", "w8a16_conv"),
+           # the training kernels at the same shapes (not a headline configuration)
+           ("train_act", "act_backward"), ("train_norm", "norm_backward"),
+           ("train_attention", "attention_backward_causal_s2048"), ("train_conv", "conv_backward")]
 
 
 def main():

@@ -180,21 +180,6 @@ __global__ __launch_bounds__(64) void fa_bwd_dkv_rows(const T *__restrict__ Q, c
 
 // ── bf16 MFMA kernels ───────────────────────────────────────────────────────
 
-// Chunk swizzle of LDS tile rows: 16 consecutive rows get 16 distinct chunk
-// positions (row reads), and 4 consecutive rows x 2 adjacent chunks land on 8
-// distinct positions (transposing reads).  For D = 64 two rows share the 64
-// banks, so the swizzle is a function of row / 2.
-template <int D>
-__device__ __forceinline__ int bswz(int row) {
-  if constexpr (D == 128) {
-    const int h = row & 15;
-    return ((h >> 2) & 1) | ((h & 3) << 1) | (h & 8);
-  } else {
-    const int h = (row >> 1) & 7;
-    return ((h >> 1) & 1) | ((h & 1) << 1) | (h & 4);
-  }
-}
-
 // Rows [row0, row0 + R) of an [n, D] bf16 matrix (buffer resource over its n
 // rows: rows past n read as zeros) into a swizzled LDS tile, by LDS-DMA.
 // Slot u = NT i + tid of the tile is row u / (D/8), chunk position u % (D/8).
@@ -216,23 +201,6 @@ template <int D>
 __device__ __forceinline__ bf16x8 frag_row(const bf16 *tile, int rb, int st, int lane) {
   const int r = lane & 31, g = lane >> 5;
   return *reinterpret_cast<const bf16x8 *>(tile + (rb + r) * D + (((2 * st + g) ^ bswz<D>(r)) << 3));
-}
-
-// Transposed A operand: lane (g, r) holds column d = 32 db + r of tile rows
-// rb + {4g .. 4g+3, 8+4g .. 8+4g+3} (rb a multiple of 16) — the k order of a
-// 32x32 result's registers 8t .. 8t+7 packed as a B operand (pack_b).  Two
-// ds_read_b64_tr_b16: lane m of each 16-lane group addresses row
-// rb + 4g + m/4 (+ 8), columns 32 db + 16 (group & 1) + 4 (m & 3) .. + 3.
-template <int D>
-__device__ __forceinline__ bf16x8 frag_tr(const bf16 *tile, int rb, int db, int lane) {
-  constexpr int HI = D == 128 ? 8 : 4;  // bswz(row + 8) = bswz(row) ^ HI for row % 16 < 8
-  const int g = lane >> 5, hh = lane >> 4, m = lane & 15;
-  const int rr = 4 * g + (m >> 2);
-  const int cc = 4 * db + 2 * (hh & 1) + ((m & 3) >> 1);
-  const int sw = bswz<D>(rr);
-  const bf16 *p0 = tile + (rb + rr) * D + ((cc ^ sw) << 3) + 4 * (m & 1);
-  const bf16 *p1 = tile + (rb + 8 + rr) * D + ((cc ^ sw ^ HI) << 3) + 4 * (m & 1);
-  return cat8(ds_read_tr16(p0), ds_read_tr16(p1));
 }
 
 // Registers 8t .. 8t+7 of a 32x32 fp32 result, rounded to bf16, as the B

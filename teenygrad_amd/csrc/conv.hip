@@ -752,6 +752,180 @@ static void launch_dw_direct(const void *dy, const void *x, void *dw, const Conv
                      static_cast<const T *>(dy), static_cast<const T *>(x), static_cast<T *>(dw), q);
 }
 
+// ── bf16 NHWC dw on the matrix cores ──
+// dw[co, (kh, kw, ci)] = sum over pixels p = (b, oh, ow) of dy[p, co] *
+// x[b, oh*SH - PH + kh, ow*SW - PW + kw, ci]: a GEMM with M = C_OUT,
+// N = KH*KW*C_IN and the reduction over the B*OH*OW pixels.  Both operands
+// arrive pixel-major (rows of dy, gathered rows of x), so stages of 64
+// pixels x 128 columns of each are moved to LDS by LDS-DMA (padding taps,
+// rows past the last pixel and columns past the edge read as zeros through
+// the buffer extent) and both MFMA operands come out of LDS through
+// transposing reads.  Workgroup tile 128 x 128, four waves of 64 x 64.  The
+// pixel range is split over workgroups; with more than one split each
+// writes fp32 partials to the stream workspace and a second kernel adds them
+// in split order (deterministic).
+constexpr int kDwTile = 128, kDwStage = 64;
+
+struct DwPlan {
+  bool ok = false;
+  int tiles_m = 0, tiles_n = 0, splits = 1, stages_per_split = 0;
+  size_t part_bytes = 0;  // workspace for splits > 1
+};
+
+// `workspace`: bytes the caller's stream offers (the split count shrinks to fit).
+static DwPlan dw_plan(const ConvGeo &q, size_t workspace) {
+  DwPlan d;
+  if (q.G != 1 || q.Cin % 8 != 0 || q.Cout % 8 != 0 || q.B == 0) return d;
+  const int64_t P = static_cast<int64_t>(q.B) * q.OH * q.OW;
+  const int64_t M = q.Cout, N = static_cast<int64_t>(q.KH) * q.KW * q.Cin;
+  // 32-bit buffer offsets into dy and x
+  if (P * M * 2 > 0x7fffff00LL || static_cast<int64_t>(q.B) * q.H * q.W * q.Cin * 2 > 0x7fffff00LL) return d;
+  d.tiles_m = static_cast<int>(cdiv(M, kDwTile));
+  d.tiles_n = static_cast<int>(cdiv(N, kDwTile));
+  const int64_t tiles = static_cast<int64_t>(d.tiles_m) * d.tiles_n, stages = cdiv(P, kDwStage);
+  int64_t splits = cdiv(2 * static_cast<int64_t>(device_cu_count()), tiles);  // about two workgroups per CU
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, stages / 4));       // at least 4 stages per split
+  while (splits > 1 && static_cast<size_t>(splits) * M * N * 4 > workspace) --splits;
+  d.stages_per_split = static_cast<int>(cdiv(stages, splits));
+  d.splits = static_cast<int>(cdiv(stages, d.stages_per_split));  // no empty split
+  d.part_bytes = d.splits > 1 ? static_cast<size_t>(d.splits) * M * N * 4 : 0;
+  d.ok = tiles * d.splits <= 0x7fffffff;
+  return d;
+}
+
+// The split count the kernel would like (what the workspace-size query reports).
+static size_t dw_scratch_bytes(const ConvGeo &q) { return dw_plan(q, static_cast<size_t>(1) << 26).part_bytes; }
+
+template <bool PART>
+__global__ __launch_bounds__(256, 2) void conv_dw_mfma(const bf16 *__restrict__ dy, const bf16 *__restrict__ x,
+                                                       bf16 *__restrict__ dw, float *__restrict__ part, ConvGeo q,
+                                                       int tiles_m, int tiles_n, int stages_per_split, int P) {
+  constexpr int NT = 256, TILE = kDwStage * kDwTile;
+  __shared__ __attribute__((aligned(16))) bf16 abuf[2][TILE], bbuf[2][TILE];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
+  const int ntiles = tiles_m * tiles_n;
+  // the tiles of one split (same pixels of dy and x) are consecutive ids: one XCD's L2
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = id / ntiles, t = id % ntiles;
+  const int co0 = (t / tiles_n) * kDwTile, n0 = (t % tiles_n) * kDwTile;
+  const int M = q.Cout, N = q.KH * q.KW * q.Cin;
+  const int wm = w >> 1, wn = w & 1;
+  const int st0 = split * stages_per_split;
+  const int nst = min(stages_per_split, (P + kDwStage - 1) / kDwStage - st0);
+  const __amdgpu_buffer_rsrc_t dys = buffer_rsrc(dy, P * M * 2);
+  const __amdgpu_buffer_rsrc_t xs = buffer_rsrc(x, q.B * q.H * q.W * q.Cin * 2);
+  // LDS-DMA slot u = 256 i + tid: stage row 16 i + tid / 16, chunk position
+  // tid % 16, holding logical 16-byte chunk `chunk` (the row swizzle depends
+  // on row % 16 only, so it is the same in every round)
+  const int lrow = tid >> 4;
+  const int chunk = (tid & 15) ^ bswz<128>(lrow);
+  const int a_col = co0 + 8 * chunk;
+  const bool a_ok = a_col < M;
+  const int nb = n0 + 8 * chunk;
+  const bool b_ok = nb < N;
+  const int tap = nb / q.Cin, ci = nb % q.Cin;  // C_IN % 8 == 0: a chunk never straddles two taps
+  const int kh = tap / q.KW, kw = tap % q.KW;
+  auto issue = [&](int s, int b) __attribute__((always_inline)) {
+    const int p0 = (st0 + s) * kDwStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = p0 + 16 * i + lrow;
+      int aoff = kOffNone, boff = kOffNone;
+      if (p < P) {
+        if (a_ok) aoff = (p * M + a_col) * 2;
+        if (b_ok) {
+          const int ow = p % q.OW, r = p / q.OW;
+          const int oh = r % q.OH, bb = r / q.OH;
+          const int ih = oh * q.SH - q.PH + kh, iw = ow * q.SW - q.PW + kw;
+          if (ih >= 0 && ih < q.H && iw >= 0 && iw < q.W) boff = (((bb * q.H + ih) * q.W + iw) * q.Cin + ci) * 2;
+        }
+      }
+      buffer_lds_dma16(dys, aoff, __builtin_amdgcn_readfirstlane(lds_address(abuf[b] + (NT * i + 64 * w) * 8)));
+      buffer_lds_dma16(xs, boff, __builtin_amdgcn_readfirstlane(lds_address(bbuf[b] + (NT * i + 64 * w) * 8)));
+    }
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+  if (nst > 0) {
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  for (int s = 0; s < nst; ++s) {
+    const int b = s & 1;
+    if (s + 1 < nst) issue(s + 1, b ^ 1);
+#pragma unroll
+    for (int kk = 0; kk < kDwStage / 16; ++kk) {
+      bf16x8 af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = frag_tr<128>(abuf[b], 16 * kk, 2 * wm + i, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfr[j] = frag_tr<128>(bbuf[b], 16 * kk, 2 * wn + j, lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  // lane (g, c) holds column n0 + 64 wn + 32 j + c, rows co0 + 64 wm + 32 i + mfma32_row(v, g)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + c;
+      if (n >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = co0 + 64 * wm + 32 * i + mfma32_row(v, g);
+        if (m >= M) continue;
+        if constexpr (PART) part[(static_cast<int64_t>(split) * M + m) * N + n] = acc[i][j][v];
+        else dw[static_cast<int64_t>(m) * N + n] = static_cast<bf16>(acc[i][j][v]);
+      }
+    }
+}
+
+// dw = sum of the splits' fp32 partials, in split order, rounded to bf16.
+__global__ __launch_bounds__(256) void conv_dw_reduce(const float *__restrict__ part, bf16 *__restrict__ dw,
+                                                      int splits, int64_t mn) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  f32x4 s = *reinterpret_cast<const f32x4 *>(part + i);
+  for (int k = 1; k < splits; ++k) s += *reinterpret_cast<const f32x4 *>(part + k * mn + i);
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(s[e]);
+  *reinterpret_cast<bf16x4 *>(dw + i) = o;
+}
+
+// bf16 NHWC dw on the MFMA path; false (nothing launched) if it does not apply.
+static bool conv_dw_mfma_launch(const void *dy, const void *x, void *dw, const ConvGeo &q, hipStream_t s,
+                                Scratch scr) {
+  if (!aligned(dy, 16) || !aligned(x, 16) || !aligned(dw, 8)) return false;
+  const DwPlan d = dw_plan(q, scr.ptr != nullptr ? scr.bytes : 0);
+  if (!d.ok) return false;
+  const int P = q.B * q.OH * q.OW;
+  const dim3 grid(static_cast<unsigned>(d.tiles_m * d.tiles_n * d.splits));
+  if (d.splits > 1) {
+    float *part = static_cast<float *>(scr.ptr);
+    hipLaunchKernelGGL(conv_dw_mfma<true>, grid, dim3(256), 0, s, static_cast<const bf16 *>(dy),
+                       static_cast<const bf16 *>(x), static_cast<bf16 *>(dw), part, q, d.tiles_m, d.tiles_n,
+                       d.stages_per_split, P);
+    const int64_t mn = static_cast<int64_t>(q.Cout) * q.KH * q.KW * q.Cin;
+    hipLaunchKernelGGL(conv_dw_reduce, dim3(static_cast<unsigned>(cdiv(mn / 4, 256))), dim3(256), 0, s, part,
+                       static_cast<bf16 *>(dw), d.splits, mn);
+  } else {
+    hipLaunchKernelGGL(conv_dw_mfma<false>, grid, dim3(256), 0, s, static_cast<const bf16 *>(dy),
+                       static_cast<const bf16 *>(x), static_cast<bf16 *>(dw), nullptr, q, d.tiles_m, d.tiles_n,
+                       d.stages_per_split, P);
+  }
+  return true;
+}
+
 static teeny_status conv_bwd_entry(const void *dy, const void *x, const void *w, void *dx, void *dw, int64_t B,
                                    int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH, int64_t OW,
                                    const teeny_conv2d_params *prm, teeny_dtype dtype, teeny_layout layout,
@@ -782,8 +956,10 @@ static teeny_status conv_bwd_entry(const void *dy, const void *x, const void *w,
     if (st != TEENY_OK) return st;
   }
   if (dw != nullptr) {
-    if (dtype == TEENY_F32) launch_dw_direct<float>(dy, x, dw, q, s);
-    else launch_dw_direct<bf16>(dy, x, dw, q, s);
+    if (!(dtype == TEENY_BF16 && nhwc && conv_dw_mfma_launch(dy, x, dw, q, s, stream_scratch(s)))) {
+      if (dtype == TEENY_F32) launch_dw_direct<float>(dy, x, dw, q, s);
+      else launch_dw_direct<bf16>(dy, x, dw, q, s);
+    }
     st = after_launch(name, s);
   }
   return st;
@@ -922,7 +1098,7 @@ teeny_status teeny_conv2d_backward_workspace_size(int64_t B, int64_t C_IN, int64
   if (st != TEENY_OK) return st;
   TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
                 "conv2d_backward_workspace_size: dtype must be F32 or BF16");
-  if (B > 0 && dtype == TEENY_BF16 && layout == TEENY_NHWC) *bytes = dx_scratch_bytes(q);
+  if (B > 0 && dtype == TEENY_BF16 && layout == TEENY_NHWC) *bytes = std::max(dx_scratch_bytes(q), dw_scratch_bytes(q));
   return TEENY_OK;
 }
 

@@ -8,7 +8,7 @@ import pytest
 
 import teenygrad_amd as tg
 from conftest import load_golden
-from gpu_util import check_bf16, check_f32, stream_workspace
+from gpu_util import check_bf16, check_bf16_normwise, check_f32, stream_workspace
 from teenygrad_amd import kernels as K
 from teenygrad_amd.dtypes import from_bf16, to_bf16
 
@@ -232,6 +232,40 @@ def test_conv_backward_dx_bf16_nhwc(dev, orc, cfg, scratch):
         dx = K.conv2d_backward_dx(dyb, wb, x_shape, s, p, 1, "nhwc")
     ref = orc.conv2d_backward_dx(dy.transpose(0, 3, 1, 2), w.transpose(0, 3, 1, 2), (B, cin, H, H), s, p)
     check_bf16(dx.to_host(), nhwc_of(ref), "dx")
+
+
+MFMA_DW_CASES = [  # bf16 NHWC, groups 1: B, H, Cin, Cout, K, stride, pad
+    (4, 14, 64, 128, 3, 1, 1),
+    (2, 28, 128, 128, 3, 2, 1),
+    (3, 7, 512, 256, 1, 1, 0),
+    (2, 15, 24, 72, 3, 1, 1),     # ragged: N = 216, C_OUT = 72, pixels 450
+    (1, 11, 40, 200, 5, 2, 2),    # 5x5 stride 2, N = 1000
+    (2, 30, 8, 64, 7, 2, 3),
+]
+
+
+@pytest.mark.parametrize("cfg", MFMA_DW_CASES)
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_conv_backward_dw_bf16_nhwc(dev, orc, cfg, scratch):
+    B, H, cin, cout, k, s, p = cfg
+    rng = np.random.default_rng(B * 7 + H * 100 + cin + 3 * cout)
+    oh = (H + 2 * p - k) // s + 1
+    x = rb(rng.normal(0, 1, (B, H, H, cin)).astype(np.float32))
+    dy = rb(rng.normal(0, 1, (B, oh, oh, cout)).astype(np.float32))
+    w_shape = (cout, k, k, cin)
+    need = K.conv2d_backward_workspace_size(x.shape, w_shape, s, p, 1, tg.bf16, "nhwc")
+    print(f"[conv dw mfma] {cfg} {scratch} need={need}", flush=True)
+    dyb, xb = dev.upload(to_bf16(dy), tg.bf16), dev.upload(to_bf16(x), tg.bf16)
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            dw = K.conv2d_backward_dw(dyb, xb, w_shape, s, p, 1, "nhwc")
+            dev.synchronize()
+    else:
+        dw = K.conv2d_backward_dw(dyb, xb, w_shape, s, p, 1, "nhwc")
+    ref = nhwc_of(orc.conv2d_backward_dw(dy.transpose(0, 3, 1, 2), x.transpose(0, 3, 1, 2), (cout, cin, k, k), s, p))
+    got = dw.to_host()
+    check_bf16(got, ref, "dw")
+    print(f"  dw norm-wise {check_bf16_normwise(got, ref, 'dw'):.3g}", flush=True)
 
 
 def test_conv_backward_combined_and_dispatch_hooks(dev, orc):
