@@ -285,6 +285,35 @@ teeny_status teeny_rms_norm_backward(const void *dy, const void *x, void *dx, co
 teeny_status teeny_norm_backward_workspace_size(int64_t M, int64_t N, int32_t is_rms, teeny_dtype dtype,
                                                 size_t *bytes);
 
+/* ── fused pointwise chains ───────────────────────────────────────────────
+ * The reference's PointwiseFuse custom op (kernels/teeny-kernels/src/graph/
+ * optimizer/ops/pointwise_fuse.rs:73-233), built by the Anduin pass
+ * (graph/optimizer/anduin.rs:27-60): members ops[0 .. n_ops-1] applied in
+ * order in one pass, member i < n_ops-1 writing its output to scratch[i]
+ * (the reference's scratch_i, kept for the backward walk; in the forward a
+ * NULL scratch array or entry skips that store), the last member to y.
+ * Values are rounded to `dtype` between members, so the chain equals the
+ * members run as separate kernels.  Member arithmetic: relu.rs, gelu.rs,
+ * sigmoid.rs (sigmoid, silu), tanh.rs forward kernels.  1 <= n_ops <= 8. */
+typedef enum {
+  TEENY_PW_RELU = 1,
+  TEENY_PW_GELU_TANH = 2,
+  TEENY_PW_SILU = 3,
+  TEENY_PW_SIGMOID = 4,
+  TEENY_PW_TANH = 5
+} teeny_pointwise_op;
+
+teeny_status teeny_pointwise_chain_forward(const void *x, void *y, void *const *scratch, const int32_t *ops,
+                                           int32_t n_ops, int64_t n, teeny_dtype dtype, teeny_stream stream);
+/* Reverse-mode walk of a chain whose members all have a y-style gradient
+ * (relu, sigmoid, tanh; pointwise_fuse.rs:276-279, the reference's
+ * lower_pointwise_fuse_backward): dx = dy, then for i = n_ops-1 .. 0
+ * dx = grad_i(dx, y_i) with y_i = y (last member) or scratch[i]; dx may
+ * alias dy. */
+teeny_status teeny_pointwise_chain_backward(const void *dy, const void *y, void *dx, const void *const *scratch,
+                                            const int32_t *ops, int32_t n_ops, int64_t n, teeny_dtype dtype,
+                                            teeny_stream stream);
+
 /* Fused norm + activation: one pass computing act(norm(x)).  No reference
  * counterpart as a single kernel: it is the composition of the two kernels
  * above with the activation kernels (the Anduin pointwise-fusion idea,
@@ -342,6 +371,25 @@ teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, con
                                                int64_t W, int64_t OH, int64_t OW,
                                                const teeny_conv2d_params *params, teeny_dtype dtype,
                                                teeny_layout layout, teeny_stream stream);
+
+/* Conv + BatchNorm (inference) + activation, fused in the conv's epilogue:
+ *   y[b,c,...] = act(bn_scale[c] * conv(x, w)[b,c,...] + bn_shift[c])
+ * with the BatchNorm folded by the caller to bn_scale = gamma / sqrt(var +
+ * eps), bn_shift = beta - bn_scale * mean (fp32 [C_OUT]), and act =
+ * params->act.  Reference: conv2d_bn_silu_forward(x, w, bn_scale, bn_shift, y,
+ * B, C_IN, C_OUT, H, W, OH, OW) (act SiLU), kernels/teeny-kernels/src/nn/
+ * fused/conv2d_bn_silu.rs:26-199, and its GEMM (1x1) and tiled variants
+ * conv2d_bn_silu_gemm.rs:61-260, conv2d_bn_silu_tiled.rs:49-293, whose
+ * padded output rows are expressed here by `y_strides` (NCHW only: element
+ * strides between consecutive b, c, oh, ow; NULL = tight).  Any dtype,
+ * layout and groups, as teeny_conv2d_forward; the bf16 NHWC groups == 1 case
+ * runs on the MFMA implicit GEMM with the affine and activation applied to
+ * the fp32 accumulator. */
+teeny_status teeny_conv2d_bn_act_forward(const void *x, const void *w, const float *bn_scale, const float *bn_shift,
+                                        void *y, int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                        int64_t OH, int64_t OW, const int64_t *y_strides,
+                                        const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                        teeny_stream stream);
 
 /* conv2d backward.  Reference: conv2d_backward_dx(dy, w, dx, B, C_IN, C_OUT,
  * H, W, OH, OW), conv2d_backward_dw(dy, x, dw, ...) and the combined

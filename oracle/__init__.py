@@ -43,9 +43,14 @@ def _load(path: str = LIB_PATH) -> ctypes.CDLL:
         "oracle_relu_backward": [P, P, P, I, I, I, I],
         "oracle_gelu_backward": [P, P, P, I, I, I, I],
         "oracle_silu_backward": [P, P, P, I, I, I, I],
+        "oracle_sigmoid_forward": [P, P, I, I, I, I],
+        "oracle_tanh_forward": [P, P, I, I, I, I],
+        "oracle_sigmoid_backward": [P, P, P, I, I, I, I],
+        "oracle_tanh_backward": [P, P, P, I, I, I, I],
         "oracle_layer_norm_forward_inference": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_rms_norm_forward": [P, P, P, P, I, I, c_float, I, I, I],
         "oracle_conv2d_forward": [P, P, P, P] + [I] * 15 + [I, I],
+        "oracle_conv2d_bn_silu_forward": [P, P, P, P, P] + [I] * 15 + [I, I],
         "oracle_conv2d_programs": [P, P, P, P] + [I] * 15 + [P, I],
         "oracle_flash_attention2_forward": [P, P, P, P, P, I, I, I, I, c_float, c_int, I, I],
         "oracle_flash_attention2_rows": [P, P, P, P, P, I, I, I, I, c_float, c_int, P, I],
@@ -140,6 +145,16 @@ def silu(x, block_size=1024, pid_begin=0, pid_end=-1):
     return _act(lib.oracle_silu_forward, x, block_size, pid_begin, pid_end)
 
 
+def sigmoid(x, block_size=1024, pid_begin=0, pid_end=-1):
+    """sigmoid.rs (sigmoid_forward): 1 / (1 + exp(-x))."""
+    return _act(lib.oracle_sigmoid_forward, x, block_size, pid_begin, pid_end)
+
+
+def tanh(x, block_size=1024, pid_begin=0, pid_end=-1):
+    """tanh.rs (tanh_forward): 2 * (1 / (1 + exp(-2x))) - 1."""
+    return _act(lib.oracle_tanh_forward, x, block_size, pid_begin, pid_end)
+
+
 def _act_grad(fn, dy, v, block_size, pid_begin, pid_end):
     dy, v = _f32(dy), _f32(v)
     if dy.shape != v.shape:
@@ -162,6 +177,49 @@ def gelu_backward(dy, x, block_size=1024, pid_begin=0, pid_end=-1):
 def silu_backward(dy, x, block_size=1024, pid_begin=0, pid_end=-1):
     """sigmoid.rs:161-210: dy * (s + y - y s), s = sigmoid(x), y = x s."""
     return _act_grad(lib.oracle_silu_backward, dy, x, block_size, pid_begin, pid_end)
+
+
+def sigmoid_backward(dy, y, block_size=1024, pid_begin=0, pid_end=-1):
+    """sigmoid.rs (sigmoid_backward): dy * (y - y y) at the forward OUTPUT y."""
+    return _act_grad(lib.oracle_sigmoid_backward, dy, y, block_size, pid_begin, pid_end)
+
+
+def tanh_backward(dy, y, block_size=1024, pid_begin=0, pid_end=-1):
+    """tanh.rs (tanh_backward): dy * (1 - y y) at the forward OUTPUT y."""
+    return _act_grad(lib.oracle_tanh_backward, dy, y, block_size, pid_begin, pid_end)
+
+
+MEMBERS = {"relu": relu, "gelu": gelu, "silu": silu, "sigmoid": sigmoid, "tanh": tanh}
+Y_STYLE_GRADS = {"relu": relu_backward, "sigmoid": sigmoid_backward, "tanh": tanh_backward}
+
+
+def pointwise_chain(x, members, round_fn=None):
+    """PointwiseFuse (graph/optimizer/ops/pointwise_fuse.rs:73-233, the
+    synthesized entry in -> m0 -> scratch0 -> ... -> out): the members' own
+    kernels run in order, each reading the previous member's stored output;
+    round_fn (e.g. a bf16 rounding) models a narrower scratch dtype.
+    Returns (y, [scratch_0 .. scratch_{n-2}])."""
+    outs = []
+    v = _f32(x)
+    for name in members:
+        v = MEMBERS[name](v)
+        if round_fn is not None:
+            v = round_fn(v)
+        outs.append(v)
+    return outs[-1], outs[:-1]
+
+
+def pointwise_chain_backward(dy, y, scratch, members, round_fn=None):
+    """The fused backward entry (pointwise_fuse.rs:352-380): dx = dy, then the
+    members' y-style gradients from the last to the first, member i reading
+    its forward output (y for the last, scratch_i otherwise)."""
+    g = _f32(dy)
+    outs = list(scratch) + [y]
+    for i in range(len(members) - 1, -1, -1):
+        g = Y_STYLE_GRADS[members[i]](g, outs[i])
+        if round_fn is not None:
+            g = round_fn(g)
+    return g
 
 
 # ── norms (layernorm.rs:42-157, rmsnorm.rs:39-119) ──────────────────────────
@@ -206,6 +264,22 @@ def conv2d_nchw(x, w, bias=None, stride=(1, 1), padding=(0, 0), groups=1, block_
     y = np.zeros((B, Cout, OH, OW), dtype=np.float32)
     _chk(lib.oracle_conv2d_forward(_p(x), _p(w), _p(bias), _p(y), B, Cin, Cout, H, W, OH, OW, KH, KW,
                                    sh, sw, ph, pw, groups, block_ow, pid_begin, pid_end), "conv2d")
+    return y
+
+
+def conv2d_bn_silu_nchw(x, w, bn_scale, bn_shift, stride=(1, 1), padding=(0, 0), groups=1, block_ow=16,
+                        pid_begin=0, pid_end=-1):
+    """conv2d_bn_silu.rs:40-199: silu(bn_scale[c] * conv(x, w) + bn_shift[c]), NCHW fp32."""
+    x, w = _f32(x), _f32(w)
+    sc, sh_ = _f32(bn_scale), _f32(bn_shift)
+    sh, sw = (stride, stride) if isinstance(stride, int) else stride
+    ph, pw = (padding, padding) if isinstance(padding, int) else padding
+    B, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    y = np.zeros((B, Cout, OH, OW), np.float32)
+    _chk(lib.oracle_conv2d_bn_silu_forward(_p(x), _p(w), _p(sc), _p(sh_), _p(y), B, Cin, Cout, H, W, OH, OW, KH, KW,
+                                           sh, sw, ph, pw, groups, block_ow, pid_begin, pid_end), "conv2d_bn_silu")
     return y
 
 

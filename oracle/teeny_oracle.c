@@ -127,13 +127,33 @@ static float relu_ref(float x) {
   return x < 0.0f ? 0.0f : x;
 }
 
+static float sigmoid_ref(float x) {
+  /* sigmoid.rs (sigmoid_forward): y = one / (one + exp(neg1 * x)) */
+  const float one = 1.0f, neg1 = -1.0f;
+  return one / (one + expf(neg1 * x));
+}
+
+static float tanh_ref(float x) {
+  /* tanh.rs (tanh_forward): s2x = one / (one + exp(neg2 * x)); y = two * s2x - one */
+  const float one = 1.0f, two = 2.0f, neg2 = -2.0f;
+  float s2x = one / (one + expf(neg2 * x));
+  return two * s2x - one;
+}
+
+static float act_ref(int kind, float v) {
+  switch (kind) {
+    case 0: return relu_ref(v);
+    case 1: return gelu_ref(v);
+    case 2: return silu_ref(v);
+    case 3: return sigmoid_ref(v);
+    default: return tanh_ref(v);
+  }
+}
+
 static void act_program(const void *c, int64_t pid) {
   const act_ctx *a = (const act_ctx *)c;
   int64_t start = pid * a->block;
-  for (int64_t i = start; i < start + a->block && i < a->n; ++i) {
-    float v = a->x[i];
-    a->y[i] = a->kind == 0 ? relu_ref(v) : a->kind == 1 ? gelu_ref(v) : silu_ref(v);
-  }
+  for (int64_t i = start; i < start + a->block && i < a->n; ++i) a->y[i] = act_ref(a->kind, a->x[i]);
 }
 
 static int act_run(const float *x, float *y, int64_t n, int64_t block, int kind, int64_t pb,
@@ -155,6 +175,14 @@ int oracle_gelu_forward(const float *x, float *y, int64_t n, int64_t block_size,
 int oracle_silu_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
                         int64_t pe) {
   return act_run(x, y, n, block_size, 2, pb, pe);
+}
+int oracle_sigmoid_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
+                           int64_t pe) {
+  return act_run(x, y, n, block_size, 3, pb, pe);
+}
+int oracle_tanh_forward(const float *x, float *y, int64_t n, int64_t block_size, int64_t pb,
+                        int64_t pe) {
+  return act_run(x, y, n, block_size, 4, pb, pe);
 }
 
 /* ── activation gradients ────────────────────────────────────────────────
@@ -202,13 +230,29 @@ static float silu_grad_ref(float dy, float x) {
   return dy * (s + y - y * s);
 }
 
+static float sigmoid_grad_ref(float dy, float y) {
+  /* sigmoid.rs (sigmoid_backward): dx = dy * (y - y * y), y the forward output */
+  return dy * (y - y * y);
+}
+
+static float tanh_grad_ref(float dy, float y) {
+  /* tanh.rs (tanh_backward): dx = dy * (one - y * y), y the forward output */
+  const float one = 1.0f;
+  return dy * (one - y * y);
+}
+
 static void act_grad_program(const void *c, int64_t pid) {
   const act_grad_ctx *a = (const act_grad_ctx *)c;
   int64_t start = pid * a->block;
   for (int64_t i = start; i < start + a->block && i < a->n; ++i) {
     float d = a->dy[i], v = a->v[i];
-    a->dx[i] = a->kind == 0 ? relu_grad_ref(d, v) : a->kind == 1 ? gelu_grad_ref(d, v)
-                                                                : silu_grad_ref(d, v);
+    switch (a->kind) {
+      case 0: a->dx[i] = relu_grad_ref(d, v); break;
+      case 1: a->dx[i] = gelu_grad_ref(d, v); break;
+      case 2: a->dx[i] = silu_grad_ref(d, v); break;
+      case 3: a->dx[i] = sigmoid_grad_ref(d, v); break;
+      default: a->dx[i] = tanh_grad_ref(d, v); break;
+    }
   }
 }
 
@@ -231,6 +275,14 @@ int oracle_gelu_backward(const float *dy, const float *x, float *dx, int64_t n,
 int oracle_silu_backward(const float *dy, const float *x, float *dx, int64_t n,
                          int64_t block_size, int64_t pb, int64_t pe) {
   return act_grad_run(dy, x, dx, n, block_size, 2, pb, pe);
+}
+int oracle_sigmoid_backward(const float *dy, const float *y, float *dx, int64_t n,
+                            int64_t block_size, int64_t pb, int64_t pe) {
+  return act_grad_run(dy, y, dx, n, block_size, 3, pb, pe);
+}
+int oracle_tanh_backward(const float *dy, const float *y, float *dx, int64_t n,
+                         int64_t block_size, int64_t pb, int64_t pe) {
+  return act_grad_run(dy, y, dx, n, block_size, 4, pb, pe);
 }
 
 /* ── LayerNorm / RMSNorm ─────────────────────────────────────────────────
@@ -334,6 +386,8 @@ typedef struct {
   float *y;
   int64_t B, Cin, Cout, H, W, OH, OW;
   int64_t KH, KW, SH, SW, PH, PW, G, block_ow;
+  /* conv2d_bn_silu_forward only (NULL otherwise) */
+  const float *bn_scale, *bn_shift;
 } conv_ctx;
 
 static void conv_program(const void *c, int64_t pid) {
@@ -374,6 +428,12 @@ static void conv_program(const void *c, int64_t pid) {
     const int64_t ow = ow_start + t;
     if (ow < a->OW) {
       float v = a->bias != NULL ? acc[t] + bias : acc[t];
+      if (a->bn_scale != NULL) {
+        /* conv2d_bn_silu.rs:153-180: bn_out = scale * acc + shift, then
+         * y = bn_out * (one / (one + exp(neg1 * bn_out))) */
+        const float bn_out = a->bn_scale[c_out] * acc[t] + a->bn_shift[c_out];
+        v = silu_ref(bn_out);
+      }
       a->y[((b * a->Cout + c_out) * a->OH + oh) * a->OW + ow] = v;
     }
   }
@@ -388,7 +448,25 @@ int oracle_conv2d_forward(const float *x, const float *w, const float *bias, flo
     return ERR_INVALID_ARGUMENT;
   if (OH != (H + 2 * PH - KH) / SH + 1 || OW != (W + 2 * PW - KW) / SW + 1)
     return ERR_SHAPE_MISMATCH;
-  conv_ctx a = {x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow};
+  conv_ctx a = {x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow, NULL, NULL};
+  const int64_t tiles = (OW + block_ow - 1) / block_ow;
+  launch(conv_program, &a, B * Cout * OH * tiles, pb, pe);
+  return OK;
+}
+
+/* conv2d_bn_silu_forward (nn/fused/conv2d_bn_silu.rs:40-199): the programs of
+ * conv2d_forward with the BatchNorm affine and SiLU applied before the store. */
+int oracle_conv2d_bn_silu_forward(const float *x, const float *w, const float *bn_scale, const float *bn_shift,
+                                  float *y, int64_t B, int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH,
+                                  int64_t OW, int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                                  int64_t G, int64_t block_ow, int64_t pb, int64_t pe) {
+  if (G <= 0 || Cin % G != 0 || Cout % G != 0) return ERR_SHAPE_MISMATCH;
+  if (block_ow <= 0 || block_ow > 512 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0)
+    return ERR_INVALID_ARGUMENT;
+  if (OH != (H + 2 * PH - KH) / SH + 1 || OW != (W + 2 * PW - KW) / SW + 1)
+    return ERR_SHAPE_MISMATCH;
+  if (bn_scale == NULL || bn_shift == NULL) return ERR_INVALID_ARGUMENT;
+  conv_ctx a = {x, w, NULL, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow, bn_scale, bn_shift};
   const int64_t tiles = (OW + block_ow - 1) / block_ow;
   launch(conv_program, &a, B * Cout * OH * tiles, pb, pe);
   return OK;
@@ -419,7 +497,7 @@ int oracle_conv2d_programs(const float *x, const float *w, const float *bias, fl
   const int64_t total = B * Cout * OH * ((OW + block_ow - 1) / block_ow);
   for (int64_t i = 0; i < n_pids; ++i)
     if (pids[i] < 0 || pids[i] >= total) return ERR_SHAPE_MISMATCH;
-  conv_list_ctx a = {{x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow},
+  conv_list_ctx a = {{x, w, bias, y, B, Cin, Cout, H, W, OH, OW, KH, KW, SH, SW, PH, PW, G, block_ow, NULL, NULL},
                      pids};
   launch(conv_list_program, &a, n_pids, 0, -1);
   return OK;

@@ -35,6 +35,7 @@ F32, BF16, I8 = 0, 1, 2
 NCHW, NHWC = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 PER_TENSOR, PER_CHANNEL, GROUP = 0, 1, 2
+PW_RELU, PW_GELU_TANH, PW_SILU, PW_SIGMOID, PW_TANH = 1, 2, 3, 4, 5
 ARG_PTR, ARG_I32, ARG_I64, ARG_F32, ARG_F64, ARG_U32, ARG_BOOL = range(7)
 
 
@@ -150,6 +151,10 @@ _SIGS = {
     "teeny_conv2d_bias_forward_noalloc": (S, [P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_flash_attention2_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
     "teeny_attention_forward": (S, [P, P, P, P, P] + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),
+    "teeny_pointwise_chain_forward": (S, [P, P, POINTER(c_void_p), POINTER(c_int32), c_int32, c_int64, c_int32, P]),
+    "teeny_pointwise_chain_backward": (S, [P, P, P, POINTER(c_void_p), POINTER(c_int32), c_int32, c_int64, c_int32,
+                                           P]),
+    "teeny_conv2d_bn_act_forward": (S, [P, P, P, P, P] + [c_int64] * 7 + [POINTER(c_int64), POINTER(Conv2dParams), c_int32, c_int32, P]),
     "teeny_flash_attention2_backward_dq": (S, [P] * 7 + [c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
     "teeny_flash_attention2_backward_dkv": (S, [P] * 8 + [c_int64, c_int64, c_float, c_int64, c_int64, c_int32, c_int32, P]),
     "teeny_attention_backward": (S, [P] * 9 + [c_int64] * 6 + [c_float, c_int32, c_int32, P]),

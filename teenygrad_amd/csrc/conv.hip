@@ -45,6 +45,7 @@ template <> __device__ __forceinline__ float wload<int8_t>(const int8_t *w, int6
 template <typename T, typename WT, int COB, int ACT>
 __global__ __launch_bounds__(64) void conv_direct(const T *__restrict__ x, const WT *__restrict__ w,
                                                   const float *__restrict__ wscale,
+                                                  const float *__restrict__ oscale,
                                                   const T *__restrict__ bias_t,
                                                   const float *__restrict__ bias_f,
                                                   T *__restrict__ y, ConvGeo q) {
@@ -89,6 +90,7 @@ __global__ __launch_bounds__(64) void conv_direct(const T *__restrict__ x, const
   for (int j = 0; j < COB; ++j) {
     const int co = co0 + j;
     float r = acc[j];
+    if (oscale != nullptr) r = r * oscale[co];  // BatchNorm scale on the accumulator
     if (bias_t != nullptr) r = r + to_f32(bias_t[co]);
     if (bias_f != nullptr) r = r + bias_f[co];
     y[b * q.ys[0] + co * q.ys[1] + oh * q.ys[2] + ow * q.ys[3]] = from_f32<T>(apply_act<ACT, fast>(r));
@@ -96,31 +98,38 @@ __global__ __launch_bounds__(64) void conv_direct(const T *__restrict__ x, const
 }
 
 template <typename T, typename WT, int ACT>
-static void launch_direct_act(const T *x, const WT *w, const float *wscale, const T *bias_t,
+static void launch_direct_act(const T *x, const WT *w, const float *wscale, const float *oscale, const T *bias_t,
                               const float *bias_f, T *y, const ConvGeo &q, hipStream_t s) {
   const int64_t npix = static_cast<int64_t>(q.B) * q.OH * q.OW;
   const int cout_g = q.Cout / q.G;
   const dim3 blk(64);
   if (cout_g % 8 == 0) {
     hipLaunchKernelGGL((conv_direct<T, WT, 8, ACT>), dim3(cdiv(npix, 64), q.Cout / 8), blk, 0, s,
-                       x, w, wscale, bias_t, bias_f, y, q);
+                       x, w, wscale, oscale, bias_t, bias_f, y, q);
   } else if (cout_g % 4 == 0) {
     hipLaunchKernelGGL((conv_direct<T, WT, 4, ACT>), dim3(cdiv(npix, 64), q.Cout / 4), blk, 0, s,
-                       x, w, wscale, bias_t, bias_f, y, q);
+                       x, w, wscale, oscale, bias_t, bias_f, y, q);
   } else {
     hipLaunchKernelGGL((conv_direct<T, WT, 1, ACT>), dim3(cdiv(npix, 64), q.Cout), blk, 0, s, x,
-                       w, wscale, bias_t, bias_f, y, q);
+                       w, wscale, oscale, bias_t, bias_f, y, q);
   }
 }
 
 template <typename T, typename WT>
 static void launch_direct(const T *x, const WT *w, const float *wscale, const T *bias_t,
-                          const float *bias_f, T *y, const ConvGeo &q, int act, hipStream_t s) {
+                          const float *bias_f, T *y, const ConvGeo &q, int act, hipStream_t s,
+                          const float *oscale = nullptr) {
   switch (act) {
-    case TEENY_ACT_RELU: launch_direct_act<T, WT, TEENY_ACT_RELU>(x, w, wscale, bias_t, bias_f, y, q, s); break;
-    case TEENY_ACT_GELU_TANH: launch_direct_act<T, WT, TEENY_ACT_GELU_TANH>(x, w, wscale, bias_t, bias_f, y, q, s); break;
-    case TEENY_ACT_SILU: launch_direct_act<T, WT, TEENY_ACT_SILU>(x, w, wscale, bias_t, bias_f, y, q, s); break;
-    default: launch_direct_act<T, WT, TEENY_ACT_NONE>(x, w, wscale, bias_t, bias_f, y, q, s); break;
+    case TEENY_ACT_RELU:
+      launch_direct_act<T, WT, TEENY_ACT_RELU>(x, w, wscale, oscale, bias_t, bias_f, y, q, s);
+      break;
+    case TEENY_ACT_GELU_TANH:
+      launch_direct_act<T, WT, TEENY_ACT_GELU_TANH>(x, w, wscale, oscale, bias_t, bias_f, y, q, s);
+      break;
+    case TEENY_ACT_SILU:
+      launch_direct_act<T, WT, TEENY_ACT_SILU>(x, w, wscale, oscale, bias_t, bias_f, y, q, s);
+      break;
+    default: launch_direct_act<T, WT, TEENY_ACT_NONE>(x, w, wscale, oscale, bias_t, bias_f, y, q, s); break;
   }
 }
 
@@ -147,6 +156,7 @@ static void launch_direct(const T *x, const WT *w, const float *wscale, const T 
 // 16), and their partial sums meet in LDS in a fixed order.
 template <int ACT>
 __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x, const float *__restrict__ w,
+                                                     const float *__restrict__ oscale,
                                                      const float *__restrict__ bias, float *__restrict__ y,
                                                      ConvGeo q, int x_bytes, int chunk, int pitch) {
   extern __shared__ __attribute__((aligned(16))) float wl[];  // [16][pitch]
@@ -221,9 +231,9 @@ __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x
     const int co = n0 + 4 * kk + v;
     if (co < q.Cout) {
       float val = acc[v];
+      if (oscale != nullptr) val *= oscale[co];
       if (bias != nullptr) val += bias[co];
-      y[(static_cast<int64_t>(b) * q.Cout + co) * q.OH * q.OW + static_cast<int64_t>(oh) * q.OW + ow] =
-          apply_act<ACT, false>(val);
+      y[b * q.ys[0] + co * q.ys[1] + oh * q.ys[2] + ow * q.ys[3]] = apply_act<ACT, false>(val);
     }
   }
 }
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x
 // offsets and whose staged weight chunk fits LDS; returns false (nothing
 // launched) otherwise.
 static bool try_conv_f32_mfma(const float *x, const float *w, const float *bias, float *y, const ConvGeo &q,
-                              int act, hipStream_t s) {
+                              int act, hipStream_t s, const float *oscale = nullptr) {
   const int64_t xb = static_cast<int64_t>(q.B) * q.Cin * q.H * q.W * 4;
   const int khw = q.KH * q.KW;
   if (q.G != 1 || xb >= (int64_t{1} << 31) || khw > 128) return false;
@@ -260,17 +270,20 @@ static bool try_conv_f32_mfma(const float *x, const float *w, const float *bias,
   const int xi = static_cast<int>(xb);
   switch (act) {
     case TEENY_ACT_RELU:
-      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_RELU>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
-      break;
-    case TEENY_ACT_GELU_TANH:
-      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_GELU_TANH>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk,
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_RELU>, grid, dim3(256), lds, s, x, w, oscale, bias, y, q, xi, chunk,
                          pitch);
       break;
+    case TEENY_ACT_GELU_TANH:
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_GELU_TANH>, grid, dim3(256), lds, s, x, w, oscale, bias, y, q, xi,
+                         chunk, pitch);
+      break;
     case TEENY_ACT_SILU:
-      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_SILU>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_SILU>, grid, dim3(256), lds, s, x, w, oscale, bias, y, q, xi, chunk,
+                         pitch);
       break;
     default:
-      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_NONE>, grid, dim3(256), lds, s, x, w, bias, y, q, xi, chunk, pitch);
+      hipLaunchKernelGGL(conv_f32_mfma<TEENY_ACT_NONE>, grid, dim3(256), lds, s, x, w, oscale, bias, y, q, xi, chunk,
+                         pitch);
       break;
   }
   return true;
@@ -488,8 +501,8 @@ static size_t conv_scratch_bytes(const ConvGeo &q) {
 // Runs the space-to-depth form of a stride-2 bf16 NHWC conv (C_IN % 8 != 0)
 // in the caller's scratch.  Returns false (nothing launched) if the scratch
 // is too small for the rewritten input and weights.
-static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, void *y, const ConvGeo &q,
-                          int act, hipStream_t s, Scratch scr) {
+static bool conv_s2d_mfma(const void *x, const void *w, const float *scale, const float *bias,
+                          const bf16 *bias_bf16, void *y, const ConvGeo &q, int act, hipStream_t s, Scratch scr) {
   const S2DPlan sp = s2d_plan(q);
   if (scr.ptr == nullptr || scr.bytes < sp.gemm_off) return false;
   const ConvGeo &g2 = sp.g2;
@@ -501,7 +514,7 @@ static bool conv_s2d_mfma(const void *x, const void *w, const bf16 *bias_bf16, v
   hipLaunchKernelGGL(s2d_kernel, dim3(static_cast<unsigned>(nbx + nbw)), dim3(256), 0, s,
                      static_cast<const bf16 *>(x), xs, static_cast<const bf16 *>(w), wsd, nbx, q.B, q.H, q.W,
                      q.Cin, q.PH, q.PW, g2.H, g2.W, q.Cout, q.KH, q.KW, g2.KH, g2.KW, g2.Cin);
-  GemmParams p = conv_gemm_params(xs, wsd, nullptr, nullptr, bias_bf16, y, g2);
+  GemmParams p = conv_gemm_params(xs, wsd, scale, bias, bias_bf16, y, g2);
   const Scratch rest{static_cast<char *>(scr.ptr) + sp.gemm_off, scr.bytes - sp.gemm_off};
   launch_gemm_mfma<false, kAConvVec>(p, act, s, rest);
   return true;
@@ -515,7 +528,7 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
   if (!aligned(x, 16) || !aligned(w, 16)) return false;
   const ConvPath path = conv_path<INT8B>(q);
   if (path == kConvNoMfma) return false;
-  if (path == kConvS2D && conv_s2d_mfma(x, w, bias_bf16, y, q, act, s, scr)) return true;
+  if (path == kConvS2D && conv_s2d_mfma(x, w, scale, bias, bias_bf16, y, q, act, s, scr)) return true;
   GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
   if (INT8B && (path == kConvPlain ? w8_dequant_pays<kAPlain>(p) : w8_dequant_pays<kAConvVec>(p)) &&
       scr.ptr != nullptr && scr.bytes >= dequant_scratch_bytes(static_cast<int64_t>(p.N) * p.K)) {
@@ -568,6 +581,48 @@ static teeny_status conv_entry(const void *x, const void *w, const void *bias, v
     return after_launch(name, s);
   }
   return fail(TEENY_ERR_UNSUPPORTED_DTYPE, std::string(name) + ": dtype must be F32 or BF16");
+}
+
+// Conv + BatchNorm (inference, folded to a per-channel affine) + activation:
+// y = act(bn_scale[c] * conv(x, w)[c] + bn_shift[c]) in the conv's own
+// epilogue (fp32 accumulator, one store).  `ys` (NCHW only, may be null)
+// replaces y's strides, for the reference's padded output rows.
+static teeny_status conv_bn_entry(const void *x, const void *w, const float *bn_scale, const float *bn_shift,
+                                  void *y, int64_t B, int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t OH,
+                                  int64_t OW, const int64_t *ys, const teeny_conv2d_params *prm, teeny_dtype dtype,
+                                  teeny_layout layout, teeny_stream stream, const char *name) {
+  const std::string nm(name);
+  ConvGeo q;
+  teeny_status st = make_geo(B, Cin, Cout, H, W, OH, OW, prm, layout, &q, name);
+  if (st != TEENY_OK) return st;
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                nm + ": dtype must be F32 or BF16");
+  if (ys != nullptr) {
+    TEENY_REQUIRE(layout == TEENY_NCHW, TEENY_ERR_UNSUPPORTED, nm + ": output strides are for NCHW");
+    // rows of one channel, channels of one image and images must not overlap
+    TEENY_REQUIRE(ys[3] == 1 && ys[2] >= OW && ys[1] >= (OH - 1) * ys[2] + OW &&
+                      ys[0] >= (Cout - 1) * ys[1] + (OH - 1) * ys[2] + OW,
+                  TEENY_ERR_SHAPE_MISMATCH, nm + ": output strides overlap or are not row-major");
+    for (int i = 0; i < 4; ++i) q.ys[i] = ys[i];
+  }
+  if (B == 0) return TEENY_OK;
+  TEENY_REQUIRE(x != nullptr && w != nullptr && bn_scale != nullptr && bn_shift != nullptr && y != nullptr,
+                TEENY_ERR_NULL_POINTER, nm + ": x/w/bn_scale/bn_shift/y");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TEENY_F32) {
+    if (!(layout == TEENY_NCHW && try_conv_f32_mfma(static_cast<const float *>(x), static_cast<const float *>(w),
+                                                    bn_shift, static_cast<float *>(y), q, prm->act, s, bn_scale))) {
+      launch_direct<float, float>(static_cast<const float *>(x), static_cast<const float *>(w), nullptr, nullptr,
+                                  bn_shift, static_cast<float *>(y), q, prm->act, s, bn_scale);
+    }
+    return after_launch(name, s);
+  }
+  if (!(layout == TEENY_NHWC &&
+        try_conv_mfma<false>(x, w, bn_scale, bn_shift, nullptr, y, q, prm->act, s, stream_scratch(s)))) {
+    launch_direct<bf16, bf16>(static_cast<const bf16 *>(x), static_cast<const bf16 *>(w), nullptr, nullptr, bn_shift,
+                              static_cast<bf16 *>(y), q, prm->act, s, bn_scale);
+  }
+  return after_launch(name, s);
 }
 
 // ── backward ────────────────────────────────────────────────────────────
@@ -1014,6 +1069,15 @@ teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void 
   TEENY_REQUIRE(bias != nullptr, TEENY_ERR_NULL_POINTER, "conv2d_bias_forward: bias");
   return conv_entry(x, w, bias, y, B, C_IN, C_OUT, H, W, OH, OW, params, dtype, layout, stream,
                     "conv2d_bias_forward");
+}
+
+teeny_status teeny_conv2d_bn_act_forward(const void *x, const void *w, const float *bn_scale, const float *bn_shift,
+                                        void *y, int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
+                                        int64_t OH, int64_t OW, const int64_t *y_strides,
+                                        const teeny_conv2d_params *params, teeny_dtype dtype, teeny_layout layout,
+                                        teeny_stream stream) {
+  return conv_bn_entry(x, w, bn_scale, bn_shift, y, B, C_IN, C_OUT, H, W, OH, OW, y_strides, params, dtype, layout,
+                       stream, "conv2d_bn_act_forward");
 }
 
 teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, const void *bias, void *y,

@@ -9,7 +9,9 @@
 // plus the kernel's const generics, and forwards to the matching teeny_*
 // entry point.  Argument kinds are checked; a mismatch is an error, never a
 // reinterpretation.
+#include <algorithm>
 #include <cstring>
+#include <string>
 
 #include "common.hpp"
 
@@ -280,6 +282,63 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
                                 syn, dtype, stream);
   }
 
+  // Conv + BatchNorm (folded scale / shift) + SiLU, the reference's three fused variants
+  // (nn/fused/): fp32 NCHW, the activation fixed to SiLU.
+  //   conv2d_bn_silu_forward<KH,KW,SH,SW,PH,PW,G,BLOCK_OW>(x, w, bn_scale, bn_shift, y,
+  //     B, C_IN, C_OUT, H, W, OH, OW)                               conv2d_bn_silu.rs:40-64
+  //   conv2d_bn_silu_gemm_forward<BLOCK_M,BLOCK_N,BLOCK_K,GROUP_M>(x, w, bn_scale, bn_shift,
+  //     y, B, C_IN, C_OUT, M, y_row_stride): 1x1 stride 1, output rows of y_row_stride
+  //                                                                 conv2d_bn_silu_gemm.rs:61-80
+  //   conv2d_bn_silu_tiled_forward<KH,KW,SH,SW,PH,PW,BLOCK_OW,BLOCK_N>(x, w, bn_scale,
+  //     bn_shift, y, B, C_IN, C_OUT, H, W, OH, OW, y_col_stride): groups 1, each oh row
+  //     y_col_stride wide                                           conv2d_bn_silu_tiled.rs:49-78
+  const bool bn_plain = name_is(entry_point, "conv2d_bn_silu_forward");
+  const bool bn_gemm = name_is(entry_point, "conv2d_bn_silu_gemm_forward");
+  const bool bn_tiled = name_is(entry_point, "conv2d_bn_silu_tiled_forward");
+  if (bn_plain || bn_gemm || bn_tiled) {
+    TEENY_REQUIRE(n_cg == (bn_gemm ? 4 : 8), TEENY_ERR_INVALID_ARGUMENT,
+                  std::string(entry_point) + (bn_gemm ? ": expects const generics BLOCK_M,BLOCK_N,BLOCK_K,GROUP_M"
+                                                      : ": expects 8 const generics"));
+    teeny_conv2d_params p{1, 1, 1, 1, 0, 0, 1, TEENY_ACT_SILU};
+    if (!bn_gemm) {
+      p.KH = static_cast<int32_t>(cg[0]);
+      p.KW = static_cast<int32_t>(cg[1]);
+      p.stride_h = static_cast<int32_t>(cg[2]);
+      p.stride_w = static_cast<int32_t>(cg[3]);
+      p.pad_h = static_cast<int32_t>(cg[4]);
+      p.pad_w = static_cast<int32_t>(cg[5]);
+      p.groups = bn_plain ? static_cast<int32_t>(cg[6]) : 1;
+    }
+    void *x = r.ptr("x_ptr"), *w = r.ptr("w_ptr"), *sc = r.ptr("bn_scale_ptr"), *sh = r.ptr("bn_shift_ptr"),
+         *y = r.ptr("y_ptr");
+    int64_t B = r.i32("B"), Ci = r.i32("C_IN"), Co = r.i32("C_OUT");
+    int64_t H, W, OH, OW, ys[4];
+    if (bn_gemm) {
+      const int64_t M = r.i32("M"), rs = r.i32("y_row_stride");
+      H = OH = 1;
+      W = OW = M;
+      ys[0] = Co * rs;
+      ys[1] = rs;
+      ys[2] = rs;
+      ys[3] = 1;
+    } else {
+      H = r.i32("H");
+      W = r.i32("W");
+      OH = r.i32("OH");
+      OW = r.i32("OW");
+      if (bn_tiled) {
+        const int64_t cs = r.i32("y_col_stride");
+        ys[0] = Co * OH * cs;
+        ys[1] = OH * cs;
+        ys[2] = cs;
+        ys[3] = 1;
+      }
+    }
+    if (r.done() != TEENY_OK) return r.st;
+    return teeny_conv2d_bn_act_forward(x, w, static_cast<const float *>(sc), static_cast<const float *>(sh), y, B, Ci,
+                                       Co, H, W, OH, OW, bn_plain ? nullptr : ys, &p, dtype, TEENY_NCHW, stream);
+  }
+
   // ── training kernels ──
   // layer_norm_forward<BLOCK_N>(x, y, weight, bias, mean, rstd, M, N, eps)        layernorm.rs:163-172
   // layer_norm_backward<BLOCK_N>(dy, x, dx, weight, dweight, dbias, mean, rstd, M, N)  :301-311
@@ -372,6 +431,49 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
                                                 grid[1], cg[0], causal, dtype, stream);
     return teeny_flash_attention2_backward_dkv(q, k, v, o, d_o, static_cast<const float *>(l), g0, g1, nq, nk, scale,
                                                grid[1], cg[0], causal, dtype, stream);
+  }
+
+  // pointwise_fuse_<m0>_<m1>..._entry_point(x, y, scratch_0 .. scratch_{n-2}, n_elements) and
+  // pointwise_fuse_<tag>_backward_entry_point(dy, y, dx, scratch_0 .., n_elements): the
+  // PointwiseFuse custom op's runtime ABI (graph/optimizer/ops/pointwise_fuse.rs:155-268);
+  // the tag joins the members' kernel names without "_forward" (:315-321).
+  {
+    const char *pre = "pointwise_fuse_";
+    const size_t lp = std::strlen(pre);
+    if (std::strncmp(entry_point, pre, lp) == 0) {
+      std::string tag(entry_point + lp);
+      const std::string ep_suffix = "_entry_point";
+      if (tag.size() > ep_suffix.size() && tag.compare(tag.size() - ep_suffix.size(), ep_suffix.size(), ep_suffix) == 0)
+        tag.resize(tag.size() - ep_suffix.size());
+      const std::string bwd_suffix = "_backward";
+      const bool bwd =
+          tag.size() > bwd_suffix.size() && tag.compare(tag.size() - bwd_suffix.size(), bwd_suffix.size(), bwd_suffix) == 0;
+      if (bwd) tag.resize(tag.size() - bwd_suffix.size());
+      int32_t ops[8];
+      int32_t n_ops = 0;
+      size_t at = 0;
+      while (at <= tag.size()) {
+        const size_t end = std::min(tag.find('_', at), tag.size());
+        const std::string m = tag.substr(at, end - at);
+        int32_t op = m == "relu" ? TEENY_PW_RELU : m == "gelu" ? TEENY_PW_GELU_TANH : m == "silu" ? TEENY_PW_SILU
+                     : m == "sigmoid" ? TEENY_PW_SIGMOID : m == "tanh" ? TEENY_PW_TANH : 0;
+        TEENY_REQUIRE(op != 0, TEENY_ERR_NOT_FOUND,
+                      std::string("dispatch: pointwise_fuse member '") + m + "' has no fused kernel");
+        TEENY_REQUIRE(n_ops < 8, TEENY_ERR_INVALID_ARGUMENT, "dispatch: pointwise_fuse: at most 8 members");
+        ops[n_ops++] = op;
+        at = end + 1;
+      }
+      TEENY_REQUIRE(n_ops >= 2, TEENY_ERR_INVALID_ARGUMENT, "dispatch: pointwise_fuse needs at least 2 members");
+      void *a = r.ptr(bwd ? "dy_ptr" : "x_ptr");
+      void *b = r.ptr("y_ptr");
+      void *dx = bwd ? r.ptr("dx_ptr") : nullptr;
+      void *scratch[8] = {nullptr};
+      for (int32_t m = 0; m + 1 < n_ops; ++m) scratch[m] = r.ptr("scratch");
+      const int64_t n = r.i32("n_elements");
+      if (r.done() != TEENY_OK) return r.st;
+      if (bwd) return teeny_pointwise_chain_backward(a, b, dx, scratch, ops, n_ops, n, dtype, stream);
+      return teeny_pointwise_chain_forward(a, b, scratch, ops, n_ops, n, dtype, stream);
+    }
   }
 
   return fail(TEENY_ERR_NOT_FOUND, std::string("dispatch: no operator for ") + entry_point);

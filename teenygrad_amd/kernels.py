@@ -297,6 +297,69 @@ class RmsNormForwardRuntimeOp(RuntimeOp):
         return (_prod(output_shape) // n, 1, 1)
 
 
+POINTWISE_MEMBERS = {"relu": _lib.PW_RELU, "gelu": _lib.PW_GELU_TANH, "silu": _lib.PW_SILU,
+                     "sigmoid": _lib.PW_SIGMOID, "tanh": _lib.PW_TANH}
+Y_STYLE_MEMBERS = ("relu", "sigmoid", "tanh")
+
+
+class PointwiseFuse(RuntimeOp):
+    """The PointwiseFuse custom op's RuntimeOp (graph/optimizer/ops/
+    pointwise_fuse.rs:155-268): params are the n-1 scratch buffers [n]
+    (member outputs kept for backward), args (x, y, scratch..., n_elements),
+    backward args (dy, y, dx, scratch..., n_elements) when every member has a
+    y-style gradient; grid ceil(n / BLOCK_SIZE)."""
+
+    def __init__(self, members, block_size: int = 1024):
+        members = list(members)
+        _need(2 <= len(members) <= 8, "PointwiseFuse: 2 to 8 members")
+        for m in members:
+            _need(m in POINTWISE_MEMBERS, f"PointwiseFuse: no fused kernel for member {m!r}")
+        self.members = members
+        self.block_size = int(block_size)
+        self.name = "pointwise_fuse_" + "_".join(members)
+
+    @property
+    def n_scratch(self) -> int:
+        return len(self.members) - 1
+
+    def const_generics(self):
+        return ()
+
+    def param_shapes(self, input_shapes, output_shape):
+        return [[_prod(output_shape)] for _ in range(self.n_scratch)]
+
+    def param_names(self):
+        return tuple(f"scratch{i}" for i in range(self.n_scratch))
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(output)
+        for p in params[:self.n_scratch]:
+            visitor.visit_ptr(p)
+        visitor.visit_i32(_prod(output_shape))
+
+    def grid(self, output_shape):
+        return (-(-_prod(output_shape) // self.block_size), 1, 1)
+
+    def has_backward(self) -> bool:
+        return all(m in Y_STYLE_MEMBERS for m in self.members)
+
+    def backward_entry_point_name(self) -> str:
+        return f"{self.name}_backward_entry_point"
+
+    def pack_backward_args(self, inputs, params, output, output_shape, grad_output, grad_output_row_stride,
+                           grad_inputs, grad_params, visitor):
+        visitor.visit_ptr(grad_output)
+        visitor.visit_ptr(output)
+        visitor.visit_ptr(grad_inputs[0])
+        for p in params[:self.n_scratch]:
+            visitor.visit_ptr(p)
+        visitor.visit_i32(_prod(output_shape))
+
+    def backward_grid(self, input_shapes, output_shape):
+        return self.grid(output_shape)
+
+
 class Conv2dForward(RuntimeOp):
     """conv2d.rs:523-618: const generics KH, KW, STRIDE_H, STRIDE_W, PAD_H,
     PAD_W, G, BLOCK_OW; args (x, w, y, B, C_IN, C_OUT, H, W, OH, OW)."""
@@ -367,6 +430,135 @@ class Conv2dForward(RuntimeOp):
 
     def backward_grid(self, input_shapes, output_shape):
         return self.grid(output_shape)
+
+
+class Conv2dBnSiluForward(Conv2dForward):
+    """conv2d_bn_silu.rs:200-245: params (weight, bn_scale, bn_shift); args
+    (x, w, bn_scale, bn_shift, y, B, C_IN, C_OUT, H, W, OH, OW); the grid of
+    conv2d_forward.  Inference only."""
+
+    name = "conv2d_bn_silu_forward"
+
+    def param_shapes(self, input_shapes, output_shape):
+        c_in, c_out = int(input_shapes[0][1]), int(output_shape[1])
+        return [[c_out, c_in // self.g, self.kh, self.kw], [c_out], [c_out]]
+
+    def param_names(self):
+        return ("weight", "bn_scale", "bn_shift")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        ish = inputs[0][1]
+        visitor.visit_ptr(inputs[0][0])
+        for p in params[:3]:
+            visitor.visit_ptr(p)
+        visitor.visit_ptr(output)
+        for v in (ish[0], ish[1], output_shape[1], ish[2], ish[3], output_shape[2], output_shape[3]):
+            visitor.visit_i32(v)
+
+    def has_backward(self) -> bool:
+        return False
+
+
+class Conv2dBnSiluGemmForward(RuntimeOp):
+    """conv2d_bn_silu_gemm.rs:200-260: 1x1 stride-1 conv as a GEMM; const
+    generics BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M; args (x, w, bn_scale,
+    bn_shift, y, B, C_IN, C_OUT, M, y_row_stride) with each (b, c_out) row of
+    y padded to a multiple of BLOCK_M."""
+
+    name = "conv2d_bn_silu_gemm_forward"
+
+    def __init__(self, block_m=32, block_n=32, block_k=32, group_m=8):
+        self.block_m, self.block_n, self.block_k, self.group_m = int(block_m), int(block_n), int(block_k), int(group_m)
+
+    def const_generics(self):
+        return (self.block_m, self.block_n, self.block_k, self.group_m)
+
+    def param_shapes(self, input_shapes, output_shape):
+        return [[int(output_shape[1]), int(input_shapes[0][1])], [int(output_shape[1])], [int(output_shape[1])]]
+
+    def param_names(self):
+        return ("weight", "bn_scale", "bn_shift")
+
+    def forward_output_row_elems(self, output_shape):
+        return int(output_shape[2]) * int(output_shape[3])
+
+    def forward_output_row_stride(self, output_shape):
+        m = self.forward_output_row_elems(output_shape)
+        return -(-m // self.block_m) * self.block_m
+
+    def check_buffers(self, inputs, params, output, output_shape):
+        rows = int(output_shape[0]) * int(output_shape[1])
+        RuntimeOp.check_buffers(self, inputs, params, None, output_shape)
+        if isinstance(output, Buffer):
+            _need(output.numel >= rows * self.forward_output_row_stride(output_shape),
+                  f"{self.name}: y must hold the padded rows")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        ish = inputs[0][1]
+        visitor.visit_ptr(inputs[0][0])
+        for p in params[:3]:
+            visitor.visit_ptr(p)
+        visitor.visit_ptr(output)
+        for v in (ish[0], ish[1], output_shape[1], int(output_shape[2]) * int(output_shape[3]), output_row_stride):
+            visitor.visit_i32(v)
+
+    def grid(self, output_shape):
+        m = int(output_shape[2]) * int(output_shape[3])
+        return (int(output_shape[0]) * -(-m // self.block_m) * -(-int(output_shape[1]) // self.block_n), 1, 1)
+
+    def has_backward(self) -> bool:
+        return False
+
+
+class Conv2dBnSiluTiledForward(RuntimeOp):
+    """conv2d_bn_silu_tiled.rs:214-293: const generics KH, KW, STRIDE_H,
+    STRIDE_W, PAD_H, PAD_W, BLOCK_OW, BLOCK_N (groups 1); args (x, w,
+    bn_scale, bn_shift, y, B, C_IN, C_OUT, H, W, OH, OW, y_col_stride), each
+    oh row of y padded to a multiple of BLOCK_OW."""
+
+    name = "conv2d_bn_silu_tiled_forward"
+
+    def __init__(self, kh, kw, stride_h=1, stride_w=1, pad_h=0, pad_w=0, block_ow=16, block_n=16):
+        self.kh, self.kw, self.sh, self.sw = int(kh), int(kw), int(stride_h), int(stride_w)
+        self.ph, self.pw, self.block_ow, self.block_n = int(pad_h), int(pad_w), int(block_ow), int(block_n)
+
+    def const_generics(self):
+        return (self.kh, self.kw, self.sh, self.sw, self.ph, self.pw, self.block_ow, self.block_n)
+
+    def param_shapes(self, input_shapes, output_shape):
+        c_in, c_out = int(input_shapes[0][1]), int(output_shape[1])
+        return [[c_out, c_in, self.kh, self.kw], [c_out], [c_out]]
+
+    def param_names(self):
+        return ("weight", "bn_scale", "bn_shift")
+
+    def forward_output_row_stride(self, output_shape):
+        return -(-int(output_shape[3]) // self.block_ow) * self.block_ow
+
+    def check_buffers(self, inputs, params, output, output_shape):
+        RuntimeOp.check_buffers(self, inputs, params, None, output_shape)
+        if isinstance(output, Buffer):
+            rows = int(output_shape[0]) * int(output_shape[1]) * int(output_shape[2])
+            _need(output.numel >= rows * self.forward_output_row_stride(output_shape),
+                  f"{self.name}: y must hold the padded rows")
+
+    def pack_args(self, inputs, params, output, output_shape, output_row_stride, visitor):
+        ish = inputs[0][1]
+        visitor.visit_ptr(inputs[0][0])
+        for p in params[:3]:
+            visitor.visit_ptr(p)
+        visitor.visit_ptr(output)
+        for v in (ish[0], ish[1], output_shape[1], ish[2], ish[3], output_shape[2], output_shape[3],
+                  output_row_stride):
+            visitor.visit_i32(v)
+
+    def grid(self, output_shape):
+        tiles_ow = -(-int(output_shape[3]) // self.block_ow)
+        tiles_n = -(-int(output_shape[1]) // self.block_n)
+        return (int(output_shape[0]) * int(output_shape[2]) * tiles_n * tiles_ow, 1, 1)
+
+    def has_backward(self) -> bool:
+        return False
 
 
 class Conv2dBiasForward(Conv2dForward):
@@ -850,6 +1042,77 @@ def conv2d(x: Buffer, w: Buffer, bias: Optional[Buffer] = None, stride=(1, 1), p
         check(lib.teeny_conv2d_bias_forward(x.ptr, w.ptr, bias.ptr, y.ptr, b, cin, cout, h, wd, oh,
                                             ow, ctypes.byref(prm), x.dtype.code, lay, _h(stream)))
     return y
+
+
+def _chain_args(members, scratch):
+    ops = (ctypes.c_int32 * len(members))(*(POINTWISE_MEMBERS[m] for m in members))
+    sc = None
+    if scratch is not None:
+        _need(len(scratch) >= len(members) - 1, "pointwise chain: one scratch buffer per member but the last")
+        sc = (ctypes.c_void_p * max(1, len(scratch)))(*((b.ptr if b is not None else None) for b in scratch))
+    return ops, sc
+
+
+def pointwise_chain(x: Buffer, members, y: Optional[Buffer] = None, scratch=None,
+                    stream: Optional[Stream] = None) -> Buffer:
+    """PointwiseFuse forward (pointwise_fuse.rs:73-233): the members applied in
+    one pass; scratch[i] (optional) receives member i's output."""
+    y = _out(x, y)
+    for b in scratch or []:
+        _need(b is None or (b.numel == x.numel and b.dtype == x.dtype), "pointwise chain: scratch like x")
+    ops, sc = _chain_args(members, scratch)
+    check(lib.teeny_pointwise_chain_forward(x.ptr, y.ptr, sc, ops, len(members), x.numel, x.dtype.code, _h(stream)))
+    return y
+
+
+def pointwise_chain_backward(dy: Buffer, y: Buffer, scratch, members, dx: Optional[Buffer] = None,
+                             stream: Optional[Stream] = None) -> Buffer:
+    """The fused chain's backward (members relu / sigmoid / tanh): dx from dy,
+    the chain output y and the kept member outputs."""
+    _need(dy.numel == y.numel and dy.dtype == y.dtype, "pointwise chain backward: dy like y")
+    for b in scratch:
+        _need(b.numel == y.numel and b.dtype == y.dtype, "pointwise chain backward: scratch like y")
+    dx = _out(dy, dx)
+    ops, sc = _chain_args(members, scratch)
+    check(lib.teeny_pointwise_chain_backward(dy.ptr, y.ptr, dx.ptr, sc, ops, len(members), dy.numel, dy.dtype.code,
+                                             _h(stream)))
+    return dx
+
+
+def conv2d_bn_act(x: Buffer, w: Buffer, bn_scale: Buffer, bn_shift: Buffer, stride=(1, 1), padding=(0, 0),
+                  groups: int = 1, act: Optional[str] = "silu", layout: str = "nchw", y: Optional[Buffer] = None,
+                  y_strides=None, stream: Optional[Stream] = None) -> Buffer:
+    """conv2d_bn_silu.rs:26-199 with any activation: act(bn_scale[c] * conv + bn_shift[c]),
+    bn_scale / bn_shift fp32 [C_OUT] (BatchNorm folded by the caller).  y_strides (NCHW)
+    addresses padded output rows; y must then hold the strided extent."""
+    nhwc = layout.lower() == "nhwc"
+    b, cin, cout, h, wd, oh, ow, kh, kw, sh, sw, ph, pw = conv2d_dims(
+        x.shape, w.shape, stride, padding, groups, "nhwc" if nhwc else "nchw")
+    _need(w.dtype == x.dtype, "conv2d_bn_act: w dtype must match x")
+    _need(bn_scale.numel == cout and bn_shift.numel == cout and bn_scale.dtype == f32 and bn_shift.dtype == f32,
+          f"conv2d_bn_act: bn_scale / bn_shift fp32 [{cout}]")
+    yshape = (b, oh, ow, cout) if nhwc else (b, cout, oh, ow)
+    strides = None
+    if y_strides is not None:
+        _need(y is not None and not nhwc, "conv2d_bn_act: y_strides needs an NCHW y buffer")
+        strides = (ctypes.c_int64 * 4)(*y_strides)
+        _need(y.numel >= (b - 1) * y_strides[0] + (cout - 1) * y_strides[1] + (oh - 1) * y_strides[2] + ow,
+              "conv2d_bn_act: y smaller than its strided extent")
+    else:
+        y = _out(x, y, yshape)
+    prm = _lib.Conv2dParams(kh, kw, sh, sw, ph, pw, groups, ACTS[act])
+    check(lib.teeny_conv2d_bn_act_forward(x.ptr, w.ptr, bn_scale.ptr, bn_shift.ptr, y.ptr, b, cin, cout, h, wd, oh,
+                                          ow, strides, ctypes.byref(prm), x.dtype.code,
+                                          _lib.NHWC if nhwc else _lib.NCHW, _h(stream)))
+    return y
+
+
+def fold_batchnorm(gamma, beta, mean, var, eps=1e-5):
+    """Host-side BatchNorm folding, the convention of conv2d_bn_silu.rs:32-35:
+    bn_scale = gamma / sqrt(var + eps), bn_shift = beta - bn_scale * mean (fp32)."""
+    gamma, beta, mean, var = (np.asarray(a, np.float32) for a in (gamma, beta, mean, var))
+    scale = (gamma / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    return scale, (beta - scale * mean).astype(np.float32)
 
 
 def _conv_bwd_args(x_shape, w_shape, stride, padding, groups, layout, dtype):
