@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
 
   // row total of a per-lane partial: wave shuffle, then across the row's waves via LDS
   auto row_sum = [&](float part_sum, int slot) {
-    part_sum = wave_sum(part_sum);
+    part_sum = wave_total(part_sum);
     if (WPR == 1) return part_sum;
     if (lane == 0) red[w][slot] = part_sum;
     __syncthreads();

@@ -14,16 +14,17 @@
 // MI355X design (HBM-bound: read x and dy, write dx).  A persistent grid of G
 // workgroups walks the rows (row r on workgroup r mod G); each thread owns
 // VPT fixed 16-byte column vectors of every row, so gamma is loaded once and
-// the per-column gradient partials stay in fp32 registers across rows.  A
-// row's one or two sums are a wave shuffle plus one LDS exchange; the LDS
-// slots alternate between rows so one barrier per row suffices.  At the end
-// each workgroup writes its column partials to the stream workspace and a
-// second kernel adds the G partials of every column, in workgroup order, to
-// dweight (and dbias).  Without a large enough workspace the parameter
-// gradients come from a column kernel that re-reads x and dy instead (no
-// scratch, two more tensor reads).  Rows that do not fit the register plan
-// (N > 8192 bf16 / 4096 fp32, N % 8 != 0, unaligned) take a multi-pass
-// wave-per-row kernel for dx and the column kernel.
+// the per-column gradient partials stay in fp32 registers across rows.  The
+// rows two ahead are loaded (raw, with their statistics) before the current
+// row's reductions, which are DPP wave sums plus one LDS exchange (one
+// barrier per row: each register set has its own LDS slot).  At the end each
+// workgroup writes its column partials to the stream workspace and two
+// small passes add them per column in a fixed order (slices of workgroups,
+// then the slices) to dweight (and dbias).  Without a large enough workspace
+// the parameter gradients come from a column kernel that re-reads x and dy
+// instead (no scratch, two more tensor reads).  Rows that do not fit the
+// register plan (N > 8192 bf16 / 4096 fp32, N % 8 != 0, unaligned) take a
+// multi-pass wave-per-row kernel for dx and the column kernel.
 #include "common.hpp"
 
 namespace teeny {
@@ -54,6 +55,8 @@ __device__ __forceinline__ void store_vec(T *p, const float *v) {
 
 // dx for rows blockIdx.x, blockIdx.x + G, ...; with PART, per-workgroup column
 // partials of dweight (part_g) and dbias (part_b, LayerNorm) as fp32 [G, N].
+// The next row's x and dy are loaded (raw, two register sets) before the
+// current row's reductions, so each workgroup keeps two rows in flight.
 template <typename T, int VPT, bool RMS, bool PART>
 __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
     const T *__restrict__ dy, const T *__restrict__ x, T *__restrict__ dx, const T *__restrict__ gamma,
@@ -61,9 +64,10 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
     float *__restrict__ part_b, int64_t M, int32_t N, float inv_n) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NS = RMS ? 1 : 2;  // row sums
-  __shared__ float red[2][kNbWaves][NS];
+  __shared__ float red[3][kNbWaves][NS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nv = N / VEC;
+  const int64_t G = gridDim.x;
   float g[VPT][VEC], acc_g[VPT][VEC], acc_b[VPT][VEC];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -76,24 +80,40 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
       acc_b[j][i] = 0.0f;
     }
   }
-  int par = 0;
-  for (int64_t row = blockIdx.x; row < M; row += gridDim.x, par ^= 1) {
-    const T *xr = x + row * N, *dyr = dy + row * N;
+  // raw 16-byte vectors of a row and its statistics: vectors past N load the
+  // row's last vector and are zeroed by a select (no branch, so the arrays
+  // stay in registers and the compiler's waits stay exact)
+  auto load_raw = [&](int64_t row, u32x4 (&rx)[VPT], u32x4 (&rd)[VPT], float &sa, float &sb)
+                      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = j * kNbThreads + tid;
+      const int vc = v < nv ? v : nv - 1;
+      const u32x4 tx = *reinterpret_cast<const u32x4 *>(x + row * N + static_cast<int64_t>(vc) * VEC);
+      const u32x4 td = *reinterpret_cast<const u32x4 *>(dy + row * N + static_cast<int64_t>(vc) * VEC);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      rx[j] = v < nv ? tx : z;
+      rd[j] = v < nv ? td : z;
+    }
+    sa = st0[row];
+    sb = RMS ? sa : st1[row];
+  };
+  auto process = [&](int64_t row, const u32x4 (&rx)[VPT], const u32x4 (&rd)[VPT], float a, float rstd, int par)
+                     __attribute__((always_inline)) {
     T *dxr = dx + row * N;
     float xv[VPT][VEC], dv[VPT][VEC];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int v = j * kNbThreads + tid;
-      if (v < nv) {
-        load_vec(xr + static_cast<int64_t>(v) * VEC, xv[j]);
-        load_vec(dyr + static_cast<int64_t>(v) * VEC, dv[j]);
-      } else {
+      T ex[VEC], ed[VEC];
+      __builtin_memcpy(ex, &rx[j], 16);
+      __builtin_memcpy(ed, &rd[j], 16);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[j][i] = dv[j][i] = 0.0f;
+      for (int i = 0; i < VEC; ++i) {
+        xv[j][i] = to_f32(ex[i]);
+        dv[j][i] = to_f32(ed[i]);
       }
     }
-    const float a = st0[row];                // LayerNorm: mean; RMSNorm: rrms
-    const float rstd = RMS ? a : st1[row];   // LayerNorm: rstd
+    // a: LayerNorm mean, RMSNorm rrms; rstd: LayerNorm rstd, RMSNorm rrms
     float s[NS];
 #pragma unroll
     for (int k = 0; k < NS; ++k) s[k] = 0.0f;
@@ -110,7 +130,7 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
         }
       }
 #pragma unroll
-    for (int k = 0; k < NS; ++k) s[k] = wave_sum(s[k]);
+    for (int k = 0; k < NS; ++k) s[k] = wave_total(s[k]);
     if (lane == 0)
 #pragma unroll
       for (int k = 0; k < NS; ++k) red[par][w][k] = s[k];
@@ -138,6 +158,28 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
       }
       if (v < nv) store_vec(dxr + static_cast<int64_t>(v) * VEC, o);
     }
+  };
+  // three register sets, two rows ahead, unrolled by three so the sets
+  // rotate without copies; each set has its own LDS slot (one barrier per
+  // row).  Past the last row a prefetch re-reads the current row (cached, and
+  // never used), so the loads need no branch.  The grid has at most M
+  // workgroups.
+  u32x4 xa[VPT], da[VPT], xb[VPT], db[VPT], xc[VPT], dc[VPT];
+  float sa0, sa1, sb0, sb1, sc0, sc1;
+  auto clamp = [&](int64_t r, int64_t cur) { return r < M ? r : cur; };
+  int64_t row = blockIdx.x;
+  load_raw(row, xa, da, sa0, sa1);
+  load_raw(clamp(row + G, row), xb, db, sb0, sb1);
+  for (; row < M; row += 3 * G) {
+    const int64_t r1 = row + G, r2 = row + 2 * G;
+    load_raw(clamp(r2, row), xc, dc, sc0, sc1);
+    process(row, xa, da, sa0, sa1, 0);
+    if (r1 >= M) break;
+    load_raw(clamp(r2 + G, r1), xa, da, sa0, sa1);
+    process(r1, xb, db, sb0, sb1, 1);
+    if (r2 >= M) break;
+    load_raw(clamp(r2 + 2 * G, r2), xb, db, sb0, sb1);
+    process(r2, xc, dc, sc0, sc1, 2);
   }
   if constexpr (PART) {
     float *pg = part_g + static_cast<int64_t>(blockIdx.x) * N;
@@ -155,32 +197,62 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
   }
 }
 
-// dweight[n] += sum_g part_g[g, n] (and dbias from part_b), g in order: a
-// workgroup owns 64 columns, its four waves take g = w, w+4, ... and the
-// wave sums are added in wave order.
-__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum_kernel(const float *__restrict__ part_g,
-                                                                     const float *__restrict__ part_b, int G,
-                                                                     int N, float *__restrict__ dweight,
-                                                                     float *__restrict__ dbias) {
+// Column sums of the per-workgroup partials, in two deterministic passes that
+// fill the chip.  Pass 1: workgroup (column block c, slice q) adds rows
+// [q G / S, (q+1) G / S) of part for 64 columns; its four waves take
+// interleaved rows with eight independent accumulators per lane (eight loads
+// in flight), combined in a fixed order, into out[q, n].  Pass 2 adds the S
+// slices in order to dweight (and dbias).
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum1(const float *__restrict__ part_g,
+                                                               const float *__restrict__ part_b, int G, int N, int S,
+                                                               float *__restrict__ out_g, float *__restrict__ out_b) {
   __shared__ float red[kNbWaves][64][2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int n = blockIdx.x * 64 + lane;
-  float sg = 0.0f, sb = 0.0f;
+  const int q = blockIdx.y;
+  const int g0 = static_cast<int>(static_cast<int64_t>(q) * G / S);
+  const int g1 = static_cast<int>(static_cast<int64_t>(q + 1) * G / S);
+  float ag[8], ab[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ag[k] = ab[k] = 0.0f;
   if (n < N) {
-    for (int gi = w; gi < G; gi += kNbWaves) {
-      sg += part_g[static_cast<int64_t>(gi) * N + n];
-      if (part_b != nullptr) sb += part_b[static_cast<int64_t>(gi) * N + n];
+    int g = g0 + w;
+    for (; g + 7 * kNbWaves < g1; g += 8 * kNbWaves) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t o = static_cast<int64_t>(g + k * kNbWaves) * N + n;
+        ag[k] += part_g[o];
+        if (part_b != nullptr) ab[k] += part_b[o];
+      }
+    }
+    for (; g < g1; g += kNbWaves) {
+      const int64_t o = static_cast<int64_t>(g) * N + n;
+      ag[0] += part_g[o];
+      if (part_b != nullptr) ab[0] += part_b[o];
     }
   }
-  red[w][lane][0] = sg;
-  red[w][lane][1] = sb;
+  red[w][lane][0] = ((ag[0] + ag[1]) + (ag[2] + ag[3])) + ((ag[4] + ag[5]) + (ag[6] + ag[7]));
+  red[w][lane][1] = ((ab[0] + ab[1]) + (ab[2] + ab[3])) + ((ab[4] + ab[5]) + (ab[6] + ab[7]));
   __syncthreads();
   if (w == 0 && n < N) {
-    const float tg = ((red[0][lane][0] + red[1][lane][0]) + red[2][lane][0]) + red[3][lane][0];
-    const float tb = ((red[0][lane][1] + red[1][lane][1]) + red[2][lane][1]) + red[3][lane][1];
-    if (dweight != nullptr) dweight[n] = dweight[n] + tg;
-    if (dbias != nullptr) dbias[n] = dbias[n] + tb;
+    out_g[static_cast<int64_t>(q) * N + n] = ((red[0][lane][0] + red[1][lane][0]) + red[2][lane][0]) + red[3][lane][0];
+    if (out_b != nullptr)
+      out_b[static_cast<int64_t>(q) * N + n] = ((red[0][lane][1] + red[1][lane][1]) + red[2][lane][1]) + red[3][lane][1];
   }
+}
+
+__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum2(const float *__restrict__ out_g,
+                                                               const float *__restrict__ out_b, int S, int N,
+                                                               float *__restrict__ dweight, float *__restrict__ dbias) {
+  const int n = blockIdx.x * kNbThreads + threadIdx.x;
+  if (n >= N) return;
+  float sg = 0.0f, sb = 0.0f;
+  for (int q = 0; q < S; ++q) {
+    sg += out_g[static_cast<int64_t>(q) * N + n];
+    if (out_b != nullptr) sb += out_b[static_cast<int64_t>(q) * N + n];
+  }
+  if (dweight != nullptr) dweight[n] = dweight[n] + sg;
+  if (dbias != nullptr) dbias[n] = dbias[n] + sb;
 }
 
 // Parameter gradients without scratch: thread = column, all rows in order.
@@ -255,8 +327,17 @@ static int bwd_vpt(int64_t N, bool vec_ok) {
   return 0;
 }
 
+// Slices of the first column-sum pass: about two workgroups per CU.
+static int colsum_slices(int64_t M, int64_t N) {
+  const int64_t blocks = cdiv(N, 64);
+  const int64_t s = std::max<int64_t>(1, 2 * static_cast<int64_t>(device_cu_count()) / blocks);
+  return static_cast<int>(std::min<int64_t>({s, 64, static_cast<int64_t>(bwd_groups(M))}));
+}
+
+// [part_g G x N][part_b G x N][out_g S x N][out_b S x N], fp32
 static size_t bwd_scratch_bytes(int64_t M, int64_t N, bool rms) {
-  return static_cast<size_t>(bwd_groups(M)) * static_cast<size_t>(N) * 4 * (rms ? 1 : 2);
+  const size_t rows = static_cast<size_t>(bwd_groups(M)) + static_cast<size_t>(colsum_slices(M, N));
+  return rows * static_cast<size_t>(N) * 4 * (rms ? 1 : 2);
 }
 
 template <typename T, int VPT, bool RMS, bool PART>
@@ -302,8 +383,13 @@ static teeny_status norm_bwd(const void *dy, const void *x, void *dx, const void
   teeny_status st = after_launch(name, s);
   if (st != TEENY_OK || !grads) return st;
   if (part) {
-    hipLaunchKernelGGL(norm_bwd_colsum_kernel, dim3(static_cast<unsigned>(cdiv(N, 64))), dim3(kNbThreads), 0, s,
-                       pg, pb, G, static_cast<int>(N), dweight, RMS ? nullptr : dbias);
+    const int S = colsum_slices(M, N);
+    float *og = pg + static_cast<int64_t>(G) * N * (RMS ? 1 : 2);
+    float *ob = RMS ? nullptr : og + static_cast<int64_t>(S) * N;
+    hipLaunchKernelGGL(norm_bwd_colsum1, dim3(static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(S)),
+                       dim3(kNbThreads), 0, s, pg, pb, G, static_cast<int>(N), S, og, ob);
+    hipLaunchKernelGGL(norm_bwd_colsum2, dim3(static_cast<unsigned>(cdiv(N, kNbThreads))), dim3(kNbThreads), 0, s,
+                       og, ob, S, static_cast<int>(N), dweight, RMS ? nullptr : dbias);
   } else {
     hipLaunchKernelGGL((norm_bwd_cols_kernel<T, RMS>), dim3(static_cast<unsigned>(cdiv(N, kNbThreads))),
                        dim3(kNbThreads), 0, s, static_cast<const T *>(dy), static_cast<const T *>(x), st0, st1, M,
