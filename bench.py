@@ -27,8 +27,9 @@ read HBM rather than the previous launch's cached bytes.
 
 The CPU baselines time the oracle (oracle/, a C restatement of the reference
 kernels' program grids and loops, rebuilt here with -march=native) on this
-host's cores: median of 3 runs after one warm-up, on the full workload or on
-a stated prefix (>= 5 %) of its program ids, scaled linearly.
+host's cores: the median of repeated runs after one warm-up (at least 3, and
+as many as fit about 2 s of CPU work per configuration), on the full workload
+or on a stated prefix (>= 5 %) of its program ids, scaled linearly.
 
 --workload NAME runs one workload (for profiling); --op-markers launches an
 empty marker kernel before each op's own timed block, so that a rocprofv3
@@ -190,14 +191,22 @@ def roofline_flops(workload, op, flops, avg_ms, peak, nbytes=None):
             "algorithmic_flop": flops, "avg_us": round(avg_ms * 1e3, 2)}
 
 
-def cpu_time(fn, runs=3):
-    """Median wall time of `runs` calls after one warm-up call."""
+CPU_MIN_SECONDS = 2.0  # CPU work per configuration: about 20 s over the default run
+_cpu_last = {}
+
+
+def cpu_time(fn, runs=3, min_seconds=None):
+    """Median wall time of at least `runs` calls, after one warm-up call, and of
+    as many more as fit `min_seconds` of CPU work in total (at most 200)."""
+    min_seconds = CPU_MIN_SECONDS if min_seconds is None else min_seconds
+    t0 = time.perf_counter()
     fn()
     times = []
-    for _ in range(runs):
+    while len(times) < runs or (time.perf_counter() - t0 < min_seconds and len(times) < 200):
         c0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - c0)
+    _cpu_last.update(runs=len(times), total_seconds=round(time.perf_counter() - t0, 2))
     return float(np.median(times))
 
 
@@ -205,6 +214,7 @@ def cpu_entry(value, unit, seconds, sample, gpu_value, extra=None):
     import oracle
     d = {"value": value, "unit": unit, "cores": oracle.threads(), "kind": "port", "cpu": cpu_model(),
          "build": oracle.BUILD_FLAGS, "seconds": round(seconds, 4), "sample": sample,
+         "runs": _cpu_last.get("runs"), "cpu_seconds_total": _cpu_last.get("total_seconds"),
          "speedup": round(gpu_value / value, 1) if value else None}
     if extra:
         d.update(extra)
