@@ -31,7 +31,8 @@
 // D_m comes from a pre-pass over O and dO (the dq kernel also computes it
 // in its own registers).  Every tile lives in LDS with an XOR swizzle of its
 // 16-byte chunks chosen so that both the row reads (16 rows of one chunk)
-// and the transposing reads (4 rows x 32 bytes) touch distinct banks.
+// and the transposing reads (4 rows x 64 bytes per half-wave) touch
+// distinct banks.
 //
 // Any other case (fp32, other head sizes, unaligned bf16): the reference's
 // per-row structure, one wave per query row (dq) or key row (dkv), with the

@@ -83,18 +83,25 @@ __device__ __forceinline__ bf16x4 ds_read_tr16(const bf16 *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p));
 }
 
-// Chunk swizzle of LDS tile rows: 16 consecutive rows get 16 distinct chunk
-// positions (row reads), and 4 consecutive rows x 2 adjacent chunks land on 8
-// distinct positions (transposing reads).  For D = 64 two rows share the 64
-// banks, so the swizzle is a function of row / 2.
+// Chunk swizzle of LDS tile rows (64 banks of 4 bytes: one 256-byte window).
+// A ds_read_b128 is served 16 lanes at a time and a ds_read_b64(_tr_b16) 32
+// lanes at a time, so the swizzle must give
+//   * row reads (frag_row): 16 consecutive rows, one logical chunk -> 16
+//     distinct 16-byte positions of the window;
+//   * transposing reads (frag_tr): 4 consecutive rows x 4 adjacent chunks
+//     (one 64-byte column block) -> 16 distinct positions.
+// D = 128 (one row per window): position = chunk ^ (4 (row % 4) + (row / 4) % 4),
+// whose high two bits differ across 4 consecutive rows.  D = 64 (two rows per
+// window, row parity picks the half): the same with k = (row / 2) % 8,
+// 4 (k % 2) + k / 2, so rows r and r + 2 use opposite 64-byte column halves.
 template <int D>
 __device__ __forceinline__ int bswz(int row) {
   if constexpr (D == 128) {
     const int h = row & 15;
-    return ((h >> 2) & 1) | ((h & 3) << 1) | (h & 8);
+    return ((h & 3) << 2) | ((h >> 2) & 3);
   } else {
-    const int h = (row >> 1) & 7;
-    return ((h >> 1) & 1) | ((h & 1) << 1) | (h & 4);
+    const int k = (row >> 1) & 7;
+    return ((k & 1) << 2) | ((k >> 1) & 3);
   }
 }
 
@@ -105,7 +112,7 @@ __device__ __forceinline__ int bswz(int row) {
 // rb + 4g + m/4 (+ 8), columns 32 db + 16 (group & 1) + 4 (m & 3) .. + 3.
 template <int D>
 __device__ __forceinline__ bf16x8 frag_tr(const bf16 *tile, int rb, int db, int lane) {
-  constexpr int HI = D == 128 ? 8 : 4;  // bswz(row + 8) = bswz(row) ^ HI for row % 16 < 8
+  constexpr int HI = 2;  // bswz(row + 8) = bswz(row) ^ 2 for row % 16 < 8 (both D)
   const int g = lane >> 5, hh = lane >> 4, m = lane & 15;
   const int rr = 4 * g + (m >> 2);
   const int cc = 4 * db + 2 * (hh & 1) + ((m & 3) >> 1);
