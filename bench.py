@@ -384,8 +384,8 @@ def bench_attention(ctx, s, causal):
 
 def attach_workspace(ctx, sizes):
     """Gives the stream one caller-owned scratch buffer big enough for every
-    op of the workload (split-K partials, space-to-depth copies, dequantized
-    weights); returns its size.  Allocated before timing, as an executor
+    op of the workload (split-K partials, space-to-depth copies); returns its
+    size.  Allocated before timing, as an executor
     would."""
     need = max(list(sizes) + [0])
     if need > 0:

@@ -479,12 +479,6 @@ template <bool INT8B>
 static size_t conv_scratch_bytes(const ConvGeo &q) {
   const GemmParams p = conv_gemm_params(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, q);
   const ConvPath path = conv_path<INT8B>(q);
-  if (INT8B && path != kConvNoMfma &&
-      (path == kConvPlain ? w8_dequant_pays<kAPlain>(p) : w8_dequant_pays<kAConvVec>(p))) {
-    // int8 weights dequantized once into scratch, then the bf16 kernels
-    const size_t wb = dequant_scratch_bytes(static_cast<int64_t>(p.N) * p.K);
-    return wb + (path == kConvPlain ? gemm_scratch_bytes<false, kAPlain>(p) : gemm_scratch_bytes<false, kAConvVec>(p));
-  }
   switch (path) {
     case kConvPlain: return gemm_scratch_bytes<INT8B, kAPlain>(p);
     case kConvVec: return gemm_scratch_bytes<INT8B, kAConvVec>(p);
@@ -530,14 +524,6 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
   if (path == kConvNoMfma) return false;
   if (path == kConvS2D && conv_s2d_mfma(x, w, scale, bias, bias_bf16, y, q, act, s, scr)) return true;
   GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
-  if (INT8B && (path == kConvPlain ? w8_dequant_pays<kAPlain>(p) : w8_dequant_pays<kAConvVec>(p)) &&
-      scr.ptr != nullptr && scr.bytes >= dequant_scratch_bytes(static_cast<int64_t>(p.N) * p.K)) {
-    // compute-bound: dequantize the weights once, then the bf16 kernels
-    Scratch rest;
-    p.B = dequant_weights(static_cast<const int8_t *>(w), static_cast<int64_t>(p.N) * p.K, scr, &rest, s);
-    return path == kConvPlain ? launch_gemm_mfma<false, kAPlain>(p, act, s, rest)
-                              : launch_gemm_mfma<false, kAConvVec>(p, act, s, rest);
-  }
   switch (path) {
     case kConvPlain: return launch_gemm_mfma<INT8B, kAPlain>(p, act, s, scr);
     case kConvVec: return launch_gemm_mfma<INT8B, kAConvVec>(p, act, s, scr);

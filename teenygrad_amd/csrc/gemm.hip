@@ -176,15 +176,9 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
   const bool mfma_ok = K > 0 && K % 16 == 0 && aligned(x, 16) && aligned(qweight, 16);
   if (mfma_ok) {
     GemmParams p = plain_params(x, K, qweight, K, y, N, scale, bias, nullptr, M, N, K);
-    const Scratch scr = stream_scratch(s);
-    if (w8_dequant_pays<kAPlain>(p) && scr.ptr != nullptr && scr.bytes >= dequant_scratch_bytes(N * K)) {
-      // compute-bound: dequantize the weights once, then the bf16 kernels
-      Scratch rest;
-      p.B = dequant_weights(qweight, N * K, scr, &rest, s);
-      launch_gemm_mfma<false, kAPlain>(p, act, s, rest);
-    } else {
-      launch_gemm_mfma<true, kAPlain>(p, act, s, scr);
-    }
+    // int8 weights stay int8 up to the registers feeding the MFMA (no
+    // dequantized copy in HBM)
+    launch_gemm_mfma<true, kAPlain>(p, act, s, stream_scratch(s));
   } else {
     teeny_status st = launch_generic<bf16, int8_t, bf16>(
         static_cast<const bf16 *>(x), K, 1, qweight, K, 1, static_cast<bf16 *>(y), N, 1, scale,
@@ -207,10 +201,7 @@ teeny_status teeny_linear_workspace_size(int64_t M, int64_t N, int64_t K, teeny_
   if (K % (dtype == TEENY_I8 ? 16 : 8) != 0) return TEENY_OK;  // generic kernel, no scratch
   // contiguous operands, as the MFMA path requires
   const GemmParams p = plain_params(nullptr, K, nullptr, K, nullptr, N, nullptr, nullptr, nullptr, M, N, K);
-  if (dtype == TEENY_I8 && w8_dequant_pays<kAPlain>(p))
-    *bytes = dequant_scratch_bytes(N * K) + gemm_scratch_bytes<false, kAPlain>(p);
-  else
-    *bytes = dtype == TEENY_I8 ? gemm_scratch_bytes<true, kAPlain>(p) : gemm_scratch_bytes<false, kAPlain>(p);
+  *bytes = dtype == TEENY_I8 ? gemm_scratch_bytes<true, kAPlain>(p) : gemm_scratch_bytes<false, kAPlain>(p);
   return TEENY_OK;
 }
 

@@ -658,45 +658,6 @@ static __global__ __launch_bounds__(256) void gemm_splitk_finalize(GemmParams p,
   }
 }
 
-// int8 -> bf16 (exact for |q| <= 128), 16 weights per thread: the one-pass
-// dequant of W8A16 weights into scratch for compute-bound shapes, where the
-// GEMM would otherwise convert every weight once per row tile.
-static __global__ __launch_bounds__(256) void i8_to_bf16_kernel(const int8_t *__restrict__ q,
-                                                                bf16 *__restrict__ out, int64_t n16) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= n16) return;
-  const u32x4 v = reinterpret_cast<const u32x4 *>(q)[t];
-  bf16 e[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j)
-    e[j] = static_cast<bf16>(static_cast<float>(static_cast<int8_t>((v[j >> 2] >> (8 * (j & 3))) & 0xffu)));
-  u32x4 lo, hi;
-  __builtin_memcpy(&lo, e, 16);
-  __builtin_memcpy(&hi, e + 8, 16);
-  reinterpret_cast<u32x4 *>(out)[2 * t] = lo;
-  reinterpret_cast<u32x4 *>(out)[2 * t + 1] = hi;
-}
-
-// W8A16 problems that take the 256 x 256 LDS-DMA kernel (so compute-bound:
-// at least 512 rows) run as a bf16 GEMM on weights dequantized once into
-// the stream's scratch (when it is large enough): converting in the MFMA
-// loop costs that kernel ~20 %, the dequant pass ~3 bytes of traffic per
-// weight.  The register-staged kernels convert while staging to LDS, where
-// it is nearly free, so there the pass would only add a launch.
-constexpr int64_t kW8DequantMinM = 512;
-inline size_t dequant_scratch_bytes(int64_t n_weights) { return (static_cast<size_t>(n_weights) * 2 + 255) / 256 * 256; }
-
-// Converts n_weights (a multiple of 16, 16-byte aligned) int8 weights into
-// the front of `scr` and returns the bf16 copy; the rest of the scratch
-// goes to `rest`.
-inline const bf16 *dequant_weights(const int8_t *q, int64_t n_weights, Scratch scr, Scratch *rest, hipStream_t s) {
-  const size_t bytes = dequant_scratch_bytes(n_weights);
-  bf16 *wb = static_cast<bf16 *>(scr.ptr);
-  const int64_t n16 = n_weights / 16;
-  hipLaunchKernelGGL(i8_to_bf16_kernel, dim3(static_cast<unsigned>((n16 + 255) / 256)), dim3(256), 0, s, q, wb, n16);
-  *rest = Scratch{static_cast<char *>(scr.ptr) + bytes, scr.bytes - bytes};
-  return wb;
-}
 
 // KVEC: K % 8 == 0 and (for the plain A path) 16-byte aligned rows, so no
 // 16-byte chunk straddles K and the element-wise tail paths are compiled out.
@@ -814,12 +775,6 @@ inline GemmTiles gemm_tiles(const GemmParams &p) {
   if (tiles_of(p, 128, 128) < device_cu_count() && (split_plan<128, 128, 64>(p).used == 1 || p.K <= 2048))
     return kTiles128x64Deep;
   return kTiles128x128;
-}
-
-// Whether a W8A16 problem runs on dequantized weights (see kW8DequantMinM).
-template <int AMODE>
-inline bool w8_dequant_pays(const GemmParams &p) {
-  return p.M >= kW8DequantMinM && gemm_tiles<true, AMODE>(p) == kTilesBig;
 }
 
 // Scratch bytes that let launch_gemm_mfma take its split plan (0: none used).

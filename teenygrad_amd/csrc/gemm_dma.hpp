@@ -326,12 +326,17 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   constexpr int kQr = H == 16 ? 16 : H == 8 ? 8 : 2;
   constexpr int kXr = H == 16 ? 20 : H == 8 ? 10 : 4;
   constexpr int kC0 = H == 16 ? 24 : H == 8 ? 14 : 6, kC0Step = H == 16 ? 2 : 1;
+  // The reads of k-tile kt+1 are issued unconditionally: on the last k-tile
+  // they read stage (kt+1) % NST, whose zero-source DMA completed with the
+  // same wait as a live tile's, and the fragments are never used.  A branch
+  // around them would split the bundles and make the compiler's LDS waits
+  // assume the path without the reads (each read then waited on at once).
   FragSet f;
   u32x4 q[NB];
   auto ktile = [&](int kt) __attribute__((always_inline)) {
     const char *cu = smem + (kt % NST) * STAGE;
     const char *nx = smem + ((kt + 1) % NST) * STAGE;
-    const bool more = kt + 1 < n_k;
+    constexpr bool more = true;
 #pragma unroll
     for (int b = 0; b < 2 * H; ++b) {
       const int st = b / H, i = (b % H) / MB, j = b % MB;

@@ -230,16 +230,14 @@ def test_workspace_registry_and_sizes():
         assert tg.kernels.linear_workspace_size(64, 256, 4096, tg.bf16) == 4 * 64 * 256 * 4
         # 64 x 64 x 4096 int8: 1 tile of 128 x 64 -> 4 slices of 64 x 64
         assert tg.kernels.linear_workspace_size(64, 64, 4096, tg.i8) == 4 * 64 * 64 * 4
-        # the two configuration GEMMs (M >= 512, compute-bound) dequantize their
-        # int8 weights once into scratch: N * K bf16, and need no split-K
-        assert tg.kernels.linear_workspace_size(4096, 11008, 4096, tg.i8) == 11008 * 4096 * 2
-        assert tg.kernels.linear_workspace_size(4096, 4096, 11008, tg.i8) == 4096 * 11008 * 2
+        # int8 weights are converted in registers on every path (no dequantized
+        # copy): the two configuration GEMMs need no scratch at all
+        assert tg.kernels.linear_workspace_size(4096, 11008, 4096, tg.i8) == 0
+        assert tg.kernels.linear_workspace_size(4096, 4096, 11008, tg.i8) == 0
         assert tg.kernels.linear_workspace_size(4096, 11008, 4096, tg.bf16) == 0
-        # int8 weights on the register-staged kernels are converted while
-        # staging: no dequant copy below 256 tiles of 256 x 256
         assert tg.kernels.linear_workspace_size(600, 96, 128, tg.i8) == 0
         assert tg.kernels.conv2d_workspace_size((32, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 0
-        assert tg.kernels.conv2d_workspace_size((128, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 256 * 9 * 256 * 2
+        assert tg.kernels.conv2d_workspace_size((128, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 0
         # stride-2 3x3 conv, 3 channels, 20 x 20 -> 10 x 10: space-to-depth input
         # [1, 11, 11, 16] bf16 (3872 B -> 4096) then weights [16, 2, 2, 16] bf16 (2048 B)
         assert tg.kernels.conv2d_workspace_size((1, 20, 20, 3), (16, 3, 3, 3), 2, 1, 1, tg.bf16) == 4096 + 2048

@@ -245,16 +245,15 @@ def test_w8a16_conv_config_batch32(dev, orc):
 def test_w8a16_conv_large_tile(dev, orc, scratch):
     # 128 x 256 x 28 x 28, 3x3 p1, with bias and ReLU: M = 100352 gives 392
     # 256 x 256 tiles, so the implicit GEMM takes the large-tile LDS-DMA
-    # kernel, on int8 weights or, given a workspace, on weights dequantized
-    # once to bf16; images 0, 77 and 127 against the oracle
+    # kernel on int8 weights (converted in registers; no scratch needed);
+    # images 0, 77 and 127 against the oracle
     B, C, H = 128, 256, 28
     rng = np.random.default_rng(0x7EE70128)
     x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
     q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
     bias = rng.normal(0, 0.1, C).astype(np.float32)
     need = K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)
-    if dev.info()["compute_units"] == 256:
-        assert need == C * 9 * C * 2, need
+    assert need == 0, need
     print(f"[w8a16 conv large tile] 128x256x28x28 scratch={scratch}", flush=True)
 
     def run():
@@ -262,7 +261,8 @@ def test_w8a16_conv_large_tile(dev, orc, scratch):
                               act="relu").to_host()
 
     if scratch == "workspace":
-        with stream_workspace(dev, need):
+        # a caller's workspace attached anyway must not change the plan
+        with stream_workspace(dev, 1 << 20):
             got = run()
     else:
         got = run()

@@ -133,8 +133,7 @@ def quantized_weight(orc, rng, n, k):
 @pytest.mark.parametrize("scratch", ["none", "workspace"])
 def test_w8a16_small(dev, orc, m, n, k, act, scratch):
     # (37, 70, 40) and (5, 9, 48): K % 16 != 0 -> generic kernel; others MFMA;
-    # given a workspace, (64, 64, 4096) splits along K (the dequantized-weight
-    # path needs 256 x 256 tiles to fill the device: test_w8a16_config)
+    # given a workspace, (64, 64, 4096) splits along K
     rng = np.random.default_rng(m * n + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
     q, s = quantized_weight(orc, rng, n, k)
@@ -164,9 +163,11 @@ def test_w8a16_config(dev, orc, k, n, scratch):
     q, s, z, _ = orc.quantize_affine(wf, [n, k], "channel", 0)
     np.testing.assert_array_equal(qg.to_host().reshape(-1), q)
     np.testing.assert_array_equal(sg.to_host(), s)
-    # with a workspace the int8 weights are dequantized once and the bf16
-    # kernel runs; without, the kernel converts them per tile
+    # the 256 x 256 LDS-DMA kernel converts the int8 weights in registers
+    # ahead of each MFMA: no scratch, and an attached workspace changes nothing
     need = K.linear_workspace_size(m, n, k, tg.i8)
+    assert need == 0, need
+    need = 1 << 20
     y = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), qg, sg).to_host())
     assert np.all(np.isfinite(from_bf16(y)))
     wdeq = orc.dequantize_affine(q, s, None, [n, k], "channel", 0)
