@@ -746,8 +746,15 @@ inline void launch_big_gemm(GemmParams p, hipStream_t s);
 template <bool INT8B, int AMODE>
 inline bool stream_gemm_fits(const GemmParams &p);
 inline void launch_stream_gemm(const GemmParams &p, hipStream_t s);
+template <bool INT8B, int AMODE>
+inline bool persist_gemm_fits(const GemmParams &p);
+template <int AMODE>
+inline void launch_persist_default(const GemmParams &p, hipStream_t s);
 
 // Tile choice (measured on MI355X over the ResNet-50 and W8A16 shapes):
+//  * the persistent LDS-DMA kernel (gemm_persist.hpp) for bf16 problems of
+//    many 128 x 128 tiles (>= 4 per CU) and K of 128 .. 512 (the 1x1 and
+//    strided 1x1 convs of a ResNet's second stage);
 //  * the streaming kernel (gemm_stream.hpp) for long, HBM-bound problems
 //    with K, N <= 256 and bf16 weights (the full-resolution 1x1 convs);
 //  * the 256 x 256 LDS-DMA kernel (gemm_dma.hpp) when its tiles fill the chip;
@@ -758,10 +765,11 @@ inline void launch_stream_gemm(const GemmParams &p, hipStream_t s);
 //  * grids of 128 x 128 tiles that leave CUs idle and do not split along K:
 //    128 x 64 x 64 (twice the workgroups);
 //  * otherwise 128 x 128 x 64, split along K when badly under-filled.
-enum GemmTiles { kTilesStream, kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
+enum GemmTiles { kTilesPersist, kTilesStream, kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
 
 template <bool INT8B, int AMODE>
 inline GemmTiles gemm_tiles(const GemmParams &p) {
+  if (persist_gemm_fits<INT8B, AMODE>(p)) return kTilesPersist;
   if (stream_gemm_fits<INT8B, AMODE>(p)) return kTilesStream;
   if constexpr (AMODE != kAConvScalar) {
     if (big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
@@ -845,6 +853,9 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
   p.act = act;
   p.ws = nullptr;
   switch (gemm_tiles<INT8B, AMODE>(p)) {
+    case kTilesPersist:
+      if constexpr (AMODE != kAConvScalar) launch_persist_default<AMODE>(p, s);
+      break;
     case kTilesStream: launch_stream_gemm(p, s); break;
     case kTilesBig:
       if constexpr (AMODE != kAConvScalar) launch_big_gemm<INT8B, AMODE>(p, s);
@@ -862,3 +873,4 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
 
 #include "gemm_dma.hpp"
 #include "gemm_stream.hpp"
+#include "gemm_persist.hpp"

@@ -142,6 +142,46 @@ def test_bf16_nhwc_large_tile(dev, orc):
         check_bf16(got[i:i + 1], ref, f"image {i}")
 
 
+@pytest.mark.parametrize("act,bn", [("gelu", False), ("silu", True), (None, False)])
+def test_bf16_nhwc_persistent_strided_1x1(dev, orc, act, bn):
+    # batch 42, 56x56, 256 -> 512, 1x1 stride 2 (a ResNet downsample at a
+    # ragged batch): M = 32928 rows, 1032 tiles of 128 x 128, K = 256 -> the
+    # persistent kernel on the strided gather; with bn the folded BatchNorm's
+    # scale and shift are its epilogue coefficients.  One output pixel of
+    # every 128-row tile, and images 0 and 41 whole, vs the oracle.
+    B, H, Cin, Cout = 42, 56, 256, 512
+    print(f"[conv bf16 persistent] B=42 56x56 256->512 1x1/2 act={act} bn={bn}", flush=True)
+    rng = np.random.default_rng(4256)
+    xb = to_bf16(rng.random((B, H, H, Cin), dtype=np.float32))
+    wb = to_bf16((rng.standard_normal((Cout, 1, 1, Cin), dtype=np.float32) * np.sqrt(2.0 / Cin)).astype(np.float32))
+    x, w = from_bf16(xb), from_bf16(wb)
+    assert K.conv2d_workspace_size((B, H, H, Cin), (Cout, 1, 1, Cin), 2, 0, 1, tg.bf16, "nhwc") == 0
+    if bn:
+        scale = rng.uniform(0.5, 1.5, Cout).astype(np.float32)
+        shift = rng.normal(0, 0.1, Cout).astype(np.float32)
+        got = K.conv2d_bn_act(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(scale), dev.upload(shift),
+                              2, 0, 1, act, layout="nhwc").to_host()
+        bias = None
+    else:
+        bias = rb(rng.normal(0, 0.1, Cout).astype(np.float32))
+        got = K.conv2d(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(to_bf16(bias), tg.bf16),
+                       2, 0, 1, act, layout="nhwc").to_host()
+
+    def post(ref):
+        if bn:
+            ref = ref * scale + shift
+        return ref if act is None else {"silu": orc.silu, "gelu": orc.gelu}[act](ref)
+
+    m = B * 28 * 28
+    starts = np.arange(0, m, 128)
+    pix = starts + (rng.random(starts.size) * np.minimum(128, m - starts)).astype(np.int64)
+    assert np.all(np.isfinite(from_bf16(got)))
+    check_bf16(got.reshape(m, Cout)[pix], post(orc.conv2d_nhwc_pixels(x, w, pix, bias, stride=2, padding=0)),
+               f"{pix.size} sampled pixels")
+    for i in (0, B - 1):
+        check_bf16(got[i:i + 1], post(orc.conv2d_nhwc(x[i:i + 1], w, bias, stride=2, padding=0)), f"image {i}")
+
+
 STREAM_CASES = [
     # B, H, W, Cin, Cout, act: 1x1 stride-1 convs with M = B*H*W >= 16384 and
     # C_IN, C_OUT in {64, 128, 256} take the streaming kernel

@@ -96,6 +96,40 @@ def test_linear_bf16_stream_padded_rows(dev, orc, pad, offset):
     check_bf16(y[rows, :n], orc.linear(x[rows], w), f"ldy={ldy} offset={offset}")
 
 
+def tile_rows(m, tile, rng):
+    """One row inside every `tile`-row block of [0, m), plus the first and last 64 rows."""
+    starts = np.arange(0, m, tile, dtype=np.int64)
+    pick = starts + (rng.random(starts.size) * np.minimum(tile, m - starts)).astype(np.int64)
+    return np.unique(np.concatenate([np.arange(64), pick, np.arange(m - 64, m)]))
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(50000, 512, 128, 0), (50000, 512, 256, 8), (131072, 128, 384, 0),
+                                       (40000, 1024, 512, 16)])
+def test_linear_bf16_persistent(dev, orc, m, n, k, pad):
+    # >= 4 tiles of 128 x 128 per CU and 128 <= K <= 512: the persistent
+    # LDS-DMA kernel (one DMA ring per workgroup across its tiles; 50000 and
+    # 40000 end in a partial row tile, K = 128 is shorter than the ring).
+    # Output rows padded to N + pad: the padding columns stay untouched.
+    # One row of every 128-row tile (each workgroup's every tile) vs the oracle.
+    print(f"[linear persistent] m={m} n={n} k={k} ldy={n + pad}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb((rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float32))
+    b = rb(rng.normal(0, 0.5, n).astype(np.float32))
+    assert K.linear_workspace_size(m, n, k, tg.bf16) == 0
+    xb, wb, bb = dev.upload(to_bf16(x), tg.bf16), dev.upload(to_bf16(w), tg.bf16), dev.upload(to_bf16(b), tg.bf16)
+    ldy = n + pad
+    sentinel = np.uint16(0x7FC1)
+    ybuf = dev.upload(np.full(m * ldy, sentinel, np.uint16), tg.bf16)
+    tg.check(_lib.lib.teeny_linear_forward(xb.ptr, wb.ptr, bb.ptr, ybuf.ptr, m, n, k, k, 1, k, 1, ldy, 1,
+                                           _lib.BF16, None))
+    y = ybuf.to_host().reshape(m, ldy)
+    assert np.all(y[:, n:] == sentinel)
+    assert np.all(np.isfinite(from_bf16(y[:, :n])))
+    rows = tile_rows(m, 128, rng)
+    check_bf16(y[rows, :n], orc.linear(x[rows], w, b), f"{rows.size} sampled rows")
+
+
 def test_linear_bf16_large_tile(dev, orc):
     # 4096 x 512 x 4096: 256 x 256 tiles fill the chip -> large-tile kernel;
     # rows 0..31 and the last 32 rows against the oracle
