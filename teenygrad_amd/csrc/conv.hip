@@ -725,6 +725,167 @@ __global__ __launch_bounds__(256) void conv_bwd_spread(const bf16 *__restrict__ 
   reinterpret_cast<u32x4 *>(dyd)[t] = v;
 }
 
+// ── strided dx as sub-pixel phases ──
+// For stride S along an axis, the dx rows i = S u + a (phase a = 0 .. S-1)
+// receive only the taps k = k0 + S t with k0 = (a + P) mod S:
+//   dx[S u + a] = sum_t dy[u + d - t] w[k0 + S t],   d = (a + P - k0) / S,
+// a stride-1 convolution of dy with the T = ceil((K - k0) / S) taps of that
+// residue, flipped (t' = T - 1 - t reads dy row u - (T - 1 - d) + t').  Each
+// of the SH x SW phases is one implicit GEMM over dy (M = B U V pixels of the
+// phase, N = C_IN, K = T_h T_w C_OUT) whose output rows are every SH-th row
+// and SW-th column of dx (GemmParams::c_ow remap).  Exactly the KH x KW taps
+// per dx pixel: the zero-spread form executes SH SW times as many MACs.
+// A phase with no taps (T = 0, e.g. odd rows of a 1x1 stride-2 conv) is zero.
+struct DxAxis {
+  int k0, T, pad, U;  // first tap, taps, stride-1 padding, phase extent
+};
+static DxAxis dx_axis(int a, int S, int P, int K, int In) {
+  DxAxis x;
+  x.k0 = (a + P) % S;
+  x.T = x.k0 < K ? (K - x.k0 + S - 1) / S : 0;
+  const int d = (a + P - x.k0) / S;
+  x.pad = x.T - 1 - d;
+  x.U = a < In ? (In - a + S - 1) / S : 0;
+  return x;
+}
+constexpr int kMaxDxPhases = 16;  // SH, SW <= 4
+struct DxPhaseTable {
+  int SH, SW;
+  int T[4], k0h[4], S[4], k0w[4];  // per row phase a: taps T, first k0h; per column phase c
+  int64_t off[kMaxDxPhases];         // element offset of phase (a, c)'s weights
+};
+// w [C_OUT, KH, KW, C_IN] -> per phase (a, c): wp[ci][t'][s'][co] =
+// w[co][k0h + SH (T - 1 - t')][k0w + SW (S - 1 - s')][ci], one element per
+// thread (every weight belongs to exactly one phase).
+__global__ __launch_bounds__(256) void conv_dx_phase_weights(const bf16 *__restrict__ w, bf16 *__restrict__ wp,
+                                                             int Cout, int KH, int KW, int Cin, DxPhaseTable tb) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(Cout) * KH * KW * Cin;
+  if (t >= total) return;
+  const int ci = static_cast<int>(t % Cin);
+  const int kw = static_cast<int>((t / Cin) % KW);
+  const int kh = static_cast<int>((t / (static_cast<int64_t>(Cin) * KW)) % KH);
+  const int co = static_cast<int>(t / (static_cast<int64_t>(Cin) * KW * KH));
+  // the phase whose residue kh belongs to: a with (a + PH) % SH == kh % SH
+  // (found by search: SH, SW <= 4)
+  int a = 0, c = 0;
+  for (int i = 0; i < tb.SH; ++i)
+    if (tb.T[i] > 0 && tb.k0h[i] == kh % tb.SH) a = i;
+  for (int i = 0; i < tb.SW; ++i)
+    if (tb.S[i] > 0 && tb.k0w[i] == kw % tb.SW) c = i;
+  const int T = tb.T[a], S = tb.S[c];
+  const int tp = T - 1 - (kh - tb.k0h[a]) / tb.SH, sp = S - 1 - (kw - tb.k0w[c]) / tb.SW;
+  wp[tb.off[a * tb.SW + c] + ((static_cast<int64_t>(ci) * T + tp) * S + sp) * Cout + co] = w[t];
+}
+// Zeroes the dx pixels of the phases with no taps (mask bit a * SW + c), one
+// 16-byte chunk (8 channels) per thread.
+__global__ __launch_bounds__(256) void conv_dx_zero_phases(bf16 *__restrict__ dx, int B, int H, int W, int C, int SH,
+                                                           int SW, unsigned mask) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int cv = C / 8;
+  const int64_t total = static_cast<int64_t>(B) * H * W * cv;
+  if (t >= total) return;
+  const int iw = static_cast<int>((t / cv) % W);
+  const int ih = static_cast<int>((t / (static_cast<int64_t>(cv) * W)) % H);
+  if ((mask >> ((ih % SH) * SW + iw % SW)) & 1u) reinterpret_cast<u32x4 *>(dx)[t] = u32x4{0u, 0u, 0u, 0u};
+}
+
+struct DxPhasePlan {
+  bool ok = false;
+  DxAxis ah[4], aw[4];
+  DxPhaseTable tb{};
+  unsigned zero_mask = 0;
+  size_t w_bytes = 0, gemm_off = 0;
+};
+static DxPhasePlan dx_phase_plan(const ConvGeo &q) {
+  DxPhasePlan d;
+  if (q.G != 1 || q.SH > 4 || q.SW > 4 || (q.SH == 1 && q.SW == 1) || q.Cout % 8 != 0 || q.Cin % 8 != 0 ||
+      static_cast<int64_t>(q.OH) * q.OW * q.Cout >= (int64_t{1} << 30))
+    return d;
+  d.tb.SH = q.SH;
+  d.tb.SW = q.SW;
+  int64_t off = 0;
+  for (int a = 0; a < q.SH; ++a) {
+    d.ah[a] = dx_axis(a, q.SH, q.PH, q.KH, q.H);
+    d.tb.T[a] = d.ah[a].T;
+    d.tb.k0h[a] = d.ah[a].k0;
+  }
+  for (int c = 0; c < q.SW; ++c) {
+    d.aw[c] = dx_axis(c, q.SW, q.PW, q.KW, q.W);
+    d.tb.S[c] = d.aw[c].T;
+    d.tb.k0w[c] = d.aw[c].k0;
+  }
+  for (int a = 0; a < q.SH; ++a)
+    for (int c = 0; c < q.SW; ++c) {
+      d.tb.off[a * q.SW + c] = off;
+      const int64_t taps = static_cast<int64_t>(d.ah[a].T) * d.aw[c].T;
+      off += taps * q.Cin * q.Cout;
+      if (taps == 0 && d.ah[a].U > 0 && d.aw[c].U > 0) d.zero_mask |= 1u << (a * q.SW + c);
+    }
+  d.w_bytes = static_cast<size_t>(off) * sizeof(bf16);
+  d.gemm_off = round256(d.w_bytes);
+  d.ok = true;
+  return d;
+}
+// The implicit GEMM of phase (a, c): A = dy as an NHWC image [OH, OW, C_OUT],
+// B = the phase's weights, C = dx rows (S_H u + a, S_W v + c).
+static GemmParams dx_phase_gemm(const DxPhasePlan &d, int a, int c, const void *dy, const bf16 *wp, void *dx,
+                                const ConvGeo &q) {
+  const DxAxis &h = d.ah[a], &w = d.aw[c];
+  GemmParams p{};
+  p.A = static_cast<const bf16 *>(dy);
+  p.lda = q.Cout;
+  p.B = wp + d.tb.off[a * q.SW + c];
+  p.ldb = static_cast<int64_t>(h.T) * w.T * q.Cout;
+  p.C = static_cast<bf16 *>(dx) + (static_cast<int64_t>(a) * q.W + c) * q.Cin;
+  p.M = q.B * h.U * w.U;
+  p.N = q.Cin;
+  p.K = h.T * w.T * q.Cout;
+  p.H = q.OH; p.W = q.OW; p.Cin = q.Cout; p.OH = h.U; p.OW = w.U;
+  p.KH = h.T; p.KW = w.T; p.SH = 1; p.SW = 1; p.PH = h.pad; p.PW = w.pad;
+  p.c_ow = w.U;
+  p.c_oh = h.U;
+  p.c_sb = static_cast<int64_t>(q.H) * q.W * q.Cin;
+  p.c_su = static_cast<int64_t>(q.SH) * q.W * q.Cin;
+  p.c_sv = static_cast<int64_t>(q.SW) * q.Cin;
+  return p;
+}
+static size_t dx_phase_scratch_bytes(const ConvGeo &q) {
+  const DxPhasePlan d = dx_phase_plan(q);
+  if (!d.ok) return 0;
+  size_t g = 0;
+  for (int a = 0; a < q.SH; ++a)
+    for (int c = 0; c < q.SW; ++c)
+      if (d.ah[a].T > 0 && d.aw[c].T > 0 && d.ah[a].U > 0 && d.aw[c].U > 0)
+        g = std::max(g, gemm_scratch_bytes<false, kAConvVec>(dx_phase_gemm(d, a, c, nullptr, nullptr, nullptr, q)));
+  return d.gemm_off + g;
+}
+// bf16 NHWC dx of a strided conv as its sub-pixel phases; false (nothing
+// launched) if it does not apply.
+static bool conv_dx_phases(const void *dy, const void *w, void *dx, const ConvGeo &q, hipStream_t s, Scratch scr) {
+  const DxPhasePlan d = dx_phase_plan(q);
+  if (!d.ok || scr.ptr == nullptr || scr.bytes < d.gemm_off || !aligned(dy, 16) || !aligned(w, 16) ||
+      !aligned(dx, 16) || !aligned(scr.ptr, 16))
+    return false;
+  bf16 *wp = static_cast<bf16 *>(scr.ptr);
+  const int64_t nw = static_cast<int64_t>(q.Cout) * q.KH * q.KW * q.Cin;
+  hipLaunchKernelGGL(conv_dx_phase_weights, dim3(static_cast<unsigned>(cdiv(nw, 256))), dim3(256), 0, s,
+                     static_cast<const bf16 *>(w), wp, q.Cout, q.KH, q.KW, q.Cin, d.tb);
+  if (d.zero_mask != 0) {
+    const int64_t nc = static_cast<int64_t>(q.B) * q.H * q.W * (q.Cin / 8);
+    hipLaunchKernelGGL(conv_dx_zero_phases, dim3(static_cast<unsigned>(cdiv(nc, 256))), dim3(256), 0, s,
+                       static_cast<bf16 *>(dx), q.B, q.H, q.W, q.Cin, q.SH, q.SW, d.zero_mask);
+  }
+  const Scratch rest{static_cast<char *>(scr.ptr) + d.gemm_off, scr.bytes - d.gemm_off};
+  for (int a = 0; a < q.SH; ++a)
+    for (int c = 0; c < q.SW; ++c) {
+      if (d.ah[a].T == 0 || d.aw[c].T == 0 || d.ah[a].U == 0 || d.aw[c].U == 0) continue;
+      GemmParams p = dx_phase_gemm(d, a, c, dy, wp, dx, q);
+      launch_gemm_mfma<false, kAConvVec>(p, TEENY_ACT_NONE, s, rest);
+    }
+  return true;
+}
+
 // The MFMA form of bf16 NHWC dx: the stride-1 conv it becomes and its scratch.
 struct DxPlan {
   bool ok = false;
@@ -752,12 +913,14 @@ static DxPlan dx_plan(const ConvGeo &q) {
 }
 
 static size_t dx_scratch_bytes(const ConvGeo &q) {
+  if (dx_phase_plan(q).ok) return dx_phase_scratch_bytes(q);
   const DxPlan d = dx_plan(q);
   return d.ok ? d.gemm_off + conv_scratch_bytes<false>(d.g2) : 0;
 }
 
 // bf16 NHWC dx on the MFMA path; false (nothing launched) if it does not apply.
 static bool conv_dx_mfma(const void *dy, const void *w, void *dx, const ConvGeo &q, hipStream_t s, Scratch scr) {
+  if (dx_phase_plan(q).ok) return conv_dx_phases(dy, w, dx, q, s, scr);
   const DxPlan d = dx_plan(q);
   if (!d.ok || scr.ptr == nullptr || scr.bytes < d.gemm_off || !aligned(dy, 16) || !aligned(w, 16)) return false;
   char *base = static_cast<char *>(scr.ptr);

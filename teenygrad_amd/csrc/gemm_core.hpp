@@ -75,7 +75,26 @@ struct GemmParams {
   // both operands are shared through its L2), then step along n_fast's
   // dimension
   int group;
+  // Output rows remapped (the sub-pixel phases of a strided conv's dx, whose
+  // rows are every SH-th row and SW-th column of dx): when c_ow > 0, row
+  // m = (b, u, v) with v = m % c_ow, u = (m / c_ow) % c_oh starts at element
+  // b c_sb + u c_su + v c_sv of C, and ldc is unused.  Only the
+  // register-staged kernels and the split-K finalize take it.
+  int c_ow, c_oh;
+  int64_t c_sb, c_su, c_sv;
 };
+
+// Element offset of output row m in C (see GemmParams::c_ow).
+__device__ __forceinline__ int64_t c_row(const GemmParams &p, int m) {
+  if (p.c_ow <= 0) return static_cast<int64_t>(m) * p.ldc;
+  const int v = m % p.c_ow, t = m / p.c_ow;
+  return (t / p.c_oh) * p.c_sb + (t % p.c_oh) * p.c_su + v * p.c_sv;
+}
+// Whether every output row starts 16-byte aligned (8 bf16).
+__host__ __device__ inline bool c_rows_vec16(const GemmParams &p) {
+  const bool strides = p.c_ow > 0 ? (p.c_sb % 8 == 0 && p.c_su % 8 == 0 && p.c_sv % 8 == 0) : (p.ldc % 8 == 0);
+  return strides && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0;
+}
 
 
 __device__ __forceinline__ void epi_coeffs(const GemmParams &p, int n, float (&mul)[4], float (&add)[4]) {
@@ -586,14 +605,14 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
   __syncthreads();
   constexpr int CPR_C = BN / 8;        // 16-byte chunks per C row
   constexpr int RPP_C = 256 / CPR_C;   // rows per pass
-  const bool vec16 = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+  const bool vec16 = c_rows_vec16(p);
 #pragma clang loop unroll(full)
   for (int r0 = 0; r0 < BM; r0 += RPP_C) {
     const int ml = r0 + tid / CPR_C, nl = (tid % CPR_C) * 8;
     const int m = m0 + ml, n = n0 + nl;
     if (m < p.M && n < p.N) {
       const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3));
-      bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
+      bf16 *dst = p.C + c_row(p, m) + n;
       if (vec16 && n + 8 <= p.N) {
         *reinterpret_cast<u32x4 *>(dst) = v;
       } else {
@@ -648,8 +667,8 @@ static __global__ __launch_bounds__(256) void gemm_splitk_finalize(GemmParams p,
     }
     o[e] = static_cast<bf16>(apply_act_rt(v, p.act));
   }
-  bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n0;
-  if (vec && (p.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0) {
+  bf16 *dst = p.C + c_row(p, m) + n0;
+  if (vec && c_rows_vec16(p)) {
     u32x4 v;
     __builtin_memcpy(&v, o, 16);
     *reinterpret_cast<u32x4 *>(dst) = v;
@@ -769,10 +788,11 @@ enum GemmTiles { kTilesPersist, kTilesStream, kTilesBig, kTiles128x64, kTiles64x
 
 template <bool INT8B, int AMODE>
 inline GemmTiles gemm_tiles(const GemmParams &p) {
-  if (persist_gemm_fits<INT8B, AMODE>(p)) return kTilesPersist;
-  if (stream_gemm_fits<INT8B, AMODE>(p)) return kTilesStream;
+  const bool plain_rows = p.c_ow <= 0;  // remapped rows: register-staged kernels only
+  if (plain_rows && persist_gemm_fits<INT8B, AMODE>(p)) return kTilesPersist;
+  if (plain_rows && stream_gemm_fits<INT8B, AMODE>(p)) return kTilesStream;
   if constexpr (AMODE != kAConvScalar) {
-    if (big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
+    if (plain_rows && big_gemm_fits<INT8B, AMODE>(p)) return kTilesBig;
   }
   if (p.N <= 64) return p.K >= 512 ? kTiles64x64 : kTiles128x64;
   if (p.K <= 256) return kTiles128x128Short;
@@ -825,7 +845,7 @@ inline bool launch_gemm_mfma(GemmParams p, int act, hipStream_t s, Scratch scr) 
       const int64_t m0 = u0 * unit;
       q.M = static_cast<int>(std::min<int64_t>(p.M - m0, per * unit));
       q.A = p.A + u0 * (AMODE == kAPlain ? p.lda : static_cast<int64_t>(p.H) * p.W * p.Cin);
-      q.C = p.C + m0 * p.ldc;
+      q.C = p.C + (p.c_ow > 0 ? u0 * p.c_sb : m0 * p.ldc);
       launch_gemm_mfma<INT8B, AMODE>(q, act, s, scr);
     }
     return true;

@@ -207,6 +207,14 @@ MFMA_DX_CASES = [  # bf16 NHWC, groups 1: B, H, Cin, Cout, K, stride, pad (ResNe
     (2, 56, 64, 256, 1, 1, 0),
     (2, 30, 3, 64, 7, 2, 3),
     (3, 9, 32, 64, 3, 2, 0),
+    # strided convs run as their sub-pixel phases (one stride-1 GEMM per
+    # (ih % S, iw % S) class, remapped output rows; phases without taps zeroed)
+    (4, 28, 256, 256, 3, 2, 1),   # the ResNet-50 stage-3 downsampling 3x3
+    (2, 15, 64, 64, 3, 2, 1),     # odd H: phases of 8 and 7 rows
+    (2, 13, 32, 48, 5, 3, 2),     # stride 3, 5x5
+    (2, 12, 16, 32, 4, 2, 1),     # even kernel
+    (2, 30, 16, 64, 7, 2, 3),     # stem-like 7x7/2: 4 x 4, 4 x 3, 3 x 4, 3 x 3 taps
+    (3, 14, 64, 128, 1, 2, 0),    # 1x1/2 on even H: odd rows and columns are zero
 ]
 
 
