@@ -25,6 +25,7 @@
 #include <mutex>
 
 #include "gemm_core.hpp"
+#include "conv_band.hpp"
 
 namespace teeny {
 
@@ -509,6 +510,7 @@ static bool conv_s2d_mfma(const void *x, const void *w, const float *scale, cons
                      static_cast<const bf16 *>(x), xs, static_cast<const bf16 *>(w), wsd, nbx, q.B, q.H, q.W,
                      q.Cin, q.PH, q.PW, g2.H, g2.W, q.Cout, q.KH, q.KW, g2.KH, g2.KW, g2.Cin);
   GemmParams p = conv_gemm_params(xs, wsd, scale, bias, bias_bf16, y, g2);
+  if (try_conv_band(p, act, s)) return true;
   const Scratch rest{static_cast<char *>(scr.ptr) + sp.gemm_off, scr.bytes - sp.gemm_off};
   launch_gemm_mfma<false, kAConvVec>(p, act, s, rest);
   return true;
@@ -524,6 +526,10 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
   if (path == kConvNoMfma) return false;
   if (path == kConvS2D && conv_s2d_mfma(x, w, scale, bias, bias_bf16, y, q, act, s, scr)) return true;
   GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
+  if constexpr (!INT8B) {
+    // stride-1 convs whose weights fit in LDS: the row-band kernel
+    if (path == kConvVec && try_conv_band(p, act, s)) return true;
+  }
   switch (path) {
     case kConvPlain: return launch_gemm_mfma<INT8B, kAPlain>(p, act, s, scr);
     case kConvVec: return launch_gemm_mfma<INT8B, kAConvVec>(p, act, s, scr);

@@ -1,0 +1,342 @@
+// Row-band convolution for stride-1 bf16 NHWC convs with 64 output channels
+// whose whole weight tensor fits in LDS (the 56x56 3x3 64 -> 64 ResNet
+// layers; the space-to-depth form of the 7x7/2 stem, 4x4 taps over 16
+// channels):
+//
+//   y[b, oh, ow, co] = act( scale[co] * sum_{kh, kw, ci} x[b, oh - PH + kh, ow - PW + kw, ci]
+//                                        * w[co, kh, kw, ci] + bias[co] )
+//
+// The implicit GEMM (gemm_core.hpp) gathers a pixel's KH x KW taps from L2
+// for every output tile and streams the weights once per tile: the 56x56
+// 3x3 layer moves ~9x its input and ~3100 copies of its 74 KiB of weights
+// through L2, and the stem ~16x its input.  Here each workgroup (one per
+// CU, persistent) loads the weights into LDS once, then walks bands of RB
+// whole output rows of one image: per channel chunk (CC <= 32 channels) the
+// band's input rows with their halo, (RB + KH - 1) x (OW + KW - 1) pixels,
+// arrive in LDS by one LDS-DMA pass (padding pixels read as zeros through
+// out-of-extent buffer offsets), and every tap is then read from LDS.
+//
+// A band has RB * OW = 32 * NW pixels (RB = 4 at OW = 56, RB = 2 at OW =
+// 112: 7 waves); wave w owns pixels 32 w .. 32 w + 31 of the band and all 64
+// output channels.  v_mfma_f32_32x32x16_bf16 computes the transposed tile
+// D[co][px] (weights as the A operand, 16 channels of one tap per k-step),
+// so a lane's registers are 4 consecutive output channels of one pixel.
+// LDS layouts: weight rows [co][(kh, kw, ci)] padded by 16 bytes (an odd
+// number of 16-byte units, so the 16-byte fragment reads of 16 consecutive
+// rows hit 16 disjoint bank quads); halo pixels of CC channels, the 16-byte
+// chunk q of halo column hc at position q ^ ((hc >> 2) & 3) when CC = 32 (a
+// fragment read touches 8 consecutive columns per quarter-wave; unswizzled,
+// columns hc and hc + 4 share banks).
+//
+// Pipeline: NHB halo buffers, the DMA NHB - 1 chunk stages ahead of the
+// MFMAs, one barrier per stage (a stage's DMA is issued after the barrier
+// that ends the stage which last read its buffer).  Every wave issues the
+// same DMA count per stage (rounds past the halo's slots go to a 1 KiB
+// dummy area), so an explicit s_waitcnt vmcnt leaves the newer stages in
+// flight; the epilogue's stores are counted with them in issue order, which
+// only makes the next waits stricter.  Epilogue: scale / bias / activation
+// on the fp32 accumulators, bf16 through a per-wave 2 KiB LDS slice (32
+// pixels x 32 channels at a time) and out as 16-byte chunks, 4 per pixel
+// row segment.
+#pragma once
+
+#include <atomic>
+
+#include "gemm_core.hpp"
+
+namespace teeny {
+
+struct BandParams {
+  const bf16 *x;  // [B, H, W, CIN]
+  const bf16 *w;  // [64, KH, KW, CIN]
+  const float *scale, *bias;
+  const bf16 *bias_bf16;
+  bf16 *y;        // [B, OH, OW, 64]
+  int B, H, W, OH, PH, PW, act;
+  int x_bytes;    // byte extent of x (below 2^31)
+};
+
+template <int CIN, int KH, int KW, int OWT, int RB>
+struct BandShape {
+  static constexpr int COUT = 64;
+  static constexpr int NPX = RB * OWT;         // pixels per band
+  static constexpr int NW = NPX / 32;          // waves
+  static constexpr int NT = 64 * NW;           // threads
+  static constexpr int CC = CIN >= 32 ? 32 : CIN;  // channels per halo chunk
+  static constexpr int NCH = CIN / CC;         // chunks per band
+  static constexpr int CPP = CC / 8;           // 16-byte chunks per halo pixel
+  static constexpr int HR = RB + KH - 1, HC = OWT + KW - 1;
+  static constexpr int SLOTS = HR * HC * CPP;  // 16-byte halo slots per chunk
+  static constexpr int INSTR = (SLOTS + 63) / 64;   // DMA instructions per chunk (workgroup)
+  static constexpr int DI = (INSTR + NW - 1) / NW;  // per wave (some go to the dummy area)
+  static constexpr int HBUF = INSTR * 1024;         // bytes of one halo buffer
+  static constexpr int K = KH * KW * CIN;
+  static constexpr int WP = K * 2 + 16;             // weight row pitch (bytes)
+  static constexpr int WBYTES = COUT * WP;
+  static constexpr int STG = 2048;                  // epilogue slice per wave
+  static_assert(NPX % 32 == 0 && NW <= 16, "a band is whole 32-pixel blocks");
+  static_assert(CIN % 16 == 0 && CC % 16 == 0 && (CPP == 2 || CPP == 4), "16-channel k-steps");
+  static_assert((WP / 16) % 2 == 1, "odd number of 16-byte units per weight row");
+};
+
+template <int CIN, int KH, int KW, int OWT, int RB, int NHB>
+constexpr int band_lds_bytes() {
+  using S = BandShape<CIN, KH, KW, OWT, RB>;
+  return S::WBYTES + NHB * S::HBUF + 1024 + S::NW * S::STG;
+}
+
+template <int CIN, int KH, int KW, int OWT, int RB, int NHB>
+__global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv_band_kernel(BandParams p) {
+  using S = BandShape<CIN, KH, KW, OWT, RB>;
+  constexpr int NW = S::NW, CC = S::CC, NCH = S::NCH, CPP = S::CPP, HC = S::HC, DI = S::DI;
+  constexpr int INFLIGHT = (NHB - 2) * DI;
+  static_assert(NHB >= 2 && INFLIGHT < 16, "halo stages / vmcnt field");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char *const wlds = smem;
+  char *const halo = smem + S::WBYTES;
+  char *const dummy = halo + NHB * S::HBUF;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 5, c = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  char *const stg = dummy + 1024 + w * S::STG;
+
+  const int bands_per_img = p.OH / RB;
+  const int n_units = p.B * bands_per_img;
+  const int G = static_cast<int>(gridDim.x);
+  const int wg = static_cast<int>(blockIdx.x);
+  const int my_units = wg < n_units ? (n_units - 1 - wg) / G + 1 : 0;
+  const int n_stages = my_units * NCH;
+
+  // ── weights into LDS once (16-byte loads; before any DMA is in flight)
+  {
+    constexpr int CPR = S::K / 8;  // 16-byte chunks per weight row
+    for (int i = tid; i < S::COUT * CPR; i += S::NT) {
+      const int co = i / CPR, j = i % CPR;
+      *reinterpret_cast<u32x4 *>(wlds + co * S::WP + 16 * j) =
+          *reinterpret_cast<const u32x4 *>(p.w + static_cast<int64_t>(co) * S::K + 8 * j);
+    }
+  }
+  // epilogue coefficients of this lane's output channels: co = 32 i + 8 q + 4 g + e,
+  // by unconditional buffer loads (an absent operand gets a zero extent and
+  // reads zeros), so they issue as one batch with one wait
+  const __amdgpu_buffer_rsrc_t s_rsrc = buffer_rsrc(p.scale, p.scale != nullptr ? 256 : 0);
+  const __amdgpu_buffer_rsrc_t b_rsrc = buffer_rsrc(p.bias, p.bias != nullptr ? 256 : 0);
+  const __amdgpu_buffer_rsrc_t h_rsrc = buffer_rsrc(p.bias_bf16, p.bias_bf16 != nullptr ? 128 : 0);
+  const bool scaled = p.scale != nullptr;
+  f32x4 mulv[2][4], addv[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int co = 32 * i + 8 * q + 4 * g + e;
+        const float m = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, 4 * co, 0, 0));
+        const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b_rsrc, 4 * co, 0, 0));
+        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(h_rsrc, 2 * co, 0, 0);
+        mulv[i][q][e] = scaled ? m : 1.0f;
+        addv[i][q][e] = a + __builtin_bit_cast(float, h << 16);
+      }
+  // materialised here, before any DMA is issued (a later first use would
+  // make the compiler's wait for these loads drain the DMA as well)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(mulv[i][q]), "+v"(addv[i][q]));
+  __syncthreads();
+
+  // ── halo DMA of stage st (unit st / NCH, chunk st % NCH) into buffer st % NHB.
+  // Slot s (16 bytes) of a buffer: halo pixel s / CPP, position s % CPP,
+  // holding data chunk (s % CPP) ^ swz(hc).  A wave's round r covers slots
+  // [(r NW + w) 64, + 64); rounds past the halo write the dummy area.
+  const __amdgpu_buffer_rsrc_t x_rsrc = buffer_rsrc(p.x, p.x_bytes);
+  const uint32_t halo0 = lds_address(halo), dummy0 = lds_address(dummy);
+  auto swz = [](int hc) { return CPP == 4 ? (hc >> 2) & 3 : 0; };
+  auto dma_stage = [&](int st) __attribute__((always_inline)) {
+    const bool live = st < n_stages;
+    const int unit = wg + (st / NCH) * G, ch = st % NCH;
+    const int b = unit / bands_per_img;
+    const int oh0 = (unit % bands_per_img) * RB;
+    const uint32_t buf = halo0 + (st % NHB) * S::HBUF;
+#pragma unroll
+    for (int r = 0; r < DI; ++r) {
+      const int base = (r * NW + w) * 64;  // wave-uniform
+      const int s = base + lane;
+      const int pix = s / CPP, pos = s % CPP;
+      const int hr = pix / HC, hc = pix % HC;
+      const int ih = oh0 - p.PH + hr, iw = hc - p.PW;
+      const bool ok = live & (s < S::SLOTS) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
+                      (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
+      const int off = ok ? static_cast<int>(((static_cast<int64_t>(b) * p.H + ih) * p.W + iw) * CIN * 2 +
+                                            (ch * CC + 8 * (pos ^ swz(hc))) * 2)
+                         : kOffNone;
+      const uint32_t dst = base < S::SLOTS ? buf + base * 16 : dummy0;
+      buffer_lds_dma16(x_rsrc, off, __builtin_amdgcn_readfirstlane(dst));
+    }
+  };
+
+  // ── MFMA side: this lane's pixel of the band and its halo position
+  const int px = 32 * w + c;
+  const int pr = px / OWT, pc = px % OWT;
+  f32x16 acc[2] = {zero16(), zero16()};
+  auto compute_stage = [&](int st) __attribute__((always_inline)) {
+    const char *hb = halo + (st % NHB) * S::HBUF;
+    const int ch = st % NCH;
+    constexpr int HS = CC / 16;  // k-steps per tap in a chunk
+    constexpr int NKS = KH * KW * HS;
+    auto frags = [&](int ks, bf16x8 &xf, bf16x8 &w0, bf16x8 &w1) __attribute__((always_inline)) {
+      const int tap = ks / HS, h = ks % HS;
+      const int kh = tap / KW, kw = tap % KW;
+      const int hc = pc + kw;
+      const int hp = (pr + kh) * HC + hc;
+      xf = *reinterpret_cast<const bf16x8 *>(hb + hp * (CC * 2) + 16 * ((2 * h + g) ^ swz(hc)));
+      const int kb = 2 * (tap * CIN + ch * CC + 16 * h + 8 * g);
+      w0 = *reinterpret_cast<const bf16x8 *>(wlds + c * S::WP + kb);
+      w1 = *reinterpret_cast<const bf16x8 *>(wlds + (32 + c) * S::WP + kb);
+    };
+    bf16x8 xa, wa0, wa1, xb, wb0, wb1;
+    frags(0, xa, wa0, wa1);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks += 2) {
+      if (ks + 1 < NKS) frags(ks + 1, xb, wb0, wb1);
+      acc[0] = mfma32x32x16(wa0, xa, acc[0]);
+      acc[1] = mfma32x32x16(wa1, xa, acc[1]);
+      if (ks + 2 < NKS) frags(ks + 2, xa, wa0, wa1);
+      if (ks + 1 < NKS) {
+        acc[0] = mfma32x32x16(wb0, xb, acc[0]);
+        acc[1] = mfma32x32x16(wb1, xb, acc[1]);
+      }
+    }
+  };
+
+  const EpiAct ea = epi_act(p.act);
+  const float lo = ea.relu ? 0.0f : -INFINITY;
+  const __amdgpu_buffer_rsrc_t y_rsrc =
+      buffer_rsrc(p.y, static_cast<int>(static_cast<int64_t>(p.B) * p.OH * OWT * S::COUT * 2));
+  // Epilogue of unit `unit`: per 32-channel block i, lane (c, g) holds
+  // channels 32 i + 8 q + 4 g + (0..3) of pixel c; a v_permlane32_swap per
+  // dword gives it the 16-byte chunk 2 pr + g of the pixel's 64-byte row
+  // segment, staged at chunk position (2 pr + g) ^ ((c >> 1) & 3), then read
+  // back as whole segments (16 lanes = 4 pixels x 64 bytes per quarter).
+  auto epilogue = [&](int unit, auto sig) __attribute__((always_inline)) {
+    const int b = unit / bands_per_img;
+    const int oh0 = (unit % bands_per_img) * RB;
+    const int64_t pix0 = (static_cast<int64_t>(b) * p.OH + oh0) * OWT + 32 * w;  // the wave's first pixel
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int prr = 0; prr < 2; ++prr) {
+        u32x2 hv[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int q = 2 * prr + t;
+          bf16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float r = __builtin_fmaf(acc[i][4 * q + e], mulv[i][q][e], addv[i][q][e]);
+            if constexpr (decltype(sig)::value) r = epi_sig(r, ea);
+            o[e] = static_cast<bf16>(r < lo ? lo : r);
+          }
+          hv[t] = __builtin_bit_cast(u32x2, o);
+        }
+        u32x4 v;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(hv[0][d], hv[1][d], false, false);
+          v[d] = sw[0];
+          v[2 + d] = sw[1];
+        }
+        const int k = 2 * prr + g;
+        *reinterpret_cast<u32x4 *>(stg + c * 64 + 16 * (k ^ ((c >> 1) & 3))) = v;
+      }
+      // 32 pixels x 64 bytes back out: round r2, lane L holds pixel 16 r2 + L / 4, chunk L % 4
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const int pl = 16 * r2 + (lane >> 2), k = lane & 3;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 64 + 16 * (k ^ ((pl >> 1) & 3)));
+        const int off = static_cast<int>(((pix0 + pl) * S::COUT + 32 * i) * 2 + 16 * k);
+        __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 0);
+      }
+    }
+  };
+
+  // prologue: stages 0 .. NHB-2 in flight
+#pragma unroll
+  for (int st = 0; st < NHB - 1; ++st) dma_stage(st);
+  for (int st = 0; st < n_stages; ++st) {
+    // this wave's part of stage st landed (newer stages may fly), then all waves'
+    __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
+    __syncthreads();
+    // every wave is past stage st-1, whose buffer the DMA of st+NHB-1 reuses
+    dma_stage(st + NHB - 1);
+    compute_stage(st);
+    if (st % NCH == NCH - 1) {
+      const int unit = wg + (st / NCH) * G;
+      if (ea.sig) epilogue(unit, std::true_type{});
+      else epilogue(unit, std::false_type{});
+      acc[0] = zero16();
+      acc[1] = zero16();
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
+}
+
+// Shapes the band kernel is built for: 64 output channels, stride 1, output
+// width OWT with OH a multiple of RB, C_IN = CIN, all operands 16-byte
+// aligned, extents below 2^31 bytes.
+template <int CIN, int KH, int KW, int OWT, int RB>
+inline bool band_fits(const GemmParams &p) {
+  return p.N == 64 && p.Cin == CIN && p.KH == KH && p.KW == KW && p.SH == 1 && p.SW == 1 && p.OW == OWT &&
+         p.OH % RB == 0 && p.PH >= 0 && p.PW >= 0 && p.ldc == 64 && p.c_ow <= 0 &&
+         (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(p.C) & 15) == 0 &&
+         static_cast<int64_t>(p.M) * 64 * 2 < 0x7fffffff &&
+         static_cast<int64_t>(p.M / (p.OH * p.OW)) * p.H * p.W * p.Cin * 2 < 0x7fffffff;
+}
+
+template <int CIN, int KH, int KW, int OWT, int RB, int NHB>
+inline void launch_band(const GemmParams &p, int act, hipStream_t s) {
+  constexpr int bytes = band_lds_bytes<CIN, KH, KW, OWT, RB, NHB>();
+  static_assert(bytes <= 160 * 1024, "LDS");
+  auto kern = &conv_band_kernel<CIN, KH, KW, OWT, RB, NHB>;
+  static const bool attr_set = [kern] {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               bytes) == hipSuccess;
+  }();
+  (void)attr_set;
+  BandParams b{};
+  b.x = p.A;
+  b.w = static_cast<const bf16 *>(p.B);
+  b.scale = p.scale;
+  b.bias = p.bias;
+  b.bias_bf16 = p.bias_bf16;
+  b.y = p.C;
+  b.B = p.M / (p.OH * p.OW);
+  b.H = p.H;
+  b.W = p.W;
+  b.OH = p.OH;
+  b.PH = p.PH;
+  b.PW = p.PW;
+  b.act = act;
+  b.x_bytes = static_cast<int>(static_cast<int64_t>(b.B) * p.H * p.W * p.Cin * 2);
+  const int units = b.B * (p.OH / RB);
+  const int grid = std::min(units, device_cu_count());
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(BandShape<CIN, KH, KW, OWT, RB>::NT), bytes, s,
+                     b);
+}
+
+// The band kernel for this conv (the GEMM view of a groups-1 bf16 NHWC conv),
+// if one is built for its shape; returns false otherwise.
+inline bool try_conv_band(const GemmParams &p, int act, hipStream_t s) {
+  if (band_fits<64, 3, 3, 56, 4>(p)) {
+    launch_band<64, 3, 3, 56, 4, 3>(p, act, s);
+    return true;
+  }
+  if (band_fits<16, 4, 4, 112, 2>(p)) {
+    launch_band<16, 4, 4, 112, 2, 3>(p, act, s);
+    return true;
+  }
+  return false;
+}
+
+}  // namespace teeny

@@ -182,6 +182,59 @@ def test_bf16_nhwc_persistent_strided_1x1(dev, orc, act, bn):
         check_bf16(got[i:i + 1], post(orc.conv2d_nhwc(x[i:i + 1], w, bias, stride=2, padding=0)), f"image {i}")
 
 
+BAND_CASES = [
+    # B, H, W, Cin, Cout, K, stride, pad, act, bias/bn: shapes the row-band
+    # kernel takes (weights resident in LDS, input row bands with their halo
+    # staged once per channel chunk)
+    (3, 56, 56, 64, 64, 3, 1, 1, "relu", "bias"),    # the 56x56 ResNet 3x3 at a ragged batch
+    (2, 58, 58, 64, 64, 3, 1, 0, "gelu", "bias"),    # no padding: a 58-wide input for 56 outputs
+    (2, 56, 56, 64, 64, 3, 1, 1, "silu", "bn"),      # folded BatchNorm scale / shift
+    (1, 56, 56, 64, 64, 3, 1, 1, None, None),        # no bias
+    (2, 224, 224, 3, 64, 7, 2, 3, "relu", "bias"),   # the stem through its space-to-depth form
+    (1, 224, 224, 3, 64, 7, 2, 3, "gelu", "bn"),
+]
+
+
+@pytest.mark.parametrize("case", BAND_CASES)
+def test_bf16_nhwc_band(dev, orc, case):
+    B, H, W, Cin, Cout, k, s, p, act, post = case
+    print(f"[conv bf16 band] {case}", flush=True)
+    rng = np.random.default_rng(H + 7 * W + Cin + k + (0 if act is None else len(act)))
+    xb = to_bf16(rng.random((B, H, W, Cin), dtype=np.float32))
+    wb = to_bf16((rng.standard_normal((Cout, k, k, Cin), dtype=np.float32) * np.sqrt(2.0 / (Cin * k * k))).astype(np.float32))
+    x, w = from_bf16(xb), from_bf16(wb)
+    oh, ow = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    need = K.conv2d_workspace_size((B, H, W, Cin), (Cout, k, k, Cin), s, p, 1, tg.bf16, "nhwc")
+    bias = scale = shift = None
+    with stream_workspace(dev, need):
+        if post == "bn":
+            scale = rng.uniform(0.5, 1.5, Cout).astype(np.float32)
+            shift = rng.normal(0, 0.1, Cout).astype(np.float32)
+            got = K.conv2d_bn_act(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(scale),
+                                  dev.upload(shift), s, p, 1, act, layout="nhwc").to_host()
+        else:
+            if post == "bias":
+                bias = rb(rng.normal(0, 0.1, Cout).astype(np.float32))
+            got = K.conv2d(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16),
+                           dev.upload(to_bf16(bias), tg.bf16) if bias is not None else None, s, p, 1, act,
+                           layout="nhwc").to_host()
+        dev.synchronize()
+
+    def finish(ref):
+        if post == "bn":
+            ref = ref * scale + shift
+        return ref if act is None else {"relu": orc.relu, "silu": orc.silu, "gelu": orc.gelu}[act](ref)
+
+    assert got.shape == (B, oh, ow, Cout)
+    assert np.all(np.isfinite(from_bf16(got)))
+    m = B * oh * ow
+    starts = np.arange(0, m, 64)
+    pix = starts + (rng.random(starts.size) * np.minimum(64, m - starts)).astype(np.int64)
+    check_bf16(got.reshape(m, Cout)[pix], finish(orc.conv2d_nhwc_pixels(x, w, pix, bias, stride=s, padding=p)),
+               f"{pix.size} sampled pixels")
+    check_bf16(got[B - 1:B], finish(orc.conv2d_nhwc(x[B - 1:B], w, bias, stride=s, padding=p)), f"image {B - 1}")
+
+
 STREAM_CASES = [
     # B, H, W, Cin, Cout, act: 1x1 stride-1 convs with M = B*H*W >= 16384 and
     # C_IN, C_OUT in {64, 128, 256} take the streaming kernel
