@@ -33,8 +33,9 @@
 // that ends the stage which last read its buffer).  Every wave issues the
 // same DMA count per stage (rounds past the halo's slots go to a 1 KiB
 // dummy area), so an explicit s_waitcnt vmcnt leaves the newer stages in
-// flight; the epilogue's stores are counted with them in issue order, which
-// only makes the next waits stricter.  Epilogue: scale / bias / activation
+// flight; the count includes the epilogue stores issued since the awaited
+// DMA (vector memory operations retire in issue order), so the stores stay
+// in flight too.  Epilogue: scale / bias / activation
 // on the fp32 accumulators, bf16 through a per-wave 2 KiB LDS slice (32
 // pixels x 32 channels at a time) and out as 16-byte chunks, 4 per pixel
 // row segment.
@@ -90,7 +91,7 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   using S = BandShape<CIN, KH, KW, OWT, RB>;
   constexpr int NW = S::NW, CC = S::CC, NCH = S::NCH, CPP = S::CPP, HC = S::HC, DI = S::DI;
   constexpr int INFLIGHT = (NHB - 2) * DI;
-  static_assert(NHB >= 2 && INFLIGHT < 16, "halo stages / vmcnt field");
+  static_assert(NHB >= 2 && NHB <= 4 && INFLIGHT < 16, "halo stages / vmcnt field");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *const wlds = smem;
   char *const halo = smem + S::WBYTES;
@@ -263,9 +264,22 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   // prologue: stages 0 .. NHB-2 in flight
 #pragma unroll
   for (int st = 0; st < NHB - 1; ++st) dma_stage(st);
+  // The wait for stage st's DMA counts, in issue order, everything issued
+  // after it: the DMAs of the NHB - 2 later stages and the epilogue stores
+  // of the iterations since (EPI_STORES per epilogue; epi_hist holds which of
+  // the last NHB - 1 iterations ended one).  A fixed count would make each
+  // stage wait for the previous epilogue's stores to complete.
+  constexpr int EPI_STORES = 4;
+  static_assert(INFLIGHT + EPI_STORES * (NHB - 1) < 16, "vmcnt field");
+  unsigned epi_hist = 0;
   for (int st = 0; st < n_stages; ++st) {
     // this wave's part of stage st landed (newer stages may fly), then all waves'
-    __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
+    switch (__builtin_popcount(epi_hist)) {
+      case 0: __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0xF70 | (INFLIGHT + EPI_STORES)); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0xF70 | (INFLIGHT + 2 * EPI_STORES)); break;
+      default: __builtin_amdgcn_s_waitcnt(0xF70 | (INFLIGHT + 3 * EPI_STORES)); break;
+    }
     __syncthreads();
     // every wave is past stage st-1, whose buffer the DMA of st+NHB-1 reuses
     dma_stage(st + NHB - 1);
@@ -277,6 +291,7 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
       acc[0] = zero16();
       acc[1] = zero16();
     }
+    epi_hist = ((epi_hist << 1) | (st % NCH == NCH - 1 ? 1u : 0u)) & ((1u << (NHB - 1)) - 1u);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
 }

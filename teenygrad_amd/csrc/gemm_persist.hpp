@@ -20,8 +20,8 @@
 // Past the workgroup's last tile it issues zero-source DMAs, so every
 // k-tile issues the same DMA count and the explicit vmcnt waits stay exact.
 // The epilogue's stores are compiler-visible buffer stores; the kernel's own
-// waits count them in issue order with the DMAs, which only makes the waits
-// of the next few k-tiles stricter.  Each store instruction writes eight
+// waits count them in issue order with the DMAs (the first k-tile after an
+// epilogue allows for them).  Each store instruction writes eight
 // whole 128-byte row segments: stores of 8 bytes per lane straight from the
 // accumulators (32 rows x 16 bytes per instruction) wrote at ~1.4 TB/s and
 // took more time than the whole k-loop on the 1x1 convs.
@@ -204,7 +204,13 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
   // DMA_PER_KT of them also one DMA of the cursor's k-tile; the fragment
   // set is refilled in place (k-step 1 of this k-tile during the k-step-0
   // MFMAs, k-step 0 of k-tile gk+1 during the k-step-1 MFMAs)
-  auto ktile = [&](int gk) __attribute__((always_inline)) {
+  // Stores of one epilogue per wave (MB row blocks x 4 instructions).  The
+  // first k-tile after an epilogue waits for the DMA issued before those
+  // stores, so its count includes them (vector memory operations retire in
+  // issue order): the stores stay in flight instead of being drained.
+  constexpr int EPI_STORES = MB * 4;
+  static_assert(INFLIGHT + EPI_STORES < 16, "vmcnt field");
+  auto ktile = [&](int gk, bool after_epilogue) __attribute__((always_inline)) {
     const char *cu = smem + (gk % NST) * STAGE;
     const char *nx = smem + ((gk + 1) % NST) * STAGE;
 #pragma unroll
@@ -223,7 +229,8 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     dma_advance();
-    __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
+    if (after_epilogue) __builtin_amdgcn_s_waitcnt(0xF70 | (INFLIGHT + EPI_STORES));
+    else __builtin_amdgcn_s_waitcnt(0xF70 | INFLIGHT);
     __syncthreads();
   };
 
@@ -343,7 +350,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
     for (int i = 0; i < NB; ++i)
 #pragma unroll
       for (int j = 0; j < MB; ++j) acc[i][j] = zero16();
-    for (int kt = 0; kt < n_k; ++kt) ktile(gk++);
+    for (int kt = 0; kt < n_k; ++kt) ktile(gk++, kt == 0 && pos > 0);
     int m0, n0;
     tile_origin(pos, m0, n0);
     const int slot = (gk - 1) % NST;  // the stage of the tile's last k-tile
