@@ -26,6 +26,7 @@
 
 #include "gemm_core.hpp"
 #include "conv_band.hpp"
+#include "conv_tile.hpp"
 
 namespace teeny {
 
@@ -530,6 +531,8 @@ static bool try_conv_mfma(const void *x, const void *w, const float *scale, cons
     // stride-1 convs whose weights fit in LDS: the row-band kernel
     if (path == kConvVec && try_conv_band(p, act, s)) return true;
   }
+  // stride-1 3x3 convs over short rows: band tiles with streamed weights
+  if (path == kConvVec && try_conv_tile<INT8B>(p, act, s)) return true;
   switch (path) {
     case kConvPlain: return launch_gemm_mfma<INT8B, kAPlain>(p, act, s, scr);
     case kConvVec: return launch_gemm_mfma<INT8B, kAConvVec>(p, act, s, scr);

@@ -1,0 +1,388 @@
+// Band-tiled convolution with streamed weights, for stride-1 NHWC convs whose
+// input rows are short (built for the 14x14 3x3 ResNet layers; the template
+// also takes 28-wide outputs and int8 weights):
+//
+//   y[b, oh, ow, n] = act( scale[n] * sum_{kh, kw, ci} x[b, oh - PH + kh, ow - PW + kw, ci]
+//                                      * w[n, kh, kw, ci] + bias[n] )
+//
+// with w bf16, or int8 whose per-channel scale multiplies the accumulator
+// (teeny-quant's dequantize_affine, affine.rs:151-161, applied in the
+// epilogue; the int8 values become bf16 in registers, exactly).
+//
+// The implicit GEMM reads every input pixel once per tap (9x for a 3x3)
+// from L2.  Here a workgroup owns RB whole output rows of one image (RB * OW
+// = 196 pixels: a 14x14 image, or 7 rows of a 28x28 one) and BN output
+// channels; per 32-channel chunk of C_IN, one LDS-DMA pass brings the rows'
+// input with its halo, (RB + KH - 1) x (OW + KW - 1) pixels (padding read as
+// zeros through out-of-extent buffer offsets), and the chunk's BN x KH x KW
+// x 32 weights; all taps are then read from LDS.  Two stages: the next
+// chunk's DMA runs under the current chunk's MFMAs.
+//
+// Seven waves; wave w owns pixels 32 w .. 32 w + 31 of the band (the last
+// wave's pixels past 196 read the last pixel's window and are not stored)
+// and all BN channels: per k-step (16 channels of one tap) one pixel
+// fragment and BN / 32 weight fragments feed BN / 32
+// v_mfma_f32_32x32x16_bf16 computing D[n][px].  LDS rows: weight rows of
+// KH*KW 64-byte (bf16) or 32-byte (int8) tap segments plus one 16-byte pad
+// slot (an odd number of 16-byte units per row: conflict-free fragment
+// reads of consecutive rows); halo pixels of 4 x 16 bytes with chunk q of
+// halo column hc at position q ^ ((hc >> 2) & 3).  Epilogue through a
+// per-wave 4 KiB LDS slice, 64 channels at a time, written back as whole
+// 128-byte segments of the pixels' rows; the vmcnt waits count the
+// epilogue's stores (operations retire in issue order), so they stay in
+// flight.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_core.hpp"
+
+namespace teeny {
+
+struct TileConvParams {
+  const bf16 *x;     // [B, H, W, C_IN]
+  const void *w;     // [C_OUT, KH, KW, C_IN], bf16 or int8
+  const float *scale, *bias;
+  const bf16 *bias_bf16;
+  bf16 *y;           // [B, OH, OW, C_OUT]
+  int B, H, W, Cin, Cout, OH, PH, PW, act;
+  int x_bytes, w_bytes;  // byte extents (below 2^31)
+};
+
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+struct TileShape {
+  static constexpr int NPX = RB * OWT;           // pixels per band
+  static constexpr int NW = (NPX + 31) / 32;     // waves
+  static constexpr int NT = 64 * NW;
+  static constexpr int HR = RB + KH - 1, HC = OWT + KW - 1;
+  static constexpr int HSLOTS = HR * HC * 4;     // 16-byte halo slots (32 channels per pixel)
+  static constexpr int QT = INT8B ? 2 : 4;       // 16-byte slots per tap segment
+  static constexpr int RS = KH * KW * QT + 1;    // slots per weight row (+ 1 pad slot)
+  static constexpr int WSLOTS = BN * RS;
+  static constexpr int HINSTR = (HSLOTS + 63) / 64, WINSTR = (WSLOTS + 63) / 64;
+  static constexpr int INSTR = HINSTR + WINSTR;  // DMA instructions per stage (workgroup)
+  static constexpr int DI = (INSTR + NW - 1) / NW;  // per wave (the excess write a dummy area)
+  static constexpr int HBYTES = HINSTR * 1024, WBYTES = WINSTR * 1024;
+  static constexpr int STAGE = HBYTES + WBYTES;
+  static constexpr int STG = 4096;               // epilogue slice per wave
+  static constexpr int LDS = 2 * STAGE + 1024 + NW * STG + 2 * BN * 4;
+  static_assert(RS % 2 == 1, "odd number of 16-byte units per weight row");
+  static_assert(BN % 64 == 0 && NW <= 16, "tile");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) void conv_tile_kernel(TileConvParams p) {
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
+  constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
+  constexpr int EPI_STORES = 4 * (BN / 64);
+  static_assert(EPI_STORES < 16, "vmcnt field");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char *const dummy = smem + 2 * S::STAGE;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 5, c = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  char *const stg = dummy + 1024 + w * S::STG;
+  float *const cmul = reinterpret_cast<float *>(dummy + 1024 + NW * S::STG);
+  float *const cadd = cmul + BN;
+
+  const int bands_per_img = p.OH / RB;
+  const int n_tiles = p.Cout / BN;
+  const int n_units = p.B * bands_per_img * n_tiles;
+  const int nch = p.Cin / 32;
+  const int G = static_cast<int>(gridDim.x);
+  const int wg = static_cast<int>(blockIdx.x);
+  const int my_units = wg < n_units ? (n_units - 1 - wg) / G + 1 : 0;
+  const int n_stages = my_units * nch;
+  // unit u: co tile fastest (the tiles of one band share its input in L2)
+  auto unit_of = [&](int st, int &b, int &oh0, int &n0) __attribute__((always_inline)) {
+    const int u = wg + (st / nch) * G;
+    n0 = (u % n_tiles) * BN;
+    const int band = u / n_tiles;
+    b = band / bands_per_img;
+    oh0 = (band % bands_per_img) * RB;
+  };
+
+  const __amdgpu_buffer_rsrc_t x_rsrc = buffer_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t w_rsrc = buffer_rsrc(p.w, p.w_bytes);
+  const uint32_t smem0 = lds_address(smem), dummy0 = lds_address(dummy);
+  const int K = KH * KW * p.Cin;
+  constexpr int ES = INT8B ? 1 : 2;  // bytes per weight element
+  // DMA of stage st (chunk st % nch of its unit) into stage buffer st % 2:
+  // instructions r NW + w; the first HINSTR fill the halo, the next WINSTR
+  // the weights, the rest go to the dummy area.
+  auto dma_stage = [&](int st) __attribute__((always_inline)) {
+    const bool live = st < n_stages;
+    int b, oh0, n0;
+    unit_of(st, b, oh0, n0);
+    const int c0 = (st % nch) * 32;
+    const uint32_t buf = smem0 + (st & 1) * S::STAGE;
+#pragma unroll
+    for (int r = 0; r < DI; ++r) {
+      const int ins = r * NW + w;  // wave-uniform
+      int off = kOffNone;
+      uint32_t dst = dummy0;
+      if (ins < S::HINSTR) {
+        const int s = ins * 64 + lane;
+        const int pix = s >> 2, pos = s & 3;
+        const int hr = pix / HC, hc = pix % HC;
+        const int ih = oh0 - p.PH + hr, iw = hc - p.PW;
+        const bool ok = live & (s < S::HSLOTS) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
+                        (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
+        if (ok)
+          off = static_cast<int>(((static_cast<int64_t>(b) * p.H + ih) * p.W + iw) * p.Cin * 2 +
+                                 (c0 + 8 * (pos ^ ((hc >> 2) & 3))) * 2);
+        dst = buf + ins * 1024;
+      } else if (ins < S::INSTR) {
+        const int s = (ins - S::HINSTR) * 64 + lane;
+        const int n = s / S::RS, j = s % S::RS;
+        const int tap = j / S::QT, q = j % S::QT;
+        const bool ok = live & (s < S::WSLOTS) & (j < S::RS - 1);
+        if (ok) off = static_cast<int>((static_cast<int64_t>(n0 + n) * K + tap * p.Cin + c0) * ES + 16 * q);
+        dst = buf + S::HBYTES + (ins - S::HINSTR) * 1024;
+      }
+      buffer_lds_dma16(ins < S::HINSTR ? x_rsrc : w_rsrc, off, __builtin_amdgcn_readfirstlane(dst));
+    }
+  };
+
+  // ── MFMA side
+  const int px = min(32 * w + c, S::NPX - 1);  // pixels past the band repeat the last one
+  const int pr = px / OWT, pc = px % OWT;
+  f32x16 acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc[i] = zero16();
+  // Weight fragment of channel block i for k-step (tap, h): bf16 straight
+  // from LDS, or int8 read raw (8 bytes) and converted in registers
+  typedef typename std::conditional<INT8B, u32x2, bf16x8>::type wraw_t;
+  auto wread = [&](const char *wb, int i, int tap, int h) __attribute__((always_inline)) {
+    const char *row = wb + (32 * i + c) * (S::RS * 16);
+    if constexpr (INT8B) return *reinterpret_cast<const u32x2 *>(row + (tap * 2 + h) * 16 + 8 * g);
+    else return *reinterpret_cast<const bf16x8 *>(row + (tap * 4 + 2 * h + g) * 16);
+  };
+  auto wconv = [&](const wraw_t &q) __attribute__((always_inline)) {
+    if constexpr (INT8B) {
+      bf16x8 f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t word = q[t >> 1] >> (16 * (t & 1));
+        const bf16x2 pr2 = cvt_pk_bf16(static_cast<float>(static_cast<int8_t>(word & 0xffu)),
+                                       static_cast<float>(static_cast<int8_t>((word >> 8) & 0xffu)));
+        f[2 * t] = pr2[0];
+        f[2 * t + 1] = pr2[1];
+      }
+      return f;
+    } else {
+      return q;
+    }
+  };
+  // One chunk: KH*KW taps x 2 k-steps.  The fragments of k-step ks + 1 are
+  // read while k-step ks multiplies; a scheduling fence per k-step keeps the
+  // compiler from hoisting every read of the unrolled loop (the int8 kernel
+  // then held ~480 registers).
+  auto compute_stage = [&](int st) __attribute__((always_inline)) {
+    const char *hb = smem + (st & 1) * S::STAGE;
+    const char *wb = hb + S::HBYTES;
+    constexpr int NKS = KH * KW * 2;
+    auto xread = [&](int ks) __attribute__((always_inline)) {
+      const int tap = ks >> 1, h = ks & 1;
+      const int kh = tap / KW, kw = tap % KW;
+      const int hc = pc + kw;
+      return *reinterpret_cast<const bf16x8 *>(hb + ((pr + kh) * HC + hc) * 64 + 16 * ((2 * h + g) ^ ((hc >> 2) & 3)));
+    };
+    bf16x8 xa = xread(0), xb;
+    wraw_t wa[NB], wn[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) wa[i] = wread(wb, i, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (ks + 1 < NKS) {
+        xb = xread(ks + 1);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) wn[i] = wread(wb, i, (ks + 1) >> 1, (ks + 1) & 1);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) acc[i] = mfma32x32x16(wconv(wa[i]), xa, acc[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      xa = xb;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) wa[i] = wn[i];
+    }
+  };
+
+  const EpiAct ea = epi_act(p.act);
+  const float lo = ea.relu ? 0.0f : -INFINITY;
+  const __amdgpu_buffer_rsrc_t y_rsrc =
+      buffer_rsrc(p.y, static_cast<int>(static_cast<int64_t>(p.B) * p.OH * OWT * p.Cout * 2));
+  // Epilogue of stage st's unit: 64 channels (blocks 2 hp, 2 hp + 1) at a
+  // time; lane (c, g) holds channels 32 i + 8 q + 4 g + (0..3) of pixel c,
+  // permlane32 swaps make 16-byte chunks 4 (i % 2) + 2 pr + g of the 128-byte
+  // segment, staged at chunk position ^ (c & 7) and stored as 8 whole rows
+  // per instruction.
+  auto epilogue = [&](int st, auto sig) __attribute__((always_inline)) {
+    int b, oh0, n0;
+    unit_of(st, b, oh0, n0);
+    const int64_t pix0 = (static_cast<int64_t>(b) * p.OH + oh0) * OWT;  // the band's first pixel
+#pragma unroll
+    for (int hp = 0; hp < NB / 2; ++hp) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * hp + ii;
+        f32x4 em[4], ead[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          em[q] = *reinterpret_cast<const f32x4 *>(cmul + 32 * i + 8 * q + 4 * g);
+          ead[q] = *reinterpret_cast<const f32x4 *>(cadd + 32 * i + 8 * q + 4 * g);
+        }
+#pragma unroll
+        for (int prr = 0; prr < 2; ++prr) {
+          u32x2 hv[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int q = 2 * prr + t;
+            bf16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float r = __builtin_fmaf(acc[i][4 * q + e], em[q][e], ead[q][e]);
+              if constexpr (decltype(sig)::value) r = epi_sig(r, ea);
+              o[e] = static_cast<bf16>(r < lo ? lo : r);
+            }
+            hv[t] = __builtin_bit_cast(u32x2, o);
+          }
+          u32x4 v;
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(hv[0][d], hv[1][d], false, false);
+            v[d] = sw[0];
+            v[2 + d] = sw[1];
+          }
+          const int k = 4 * ii + 2 * prr + g;
+          *reinterpret_cast<u32x4 *>(stg + c * 128 + 16 * (k ^ (c & 7))) = v;
+        }
+      }
+#pragma unroll
+      for (int r8 = 0; r8 < 4; ++r8) {
+        const int pl = 8 * r8 + (lane >> 3), k = lane & 7;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 128 + 16 * (k ^ (pl & 7)));
+        const int pxl = 32 * w + pl;
+        const int off = pxl < S::NPX
+                            ? static_cast<int>(((pix0 + pxl) * p.Cout + n0 + 64 * hp) * 2 + 16 * k)
+                            : kOffNone;
+        __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 0);
+      }
+    }
+  };
+
+  // coefficient table of the unit's channels (refilled when n0 changes):
+  // filled by plain loads before the first DMA and at unit boundaries after
+  // the stage barrier (a unit's first epilogue is nch stages later)
+  auto fill_coeffs = [&](int n0) __attribute__((always_inline)) {
+    for (int j = tid; j < BN; j += S::NT) {
+      const int n = n0 + j;
+      float m = 1.0f, a = 0.0f;
+      if (p.scale != nullptr) m = p.scale[n];
+      if (p.bias != nullptr) a = p.bias[n];
+      if (p.bias_bf16 != nullptr) a += static_cast<float>(p.bias_bf16[n]);
+      cmul[j] = m;
+      cadd[j] = a;
+    }
+  };
+  if (my_units > 0) {
+    int b, oh0, n0;
+    unit_of(0, b, oh0, n0);
+    fill_coeffs(n0);
+  }
+  __syncthreads();
+
+  dma_stage(0);
+  unsigned epi_prev = 0;  // whether the previous iteration ended an epilogue
+  for (int st = 0; st < n_stages; ++st) {
+    // stage st landed: allow the epilogue stores issued after its DMA
+    if (epi_prev) __builtin_amdgcn_s_waitcnt(0xF70 | EPI_STORES);
+    else __builtin_amdgcn_s_waitcnt(0xF70);
+    __syncthreads();
+    // every wave is past stage st-1, whose buffer stage st+1 reuses
+    dma_stage(st + 1);
+    compute_stage(st);
+    epi_prev = 0;
+    if (st % nch == nch - 1) {
+      if (ea.sig) epilogue(st, std::true_type{});
+      else epilogue(st, std::false_type{});
+#pragma unroll
+      for (int i = 0; i < NB; ++i) acc[i] = zero16();
+      epi_prev = 1;
+      if (st + 1 < n_stages) {
+        int b2, oh2, n2, b1, oh1, n1;
+        unit_of(st, b1, oh1, n1);
+        unit_of(st + 1, b2, oh2, n2);
+        if (n2 != n1) {
+          // every wave is done with this unit's coefficients (all passed its epilogue)
+          __syncthreads();
+          fill_coeffs(n2);
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
+}
+
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+inline bool tile_conv_fits(const GemmParams &p) {
+  return p.KH == KH && p.KW == KW && p.SH == 1 && p.SW == 1 && p.OW == OWT && p.OH % RB == 0 && p.PH >= 0 &&
+         p.PW >= 0 && p.Cin % 32 == 0 && p.N % BN == 0 && p.ldc == p.N && p.c_ow <= 0 &&
+         (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(p.C) & 15) == 0 &&
+         static_cast<int64_t>(p.M) * p.N * 2 < 0x7fffffff &&
+         static_cast<int64_t>(p.M / (p.OH * p.OW)) * p.H * p.W * p.Cin * 2 < 0x7fffffff &&
+         static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2) < 0x7fffffff;
+}
+
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
+  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B>;
+  static const bool attr_set = [kern] {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               S::LDS) == hipSuccess;
+  }();
+  (void)attr_set;
+  TileConvParams t{};
+  t.x = p.A;
+  t.w = p.B;
+  t.scale = p.scale;
+  t.bias = p.bias;
+  t.bias_bf16 = p.bias_bf16;
+  t.y = p.C;
+  t.B = p.M / (p.OH * p.OW);
+  t.H = p.H;
+  t.W = p.W;
+  t.Cin = p.Cin;
+  t.Cout = p.N;
+  t.OH = p.OH;
+  t.PH = p.PH;
+  t.PW = p.PW;
+  t.act = act;
+  t.x_bytes = static_cast<int>(static_cast<int64_t>(t.B) * p.H * p.W * p.Cin * 2);
+  t.w_bytes = static_cast<int>(static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2));
+  const int units = t.B * (p.OH / RB) * (p.N / BN);
+  const int grid = std::min(units, device_cu_count());
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(S::NT), S::LDS, s, t);
+}
+
+// The band-tiled kernel for this conv, if one is built for its shape: the
+// 14x14 bf16 3x3 convs (ResNet stage 3, 256 -> 256 at batch 64: 33.4 -> 26.1
+// us).  Measured and not taken: the 28x28 bf16 3x3 (128 -> 128: 28.5 us,
+// as the implicit GEMM) and the int8 28x28 conv (62 us against 54 us: each
+// converted weight fragment feeds one MFMA here, so the int8 -> bf16
+// conversion outweighs the matrix work; the GEMM reuses it across row blocks).
+template <bool INT8B>
+inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
+  if constexpr (!INT8B) {
+    if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) {
+      launch_tile_conv<3, 3, 14, 14, 64, false>(p, act, s);
+      return true;
+    }
+  }
+  return false;
+}
+
+}  // namespace teeny

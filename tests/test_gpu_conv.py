@@ -235,6 +235,64 @@ def test_bf16_nhwc_band(dev, orc, case):
     check_bf16(got[B - 1:B], finish(orc.conv2d_nhwc(x[B - 1:B], w, bias, stride=s, padding=p)), f"image {B - 1}")
 
 
+TILE_CASES = [
+    # B, H, W, Cin, Cout, pad, act, post, int8: stride-1 bf16 3x3 convs with
+    # 14-wide outputs take the band-tiled kernel (a band of 196 output pixels x
+    # 64 channels per workgroup, input rows with their halo and the chunk's
+    # weights staged per 32 input channels); the 28-wide and int8 cases run
+    # the implicit GEMM, at the same shapes as the band-tiled kernel's other
+    # instantiations would
+    (5, 14, 14, 256, 256, 1, "relu", "bias", False),   # the 14x14 ResNet 3x3 at a ragged batch
+    (2, 14, 14, 64, 128, 1, "gelu", "bn", False),      # two channel tiles, folded BatchNorm
+    (2, 16, 16, 96, 64, 0, None, None, False),         # no padding: 16 -> 14, three chunks
+    (3, 28, 28, 128, 128, 1, "relu", "bias", False),   # the 28x28 ResNet 3x3
+    (1, 28, 28, 32, 192, 1, "silu", None, False),      # one chunk, three channel tiles
+    (3, 28, 28, 256, 256, 1, None, "bias", True),      # the W8A16 conv at a ragged batch
+    (2, 28, 28, 64, 128, 1, "relu", None, True),
+]
+
+
+@pytest.mark.parametrize("case", TILE_CASES)
+def test_nhwc_band_tiles(dev, orc, case):
+    B, H, W, Cin, Cout, p, act, post, int8 = case
+    print(f"[conv band tiles] {case}", flush=True)
+    rng = np.random.default_rng(H * W + Cin + Cout + p)
+    xb = to_bf16(rng.standard_normal((B, H, W, Cin), dtype=np.float32))
+    x = from_bf16(xb)
+    oh, ow = H + 2 * p - 2, W + 2 * p - 2
+    bias = scale = shift = None
+    if int8:
+        q, qs = quantized_conv_weight(orc, rng, Cout, 3, 3, Cin)
+        w = orc.dequantize_affine(q.reshape(-1), qs, None, q.shape, "channel", 0)
+        if post == "bias":
+            bias = rng.normal(0, 0.1, Cout).astype(np.float32)
+        got = K.w8a16_conv2d(dev.upload(xb, tg.bf16), dev.upload(q), dev.upload(qs),
+                             dev.upload(bias) if bias is not None else None, 1, p, act=act).to_host()
+    else:
+        wb = to_bf16((rng.standard_normal((Cout, 3, 3, Cin), dtype=np.float32) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32))
+        w = from_bf16(wb)
+        if post == "bn":
+            scale = rng.uniform(0.5, 1.5, Cout).astype(np.float32)
+            shift = rng.normal(0, 0.1, Cout).astype(np.float32)
+            got = K.conv2d_bn_act(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(scale),
+                                  dev.upload(shift), 1, p, 1, act, layout="nhwc").to_host()
+        else:
+            if post == "bias":
+                bias = rb(rng.normal(0, 0.1, Cout).astype(np.float32))
+            got = K.conv2d(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16),
+                           dev.upload(to_bf16(bias), tg.bf16) if bias is not None else None, 1, p, 1, act,
+                           layout="nhwc").to_host()
+
+    def finish(ref):
+        if post == "bn":
+            ref = ref * scale + shift
+        return ref if act is None else {"relu": orc.relu, "silu": orc.silu, "gelu": orc.gelu}[act](ref)
+
+    assert got.shape == (B, oh, ow, Cout)
+    assert np.all(np.isfinite(from_bf16(got)))
+    check_bf16(got, finish(orc.conv2d_nhwc(x, w, bias, stride=1, padding=p)), str(case))
+
+
 STREAM_CASES = [
     # B, H, W, Cin, Cout, act: 1x1 stride-1 convs with M = B*H*W >= 16384 and
     # C_IN, C_OUT in {64, 128, 256} take the streaming kernel
