@@ -240,11 +240,17 @@ __global__ __launch_bounds__(256) void conv_f32_mfma(const float *__restrict__ x
   }
 }
 
+}  // namespace teeny
+#include "conv_f32_row.hpp"
+namespace teeny {
+
 // Takes an fp32 NCHW conv with groups == 1 whose input fits 32-bit byte
-// offsets and whose staged weight chunk fits LDS; returns false (nothing
-// launched) otherwise.
+// offsets and whose staged weight chunk fits LDS (3x3 stride-1 convs over
+// rows of <= 56 pixels: the row kernel); returns false (nothing launched)
+// otherwise.
 static bool try_conv_f32_mfma(const float *x, const float *w, const float *bias, float *y, const ConvGeo &q,
                               int act, hipStream_t s, const float *oscale = nullptr) {
+  if (try_conv_f32_row(x, w, bias, y, q, act, s, oscale)) return true;
   const int64_t xb = static_cast<int64_t>(q.B) * q.Cin * q.H * q.W * 4;
   const int khw = q.KH * q.KW;
   if (q.G != 1 || xb >= (int64_t{1} << 31) || khw > 128) return false;

@@ -68,6 +68,39 @@ def test_f32_cases(dev, orc, case, layout):
     check_f32(got, ref, f"{case} {layout}")
 
 
+# fp32 NCHW 3x3 stride-1 convs with C_IN % 16 == 0 and W % 4 == 0, W <= 56:
+# the row kernel (one output row x 16 output channels per workgroup)
+ROW_CASES = [
+    # B, Cin, Cout, H, W, pad (h, w), act, bias
+    (2, 32, 40, 12, 12, (1, 1), "relu", True),   # ragged channel tile (40 = 2 x 16 + 8)
+    (1, 16, 16, 8, 4, (0, 0), None, True),       # W = 4, no padding: OW = 2
+    (3, 48, 20, 7, 56, (2, 4), "gelu", False),  # widest padding, OW = 62, Cout % 16 != 0
+    (1, 64, 64, 56, 56, (1, 1), "silu", False),  # the 56 x 56 config without bias
+    (2, 16, 8, 5, 52, (0, 3), None, True),       # H < KH + PH rows, one ragged tile only
+]
+
+
+@pytest.mark.parametrize("case", ROW_CASES)
+def test_f32_nchw_row(dev, orc, case):
+    B, Cin, Cout, H, W, pd, act, with_bias = case
+    print(f"[conv f32 row] {case}", flush=True)
+    rng = np.random.default_rng(Cin * 13 + Cout + W)
+    x = rng.standard_normal((B, Cin, H, W), dtype=np.float32)
+    w = (rng.standard_normal((Cout, Cin, 3, 3), dtype=np.float32) * np.sqrt(2.0 / (Cin * 9))).astype(np.float32)
+    b = rng.normal(0, 0.1, Cout).astype(np.float32) if with_bias else None
+    got = K.conv2d(dev.upload(x), dev.upload(w), dev.upload(b) if with_bias else None, 1, pd, act=act).to_host()
+    ref = orc.conv2d_nchw(x, w, b, padding=pd)
+    if act is not None:
+        ref = getattr(orc, act)(ref)
+    check_f32(got, ref, f"row {case}")
+    # folded BatchNorm through the same kernel (per-channel scale before the shift)
+    sc = rng.normal(1, 0.2, Cout).astype(np.float32)
+    sh = rng.normal(0, 0.3, Cout).astype(np.float32)
+    y = K.conv2d_bn_act(dev.upload(x), dev.upload(w), dev.upload(sc), dev.upload(sh), 1, pd, 1, "relu").to_host()
+    c = orc.conv2d_nchw(x, w, None, padding=pd)
+    check_f32(y, orc.relu(sc[None, :, None, None] * c + sh[None, :, None, None]), f"row+bn {case}")
+
+
 BF16_CASES = [
     # B, Cin, Cout, H, W, KH, KW, stride, pad, act     (path)
     (2, 64, 64, 14, 14, 3, 3, 1, 1, "relu"),   # 3x3 implicit GEMM, 16-byte gather
