@@ -16,11 +16,17 @@ batch 64; 5: the two W8A16 GEMMs and the int8 3x3 conv), each with its own
 roofline object (dominant kernel) and CPU baseline.
 
 Inputs are resident in HBM before any timed region.  Each workload runs W
-warmup steps eagerly, then K steps captured into one HIP graph, replayed once
-untimed and once between two HIP events on the launch stream (the step time).
+warmup steps eagerly, then K steps captured into one HIP graph, replayed
+untimed back to back for at least WARM_MS (60 ms, --warm-ms) of device time,
+then once between two HIP events on the launch stream (the step time).  The warm replays are
+there for the clock: under load the MI355X raises its shader clock over tens
+of milliseconds (measured with s_memtime against s_memrealtime in a causal
+attention kernel: 1.45 GHz after 4 ms of back-to-back launches, 1.64 GHz
+after 13 ms, a settled 1.78-1.81 GHz from 40 ms on), so a short op timed
+right after a few launches would be timed on the ramp.
 Then every op of the step is captured K times over into a graph of its own
-and timed the same way (its average launch duration, used by the roofline
-objects).  Graph replay keeps Python's launch overhead out of the GPU's
+and timed the same way after 10 ms of its own warm replays (its average
+launch duration, used by the roofline objects).  Graph replay keeps Python's launch overhead out of the GPU's
 timeline, as an executor's captured graph would.  Ops whose buffers would fit the 256 MB Infinity Cache
 cycle through 2-4 device copies of their operands, so that repeated launches
 read HBM rather than the previous launch's cached bytes.
@@ -54,6 +60,8 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 FP32_PEAK_TFLOPS = 157.3     # fp32 (vector and matrix)
 CPU_PREFIX = 0.05            # minimum fraction of program ids in a sampled CPU baseline
+WARM_MS = 60.0               # untimed back-to-back replays of a step graph before its timed replay
+OP_WARM_MS = 10.0            # the same before each op's own timed replay (the clock is already up)
 
 
 def log(msg):
@@ -131,16 +139,23 @@ class Ctx:
             for _, fns in ops:
                 fns[i % len(fns)]()
 
-        def replay_ms(enqueue, count):
-            """Captures `count` launches into one HIP graph, replays it once to
-            warm up, then times one replay: ms per launch, free of host
-            launch overhead (a 10-20 us kernel issued from Python otherwise
-            leaves the GPU idle between launches)."""
+        def replay_ms(enqueue, count, warm_ms):
+            """Captures `count` launches into one HIP graph, replays it back to
+            back for at least `warm_ms` of device time (the shader clock
+            settles under sustained load), then times one replay: ms per launch, free
+            of host launch overhead (a 10-20 us kernel issued from Python
+            otherwise leaves the GPU idle between launches)."""
             stream.begin_capture()
             for i in range(count):
                 enqueue(i)
             g = stream.end_capture()
+            t0.record(stream)
             g.launch(stream)
+            t1.record(stream)
+            t1.synchronize()
+            reps = max(1, math.ceil(warm_ms / max(t0.elapsed_ms(t1), 1e-3)))
+            for _ in range(reps):
+                g.launch(stream)
             stream.synchronize()
             t0.record(stream)
             g.launch(stream)
@@ -153,12 +168,13 @@ class Ctx:
         for i in range(warmup):
             step(i)
         dev.synchronize()
-        ms = replay_ms(step, steps)
+        scale = self.args.warm_ms / WARM_MS
+        ms = replay_ms(step, steps, self.args.warm_ms)
         per = {}
         for name, fns in ops:
             if self.marker is not None:
                 self.marker(1)
-            per[name] = replay_ms(lambda i, fns=fns: fns[i % len(fns)](), steps)
+            per[name] = replay_ms(lambda i, fns=fns: fns[i % len(fns)](), steps, OP_WARM_MS * scale)
         if self.marker is not None:
             self.marker(2)
         dev.synchronize()
@@ -790,6 +806,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warm-ms", type=float, default=WARM_MS,
+                    help="device time of untimed graph replays before each timed step replay (ops get "
+                         f"{OP_WARM_MS / WARM_MS:.3g}x of it); 0 for a single warm replay, as counter runs use")
     ap.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--op-markers", action="store_true",

@@ -6,12 +6,15 @@
 //                                      * w[n, ci, kh, kw] + bias[n] )
 //
 // A workgroup owns one output row (b, oh), OW <= 64 pixels as four 16-pixel
-// blocks (one per wave), and 16 output channels.  Per chunk of 16 input
-// channels one LDS-DMA pass stages the KH input rows the row needs (each
-// row 64 floats wide: the data at columns 4 .. 4 + W - 1, zeros around it,
-// so a padding tap reads zero) and the chunk's 16 x 16 x KH x KW weights;
-// four stages, the DMA three chunks ahead of the MFMAs (the config's 64
-// channels are all in flight from the start).
+// blocks, and 16 output channels, with eight waves: wave w takes pixel block
+// w % 4 and half of every chunk's input channels (w / 4), so each SIMD runs
+// two waves (one would leave the barrier and LDS latencies of every chunk
+// exposed); the two halves are summed through LDS at the end.  Per chunk of
+// 16 input channels one LDS-DMA pass stages the KH input rows the row needs
+// (each row 64 floats wide: the data at columns 4 .. 4 + W - 1, zeros around
+// it, so a padding tap reads zero) and the chunk's 16 x 16 x KH x KW
+// weights; four stages, the DMA three chunks ahead of the MFMAs (the
+// config's 64 channels are all in flight from the start).
 // v_mfma_f32_16x16x4_f32 (A 16 x 4: weights, lane l holds A[l % 16][l / 16];
 // B 4 x 16: activations, lane l holds B[l / 16][l % 16]; D: lane l holds
 // D[4 (l / 16) + v][l % 16]) with four accumulator chains per wave (k-steps
@@ -35,16 +38,18 @@ struct F32RowShape {
   static constexpr int WSLOTS = 16 * WROW / 4;
   static constexpr int XINSTR = (XSLOTS + 63) / 64, WINSTR = (WSLOTS + 63) / 64;
   static constexpr int INSTR = XINSTR + WINSTR;
-  static constexpr int DI = (INSTR + 3) / 4;          // DMA instructions per wave per stage
+  static constexpr int NWV = 8;                       // waves
+  static constexpr int DI = (INSTR + NWV - 1) / NWV;  // DMA instructions per wave per stage
   static constexpr int XBYTES = XINSTR * 1024, WBYTES = WINSTR * 1024;
   static constexpr int STAGE = XBYTES + WBYTES;
   static constexpr int NST = 4;
-  static constexpr int LDS = NST * STAGE + 1024;
+  static constexpr int RED = 4 * 64 * 16;             // the second channel half's sums
+  static constexpr int LDS = NST * STAGE + 1024 + RED;
   static_assert((NST - 2) * DI < 16, "vmcnt field");
 };
 
 template <int KH, int KW, int ACT>
-__global__ __launch_bounds__(256) void conv_f32_row_kernel(const float *__restrict__ x, const float *__restrict__ w,
+__global__ __launch_bounds__(512) void conv_f32_row_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                            const float *__restrict__ oscale,
                                                            const float *__restrict__ bias, float *__restrict__ y,
                                                            ConvGeo q, int x_bytes, int w_bytes) {
@@ -53,6 +58,7 @@ __global__ __launch_bounds__(256) void conv_f32_row_kernel(const float *__restri
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, kk = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pb = wv & 3, half = wv >> 2;  // pixel block, channel half
   const int row = blockIdx.x;  // (b, oh)
   const int oh = row % q.OH, b = row / q.OH;
   const int n0 = blockIdx.y * 16;
@@ -66,7 +72,7 @@ __global__ __launch_bounds__(256) void conv_f32_row_kernel(const float *__restri
     const uint32_t buf = smem0 + (ch % S::NST) * S::STAGE;
 #pragma unroll
     for (int rr = 0; rr < S::DI; ++rr) {
-      const int ins = rr * 4 + wv;
+      const int ins = rr * S::NWV + wv;
       int off = kOffNone;
       uint32_t dst = dummy0;
       if (ins < S::XINSTR) {
@@ -89,7 +95,7 @@ __global__ __launch_bounds__(256) void conv_f32_row_kernel(const float *__restri
     }
   };
 
-  const int ow = 16 * wv + r;  // this lane's output pixel (B operand column)
+  const int ow = 16 * pb + r;  // this lane's output pixel (B operand column)
   f32x4 acc[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) acc[a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -102,23 +108,31 @@ __global__ __launch_bounds__(256) void conv_f32_row_kernel(const float *__restri
     dma(ch + S::NST - 1);
     const float *xs = reinterpret_cast<const float *>(smem + (ch % S::NST) * S::STAGE);
     const float *ws = reinterpret_cast<const float *>(smem + (ch % S::NST) * S::STAGE + S::XBYTES);
-    // k-steps (tap, channel group g4): A = w[n0 + r][16 ch + 4 g4 + kk][tap],
-    // B = x[16 ch + 4 g4 + kk][oh + kh][ow + kw]
+    // k-steps (tap, channel group g4 of this wave's half): A = w[n0 + r][16 ch
+    // + 4 g4 + kk][tap], B = x[16 ch + 4 g4 + kk][oh + kh][ow + kw]
 #pragma unroll
     for (int tap = 0; tap < KHW; ++tap) {
       const int kh = tap / KW, kw = tap % KW;
       const int col = 4 + ow * q.SW - q.PW + kw;
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int cl = 4 * g4 + kk;
+      for (int g = 0; g < 2; ++g) {
+        const int cl = 4 * (2 * half + g) + kk;
         const float av = ws[r * S::WROW + cl * KHW + tap];
         const float bv = xs[cl * S::CPLANE + kh * S::RW + col];
-        acc[g4] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[g4], 0, 0, 0);
+        const int a = 2 * (tap & 1) + g;
+        acc[a] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[a], 0, 0, 0);
       }
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
-  const f32x4 sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  f32x4 sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  // the second half's sums through LDS (a region of its own: the trailing
+  // DMA may still land in the stages of other waves)
+  f32x4 *red = reinterpret_cast<f32x4 *>(smem + S::NST * S::STAGE + 1024);
+  if (half == 1) red[pb * 64 + lane] = sum;
+  __syncthreads();
+  if (half == 1) return;
+  sum += red[pb * 64 + lane];
   if (ow >= q.OW) return;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -159,7 +173,7 @@ inline void launch_f32_row_act(const float *x, const float *w, const float *osca
   const int xb = static_cast<int>(static_cast<int64_t>(q.B) * q.Cin * q.H * q.W * 4);
   const int wb = static_cast<int>(static_cast<int64_t>(q.Cout) * q.Cin * 9 * 4);
   const dim3 grid(static_cast<unsigned>(q.B * q.OH), static_cast<unsigned>((q.Cout + 15) / 16));
-  hipLaunchKernelGGL(kern, grid, dim3(256), S::LDS, s, x, w, oscale, bias, y, q, xb, wb);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * S::NWV), S::LDS, s, x, w, oscale, bias, y, q, xb, wb);
 }
 
 inline bool try_conv_f32_row(const float *x, const float *w, const float *bias, float *y, const ConvGeo &q, int act,

@@ -310,7 +310,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
         const int r = 8 * r8 + (lane >> 3), pos = lane & 7;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(c_stg + r * 128 + 16 * pos);
         const int m = m0 + wm * WM + 32 * j + r;
-        const int off = (m < p.M) & (nw < p.N)
+        const int off = ((m < p.M) & (nw < p.N))
                             ? static_cast<int>((static_cast<uint32_t>(m) * static_cast<uint32_t>(p.ldc) +
                                                 static_cast<uint32_t>(nw)) * 2u) + 16 * (pos ^ (r & 7))
                             : kOffNone;
