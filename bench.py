@@ -101,7 +101,7 @@ class Ctx:
         """Marks op boundaries in a profiler's dispatch list with an empty
         launch (n = 0) of the stand-alone example kernel, whose name no op
         uses: one workgroup before each op's own block (its warm and timed
-        graph replays, 2 K launches), two after a workload's last block."""
+        graph replays of K launches each), two after a workload's last block."""
         import ctypes
         lib = self.tg._lib.lib
         mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
