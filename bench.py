@@ -16,17 +16,18 @@ batch 64; 5: the two W8A16 GEMMs and the int8 3x3 conv), each with its own
 roofline object (dominant kernel) and CPU baseline.
 
 Inputs are resident in HBM before any timed region.  Each workload runs W
-warmup steps eagerly, then K steps captured into one HIP graph, replayed
-untimed back to back for at least WARM_MS (60 ms, --warm-ms) of device time,
-then once between two HIP events on the launch stream (the step time).  The warm replays are
-there for the clock: under load the MI355X raises its shader clock over tens
-of milliseconds (measured with s_memtime against s_memrealtime in a causal
-attention kernel: 1.45 GHz after 4 ms of back-to-back launches, 1.64 GHz
-after 13 ms, a settled 1.78-1.81 GHz from 40 ms on), so a short op timed
-right after a few launches would be timed on the ramp.
-Then every op of the step is captured K times over into a graph of its own
-and timed the same way after 10 ms of its own warm replays (its average
-launch duration, used by the roofline objects).  Graph replay keeps Python's launch overhead out of the GPU's
+warmup steps eagerly, then more eager steps for at least WARM_MS (60 ms,
+--warm-ms) of wall time, then K steps captured into one HIP graph, replayed
+once untimed and once between two HIP events on the launch stream (the step
+time).  The time-based warm-up is there for the clock: under load the
+MI355X raises its shader clock over tens of milliseconds (measured with
+s_memtime against s_memrealtime in a causal attention kernel: 1.45 GHz
+after 4 ms of back-to-back launches, 1.64 GHz after 13 ms, a settled
+1.78-1.81 GHz from 40 ms on), so a short op timed right after a few
+launches would be timed on the ramp.  Then every op of the step is captured
+K times over into a graph of its own and timed the same way after 10 ms of
+its own eager launches (its average launch duration, used by the roofline
+objects).  Graph replay keeps Python's launch overhead out of the GPU's
 timeline, as an executor's captured graph would.  Ops whose buffers would fit the 256 MB Infinity Cache
 cycle through 2-4 device copies of their operands, so that repeated launches
 read HBM rather than the previous launch's cached bytes.
@@ -60,8 +61,8 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 FP32_PEAK_TFLOPS = 157.3     # fp32 (vector and matrix)
 CPU_PREFIX = 0.05            # minimum fraction of program ids in a sampled CPU baseline
-WARM_MS = 60.0               # untimed back-to-back replays of a step graph before its timed replay
-OP_WARM_MS = 10.0            # the same before each op's own timed replay (the clock is already up)
+WARM_MS = 60.0               # eager steps before a workload's step graph (clock ramp), ms of wall time
+OP_WARM_MS = 10.0            # eager launches before each op's own graph (the clock is already up)
 
 
 def log(msg):
@@ -100,8 +101,9 @@ class Ctx:
     def _marker_kernel(self):
         """Marks op boundaries in a profiler's dispatch list with an empty
         launch (n = 0) of the stand-alone example kernel, whose name no op
-        uses: one workgroup before each op's own block (its warm and timed
-        graph replays of K launches each), two after a workload's last block."""
+        uses: one workgroup before each op's own block (its eager warm-up
+        launches, then the warm and timed replays of its K-launch graph), two
+        after a workload's last block."""
         import ctypes
         lib = self.tg._lib.lib
         mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
@@ -139,23 +141,16 @@ class Ctx:
             for _, fns in ops:
                 fns[i % len(fns)]()
 
-        def replay_ms(enqueue, count, warm_ms):
-            """Captures `count` launches into one HIP graph, replays it back to
-            back for at least `warm_ms` of device time (the shader clock
-            settles under sustained load), then times one replay: ms per launch, free
-            of host launch overhead (a 10-20 us kernel issued from Python
-            otherwise leaves the GPU idle between launches)."""
+        def replay_ms(enqueue, count):
+            """Captures `count` launches into one HIP graph, replays it once to
+            warm up, then times one replay: ms per launch, free of host
+            launch overhead (a 10-20 us kernel issued from Python otherwise
+            leaves the GPU idle between launches)."""
             stream.begin_capture()
             for i in range(count):
                 enqueue(i)
             g = stream.end_capture()
-            t0.record(stream)
             g.launch(stream)
-            t1.record(stream)
-            t1.synchronize()
-            reps = max(1, math.ceil(warm_ms / max(t0.elapsed_ms(t1), 1e-3)))
-            for _ in range(reps):
-                g.launch(stream)
             stream.synchronize()
             t0.record(stream)
             g.launch(stream)
@@ -164,17 +159,27 @@ class Ctx:
             g.destroy()
             return t0.elapsed_ms(t1) / count
 
+        def warm(fn, ms):
+            """Eager launches of fn(i) for at least `ms` of wall time: the
+            shader clock settles under sustained load."""
+            t_end = time.perf_counter() + ms / 1e3
+            i = 0
+            while i == 0 or time.perf_counter() < t_end:
+                fn(i)
+                i += 1
+            dev.synchronize()
+
         t0, t1 = tg.Event(), tg.Event()
         for i in range(warmup):
             step(i)
-        dev.synchronize()
-        scale = self.args.warm_ms / WARM_MS
-        ms = replay_ms(step, steps, self.args.warm_ms)
+        warm(step, self.args.warm_ms)
+        ms = replay_ms(step, steps)
         per = {}
         for name, fns in ops:
             if self.marker is not None:
                 self.marker(1)
-            per[name] = replay_ms(lambda i, fns=fns: fns[i % len(fns)](), steps, OP_WARM_MS * scale)
+            warm(lambda i, fns=fns: fns[i % len(fns)](), self.args.warm_ms * OP_WARM_MS / WARM_MS)
+            per[name] = replay_ms(lambda i, fns=fns: fns[i % len(fns)](), steps)
         if self.marker is not None:
             self.marker(2)
         dev.synchronize()
@@ -807,8 +812,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--warm-ms", type=float, default=WARM_MS,
-                    help="device time of untimed graph replays before each timed step replay (ops get "
-                         f"{OP_WARM_MS / WARM_MS:.3g}x of it); 0 for a single warm replay, as counter runs use")
+                    help="wall time of eager warm-up steps before each step graph (ops get "
+                         f"{OP_WARM_MS / WARM_MS:.3g}x of it); 0: one step, as the counter runs use")
     ap.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--op-markers", action="store_true",

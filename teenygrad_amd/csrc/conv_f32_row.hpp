@@ -59,7 +59,9 @@ __global__ __launch_bounds__(512) void conv_f32_row_kernel(const float *__restri
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, kk = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pb = wv & 3, half = wv >> 2;  // pixel block, channel half
-  const int row = blockIdx.x;  // (b, oh)
+  // (b, oh): consecutive rows on one XCD (the hardware deals workgroups to
+  // the XCDs round-robin), so that the rows' shared halo comes from its L2
+  const int row = xcd_remap(blockIdx.x, gridDim.x);
   const int oh = row % q.OH, b = row / q.OH;
   const int n0 = blockIdx.y * 16;
   const int nch = q.Cin / 16;
