@@ -10,24 +10,26 @@
 //   silu_backward kernels/teeny-kernels/src/nn/activation/sigmoid.rs:161-210
 //
 // MI355X design: the op moves 2 bytes in and 2 out per bf16 element with a
-// handful of VALU ops, so it is bound by HBM.  Each thread moves UNROLL = 2
-// 16-byte vectors with both loads issued before any math; lanes of a wave
-// touch consecutive 16-byte chunks so every load instruction is one fully
-// coalesced 1 KiB request; results leave through non-temporal stores (the
-// output is not re-read by this kernel).  With ~16 VGPRs the kernel runs at
-// 8 waves per SIMD; a [16384, 4096] bf16 tensor is 16384 workgroups.  This
-// shape (2 vectors per thread, non-temporal stores) measured fastest on
-// MI355X among 1/2/4/8 vectors per thread and temporal/non-temporal
-// loads/stores, at the rate of a plain device copy.  Unaligned pointers or a
-// ragged tail take a scalar kernel.  The backward kernels have the same
-// shape with two input streams: both tensors' vectors are loaded before any
-// math (4 loads of 16 bytes in flight per thread), 6 bytes per bf16 element.
+// handful of VALU ops, so it is bound by HBM.  Each thread moves one 16-byte
+// vector; lanes of a wave touch consecutive 16-byte chunks so every load
+// instruction is one fully coalesced 1 KiB request; both the loads and the
+// stores are non-temporal (the data streams through once).  With ~16 VGPRs
+// the kernel runs at 8 waves per SIMD; a [16384, 4096] bf16 tensor is 32768
+// workgroups.  Measured on MI355X at the settled clock over rotating 128 MiB
+// buffers (GELU, [16384, 4096] bf16): one vector per thread with
+// non-temporal loads 42.3 us (0.79 of 8 TB/s), against 45.1 us for two
+// vectors with temporal loads, 43.4-43.5 us for either change alone, 46.5 us
+// for four vectors and 46-47 us for persistent grid-stride loops; a device
+// copy (hipMemcpyAsync) takes 50.9 us.  Unaligned pointers or a ragged tail
+// take a scalar kernel.  The backward kernels have the same shape with two
+// input streams, 6 bytes per bf16 element (GELU gradient 69.9 -> 62.5 us,
+// 0.81 of 8 TB/s).
 #include "common.hpp"
 
 namespace teeny {
 
 constexpr int kActThreads = 256;
-constexpr int kActUnroll = 2;
+constexpr int kActUnroll = 1;
 
 template <typename T, int ACT>
 __device__ __forceinline__ T act_one(T v) {
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(kActThreads) void act_vec_kernel(const T *x, T *y, 
 #pragma unroll
   for (int u = 0; u < kActUnroll; ++u) {
     int64_t v = base + u * kActThreads;
-    if (v < n_vec) r[u] = reinterpret_cast<const raw_t *>(x)[v];
+    if (v < n_vec) r[u] = __builtin_nontemporal_load(reinterpret_cast<const raw_t *>(x) + v);
   }
 #pragma unroll
   for (int u = 0; u < kActUnroll; ++u) {
@@ -161,8 +163,8 @@ __global__ __launch_bounds__(kActThreads) void act_bwd_vec_kernel(const T *dy, c
   for (int u = 0; u < kActUnroll; ++u) {
     const int64_t i = base + u * kActThreads;
     if (i < n_vec) {
-      rd[u] = reinterpret_cast<const u32x4 *>(dy)[i];
-      rv[u] = reinterpret_cast<const u32x4 *>(v)[i];
+      rd[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dy) + i);
+      rv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(v) + i);
     }
   }
 #pragma unroll
