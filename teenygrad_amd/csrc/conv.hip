@@ -770,27 +770,35 @@ struct DxPhaseTable {
   int64_t off[kMaxDxPhases];         // element offset of phase (a, c)'s weights
 };
 // w [C_OUT, KH, KW, C_IN] -> per phase (a, c): wp[ci][t'][s'][co] =
-// w[co][k0h + SH (T - 1 - t')][k0w + SW (S - 1 - s')][ci], one element per
-// thread (every weight belongs to exactly one phase).
+// w[co][k0h + SH (T - 1 - t')][k0w + SW (S - 1 - s')][ci], one thread per
+// element of wp (consecutive threads write consecutive co: coalesced; the
+// gathered reads hit L2).  Every weight belongs to exactly one phase, so wp
+// has as many elements as w.
 __global__ __launch_bounds__(256) void conv_dx_phase_weights(const bf16 *__restrict__ w, bf16 *__restrict__ wp,
                                                              int Cout, int KH, int KW, int Cin, DxPhaseTable tb) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t total = static_cast<int64_t>(Cout) * KH * KW * Cin;
   if (t >= total) return;
-  const int ci = static_cast<int>(t % Cin);
-  const int kw = static_cast<int>((t / Cin) % KW);
-  const int kh = static_cast<int>((t / (static_cast<int64_t>(Cin) * KW)) % KH);
-  const int co = static_cast<int>(t / (static_cast<int64_t>(Cin) * KW * KH));
-  // the phase whose residue kh belongs to: a with (a + PH) % SH == kh % SH
-  // (found by search: SH, SW <= 4)
+  // the phase (a, c) whose block [off, off + Cin T S Cout) holds t
   int a = 0, c = 0;
   for (int i = 0; i < tb.SH; ++i)
-    if (tb.T[i] > 0 && tb.k0h[i] == kh % tb.SH) a = i;
-  for (int i = 0; i < tb.SW; ++i)
-    if (tb.S[i] > 0 && tb.k0w[i] == kw % tb.SW) c = i;
+    for (int j = 0; j < tb.SW; ++j) {
+      const int64_t n = static_cast<int64_t>(Cin) * tb.T[i] * tb.S[j] * Cout;
+      if (n > 0 && t >= tb.off[i * tb.SW + j] && t < tb.off[i * tb.SW + j] + n) {
+        a = i;
+        c = j;
+      }
+    }
   const int T = tb.T[a], S = tb.S[c];
-  const int tp = T - 1 - (kh - tb.k0h[a]) / tb.SH, sp = S - 1 - (kw - tb.k0w[c]) / tb.SW;
-  wp[tb.off[a * tb.SW + c] + ((static_cast<int64_t>(ci) * T + tp) * S + sp) * Cout + co] = w[t];
+  int64_t r = t - tb.off[a * tb.SW + c];
+  const int co = static_cast<int>(r % Cout);
+  r /= Cout;
+  const int sp = static_cast<int>(r % S);
+  r /= S;
+  const int tp = static_cast<int>(r % T);
+  const int ci = static_cast<int>(r / T);
+  const int kh = tb.k0h[a] + tb.SH * (T - 1 - tp), kw = tb.k0w[c] + tb.SW * (S - 1 - sp);
+  wp[t] = w[((static_cast<int64_t>(co) * KH + kh) * KW + kw) * Cin + ci];
 }
 // Zeroes the dx pixels of the phases with no taps (mask bit a * SW + c), one
 // 16-byte chunk (8 channels) per thread.
