@@ -1121,8 +1121,19 @@ __global__ __launch_bounds__(256) void conv_dw_reduce(const float *__restrict__ 
                                                       int splits, int64_t mn) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= mn) return;
-  f32x4 s = *reinterpret_cast<const f32x4 *>(part + i);
-  for (int k = 1; k < splits; ++k) s += *reinterpret_cast<const f32x4 *>(part + k * mn + i);
+  auto at = [&](int k) { return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(part + k * mn + i)); };
+  f32x4 s = at(0);
+  int k = 1;
+  // eight splits' loads in flight, added in split order (the sum is the
+  // same, bit for bit, as one load and add at a time)
+  for (; k + 8 <= splits; k += 8) {
+    f32x4 t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = at(k + u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += t[u];
+  }
+  for (; k < splits; ++k) s += at(k);
   bf16x4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(s[e]);
