@@ -396,6 +396,31 @@ __global__ __launch_bounds__(256) void s2d_kernel(const bf16 *__restrict__ x, bf
     const int u = static_cast<int>((t / Ws) % Hs);
     const int b = static_cast<int>(t / (static_cast<int64_t>(Ws) * Hs));
     bf16 *dst = xs + t * C2;
+    if (C == 3 && C2 == 16) {
+      // the RGB stem: the four sub-pixels' 3 channels each, all twelve loads
+      // issued before any use (clamped addresses, zeros selected for the
+      // padding), then two 16-byte stores
+      float val[12];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int ih = 2 * u + (q4 >> 1) - PH, iw = 2 * v + (q4 & 1) - PW;
+        const bool ok = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        const int64_t base = ((static_cast<int64_t>(b) * H + (ok ? ih : 0)) * W + (ok ? iw : 0)) * 3;
+#pragma unroll
+        for (int c3 = 0; c3 < 3; ++c3) {
+          const float xv = static_cast<float>(x[base + c3]);
+          val[3 * q4 + c3] = ok ? xv : 0.0f;
+        }
+      }
+      bf16 e[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) e[k] = static_cast<bf16>(k < 12 ? val[k] : 0.0f);
+      u32x4 pk[2];
+      __builtin_memcpy(pk, e, 32);
+      reinterpret_cast<u32x4 *>(dst)[0] = pk[0];
+      reinterpret_cast<u32x4 *>(dst)[1] = pk[1];
+      return;
+    }
     int q = 0, c = 0;  // sub-pixel and channel of output channel c0 + k
     for (int c0 = 0; c0 < C2; c0 += 8) {
       bf16 e[8];
