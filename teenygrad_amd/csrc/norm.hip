@@ -19,10 +19,12 @@
 // workgroup) and 4 vectors per lane, which keeps enough 16-byte loads in
 // flight to stream at about the chip's copy rate; gamma/beta (L2-resident,
 // 8 KiB) are loaded right after x, ahead of the reductions.  Outputs use
-// non-temporal stores; x keeps temporal loads: non-temporal ones made a
-// LayerNorm on cold data 2 % faster (47.9 -> 46.8 us) but the chain of
-// LayerNorm, GELU, SiLU and RMSNorm over one X 2 % slower (the RMSNorm
-// re-reads X, part of it from the Infinity Cache).  Longer
+// non-temporal stores.  RMSNorm reads x by non-temporal loads; LayerNorm
+// keeps temporal ones: non-temporal loads made a LayerNorm on cold data 2 %
+// faster (47.9 -> 46.8 us) but the chain of LayerNorm, GELU, SiLU and
+// RMSNorm over one X 2 % slower (the RMSNorm re-reads X, part of it from the
+// Infinity Cache), while in RMSNorm alone they take the chain from 6281 to
+// 6370 GB/s.  Longer
 // rows, unaligned pointers or N % VEC != 0 take a multi-pass kernel with the
 // reference's pass structure.
 #include "common.hpp"
@@ -55,7 +57,8 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
   for (int j = 0; j < VPL; ++j) {
     const int col = ((part * VPL + j) * 64 + lane) * VEC;
     valid[j] = row_ok && col < N;
-    raw[j] = valid[j] ? *reinterpret_cast<const u32x4 *>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(xr + col);
+    raw[j] = valid[j] ? (RMS ? __builtin_nontemporal_load(src) : *src) : u32x4{0u, 0u, 0u, 0u};
   }
   // gamma / beta are issued right behind x, so their (L2) latency overlaps
   // the row's reductions instead of following them
