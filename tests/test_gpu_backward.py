@@ -249,6 +249,10 @@ MFMA_DW_CASES = [  # bf16 NHWC, groups 1: B, H, Cin, Cout, K, stride, pad
     (2, 15, 24, 72, 3, 1, 1),     # ragged: N = 216, C_OUT = 72, pixels 450
     (1, 11, 40, 200, 5, 2, 2),    # 5x5 stride 2, N = 1000
     (2, 30, 8, 64, 7, 2, 3),
+    # few tiles over many pixels: with a workspace the pixel range splits 20
+    # and 10 ways (the split sum loads eight partials at a time, then a tail)
+    (8, 28, 64, 64, 3, 1, 1),
+    (16, 14, 32, 32, 3, 1, 1),
 ]
 
 
