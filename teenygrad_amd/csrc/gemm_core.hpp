@@ -707,7 +707,8 @@ inline int64_t tiles_of(const GemmParams &p, int bm, int bn) {
 // 2048 and 4608) are split, towards two workgroups per CU, with at most
 // four splits (the fp32 partials cost 8 * S * M * N bytes of extra
 // traffic).  Measured on MI355X: at 196 tiles (stage 3) splitting does not
-// pay.
+// pay; the 7x7 3x3 512 -> 512 layers (K = 4608) take 36 us with four
+// splits against 44, 41, 43 and 44 us with 2, 3, 6 and 8.
 inline int splitk_factor(const GemmParams &p, int bm, int bn, int bk) {
   const int64_t tiles = tiles_of(p, bm, bn);
   const int n_k = (p.K + bk - 1) / bk;
