@@ -784,7 +784,10 @@ inline void launch_persist_default(const GemmParams &p, hipStream_t s);
 //    prefetch, so the few k-tiles still overlap loads with MFMAs;
 //  * grids of 128 x 128 tiles that leave CUs idle and do not split along K:
 //    128 x 64 x 64 (twice the workgroups);
-//  * otherwise 128 x 128 x 64, split along K when badly under-filled.
+//  * otherwise 128 x 128 x 64, split along K when badly under-filled (the
+//    int8 3x3 conv 32 x 256 x 28 x 28 -> 256, 392 tiles: 48.7 us, against
+//    54.4 us for 128 x 128 x 32 with the two-tile prefetch and 70 us for
+//    128 x 64 x 64).
 enum GemmTiles { kTilesPersist, kTilesStream, kTilesBig, kTiles128x64, kTiles64x64, kTiles128x128Short, kTiles128x64Deep, kTiles128x128 };
 
 template <bool INT8B, int AMODE>
