@@ -8,7 +8,7 @@
 // bound by HBM traffic, and a tiled GEMM's per-tile prologue (first loads)
 // and epilogue stretch it to about twice the copy time.  Here each
 // workgroup stages all of B (N x K bf16, at most 64 KiB) and the per-column
-// scale / bias in LDS once; then each of its four waves walks its own
+// scale / bias in LDS once; then each of its waves walks its own
 // sequence of 32-row blocks of A without further barriers:
 //   * a block's rows arrive by LDS DMA, 1 KiB of consecutive bytes per
 //     instruction (16-byte chunk k of row r lands at position k ^ (r % 8),
@@ -32,8 +32,27 @@
 
 namespace teeny {
 
+// Waves per workgroup.  A wave keeps one 32-row block of A in flight while
+// it computes the previous one, and at these sizes the layer is bound by the
+// bytes in flight per CU (about 16 KiB per wave against HBM latency), so a
+// workgroup takes as many waves as its LDS holds beside B (one 32 x K A
+// slice and one 4 KiB output slice per wave) and as the registers allow (an
+// estimate of N/2 accumulator, K/4 fragment and 32 other registers per lane,
+// against 512 per SIMD lane).  Measured on MI355X against four-wave
+// workgroups, the stage-1 1x1 convs of ResNet-50 at batch 64: 64 -> 64
+// 11.4 -> 10.3 us, 256 -> 64 25.8 -> 25.3 us, 64 -> 256 26-28 -> 25-29 us
+// (eight waves either way; the 53-conv step 1.501 -> 1.485 ms).  The
+// gain is small: bytes in flight are not the main limit of these layers.
+constexpr int stream_waves(int K, int N) {
+  const int by_lds = (160 * 1024 - N * (K + 8) * 2 - 2 * N * 4) / (32 * K * 2 + 32 * 64 * 2);
+  const int by_regs = 4 * (512 / (N / 2 + K / 4 + 32));
+  const int w = by_lds < by_regs ? by_lds : by_regs;
+  return w < 16 ? w : 16;
+}
+
 template <int K, int N>
-__global__ __launch_bounds__(256, 2) void gemm_stream_kernel(GemmParams p) {
+__global__ __launch_bounds__(64 * stream_waves(K, N), 1) void gemm_stream_kernel(GemmParams p) {
+  constexpr int WV = stream_waves(K, N);
   constexpr int KS = K / 16;         // MFMA k-steps
   constexpr int NB = N / 32;         // 32-column output blocks
   constexpr int KP = K + 8;          // LDS pitch of a B row (elements): 16-byte reads of 8 rows hit disjoint banks
@@ -45,7 +64,7 @@ __global__ __launch_bounds__(256, 2) void gemm_stream_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) bf16 bs[N * KP];
   __shared__ __attribute__((aligned(16))) float cmul[N];
   __shared__ __attribute__((aligned(16))) float cadd[N];
-  __shared__ __attribute__((aligned(16))) char stg[4 * (A_STG + C_STG)];
+  __shared__ __attribute__((aligned(16))) char stg[WV * (A_STG + C_STG)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, c = lane & 31;
@@ -55,8 +74,8 @@ __global__ __launch_bounds__(256, 2) void gemm_stream_kernel(GemmParams p) {
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds_address(a_stg));
 
   const int nblk = (p.M + 31) / 32;
-  const int stride = static_cast<int>(gridDim.x) * 4;
-  int blk = static_cast<int>(blockIdx.x) * 4 + w;
+  const int stride = static_cast<int>(gridDim.x) * WV;
+  int blk = static_cast<int>(blockIdx.x) * WV + w;
   const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(p.A, p.a_bytes);
   const __amdgpu_buffer_rsrc_t c_rsrc = buffer_rsrc(p.C, static_cast<int>((static_cast<int64_t>(p.M - 1) * p.ldc + N) * 2));
   // DMA of block b: instruction i, lane j fills LDS chunk 64 i + j = row r,
@@ -78,12 +97,12 @@ __global__ __launch_bounds__(256, 2) void gemm_stream_kernel(GemmParams p) {
   // ── prologue: B and the epilogue coefficients into LDS ──────────────
   constexpr int CPR = K / 8;  // 16-byte chunks per B row
   const bf16 *B = static_cast<const bf16 *>(p.B);
-  for (int i = tid; i < N * CPR; i += 256) {
+  for (int i = tid; i < N * CPR; i += 64 * WV) {
     const int n = i / CPR, j = i % CPR;
     *reinterpret_cast<u32x4 *>(bs + n * KP + 8 * j) =
         *reinterpret_cast<const u32x4 *>(B + static_cast<int64_t>(n) * p.ldb + 8 * j);
   }
-  for (int n = tid; n < N; n += 256) {
+  for (int n = tid; n < N; n += 64 * WV) {
     float m = 1.0f, a = 0.0f;
     if (p.scale != nullptr) m = p.scale[n];
     if (p.bias != nullptr) a = p.bias[n];
@@ -219,6 +238,7 @@ inline bool stream_gemm_fits(const GemmParams &p) {
 
 template <int K, int N>
 inline void launch_stream_kn(const GemmParams &p, hipStream_t s) {
+  constexpr int WV = stream_waves(K, N);
   // resident workgroups per CU, cached per device ordinal (relaxed atomics:
   // racing threads compute and store the same value)
   static std::atomic<int> occupancy[64];
@@ -226,7 +246,7 @@ inline void launch_stream_kn(const GemmParams &p, hipStream_t s) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = -1;
   int per_cu = dev >= 0 ? occupancy[dev].load(std::memory_order_relaxed) : 0;
   if (per_cu <= 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm_stream_kernel<K, N>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm_stream_kernel<K, N>, 64 * WV, 0) != hipSuccess ||
         per_cu < 1)
       per_cu = 1;
     if (dev >= 0) occupancy[dev].store(per_cu, std::memory_order_relaxed);
@@ -234,10 +254,10 @@ inline void launch_stream_kn(const GemmParams &p, hipStream_t s) {
   // Every wave walks the same number of blocks (the last round of a
   // ragged split would run a small fraction of the waves alone).
   const int64_t nblk = (p.M + 31) / 32;
-  const int64_t slots = static_cast<int64_t>(per_cu) * device_cu_count() * 4;
+  const int64_t slots = static_cast<int64_t>(per_cu) * device_cu_count() * WV;
   const int64_t per_wave = (nblk + slots - 1) / slots;
-  const int64_t grid = ((nblk + per_wave - 1) / per_wave + 3) / 4;
-  hipLaunchKernelGGL((gemm_stream_kernel<K, N>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, p);
+  const int64_t grid = ((nblk + per_wave - 1) / per_wave + WV - 1) / WV;
+  hipLaunchKernelGGL((gemm_stream_kernel<K, N>), dim3(static_cast<unsigned>(grid)), dim3(64 * WV), 0, s, p);
 }
 
 inline void launch_stream_gemm(const GemmParams &p, hipStream_t s) {
