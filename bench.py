@@ -307,11 +307,47 @@ def bench_norm_act(ctx):
         cpu = cpu_entry(round(step_bytes / cs / 1e9, 2), "GB/s", cs,
                         "the full step (6 ops on [16384, 4096]) in fp32 on the bf16-rounded inputs; bytes "
                         "counted as bf16 like the GPU line", value)
+    # the measured HBM traffic of one step (rocprofv3 FETCH_SIZE + WRITE_SIZE
+    # per op, scaled by a copy of known size), when every op has a figure
+    traffic = [load_traffic("norm_act", k) for k in bytes_of]
+    hbm_step = sum(traffic) if all(t is not None for t in traffic) else None
     return {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
             "config": {"workload": "norm_act_chain: X[16384,4096] bf16 -> LayerNorm -> GELU-tanh, SiLU; "
                                    "RMSNorm -> GELU-tanh, SiLU (fp32 stats)",
-                       "M": NORM_M, "N": NORM_N, "ops_per_step": 6, "bytes_per_step": step_bytes},
+                       "M": NORM_M, "N": NORM_N, "ops_per_step": 6, "bytes_per_step": step_bytes,
+                       "value_counts": "algorithmic bytes / step time; each GELU/SiLU reads the tensor the "
+                                       "norm before it has just written, part of it from the 256 MB Infinity "
+                                       "Cache, so the step value is not a pure HBM rate (the per-op roofline "
+                                       "entries time each op on rotated, cold operands)",
+                       "hbm_bytes_per_step": hbm_step,
+                       "hbm_GBs": round(hbm_step / (ms * 1e-3) / 1e9, 1) if hbm_step else None},
             "roofline": roof, "cpu_baseline": cpu, "ops": opsd}
+
+
+COPY_BYTES = 128 << 20
+
+
+def copy_ceiling(ctx):
+    """The achievable HBM rate next to the 8 TB/s datasheet peak: a plain
+    device-to-device hipMemcpyAsync of 128 MiB (128 MiB read + 128 MiB
+    written), over four rotating source/destination pairs so that no copy
+    finds its source in the Infinity Cache, timed like every op here."""
+    tg, stream = ctx.tg, ctx.stream
+    R = 4
+    src = [tg.Buffer(tg.i8, (COPY_BYTES,)) for _ in range(R)]
+    dst = [tg.Buffer(tg.i8, (COPY_BYTES,)) for _ in range(R)]
+    for b in src:
+        b.zero_(stream)
+    lib = tg._lib.lib
+    fns = [lambda r=r: tg.check(lib.teeny_hip_memcpy_d2d(dst[r].ptr, src[r].ptr, COPY_BYTES, stream.handle))
+           for r in range(R)]
+    _, per = ctx.measure([("d2d_copy", fns)])
+    ms = per["d2d_copy"]
+    moved = 2 * COPY_BYTES
+    gbs = moved / (ms * 1e-3) / 1e9
+    return {"GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "avg_us": round(ms * 1e3, 2),
+            "bytes_per_copy": moved, "how": "hipMemcpyAsync device-to-device, 128 MiB, 4 rotating buffer pairs, "
+                                           "graph-replayed; bytes = read + written"}
 
 
 def bench_act_backward(ctx):
@@ -456,10 +492,24 @@ def bench_resnet(ctx):
            for name, x, w, b, y, s, p, relu, _, _ in bufs]
     ms, per = ctx.measure(ops)
     value = flops / (ms * 1e-3) / 1e12
+    # each layer's own floor: the longer of its MFMA time at the bf16 peak and
+    # its algorithmic bytes at the HBM peak; the stack's floor is their sum
     by_layer = {}
+    floor_sum = 0.0
     for bb in bufs:
-        n, f = bb[0], bb[8]
-        by_layer[n] = {"us": round(per[n] * 1e3, 1), "TFLOP/s": round(f / (per[n] * 1e-3) / 1e12, 1)}
+        n, f, nb = bb[0], bb[8], bb[9]
+        t_mfma, t_hbm = f / (BF16_PEAK_TFLOPS * 1e12) * 1e6, nb / (HBM_PEAK_GBS * 1e9) * 1e6
+        floor_us = max(t_mfma, t_hbm)
+        floor_sum += floor_us
+        by_layer[n] = {"us": round(per[n] * 1e3, 1), "TFLOP/s": round(f / (per[n] * 1e-3) / 1e12, 1),
+                       "bound": "mfma" if t_mfma >= t_hbm else "hbm", "floor_us": round(floor_us, 2),
+                       "frac_of_floor": round(floor_us / (per[n] * 1e3), 4)}
+    kernel_sum_us = sum(per.values()) * 1e3
+    stack = {"floor_us": round(floor_sum, 1), "step_us": round(ms * 1e3, 1),
+             "frac_of_floor": round(floor_sum / (ms * 1e3), 4), "kernel_sum_us": round(kernel_sum_us, 1),
+             "launch_gap_us": round(ms * 1e3 - kernel_sum_us, 1),
+             "how": "floor = sum over layers of max(FLOP / 2.5 PFLOP/s, algorithmic bytes / 8 TB/s); "
+                    "kernel_sum = the layers timed alone; launch_gap = step - kernel_sum"}
     dom = max(per, key=per.get)
     fdom, bdom = [(bb[8], bb[9]) for bb in bufs if bb[0] == dom][0]
     cpu = None
@@ -485,7 +535,9 @@ def bench_resnet(ctx):
     return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
             "config": {"workload": "resnet50 53 convs bf16 NHWC batch 64 224x224, BN folded to bias, ReLU fused",
                        "flop_per_step": flops, "bytes_per_step": total_bytes, "workspace_bytes": ws},
-            "roofline": roofline_flops("resnet50_convs", dom, fdom, per[dom], BF16_PEAK_TFLOPS, bdom),
+            "roofline": dict(roofline_flops("resnet50_convs", dom, fdom, per[dom], BF16_PEAK_TFLOPS, bdom),
+                             layer_bound=by_layer[dom]["bound"], layer_floor_us=by_layer[dom]["floor_us"],
+                             frac_of_layer_floor=by_layer[dom]["frac_of_floor"], stack=stack),
             "layers": by_layer, "cpu_baseline": cpu}
 
 
@@ -855,6 +907,8 @@ def main():
                 f"in {time.perf_counter() - c0:.1f} s")
         res = dict(configs["cfg2"])
         res["configs"] = configs
+        res["copy_ceiling"] = copy_ceiling(ctx)
+        log(f"[bench] copy ceiling: {res['copy_ceiling']['GB/s']} GB/s")
     else:
         res = WORKLOADS[args.workload](ctx)
     line = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,

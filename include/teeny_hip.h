@@ -630,8 +630,10 @@ teeny_status teeny_checkpoint_read(teeny_checkpoint ckpt, int64_t index, void *d
  * entries.  Other schemes are TEENY_ERR_UNSUPPORTED (read the tensors and use
  * teeny_dequantize_affine).  _shape reports N and K; _load copies the int8
  * weights to qweight [N, K] and N fp32 scales (a per-tensor scale repeated)
- * to scale, both device buffers, ready for teeny_w8a16_linear_forward
- * (conv weights [C_OUT, KH, KW, C_IN] for teeny_w8a16_conv2d_forward). */
+ * to scale, both device buffers, ready for teeny_w8a16_linear_forward.  A
+ * rank-4 weight is a conv weight stored in the reference's order [C_OUT,
+ * C_IN/G, KH, KW] (conv2d.rs:43-156); _load repacks it to [C_OUT, KH, KW,
+ * C_IN/G], the layout teeny_w8a16_conv2d_forward reads. */
 teeny_status teeny_checkpoint_w8a16_shape(teeny_checkpoint ckpt, const char *weight_name, int64_t *N,
                                           int64_t *K);
 teeny_status teeny_checkpoint_load_w8a16(teeny_checkpoint ckpt, const char *weight_name, int8_t *qweight,

@@ -110,11 +110,15 @@ class Checkpoint:
         return buf
 
     def load_w8a16(self, weight_name: str, stream: Optional[Stream] = None) -> Tuple[Buffer, Buffer]:
-        """(qweight int8 in the weight's own shape, scale fp32 [N]) on the
-        device, for w8a16_linear ([N, K]) or w8a16_conv2d ([C_OUT, KH, KW, C_IN])."""
+        """(qweight int8, scale fp32 [N]) on the device, for w8a16_linear
+        ([N, K], the file's own shape) or w8a16_conv2d: a rank-4 conv weight
+        is stored in the reference's order [C_OUT, C_IN/G, KH, KW] and comes
+        back repacked as [C_OUT, KH, KW, C_IN/G]."""
         n, k = ctypes.c_int64(), ctypes.c_int64()
         check(lib.teeny_checkpoint_w8a16_shape(self.handle, weight_name.encode(), ctypes.byref(n), ctypes.byref(k)))
-        shape = self._entry(weight_name)["shape"]
+        shape = tuple(self._entry(weight_name)["shape"])
+        if len(shape) == 4:
+            shape = (shape[0], shape[2], shape[3], shape[1])
         q = Buffer(i8, shape)
         s = Buffer(f32, (n.value,))
         check(lib.teeny_checkpoint_load_w8a16(self.handle, weight_name.encode(), q.ptr, s.ptr, n.value, k.value,
@@ -128,6 +132,12 @@ class Checkpoint:
         sch = self.quant_scheme()
         if sch is None or sch["type"] != "int" or sch["num_bits"] != 8 or sch["format"] != "int-quantized":
             raise ValueError(f"{weight_name}: not an 8-bit int-quantized compressed-tensors checkpoint")
+        # channel / group strategies must name their axis (and group the
+        # group size), as granularity_from_config requires (validate.rs:94-103)
+        if sch["strategy"] in ("channel", "group") and sch["axis"] < 0:
+            raise ValueError(f"{weight_name}: strategy '{sch['strategy']}' without an axis is ambiguous")
+        if sch["strategy"] == "group" and not sch["group_size"]:
+            raise ValueError(f"{weight_name}: strategy 'group' without a group_size")
         shape = self._entry(weight_name)["shape"]
         q = self.to_device(weight_name, i8, stream)
         s = self.to_device(weight_name + "_scale", f32, stream)

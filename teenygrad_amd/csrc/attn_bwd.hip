@@ -674,6 +674,12 @@ teeny_status teeny_attention_backward_workspace_size(int64_t batch, int64_t q_he
   *bytes = 0;
   TEENY_REQUIRE(batch >= 0 && q_heads >= 0 && n_ctx_q >= 0, TEENY_ERR_SHAPE_MISMATCH,
                 "attention_backward_workspace_size: negative size");
+  // the limits the backward itself enforces: B*H <= 65535 and n_ctx_q < 2^31,
+  // so the product below is at most 2^47 and cannot overflow
+  TEENY_REQUIRE(q_heads == 0 || batch <= 65535 / q_heads, TEENY_ERR_SHAPE_MISMATCH,
+                "attention_backward_workspace_size: batch * q_heads exceeds 65535");
+  TEENY_REQUIRE(n_ctx_q <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                "attention_backward_workspace_size: n_ctx_q exceeds 2^31 - 1");
   *bytes = static_cast<size_t>(batch * q_heads * n_ctx_q) * sizeof(float);
   return TEENY_OK;
 }

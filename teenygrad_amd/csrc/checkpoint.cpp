@@ -176,6 +176,9 @@ static teeny_status w8a16_layer(Checkpoint *c, const char *weight_name, const st
                 nm + ": scheme is " + q.type + std::to_string(q.num_bits) + " '" + q.format +
                     "'; W8A16 needs 8-bit int-quantized");
   TEENY_REQUIRE(q.symmetric, TEENY_ERR_UNSUPPORTED, nm + ": asymmetric scheme (zero points): dequantize instead");
+  // a channel or group strategy names its axis (validate.rs:94-103)
+  TEENY_REQUIRE(q.strategy == "tensor" || q.axis >= 0, TEENY_ERR_INVALID_ARGUMENT,
+                nm + ": strategy '" + q.strategy + "' without an axis is ambiguous");
   TEENY_REQUIRE(q.strategy == "tensor" || (q.strategy == "channel" && q.axis == 0), TEENY_ERR_UNSUPPORTED,
                 nm + ": strategy '" + q.strategy + "' (axis " + std::to_string(q.axis) +
                     "): W8A16 takes per-output-channel (axis 0) or per-tensor scales; dequantize instead");
@@ -184,6 +187,10 @@ static teeny_status w8a16_layer(Checkpoint *c, const char *weight_name, const st
   *w = c->file.find(wn);
   *s = c->file.find(wn + "_scale");
   TEENY_REQUIRE(*w != nullptr, TEENY_ERR_NOT_FOUND, nm + ": no tensor " + wn);
+  // a symmetric scheme has an implicit zero point of 0 and omits the tensor
+  // (format.rs:25-26); one present contradicts the scheme
+  TEENY_REQUIRE(c->file.find(wn + "_zero_point") == nullptr, TEENY_ERR_INVALID_ARGUMENT,
+                nm + ": " + wn + "_zero_point present under a symmetric scheme");
   TEENY_REQUIRE(*s != nullptr, TEENY_ERR_NOT_FOUND, nm + ": no tensor " + wn + "_scale");
   TEENY_REQUIRE((*w)->dtype == st::DType::I8 && (*w)->shape.size() >= 2, TEENY_ERR_UNSUPPORTED_DTYPE,
                 nm + ": " + wn + " must be I8 of rank >= 2, is " + (*w)->dtype_name);
@@ -226,7 +233,24 @@ teeny_status teeny_checkpoint_load_w8a16(teeny_checkpoint ckpt, const char *weig
   if (N == 0) return TEENY_OK;
   TEENY_REQUIRE(qweight != nullptr && scale != nullptr, TEENY_ERR_NULL_POINTER, "checkpoint_load_w8a16: qweight/scale");
   hipStream_t hs = static_cast<hipStream_t>(stream);
-  st = copy_out(c->file.data(*w), qweight, static_cast<size_t>(w->end - w->begin), 1, hs);
+  if (w->shape.size() == 4) {
+    // A conv weight: teeny-quant stores the tensor in the reference's own
+    // order [C_OUT, C_IN/G, KH, KW] (conv2d.rs:43-156); the W8A16 conv takes
+    // [C_OUT, KH, KW, C_IN/G] (K = (kh, kw, ci) contiguous per channel).  The
+    // per-output-channel scales are unaffected by the repack.
+    const int64_t ci = w->shape[1], kh = w->shape[2], kw = w->shape[3];
+    const int8_t *src = reinterpret_cast<const int8_t *>(c->file.data(*w));
+    std::vector<int8_t> packed(static_cast<size_t>(N * K));
+    for (int64_t o = 0; o < N; ++o)
+      for (int64_t c_ = 0; c_ < ci; ++c_)
+        for (int64_t y = 0; y < kh; ++y)
+          for (int64_t x = 0; x < kw; ++x)
+            packed[static_cast<size_t>(((o * kh + y) * kw + x) * ci + c_)] =
+                src[((o * ci + c_) * kh + y) * kw + x];
+    st = copy_out(packed.data(), qweight, packed.size(), 1, hs);
+  } else {
+    st = copy_out(c->file.data(*w), qweight, static_cast<size_t>(w->end - w->begin), 1, hs);
+  }
   if (st != TEENY_OK) return st;
   if (s->numel() == N) return copy_out(c->file.data(*s), scale, static_cast<size_t>(N) * 4, 1, hs);
   // per-tensor: the one scale for every output channel

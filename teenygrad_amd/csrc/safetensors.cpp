@@ -452,7 +452,14 @@ bool File::parse(std::string *err) {
     }
     c.num_bits = static_cast<int>(nb);
     if (const Json *v = w->get("type"); v != nullptr && v->kind == Json::String) c.type = v->str;
-    if (const Json *v = w->get("symmetric"); v != nullptr && v->kind == Json::Bool) c.symmetric = v->b;
+    // WeightsConfig.symmetric is a required bool (format.rs:52-70): a file
+    // without it does not state its zero points, so it is refused
+    if (const Json *v = w->get("symmetric"); v != nullptr && v->kind == Json::Bool) {
+      c.symmetric = v->b;
+    } else {
+      *err = "quantization_config: weights.symmetric missing or not a bool";
+      return false;
+    }
     if (const Json *v = w->get("strategy"); v != nullptr && v->kind == Json::String) c.strategy = v->str;
     int64_t v64;
     if (const Json *v = w->get("axis"); v != nullptr && v->kind != Json::Null) {

@@ -59,7 +59,7 @@ struct QuantConfig {
   std::string quant_method, format;
   int num_bits = 0;
   std::string type;  // "int" or "float"
-  bool symmetric = true;
+  bool symmetric = true;  // required in the file: parse fails without it
   std::string strategy;  // "tensor", "channel" or "group"
   int64_t axis = -1;     // -1 when absent
   int64_t group_size = 0;

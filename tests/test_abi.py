@@ -389,3 +389,11 @@ def test_attention_backward_errors():
     assert lib.teeny_attention_backward_workspace_size(2, 8, 1000, ctypes.byref(size)) == _lib.OK
     assert size.value == 2 * 8 * 1000 * 4
     expect(lib.teeny_attention_backward_workspace_size(2, 8, 10, None), _lib.ERR_NULL_POINTER)
+    # the backward's own limits (B*H <= 65535, n_ctx_q < 2^31) bound the size:
+    # no wrapped products
+    expect(lib.teeny_attention_backward_workspace_size(2 ** 40, 2 ** 30, 2 ** 20, ctypes.byref(size)),
+           _lib.ERR_SHAPE_MISMATCH)
+    expect(lib.teeny_attention_backward_workspace_size(256, 256, 8, ctypes.byref(size)), _lib.ERR_SHAPE_MISMATCH)
+    expect(lib.teeny_attention_backward_workspace_size(1, 1, 2 ** 31, ctypes.byref(size)), _lib.ERR_SHAPE_MISMATCH)
+    assert lib.teeny_attention_backward_workspace_size(255, 257, 2 ** 31 - 1, ctypes.byref(size)) == _lib.OK
+    assert size.value == 255 * 257 * (2 ** 31 - 1) * 4

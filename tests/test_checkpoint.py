@@ -146,3 +146,63 @@ def test_open_errors(tmp_path):
         buf = np.empty(11, np.float32)
         assert _lib.lib.teeny_checkpoint_read(ck.handle, 0, buf.ctypes.data, 44, 0, None) == _lib.ERR_SHAPE_MISMATCH
         assert _lib.lib.teeny_checkpoint_read(ck.handle, 5, buf.ctypes.data, 44, 0, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def _scheme_file(weights: dict, extra=None) -> bytes:
+    """A file with fc.weight I8 [4, 8] + fc.weight_scale F32 [4] under a
+    quantization_config whose weights block is `weights`."""
+    t = {"fc.weight": ("I8", (4, 8), bytes(32)), "fc.weight_scale": ("F32", (4,), bytes(16))}
+    t.update(extra or {})
+    cfg = {"quant_method": "compressed-tensors", "format": "int-quantized",
+           "config_groups": {"group_0": {"weights": weights, "targets": ["*"]}}}
+    return serialize_safetensors(t, {"quantization_config": json.dumps(cfg)})
+
+
+@pytest.mark.parametrize("sym", [None, "yes", 1])
+def test_scheme_without_bool_symmetric_is_rejected(sym):
+    # WeightsConfig.symmetric is a required bool (format.rs:52-70): a file
+    # that does not state it does not say whether zero points exist
+    w = {"num_bits": 8, "type": "int", "strategy": "channel", "axis": 0}
+    if sym is not None:
+        w["symmetric"] = sym
+    with pytest.raises(TeenyError) as e:
+        Checkpoint(image=_scheme_file(w))
+    assert e.value.status == _lib.ERR_INVALID_ARGUMENT
+    assert "symmetric" in str(e.value)
+
+
+@pytest.mark.parametrize("strategy", ["channel", "group"])
+def test_strategy_without_axis_is_ambiguous(strategy):
+    # granularity_from_config rejects channel / group without an axis
+    # (validate.rs:94-103); neither the W8A16 loader nor dequantize guesses 0
+    import ctypes
+    w = {"num_bits": 8, "type": "int", "symmetric": True, "strategy": strategy}
+    if strategy == "group":
+        w["group_size"] = 4
+    with Checkpoint(image=_scheme_file(w)) as ck:
+        assert ck.quant_scheme()["axis"] == -1
+        n, k = ctypes.c_int64(), ctypes.c_int64()
+        assert _lib.lib.teeny_checkpoint_w8a16_shape(ck.handle, b"fc.weight", ctypes.byref(n),
+                                                     ctypes.byref(k)) == _lib.ERR_INVALID_ARGUMENT
+        assert "axis" in _lib.last_error()
+        with pytest.raises(ValueError, match="axis"):
+            ck.dequantize("fc.weight")
+
+
+def test_zero_point_under_symmetric_scheme_is_rejected():
+    # a symmetric scheme omits the zero points (format.rs:25-26): a file that
+    # carries them anyway is inconsistent and not loaded as W8A16
+    import ctypes
+    w = {"num_bits": 8, "type": "int", "symmetric": True, "strategy": "channel", "axis": 0}
+    blob = _scheme_file(w, {"fc.weight_zero_point": ("I32", (4,), bytes(16))})
+    with Checkpoint(image=blob) as ck:
+        n, k = ctypes.c_int64(), ctypes.c_int64()
+        assert _lib.lib.teeny_checkpoint_w8a16_shape(ck.handle, b"fc.weight", ctypes.byref(n),
+                                                     ctypes.byref(k)) == _lib.ERR_INVALID_ARGUMENT
+        assert "zero_point" in _lib.last_error()
+    # the same file without it loads
+    with Checkpoint(image=_scheme_file(w)) as ck:
+        n, k = ctypes.c_int64(), ctypes.c_int64()
+        assert _lib.lib.teeny_checkpoint_w8a16_shape(ck.handle, b"fc.weight", ctypes.byref(n),
+                                                     ctypes.byref(k)) == _lib.OK
+        assert (n.value, k.value) == (4, 8)

@@ -49,20 +49,31 @@ def test_checkpoint_to_w8a16_linear(dev, orc, tmp_path, gran):
         np.testing.assert_array_equal(s.to_host(), np.full(n, os_[0], np.float32))
 
 
-def test_checkpoint_to_w8a16_conv(dev, orc, tmp_path):
+@pytest.mark.parametrize("kh,kw", [(3, 3), (1, 3)])
+def test_checkpoint_to_w8a16_conv(dev, orc, tmp_path, kh, kw):
+    # teeny-quant stores a conv weight in the reference's order [C_OUT, C_IN,
+    # KH, KW] (conv2d.rs:43-156); the loader repacks it for the NHWC conv.
+    # A non-square kernel makes a swapped KH/KW visible too.
     rng = np.random.default_rng(4)
     B, H, cin, cout = 2, 14, 64, 128
-    w = rng.normal(0, 0.02, (cout, 3, 3, cin)).astype(np.float32)
+    w = rng.normal(0, 0.02, (cout, cin, kh, kw)).astype(np.float32)
     blob, _ = oracle_ct_file(orc, {"conv.weight": w}, "channel", 0)
     (tmp_path / "c.safetensors").write_bytes(blob)
     x = rb(rng.standard_normal((B, H, H, cin), dtype=np.float32))
+    print(f"[checkpoint] w8a16 conv {kh}x{kw} from an NCHW-ordered file", flush=True)
     with Checkpoint(str(tmp_path / "c.safetensors")) as ck:
         q, s = ck.load_w8a16("conv.weight")
-    assert q.shape == (cout, 3, 3, cin)
-    y = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), q, s, None, 1, 1).to_host()
+    assert q.shape == (cout, kh, kw, cin)
+    ph, pw = kh // 2, kw // 2
+    y = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), q, s, None, 1, (ph, pw)).to_host()
     oq, os_, _, _ = orc.quantize_affine(w, list(w.shape), "channel", 0)
-    wdeq = orc.dequantize_affine(oq, os_, None, list(w.shape), "channel", 0)
-    check_bf16(y, orc.conv2d_nhwc(x, wdeq, None, stride=1, padding=1), "w8a16 conv from checkpoint")
+    wdeq = orc.dequantize_affine(oq, os_, None, list(w.shape), "channel", 0).reshape(w.shape)
+    ref = orc.conv2d_nchw(np.ascontiguousarray(x.transpose(0, 3, 1, 2)), wdeq, None, stride=1,
+                          padding=(ph, pw)).transpose(0, 2, 3, 1)
+    check_bf16(y, ref, "w8a16 conv from checkpoint")
+    # the repacked int8 weights are exactly the file's, transposed
+    np.testing.assert_array_equal(q.to_host().reshape(cout, kh, kw, cin),
+                                  oq.reshape(cout, cin, kh, kw).transpose(0, 2, 3, 1))
 
 
 @pytest.mark.parametrize("gran,axis,gs,sym", [("channel", 0, 1, True), ("group", 1, 32, True),

@@ -5,7 +5,7 @@ The reference executor captures a whole model into one CUDA graph
 (LoadedModel::capture_graph, drivers/teeny-cuda/src/model/mod.rs:1245-1640).
 Here a sequence covering every kernel family — LayerNorm -> GELU, a split-K
 conv using the stream workspace, a space-to-depth stem conv, a W8A16 GEMM
-dequantizing into the workspace, causal attention — is captured once and
+(int8 weights converted in registers), causal attention — is captured once and
 replayed several times.  Before every replay the outputs are overwritten
 (eagerly, outside the graph), other eager work runs on the same stream, and
 the stream is synchronized; after it, every output must equal the eager
@@ -44,8 +44,8 @@ def test_graph_replays_equal_eager(dev, orc):
     sw = up(dev, rng.standard_normal((64, 7, 7, 3), dtype=np.float32) * np.float32(0.1))
     sb = up(dev, rng.normal(0, 0.01, 64).astype(np.float32))
     sy = tg.Buffer(tg.bf16, (4, 32, 32, 64))
-    # W8A16 GEMM at M = 4096 (dequantizes its weights into the workspace) and
-    # a decode-sized one (split-K partials in the workspace)
+    # W8A16 GEMM at M = 4096 (the 256 x 256 LDS-DMA kernel) and a
+    # decode-sized one (split-K partials in the workspace)
     wf = rng.normal(0, 0.02, (1024, 1024)).astype(np.float32)
     q, s, _, _ = K.quantize_affine(dev.upload(wf), [1024, 1024], "channel", 0)
     lx = up(dev, rng.standard_normal((4096, 1024), dtype=np.float32))
