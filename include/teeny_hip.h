@@ -430,10 +430,12 @@ teeny_status teeny_conv2d_backward_workspace_size(int64_t B, int64_t C_IN, int64
  * kernels/teeny-kernels/src/nn/attention/flash_attn2.rs:52-158.  Here BH and
  * head_dim are arguments, neg_inf is internal, and `causal` != 0 masks key j
  * from query i when j > i (top-left aligned, as torch's is_causal).
- * l is fp32 for every dtype and may be NULL.  dtype F32: head_dim a power of
- * two <= 256.  dtype BF16: MFMA flash kernel, head_dim 64 or 128, 16-byte
- * aligned q/k/v/o, and one head's K (and V) below 2 GiB (n_ctx_k * head_dim
- * * 2 bytes; TEENY_ERR_SHAPE_MISMATCH otherwise). */
+ * l is fp32 for every dtype and may be NULL.  head_dim 16, 32, 64, 128 or
+ * 256 for both dtypes.  dtype BF16 at head_dim 64 and 128 runs the MFMA flash
+ * kernel, which needs 16-byte aligned q/k/v/o and one head's K (and V) below
+ * 2 GiB (n_ctx_k * head_dim * 2 bytes; TEENY_ERR_SHAPE_MISMATCH otherwise);
+ * the other bf16 head sizes and fp32 run the reference's per-query-row
+ * structure (fp32 arithmetic on bf16 operands). */
 teeny_status teeny_flash_attention2_forward(const void *q, const void *k, const void *v, void *o,
                                             float *l, int64_t n_ctx_q, int64_t n_ctx_k,
                                             float softmax_scale, int64_t BH, int64_t head_dim,
@@ -542,6 +544,25 @@ teeny_status teeny_linear_forward(const void *x, const void *w, const void *b, v
                                   int64_t stride_xk, int64_t stride_wn, int64_t stride_wk,
                                   int64_t stride_ym, int64_t stride_yn, teeny_dtype dtype,
                                   teeny_stream stream);
+
+/* Gradients of linear_forward.  Reference: linear_backward(x, w, dy, dx, dw,
+ * db, M, N, K, stride_xm, stride_xk, stride_wk, stride_wn, stride_dym,
+ * stride_dyn, stride_dxm, stride_dxk, stride_dwk, stride_dwn, stride_dbn),
+ * kernels/teeny-kernels/src/nn/mlp/linear.rs:118-250 (RuntimeOp hooks
+ * :324-385): dx [M,K] = dy W, dw [N,K] = dy^T x, db [N] = sum over m of dy
+ * (db NULL: USE_BIAS = false).  All three are written, not accumulated.
+ * dtype F32 or BF16 (every tensor shares it), fp32 accumulation.  Contiguous
+ * bf16 operands with N and K multiples of 8 run on the matrix cores (as the
+ * gradients of a 1x1 convolution; faster with a stream workspace of
+ * teeny_linear_backward_workspace_size bytes); any strides take a tiled
+ * fp32-accumulating kernel. */
+teeny_status teeny_linear_backward(const void *x, const void *w, const void *dy, void *dx, void *dw, void *db,
+                                   int64_t M, int64_t N, int64_t K, int64_t stride_xm, int64_t stride_xk,
+                                   int64_t stride_wk, int64_t stride_wn, int64_t stride_dym, int64_t stride_dyn,
+                                   int64_t stride_dxm, int64_t stride_dxk, int64_t stride_dwk, int64_t stride_dwn,
+                                   int64_t stride_dbn, teeny_dtype dtype, teeny_stream stream);
+teeny_status teeny_linear_backward_workspace_size(int64_t M, int64_t N, int64_t K, teeny_dtype dtype,
+                                                  size_t *bytes);
 
 /* Stream workspace (teeny_hip_stream_set_workspace) that lets linear_forward
  * (dtype F32/BF16, contiguous operands) or w8a16_linear_forward (dtype I8)

@@ -55,6 +55,7 @@ def _load(path: str = LIB_PATH) -> ctypes.CDLL:
         "oracle_flash_attention2_forward": [P, P, P, P, P, I, I, I, I, c_float, c_int, I, I],
         "oracle_flash_attention2_rows": [P, P, P, P, P, I, I, I, I, c_float, c_int, P, I],
         "oracle_linear_forward": [P, P, P, P] + [I] * 9 + [I, I],
+        "oracle_linear_backward": [P] * 6 + [I] * 14,
         "oracle_layer_norm_forward": [P, P, P, P, P, P, I, I, c_float, I, I, I],
         "oracle_layer_norm_backward": [P, P, P, P, P, P, P, P, I, I, I],
         "oracle_rms_norm_backward": [P, P, P, P, P, P, I, I, I],
@@ -363,6 +364,20 @@ def linear(x, w, b=None, pid_begin=0, pid_end=-1):
     _chk(lib.oracle_linear_forward(_p(x), _p(w), _p(b), _p(y), M, N, K, K, 1, K, 1, N, 1, pid_begin,
                                    pid_end), "linear")
     return y
+
+
+def linear_backward(x, w, dy, use_bias=True):
+    """linear.rs:118-250: x [M,K], w [N,K], dy [M,N] -> (dx [M,K], dw [N,K],
+    db [N] or None), contiguous operands."""
+    x, w, dy = _f32(x), _f32(w), _f32(dy)
+    M, K = x.shape
+    N = w.shape[0]
+    dx = np.zeros((M, K), np.float32)
+    dw = np.zeros((N, K), np.float32)
+    db = np.zeros(N, np.float32) if use_bias else None
+    _chk(lib.oracle_linear_backward(_p(x), _p(w), _p(dy), _p(dx), _p(dw), _p(db), M, N, K, K, 1, 1, K, N, 1,
+                                    K, 1, 1, K, 1), "linear_backward")
+    return dx, dw, db
 
 
 # ── training: saved statistics and backward kernels ─────────────────────────

@@ -606,6 +606,53 @@ int oracle_linear_forward(const float *x, const float *w, const float *b, float 
   return OK;
 }
 
+/* linear.rs:118-250 (linear_backward): dx = dy W ([M, K], reduction over n),
+ * dw = dy^T x ([N, K], reduction over m), db[n] = sum_m dy[m, n], all
+ * written (not accumulated), fp32 accumulation in reduction order.  The
+ * reference's programs are (m, n, k) tiles of which the pid_n == 0 ones write
+ * dx and the pid_m == 0 ones write dw and db; here program p < M is dx row p
+ * and program M + n is dw row n (with db[n]): the same sums per element. */
+
+typedef struct {
+  const float *x, *w, *dy;
+  float *dx, *dw, *db;
+  int64_t M, N, K, sxm, sxk, swk, swn, sdym, sdyn, sdxm, sdxk, sdwk, sdwn, sdbn;
+} linb_ctx;
+
+static void linear_bwd_program(const void *c, int64_t p) {
+  const linb_ctx *a = (const linb_ctx *)c;
+  if (p < a->M) {
+    const int64_t m = p;
+    for (int64_t k = 0; k < a->K; ++k) {
+      float acc = 0.0f;
+      for (int64_t n = 0; n < a->N; ++n) acc += a->dy[m * a->sdym + n * a->sdyn] * a->w[n * a->swn + k * a->swk];
+      a->dx[m * a->sdxm + k * a->sdxk] = acc;
+    }
+    return;
+  }
+  const int64_t n = p - a->M;
+  for (int64_t k = 0; k < a->K; ++k) {
+    float acc = 0.0f;
+    for (int64_t m = 0; m < a->M; ++m) acc += a->dy[m * a->sdym + n * a->sdyn] * a->x[m * a->sxm + k * a->sxk];
+    a->dw[n * a->sdwn + k * a->sdwk] = acc;
+  }
+  if (a->db != NULL) {
+    float acc = 0.0f;
+    for (int64_t m = 0; m < a->M; ++m) acc += a->dy[m * a->sdym + n * a->sdyn];
+    a->db[n * a->sdbn] = acc;
+  }
+}
+
+int oracle_linear_backward(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                           int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swk, int64_t swn,
+                           int64_t sdym, int64_t sdyn, int64_t sdxm, int64_t sdxk, int64_t sdwk, int64_t sdwn,
+                           int64_t sdbn) {
+  if (M < 0 || N < 0 || K < 0) return ERR_SHAPE_MISMATCH;
+  linb_ctx a = {x, w, dy, dx, dw, db, M, N, K, sxm, sxk, swk, swn, sdym, sdyn, sdxm, sdxk, sdwk, sdwn, sdbn};
+  launch(linear_bwd_program, &a, M + N, 0, -1);
+  return OK;
+}
+
 /* ── teeny-quant affine quantization ─────────────────────────────────────
  * utilities/teeny-quant/src/quant/affine.rs:47-161 and groups.rs:20-100.
  * Rust semantics restated: f32::round rounds half away from zero; `as i32`

@@ -165,6 +165,8 @@ _SIGS = {
     "teeny_linear_forward": (S, [P, P, P, P] + [c_int64] * 9 + [c_int32, P]),
     "teeny_w8a16_linear_forward": (S, [P, P, P, P, P, c_int64, c_int64, c_int64, c_int32, P]),
     "teeny_linear_workspace_size": (S, [c_int64, c_int64, c_int64, c_int32, POINTER(c_size_t)]),
+    "teeny_linear_backward": (S, [P] * 6 + [c_int64] * 14 + [c_int32, P]),
+    "teeny_linear_backward_workspace_size": (S, [c_int64, c_int64, c_int64, c_int32, POINTER(c_size_t)]),
     "teeny_conv2d_workspace_size": (S, [c_int64] * 7 + [POINTER(Conv2dParams), c_int32, c_int32, POINTER(c_size_t)]),
     "teeny_w8a16_conv2d_forward": (S, [P, P, P, P, P] + [c_int64] * 7 + [POINTER(Conv2dParams), P]),
     "teeny_checkpoint_open": (S, [c_char_p, POINTER(c_void_p)]),

@@ -31,10 +31,12 @@
 // (b, h) pairs at a time: they stream the same K/V tiles, which then come
 // from that XCD's L2 rather than once per workgroup from HBM.
 //
-// fa_fwd_f32 (fp32, any power-of-two head_dim <= 256).  The reference's
+// fa_fwd_rows (fp32 at any power-of-two head_dim <= 256, and bf16 at the
+// head sizes the MFMA kernel does not take: 16, 32, 256).  The reference's
 // per-query-row structure — grid (N_q, BH), one wave per query row — with
 // the key loop vectorised across lanes: each lane scores one key of a
 // 64-key chunk, and the chunk is folded into the running (m, l, acc) state.
+// bf16 operands are widened to fp32 on load; all arithmetic is fp32.
 #include "mfma.hpp"
 
 namespace teeny {
@@ -395,23 +397,22 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fa_fwd_bf16(const bf16 
   }  // pass
 }
 
-// fp32 path: grid (nq, BH), one wave per query row (flash_attn2.rs:48-51).
-template <int D>
-__global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
-                                                 const float *__restrict__ K,
-                                                 const float *__restrict__ V,
-                                                 float *__restrict__ O, float *__restrict__ L,
-                                                 int nq, int nk, float scale, int causal, int kv_group) {
+// Per-row path: grid (nq, BH), one wave per query row (flash_attn2.rs:48-51).
+template <typename T, int D>
+__global__ __launch_bounds__(64) void fa_fwd_rows(const T *__restrict__ Q, const T *__restrict__ K,
+                                                  const T *__restrict__ V, T *__restrict__ O,
+                                                  float *__restrict__ L, int nq, int nk, float scale, int causal,
+                                                  int kv_group) {
   constexpr int DPL = (D + 63) / 64;  // output elements per lane
   __shared__ float qs[D];
   __shared__ float ps[64];
   const int qi = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int lane = threadIdx.x;
-  const float *qrow = Q + (bh * nq + qi) * D;
-  const float *Kb = K + (bh / kv_group) * nk * D;
-  const float *Vb = V + (bh / kv_group) * nk * D;
-  for (int d = lane; d < D; d += 64) qs[d] = qrow[d];
+  const T *qrow = Q + (bh * nq + qi) * D;
+  const T *Kb = K + (bh / kv_group) * nk * D;
+  const T *Vb = V + (bh / kv_group) * nk * D;
+  for (int d = lane; d < D; d += 64) qs[d] = to_f32(qrow[d]);
   __syncthreads();
 
   float acc[DPL];
@@ -423,10 +424,10 @@ __global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
     const int key = k0 + lane;
     float s = -INFINITY;
     if (key < kend) {
-      const float *krow = Kb + static_cast<int64_t>(key) * D;
+      const T *krow = Kb + static_cast<int64_t>(key) * D;
       float dot = 0.0f;
 #pragma unroll 8
-      for (int d = 0; d < D; ++d) dot += qs[d] * krow[d];
+      for (int d = 0; d < D; ++d) dot += qs[d] * to_f32(krow[d]);
       s = dot * scale;
     }
     const float m_new = fmaxf(m_i, wave_max(s));
@@ -441,28 +442,28 @@ __global__ __launch_bounds__(64) void fa_fwd_f32(const float *__restrict__ Q,
       const int d = lane + 64 * i;
       if (d < D) {
         float a = ed * acc[i];
-        for (int j = 0; j < cnt; ++j) a += ps[j] * Vb[static_cast<int64_t>(k0 + j) * D + d];
+        for (int j = 0; j < cnt; ++j) a += ps[j] * to_f32(Vb[static_cast<int64_t>(k0 + j) * D + d]);
         acc[i] = a;
       }
     }
     m_i = m_new;
     __syncthreads();
   }
-  float *orow = O + (bh * nq + qi) * D;
+  T *orow = O + (bh * nq + qi) * D;
 #pragma unroll
   for (int i = 0; i < DPL; ++i) {
     const int d = lane + 64 * i;
-    if (d < D) orow[d] = acc[i] / l_i;
+    if (d < D) orow[d] = from_f32<T>(acc[i] / l_i);
   }
   if (L != nullptr && lane == 0) L[bh * nq + qi] = m_i + logf(l_i);
 }
 
-template <int D>
-static void launch_f32(const void *q, const void *k, const void *v, void *o, float *l, int nq,
-                       int nk, float scale, int BH, int causal, int kv_group, hipStream_t s) {
-  hipLaunchKernelGGL((fa_fwd_f32<D>), dim3(nq, BH), dim3(64), 0, s, static_cast<const float *>(q),
-                     static_cast<const float *>(k), static_cast<const float *>(v),
-                     static_cast<float *>(o), l, nq, nk, scale, causal, kv_group);
+template <typename T, int D>
+static void launch_rows(const void *q, const void *k, const void *v, void *o, float *l, int nq,
+                        int nk, float scale, int BH, int causal, int kv_group, hipStream_t s) {
+  hipLaunchKernelGGL((fa_fwd_rows<T, D>), dim3(nq, BH), dim3(64), 0, s, static_cast<const T *>(q),
+                     static_cast<const T *>(k), static_cast<const T *>(v), static_cast<T *>(o), l, nq, nk,
+                     scale, causal, kv_group);
 }
 
 template <int D>
@@ -510,26 +511,32 @@ static teeny_status attention_entry(const void *q, const void *k, const void *v,
   const int bh = static_cast<int>(BH), group = static_cast<int>(q_heads / kv_heads);
   if (dtype == TEENY_F32) {
     switch (head_dim) {
-      case 16: launch_f32<16>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      case 32: launch_f32<32>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      case 64: launch_f32<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      case 128: launch_f32<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      case 256: launch_f32<256>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 16: launch_rows<float, 16>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 32: launch_rows<float, 32>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 64: launch_rows<float, 64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 128: launch_rows<float, 128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 256: launch_rows<float, 256>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
       default: return fail(TEENY_ERR_UNSUPPORTED, nm + ": f32 head_dim must be 16, 32, 64, 128 or 256");
     }
     return after_launch(name, s);
   }
   if (dtype == TEENY_BF16) {
+    switch (head_dim) {  // head sizes off the matrix-core kernel: the per-row kernel
+      case 16: launch_rows<bf16, 16>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 32: launch_rows<bf16, 32>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 256: launch_rows<bf16, 256>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
+      case 64:
+      case 128: break;
+      default: return fail(TEENY_ERR_UNSUPPORTED, nm + ": bf16 head_dim must be 16, 32, 64, 128 or 256");
+    }
+    if (head_dim != 64 && head_dim != 128) return after_launch(name, s);
     TEENY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
                   TEENY_ERR_MISALIGNED, nm + ": bf16 q/k/v/o must be 16-byte aligned");
     // K and V of one (batch, head) are read through 32-bit buffer offsets
     TEENY_REQUIRE(n_ctx_k * head_dim * 2 <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
                   nm + ": bf16 K/V of one head must be below 2 GiB");
-    switch (head_dim) {
-      case 64: launch_bf16<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      case 128: launch_bf16<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s); break;
-      default: return fail(TEENY_ERR_UNSUPPORTED, nm + ": bf16 head_dim must be 64 or 128");
-    }
+    if (head_dim == 64) launch_bf16<64>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s);
+    else launch_bf16<128>(q, k, v, o, l, nq, nk, softmax_scale, bh, causal, group, s);
     return after_launch(name, s);
   }
   return fail(TEENY_ERR_UNSUPPORTED_DTYPE, nm + ": dtype must be F32 or BF16");

@@ -282,6 +282,24 @@ extern "C" teeny_status teeny_dispatch(const char *entry_point, const int64_t *c
                                 syn, dtype, stream);
   }
 
+  // linear_backward<USE_BIAS,BLOCK_M,BLOCK_N,BLOCK_K,GROUP_M>(x, w, dy, dx, dw, db, M, N, K,
+  //   stride_xm, stride_xk, stride_wk, stride_wn, stride_dym, stride_dyn, stride_dxm, stride_dxk,
+  //   stride_dwk, stride_dwn, stride_dbn)                                   linear.rs:118-150, :341-384
+  if (name_is(entry_point, "linear_backward")) {
+    TEENY_REQUIRE(n_cg == 5, TEENY_ERR_INVALID_ARGUMENT,
+                  "linear_backward: expects const generics USE_BIAS,BLOCK_M,BLOCK_N,BLOCK_K,GROUP_M");
+    void *x = r.ptr("x_ptr"), *w = r.ptr("w_ptr"), *dy = r.ptr("dy_ptr"), *dx = r.ptr("dx_ptr"),
+         *dw = r.ptr("dw_ptr"), *db = r.ptr("db_ptr");
+    int64_t M = r.i32("M"), N = r.i32("N"), K = r.i32("K");
+    int64_t sxm = r.i32("stride_xm"), sxk = r.i32("stride_xk"), swk = r.i32("stride_wk"),
+            swn = r.i32("stride_wn"), sdym = r.i32("stride_dym"), sdyn = r.i32("stride_dyn"),
+            sdxm = r.i32("stride_dxm"), sdxk = r.i32("stride_dxk"), sdwk = r.i32("stride_dwk"),
+            sdwn = r.i32("stride_dwn"), sdbn = r.i32("stride_dbn");
+    if (r.done() != TEENY_OK) return r.st;
+    return teeny_linear_backward(x, w, dy, dx, dw, cg[0] ? db : nullptr, M, N, K, sxm, sxk, swk, swn, sdym, sdyn,
+                                 sdxm, sdxk, sdwk, sdwn, sdbn, dtype, stream);
+  }
+
   // Conv + BatchNorm (folded scale / shift) + SiLU, the reference's three fused variants
   // (nn/fused/): fp32 NCHW, the activation fixed to SiLU.
   //   conv2d_bn_silu_forward<KH,KW,SH,SW,PH,PW,G,BLOCK_OW>(x, w, bn_scale, bn_shift, y,

@@ -97,6 +97,19 @@ static teeny_status launch_generic(const TA *A, int64_t sam, int64_t sak, const 
   return TEENY_OK;
 }
 
+// db[n] = sum_m dy[m, n] in m order, fp32 (linear_backward's bias gradient).
+// 64 threads per block: one column each, consecutive columns per wave.
+template <typename T>
+__global__ __launch_bounds__(64) void linear_bwd_db(const T *__restrict__ dy, int64_t sm, int64_t sn,
+                                                    T *__restrict__ db, int64_t sdb, int M, int N) {
+  const int n = blockIdx.x * 64 + threadIdx.x;
+  if (n >= N) return;
+  float acc = 0.0f;
+  const T *col = dy + n * sn;
+  for (int m = 0; m < M; ++m) acc += to_f32(col[m * sm]);
+  db[n * sdb] = from_f32<T>(acc);
+}
+
 static GemmParams plain_params(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                                int64_t ldc, const float *scale, const float *bias,
                                const bf16 *bias_bf16, int64_t M, int64_t N, int64_t K) {
@@ -186,6 +199,99 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
     if (st != TEENY_OK) return st;
   }
   return after_launch("w8a16_linear_forward", s);
+}
+
+// linear_backward's MFMA plan: the gradients of a 1x1 convolution over M
+// one-pixel images (x [M,1,1,K], w [N,1,1,K], dy [M,1,1,N]); contiguous bf16
+// operands with N and K multiples of 8 and 32-bit buffer extents.
+static bool linear_bwd_as_conv(int64_t M, int64_t N, int64_t K, teeny_dtype dtype) {
+  return dtype == TEENY_BF16 && N % 8 == 0 && K % 8 == 0 && N * K <= 0x7fffffff && M * N * 2 <= 0x7fffff00LL &&
+         M * K * 2 <= 0x7fffff00LL;
+}
+
+static const teeny_conv2d_params kConv1x1 = {1, 1, 1, 1, 0, 0, 1, TEENY_ACT_NONE};
+
+teeny_status teeny_linear_backward(const void *x, const void *w, const void *dy, void *dx, void *dw, void *db,
+                                   int64_t M, int64_t N, int64_t K, int64_t stride_xm, int64_t stride_xk,
+                                   int64_t stride_wk, int64_t stride_wn, int64_t stride_dym, int64_t stride_dyn,
+                                   int64_t stride_dxm, int64_t stride_dxk, int64_t stride_dwk, int64_t stride_dwn,
+                                   int64_t stride_dbn, teeny_dtype dtype, teeny_stream stream) {
+  const char *nm = "linear_backward";
+  TEENY_REQUIRE(M >= 0 && N >= 0 && K >= 0, TEENY_ERR_SHAPE_MISMATCH, "linear_backward: negative size");
+  TEENY_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                "linear_backward: size exceeds 2^31-1");
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                "linear_backward: dtype must be F32 or BF16");
+  const bool want_dx = M > 0 && K > 0, want_dw = N > 0 && K > 0, want_db = db != nullptr && N > 0;
+  TEENY_REQUIRE((!want_dx || dx != nullptr) && (!want_dw || dw != nullptr), TEENY_ERR_NULL_POINTER,
+                "linear_backward: dx/dw");
+  TEENY_REQUIRE((!want_dx || N == 0 || (dy != nullptr && w != nullptr)) &&
+                    (!want_dw || M == 0 || (dy != nullptr && x != nullptr)) && (!want_db || M == 0 || dy != nullptr),
+                TEENY_ERR_NULL_POINTER, "linear_backward: x/w/dy");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool contiguous = stride_xk == 1 && stride_xm == K && stride_wk == 1 && stride_wn == K && stride_dyn == 1 &&
+                          stride_dym == N && stride_dxk == 1 && stride_dxm == K && stride_dwk == 1 &&
+                          stride_dwn == K;
+  const bool conv = contiguous && M > 0 && N > 0 && linear_bwd_as_conv(M, N, K, dtype);
+  teeny_status st = TEENY_OK;
+  // dx [M, K] = dy [M, N] W [N, K]: C[m, k] = sum_n dy[m, n] w[n, k]
+  if (want_dx) {
+    if (conv) {
+      st = teeny_conv2d_backward_dx(dy, w, dx, M, K, N, 1, 1, 1, 1, &kConv1x1, dtype, TEENY_NHWC, stream);
+    } else if (dtype == TEENY_F32) {
+      st = launch_generic<float, float, float>(static_cast<const float *>(dy), stride_dym, stride_dyn,
+                                               static_cast<const float *>(w), stride_wk, stride_wn,
+                                               static_cast<float *>(dx), stride_dxm, stride_dxk, nullptr, nullptr,
+                                               nullptr, M, K, N, TEENY_ACT_NONE, s);
+    } else {
+      st = launch_generic<bf16, bf16, bf16>(static_cast<const bf16 *>(dy), stride_dym, stride_dyn,
+                                            static_cast<const bf16 *>(w), stride_wk, stride_wn,
+                                            static_cast<bf16 *>(dx), stride_dxm, stride_dxk, nullptr, nullptr,
+                                            nullptr, M, K, N, TEENY_ACT_NONE, s);
+    }
+    if (st != TEENY_OK) return st;
+  }
+  // dw [N, K] = dy^T x: C[n, k] = sum_m dy[m, n] x[m, k]
+  if (want_dw) {
+    if (conv) {
+      st = teeny_conv2d_backward_dw(dy, x, dw, M, K, N, 1, 1, 1, 1, &kConv1x1, dtype, TEENY_NHWC, stream);
+    } else if (dtype == TEENY_F32) {
+      st = launch_generic<float, float, float>(static_cast<const float *>(dy), stride_dyn, stride_dym,
+                                               static_cast<const float *>(x), stride_xk, stride_xm,
+                                               static_cast<float *>(dw), stride_dwn, stride_dwk, nullptr, nullptr,
+                                               nullptr, N, K, M, TEENY_ACT_NONE, s);
+    } else {
+      st = launch_generic<bf16, bf16, bf16>(static_cast<const bf16 *>(dy), stride_dyn, stride_dym,
+                                            static_cast<const bf16 *>(x), stride_xk, stride_xm,
+                                            static_cast<bf16 *>(dw), stride_dwn, stride_dwk, nullptr, nullptr,
+                                            nullptr, N, K, M, TEENY_ACT_NONE, s);
+    }
+    if (st != TEENY_OK) return st;
+  }
+  // db [N] = column sums of dy (USE_BIAS)
+  if (want_db) {
+    const dim3 grid(static_cast<unsigned>(cdiv(N, 64)));
+    if (dtype == TEENY_F32)
+      hipLaunchKernelGGL(linear_bwd_db<float>, grid, dim3(64), 0, s, static_cast<const float *>(dy), stride_dym,
+                         stride_dyn, static_cast<float *>(db), stride_dbn, static_cast<int>(M), static_cast<int>(N));
+    else
+      hipLaunchKernelGGL(linear_bwd_db<bf16>, grid, dim3(64), 0, s, static_cast<const bf16 *>(dy), stride_dym,
+                         stride_dyn, static_cast<bf16 *>(db), stride_dbn, static_cast<int>(M), static_cast<int>(N));
+  }
+  return after_launch(nm, s);
+}
+
+teeny_status teeny_linear_backward_workspace_size(int64_t M, int64_t N, int64_t K, teeny_dtype dtype,
+                                                  size_t *bytes) {
+  TEENY_REQUIRE(bytes != nullptr, TEENY_ERR_NULL_POINTER, "linear_backward_workspace_size: bytes");
+  *bytes = 0;
+  TEENY_REQUIRE(M >= 0 && N >= 0 && K >= 0, TEENY_ERR_SHAPE_MISMATCH, "linear_backward_workspace_size: negative size");
+  TEENY_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, TEENY_ERR_SHAPE_MISMATCH,
+                "linear_backward_workspace_size: size exceeds 2^31-1");
+  TEENY_REQUIRE(dtype == TEENY_F32 || dtype == TEENY_BF16, TEENY_ERR_UNSUPPORTED_DTYPE,
+                "linear_backward_workspace_size: dtype must be F32 or BF16");
+  if (M == 0 || N == 0 || K == 0 || !linear_bwd_as_conv(M, N, K, dtype)) return TEENY_OK;
+  return teeny_conv2d_backward_workspace_size(M, K, N, 1, 1, 1, 1, &kConv1x1, dtype, TEENY_NHWC, bytes);
 }
 
 teeny_status teeny_linear_workspace_size(int64_t M, int64_t N, int64_t K, teeny_dtype dtype,

@@ -817,6 +817,41 @@ class LinearForward(RuntimeOp):
         pn = -(-int(output_shape[1]) // self.block_n)
         return (pm * pn, 1, 1)
 
+    # training hooks (linear.rs:322-385): linear_backward
+    def has_backward(self) -> bool:
+        return True
+
+    def backward_entry_point_name(self) -> str:
+        return "linear_backward_entry_point"
+
+    def backward_grad_output_row_stride(self, output_shape, elem_bytes=4) -> int:
+        """dy rows padded to 16 bytes (linear.rs:329-334)."""
+        n = int(output_shape[-1])
+        align = 16 // elem_bytes
+        return -(-n // align) * align
+
+    def pack_backward_args(self, inputs, params, output, output_shape, grad_output,
+                           grad_output_row_stride, grad_inputs, grad_params, visitor):
+        """(x, w, dy, dx, dw, db, M, N, K, stride_xm, stride_xk, stride_wk,
+        stride_wn, stride_dym, stride_dyn, stride_dxm, stride_dxk, stride_dwk,
+        stride_dwn, stride_dbn), linear.rs:341-384; db is null without bias."""
+        m, n = int(output_shape[0]), int(output_shape[1])
+        k = int(inputs[0][1][1])
+        visitor.visit_ptr(inputs[0][0])
+        visitor.visit_ptr(params[0])
+        visitor.visit_ptr(grad_output)
+        visitor.visit_ptr(grad_inputs[0])
+        visitor.visit_ptr(grad_params[0])
+        visitor.visit_ptr(grad_params[1] if self.use_bias else None)
+        for v in (m, n, k, k, 1, 1, k, grad_output_row_stride, 1, k, 1, 1, k, 1):
+            visitor.visit_i32(v)
+
+    def backward_grid(self, input_shapes, output_shape):
+        pm = -(-int(output_shape[0]) // self.block_m)
+        pn = -(-int(output_shape[1]) // self.block_n)
+        pk = -(-int(input_shapes[0][1]) // self.block_k)
+        return (pm * pn * pk, 1, 1)
+
 
 # ── direct entry points on Buffers ──────────────────────────────────────────
 
@@ -1318,6 +1353,30 @@ def linear(x: Buffer, w: Buffer, b: Optional[Buffer] = None, y: Optional[Buffer]
     check(lib.teeny_linear_forward(x.ptr, w.ptr, b.ptr if b is not None else None, y.ptr, m, n, k,
                                    k, 1, k, 1, n, 1, x.dtype.code, _h(stream)))
     return y
+
+
+def linear_backward(x: Buffer, w: Buffer, dy: Buffer, use_bias: bool = True, dx: Optional[Buffer] = None,
+                    dw: Optional[Buffer] = None, db: Optional[Buffer] = None,
+                    stream: Optional[Stream] = None) -> Tuple[Buffer, Buffer, Optional[Buffer]]:
+    """Gradients of ``linear`` (linear.rs:118-250): x [M,K], w [N,K], dy [M,N]
+    -> (dx [M,K] = dy w, dw [N,K] = dy^T x, db [N] = column sums of dy, or
+    None without bias).  Written, not accumulated."""
+    m, n, k = linear_dims(x.shape, w.shape)
+    _need(tuple(dy.shape) == (m, n), f"linear_backward: dy must be [{m}, {n}], is {list(dy.shape)}")
+    _need(w.dtype == x.dtype and dy.dtype == x.dtype, "linear_backward: x/w/dy dtypes differ")
+    dx = _out(x, dx, (m, k))
+    dw = _out(x, dw, (n, k))
+    db = _out(x, db, (n,)) if use_bias else None
+    check(lib.teeny_linear_backward(x.ptr, w.ptr, dy.ptr, dx.ptr, dw.ptr, db.ptr if db is not None else None,
+                                    m, n, k, k, 1, 1, k, n, 1, k, 1, 1, k, 1, x.dtype.code, _h(stream)))
+    return dx, dw, db
+
+
+def linear_backward_workspace_size(m: int, n: int, k: int, dtype=bf16) -> int:
+    """Stream workspace bytes that let ``linear_backward`` take its fastest plan."""
+    out = ctypes.c_size_t(0)
+    check(lib.teeny_linear_backward_workspace_size(m, n, k, from_any(dtype).code, ctypes.byref(out)))
+    return int(out.value)
 
 
 def w8a16_linear(x: Buffer, qweight: Buffer, scale: Buffer, bias: Optional[Buffer] = None,

@@ -163,6 +163,22 @@ def test_linear_errors():
     expect(w8(FAKE, FAKE, None, None, FAKE, 4, 4, 16, 0, None), _lib.ERR_NULL_POINTER)
     expect(w8(FAKE, FAKE, FAKE, None, FAKE, -1, 4, 16, 0, None), _lib.ERR_SHAPE_MISMATCH)
     expect(w8(FAKE, FAKE, FAKE, None, FAKE, 4, 4, 16, 9, None), _lib.ERR_INVALID_ARGUMENT)
+    lb = lib.teeny_linear_backward
+    strides = (4, 1, 1, 4, 4, 1, 4, 1, 1, 4, 1)
+    expect(lb(FAKE, FAKE, FAKE, None, FAKE, None, 4, 4, 4, *strides, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, None, None, 4, 4, 4, *strides, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(lb(FAKE, None, FAKE, FAKE, FAKE, None, 4, 4, 4, *strides, _lib.F32, None), _lib.ERR_NULL_POINTER)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, FAKE, None, -1, 4, 4, *strides, _lib.F32, None), _lib.ERR_SHAPE_MISMATCH)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, FAKE, None, 4, 2 ** 31, 4, *strides, _lib.F32, None),
+           _lib.ERR_SHAPE_MISMATCH)
+    expect(lb(FAKE, FAKE, FAKE, FAKE, FAKE, None, 4, 4, 4, *strides, _lib.I8, None), _lib.ERR_UNSUPPORTED_DTYPE)
+    size = ctypes.c_size_t(1)
+    assert lib.teeny_linear_backward_workspace_size(64, 48, 64, _lib.F32, ctypes.byref(size)) == _lib.OK
+    assert size.value == 0  # fp32 takes the generic kernel: no scratch
+    assert lib.teeny_linear_backward_workspace_size(64, 30, 64, _lib.BF16, ctypes.byref(size)) == _lib.OK
+    assert size.value == 0  # N % 8 != 0: generic kernel
+    expect(lib.teeny_linear_backward_workspace_size(4, 4, 4, _lib.BF16, None), _lib.ERR_NULL_POINTER)
+    expect(lib.teeny_linear_backward_workspace_size(-4, 4, 4, _lib.BF16, ctypes.byref(size)), _lib.ERR_SHAPE_MISMATCH)
 
 
 def packed(*kinds_values):

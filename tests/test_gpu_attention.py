@@ -62,7 +62,11 @@ def run_bf16(dev, q, k, v, causal):
     (2, 128, 128, 128, False), (2, 128, 128, 128, True), (3, 200, 200, 128, True),
     (2, 100, 300, 64, False), (1, 257, 129, 128, True), (4, 64, 64, 64, True),
     (1, 1000, 1000, 128, True), (2, 300, 77, 128, False), (1, 512, 512, 64, False),
-    (1, 33, 17, 128, False), (2, 70, 5, 64, True), (1, 130, 190, 64, True)])
+    (1, 33, 17, 128, False), (2, 70, 5, 64, True), (1, 130, 190, 64, True),
+    # head sizes off the matrix-core kernel (the per-row kernel, as the
+    # reference takes any HEAD_DIM, flash_attn2.rs:53)
+    (2, 100, 130, 16, True), (3, 70, 70, 32, False), (1, 129, 200, 32, True), (2, 65, 90, 256, False),
+    (1, 140, 140, 256, True)])
 def test_bf16_vs_oracle(dev, orc, bh, nq, nk, d, causal):
     print(f"[attn bf16] bh={bh} nq={nq} nk={nk} d={d} causal={causal}", flush=True)
     q, k, v = bf16_inputs(np.random.default_rng(nq * 31 + nk), bh, nq, nk, d)
@@ -88,37 +92,16 @@ def test_bf16_scale(dev, orc, scale, causal):
     assert np.max(np.abs(lse.to_host() - ol)) < 1e-3
 
 
-def sample_rows(bh, nq, n=48, seed=0):
-    """Fixed tile-border rows, random rows, and two rows of every (b, h): one
-    in query block p and one in block nqb-1-p (128-query blocks; the causal
-    kernel pairs exactly those two in one workgroup), at the 32-query slice
-    of wave h % 4, so every head and, over the heads, every wave is covered."""
-    rng = np.random.default_rng(seed)
-    fixed = [0, 1, 63, 64, 127, 128, nq - 1, (bh - 1) * nq, bh * nq - 1, (bh // 2) * nq + nq // 2]
-    nqb = max(1, nq // 128)
-    heads = np.arange(bh)
-    p = (heads * 5) % nqb
-    within = (heads % 4) * 32 + rng.integers(0, 32, bh)
-    per_head = [heads * nq + p * 128 + within, heads * nq + (nqb - 1 - p) * 128 + within]
-    rows = np.concatenate([fixed, rng.integers(0, bh * nq, n)] + per_head)
-    return np.unique(rows[(rows >= 0) & (rows < bh * nq)]).astype(np.int64)
-
-
 @pytest.mark.parametrize("s,causal", [(2048, True), (4096, False)])
 def test_bf16_config(dev, orc, s, causal):
-    # causal S=2048 and non-causal S=4096, B*H = 8*32, D = 128: every row of the
-    # output is checked for finiteness, a sample of rows against the oracle
+    # causal S=2048 and non-causal S=4096, B*H = 8*32, D = 128: the whole
+    # output (every row of every head) and every LSE entry against the oracle
     bh, d = 256, 128
     print(f"[attn bf16 config] BH={bh} S={s} causal={causal}", flush=True)
     q, k, v = bf16_inputs(np.random.default_rng(0x7EE70002 + s), bh, s, s, d)
     o, lse = run_bf16(dev, q, k, v, causal)
-    assert np.all(np.isfinite(from_bf16(o))) and np.all(np.isfinite(lse))
-    rows = sample_rows(bh, s)
-    oo, ol = orc.flash_attention_rows(q, k, v, rows, causal=causal)
-    check_bf16(o.reshape(-1, d)[rows], oo, "o rows")
-    assert np.max(np.abs(lse.reshape(-1)[rows] - ol)) < 1e-3
-    # every output row is a convex combination of V rows: within [min V, max V] per column
-    vmin = v.min(axis=1, keepdims=True)
-    vmax = v.max(axis=1, keepdims=True)
-    of = from_bf16(o).reshape(bh, s, d)
-    assert np.all(of >= vmin - 2e-2) and np.all(of <= vmax + 2e-2)
+    oo, ol = orc.flash_attention(q, k, v, causal=causal)
+    print(f"[attn bf16 config] oracle done, comparing {o.size} outputs", flush=True)
+    for h0 in range(0, bh, 32):  # in head blocks, to bound the float64 temporaries
+        check_bf16(o[h0:h0 + 32], oo[h0:h0 + 32], f"o heads {h0}..{h0 + 31}")
+    assert np.max(np.abs(lse - ol)) < 1e-3

@@ -173,3 +173,27 @@ def test_no_queries_gives_zero_dkv(dev):
                                                          0, 5, ctypes.c_float(0.1), 2, 32, 0, _lib.F32, None))
     np.testing.assert_array_equal(dk.to_host(), 0.0)
     np.testing.assert_array_equal(dv.to_host(), 0.0)
+
+
+@pytest.mark.parametrize("d", [16, 32, 256])
+def test_bf16_forward_then_backward_small_and_large_heads(dev, orc, d):
+    # bf16 at head sizes off the matrix-core kernels: the GPU forward's own O
+    # and L feed the GPU backward, as a lowered training graph runs them
+    bh, nq, nk, causal = 3, 90, 120, True
+    rng = np.random.default_rng(d)
+    q = rb(rng.normal(0, 1, (bh, nq, d)).astype(np.float32))
+    k = rb(rng.normal(0, 1, (bh, nk, d)).astype(np.float32))
+    v = rb(rng.normal(0, 1, (bh, nk, d)).astype(np.float32))
+    do = rb(rng.normal(0, 1, (bh, nq, d)).astype(np.float32))
+    scale = 1.0 / np.sqrt(d)
+    print(f"[attn fwd+bwd bf16] d={d}", flush=True)
+    qb, kb, vb, dob = (dev.upload(to_bf16(a), tg.bf16) for a in (q, k, v, do))
+    lse = tg.Buffer(tg.f32, (bh, nq))
+    ob = K.flash_attention(qb, kb, vb, scale, causal, lse=lse)
+    o_ref, l_ref = oracle_forward(orc, q, k, v, scale, causal, 1)
+    check_bf16(ob.to_host(), o_ref, "o")
+    assert np.max(np.abs(lse.to_host() - l_ref)) < 1e-3
+    dq, dk, dv = K.attention_backward(qb, kb, vb, ob, dob, lse, q_heads=1, kv_heads=1, causal=causal)
+    rq, rk, rv = backward_ref(orc, q, k, v, rb(o_ref), do, l_ref, scale, causal, 1)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), (rq, rk, rv)):
+        check_grad(got, ref, name)

@@ -312,3 +312,115 @@ def test_conv_backward_empty_batch_zeroes_dw(dev):
     tg.check(_lib.lib.teeny_conv2d_backward_dw(dy.ptr, x.ptr, dw.ptr, 0, 4, 8, 6, 6, 6, 6, ctypes.byref(prm),
                                                _lib.F32, _lib.NCHW, None))
     np.testing.assert_array_equal(dw.to_host(), 0.0)
+
+
+# ── linear backward ─────────────────────────────────────────────────────────
+# linear_backward, kernels/teeny-kernels/src/nn/mlp/linear.rs:118-250:
+# dx = dy W, dw = dy^T x, db = column sums of dy.
+
+
+def test_linear_backward_fixture(dev):
+    # test_linear.rs:434-626: M=64, N=48, K=64 fp32, with and without bias
+    x = load_golden("linear/input.bin").reshape(64, 64)
+    w = load_golden("linear/weight.bin").reshape(48, 64)
+    dy = load_golden("linear/dy.bin").reshape(64, 48)
+    for use_bias in (True, False):
+        print(f"[linear bwd fixture] bias={use_bias}", flush=True)
+        dx, dw, db = K.linear_backward(dev.upload(x), dev.upload(w), dev.upload(dy), use_bias)
+        check_f32(dx.to_host(), load_golden("linear/expected_dx.bin"), "dx")
+        check_f32(dw.to_host(), load_golden("linear/expected_dw.bin"), "dw")
+        if use_bias:
+            check_f32(db.to_host(), load_golden("linear/expected_db.bin"), "db")
+        else:
+            assert db is None
+
+
+LINEAR_BWD = [  # (M, N, K): the matrix-core plan (N, K multiples of 8) and the generic kernel
+    (512, 256, 384), (4096, 1024, 512), (100, 40, 24), (37, 30, 20), (3, 8, 8)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("m,n,k", LINEAR_BWD)
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_linear_backward(dev, orc, dtype, m, n, k, scratch):
+    rng = np.random.default_rng(m + 7 * n + 13 * k)
+    x = rb(rng.standard_normal((m, k), dtype=np.float32))
+    w = rb(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.1))
+    dy = rb(rng.standard_normal((m, n), dtype=np.float32))
+    tdt = tg.bf16 if dtype == "bf16" else tg.f32
+    need = K.linear_backward_workspace_size(m, n, k, tdt)
+    if scratch == "workspace" and need == 0:
+        pytest.skip("no workspace plan at this shape")
+    print(f"[linear bwd] {dtype} M={m} N={n} K={k} workspace={need if scratch == 'workspace' else 0}", flush=True)
+    xb, wb, dyb = up(dev, x, dtype), up(dev, w, dtype), up(dev, dy, dtype)
+
+    def run():
+        return K.linear_backward(xb, wb, dyb)
+
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            dx, dw, db = run()
+    else:
+        dx, dw, db = run()
+    rdx, rdw, rdb = orc.linear_backward(x, w, dy)
+    check(dtype, dx, rdx, "dx")
+    check(dtype, dw, rdw, "dw")
+    check(dtype, db, rdb, "db")
+    if dtype == "bf16":  # gradients near zero next to the 2e-2 bound: also norm-wise
+        check_bf16_normwise(dw.to_host(), rdw, "dw")
+
+
+def test_linear_backward_strided_and_empty(dev, orc):
+    # x given transposed in memory (stride_xm 1, stride_xk M) and dy rows
+    # padded to 16 bytes (the RuntimeOp's backward_grad_output_row_stride):
+    # the generic kernel reads any strides
+    import ctypes
+    from teenygrad_amd._lib import check as chk, lib
+    rng = np.random.default_rng(11)
+    m, n, k, pad = 50, 21, 33, 24
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w = rng.standard_normal((n, k), dtype=np.float32)
+    dy = rng.standard_normal((m, n), dtype=np.float32)
+    dyp = np.zeros((m, pad), np.float32)
+    dyp[:, :n] = dy
+    # every device buffer stays referenced until the call has completed
+    xt, wb, dyb = dev.upload(np.ascontiguousarray(x.T)), dev.upload(w), dev.upload(dyp)
+    dx, dw, db = tg.Buffer(tg.f32, (m, k)), tg.Buffer(tg.f32, (n, k)), tg.Buffer(tg.f32, (n,))
+    chk(lib.teeny_linear_backward(xt.ptr, wb.ptr, dyb.ptr, dx.ptr, dw.ptr, db.ptr, m, n, k,
+                                  1, m, 1, k, pad, 1, k, 1, 1, k, 1, tg.f32.code, None))
+    rdx, rdw, rdb = orc.linear_backward(x, w, dy)
+    check_f32(dx.to_host(), rdx, "dx strided")
+    check_f32(dw.to_host(), rdw, "dw strided")
+    check_f32(db.to_host(), rdb, "db strided")
+    # M = 0: no rows, so dw and db are sums over nothing (zero); dx is empty
+    dw0, db0 = dev.upload(np.full((n, k), 7.0, np.float32)), dev.upload(np.full(n, 7.0, np.float32))
+    chk(lib.teeny_linear_backward(None, wb.ptr, None, None, dw0.ptr, db0.ptr, 0, n, k, k, 1, 1, k, n, 1,
+                                  k, 1, 1, k, 1, tg.f32.code, None))
+    assert not np.any(dw0.to_host()) and not np.any(db0.to_host())
+
+
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_linear_backward_runtime_op(dev, use_bias):
+    # LinearForward.pack_backward_args + backward_grid through
+    # "linear_backward_entry_point" (linear.rs:322-385), against the fixtures
+    import ctypes
+    from teenygrad_amd._lib import check as chk, lib
+    x = load_golden("linear/input.bin").reshape(64, 64)
+    w = load_golden("linear/weight.bin").reshape(48, 64)
+    dy = load_golden("linear/dy.bin").reshape(64, 48)
+    op = K.LinearForward(use_bias, 32, 32, 32, 8)
+    xb, wb, dyb = dev.upload(x), dev.upload(w), dev.upload(dy)
+    dx, dw = tg.Buffer(tg.f32, (64, 64)), tg.Buffer(tg.f32, (48, 64))
+    db = tg.Buffer(tg.f32, (48,))
+    packer = K.DispatchPacker()
+    op.pack_backward_args([(xb, [64, 64])], [wb], None, [64, 48], dyb, op.backward_grad_output_row_stride([64, 48]), [dx],
+                          [dw] + ([db] if use_bias else []), packer)
+    args, n = packer.array()
+    cg = (ctypes.c_int64 * 5)(*op.const_generics())
+    grid = (ctypes.c_uint32 * 3)(*op.backward_grid([[64, 64]], [64, 48]))
+    assert tuple(grid) == (2 * 2 * 2, 1, 1)
+    chk(lib.teeny_dispatch(op.backward_entry_point_name().encode(), cg, 5, args, n, grid, tg.f32.code, None))
+    check_f32(dx.to_host(), load_golden("linear/expected_dx.bin"), "dx")
+    check_f32(dw.to_host(), load_golden("linear/expected_dw.bin"), "dw")
+    if use_bias:
+        check_f32(db.to_host(), load_golden("linear/expected_db.bin"), "db")

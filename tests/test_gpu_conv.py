@@ -406,7 +406,7 @@ def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act, scratch):
 
 
 def test_w8a16_conv_config_batch32(dev, orc):
-    # 32 x 256 x 28 x 28, 3x3 p1: first and last image against the oracle
+    # 32 x 256 x 28 x 28, 3x3 p1: the whole output against the oracle
     B, C, H = 32, 256, 28
     rng = np.random.default_rng(0x7EE70004)
     x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
@@ -415,14 +415,8 @@ def test_w8a16_conv_config_batch32(dev, orc):
     got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), None, 1, 1).to_host()
     assert np.all(np.isfinite(from_bf16(got)))
     wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
-    for b in (0, B - 1):
-        ref = orc.conv2d_nhwc(x[b:b + 1], wdeq, None, stride=1, padding=1)
-        check_bf16(got[b:b + 1], ref, f"image {b}")
-    # one output pixel (all 256 channels) from every 64-row block of M = B*28*28
-    m = B * H * H
-    pix = np.arange(0, m, 64) + (np.arange(m // 64) * 29) % 64
-    ref = orc.conv2d_nhwc_pixels(x, wdeq, pix, None, stride=1, padding=1)
-    check_bf16(got.reshape(m, C)[pix], ref, f"{pix.size} pixels, one per 64-row block")
+    ref = orc.conv2d_nhwc(x, wdeq, None, stride=1, padding=1)
+    check_bf16(got, ref, "all 32 images")
 
 
 @pytest.mark.parametrize("scratch", ["none", "workspace"])

@@ -183,11 +183,14 @@ def test_w8a16_small(dev, orc, m, n, k, act, scratch):
     check_bf16(got, ref, "w8a16")
 
 
-@pytest.mark.parametrize("k,n", [(4096, 11008), (11008, 4096)])
+_CONFIG_REF = {}
+
+
 @pytest.mark.parametrize("scratch", ["none", "workspace"])
+@pytest.mark.parametrize("k,n", [(4096, 11008), (11008, 4096)])
 def test_w8a16_config(dev, orc, k, n, scratch):
     # M = 4096 tokens; weights N(0, 0.02) quantised per output channel on the GPU
-    # (bit-exact with the oracle); output rows 0..31 and M-32..M-1 vs the oracle
+    # (bit-exact with the oracle); the whole [M, N] output against the oracle
     m = 4096
     rng = np.random.default_rng(0x7EE70005 + k)
     x = rb(rng.standard_normal((m, k), dtype=np.float32))
@@ -203,15 +206,13 @@ def test_w8a16_config(dev, orc, k, n, scratch):
     assert need == 0, need
     need = 1 << 20
     y = with_scratch(dev, scratch, need, lambda: K.w8a16_linear(dev.upload(to_bf16(x), tg.bf16), qg, sg).to_host())
-    assert np.all(np.isfinite(from_bf16(y)))
-    wdeq = orc.dequantize_affine(q, s, None, [n, k], "channel", 0)
-    for lo, hi in ((0, 32), (m - 32, m)):
-        ref = orc.linear(x[lo:hi], wdeq)
-        check_bf16(y[lo:hi], ref, f"rows {lo}..{hi}")
-    # one row from every 64-row block (each 256 x 256 and 128 x 128 row tile,
-    # and every wave's 64-row slice of one over the blocks), all N columns
-    rows = np.arange(0, m, 64) + (np.arange(m // 64) * 13) % 64
-    check_bf16(y[rows], orc.linear(x[rows], wdeq), f"{rows.size} rows, one per 64-row block")
+    if (k, n) not in _CONFIG_REF:  # one oracle run per shape, shared by both scratch modes
+        _CONFIG_REF.clear()
+        wdeq = orc.dequantize_affine(q, s, None, [n, k], "channel", 0)
+        _CONFIG_REF[(k, n)] = orc.linear(x, wdeq)
+    ref = _CONFIG_REF[(k, n)]
+    for lo in range(0, m, 1024):
+        check_bf16(y[lo:lo + 1024], ref[lo:lo + 1024], f"rows {lo}..{lo + 1023}")
 
 
 # ── teeny-quant on the GPU: bit-exact with the oracle ──────────────────────

@@ -3,10 +3,8 @@ bf16 NHWC with BN folded into a bias and ReLU fused where the network has it
 (the ResNet-50 conv stack workload), each at its own shape and tile plan,
 with and without the stream workspace the benchmark attaches.
 
-Per layer: images 0 and 63 are checked whole against the oracle, plus one
-output pixel (all channels) drawn from every 128-row tile of the implicit
-GEMM's M = B*OH*OW, so that every workgroup's row tile and every column tile
-is compared; the whole output must be finite.
+Per layer, the whole output (all 64 images, every pixel and channel) is
+checked against the oracle, for each scratch mode.
 Reference semantics: conv2d_bias_forward, kernels/teeny-kernels/src/nn/conv/
 conv2d.rs:642-764 (NCHW there; NHWC here, an exact transpose)."""
 import numpy as np
@@ -22,13 +20,6 @@ pytestmark = pytest.mark.gpu
 
 BATCH = 64
 LAYERS = synthetic.resnet50_convs()
-
-
-def tile_samples(m, tile, rng):
-    """One index inside every `tile`-row block of [0, m)."""
-    starts = np.arange(0, m, tile, dtype=np.int64)
-    span = np.minimum(tile, m - starts)
-    return starts + (rng.random(starts.size) * span).astype(np.int64)
 
 
 @pytest.mark.parametrize("layer", LAYERS, ids=[l[0] for l in LAYERS])
@@ -55,16 +46,11 @@ def test_resnet50_layer_batch64(dev, orc, layer):
             outs["workspace"] = run()
     del xd
 
-    m = BATCH * oh * oh
-    pix = tile_samples(m, 128, rng)
-    ref_pix = orc.conv2d_nhwc_pixels(x, w, pix, b, stride=s, padding=p)
-    ref_img = {i: orc.conv2d_nhwc(x[i:i + 1], w, b, stride=s, padding=p) for i in (0, BATCH - 1)}
+    ref = orc.conv2d_nhwc(x, w, b, stride=s, padding=p)
     if relu:
-        ref_pix = orc.relu(ref_pix)
-        ref_img = {i: orc.relu(r) for i, r in ref_img.items()}
+        ref = orc.relu(ref)
+    del x
     for mode, y in outs.items():
         assert y.shape == (BATCH, oh, oh, cout)
-        assert np.all(np.isfinite(from_bf16(y))), f"{name} {mode}: non-finite output"
-        check_bf16(y.reshape(m, cout)[pix], ref_pix, f"{name} {mode}: {pix.size} sampled pixels")
-        for i, r in ref_img.items():
-            check_bf16(y[i:i + 1], r, f"{name} {mode}: image {i}")
+        for i0 in range(0, BATCH, 16):  # in image blocks, to bound the float64 temporaries
+            check_bf16(y[i0:i0 + 16], ref[i0:i0 + 16], f"{name} {mode}: images {i0}..{i0 + 15}")

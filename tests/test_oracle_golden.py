@@ -93,3 +93,18 @@ def test_linear_matches_fixture(orc, with_bias):
     got = orc.linear(x, w, b if with_bias else None)
     # fp32 accumulation is much tighter than the reference's TF32 bound
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-3)
+
+
+def test_linear_backward_matches_fixture(orc):
+    # test_linear.rs:434-626 — dx, dw, db against the committed fixtures
+    # (M=64, N=48, K=64); the reference's bound is TF32-sized (atol 0.1 +
+    # rtol 0.02), the fp32 oracle meets 1e-5 relative
+    x = load_golden("linear/input.bin").reshape(64, 64)
+    w = load_golden("linear/weight.bin").reshape(48, 64)
+    dy = load_golden("linear/dy.bin").reshape(64, 48)
+    dx, dw, db = orc.linear_backward(x, w, dy)
+    for got, name, shape in ((dx, "dx", (64, 64)), (dw, "dw", (48, 64)), (db, "db", (48,))):
+        want = load_golden(f"linear/expected_{name}.bin").reshape(shape)
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * float(np.abs(want).max()), err_msg=name)
+    _, _, none = orc.linear_backward(x, w, dy, use_bias=False)
+    assert none is None

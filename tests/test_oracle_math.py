@@ -291,3 +291,24 @@ def test_linear_closed_form(orc):
     want = x.astype(np.float64) @ w.astype(np.float64).T + b
     assert rel_inf(orc.linear(x, w, b), want) < 1e-5
     assert rel_inf(orc.linear(x, w, None), want - b) < 1e-5
+
+
+def test_linear_backward_closed_form(orc):
+    # dx = dy W, dw = dy^T x, db = column sums of dy, in float64; a transposed
+    # operand or a dropped bias gradient fails
+    x = RNG.normal(0, 1, (37, 50)).astype(np.float32)
+    w = RNG.normal(0, 1, (23, 50)).astype(np.float32)
+    dy = RNG.normal(0, 1, (37, 23)).astype(np.float32)
+    x64, w64, dy64 = (a.astype(np.float64) for a in (x, w, dy))
+    dx, dw, db = orc.linear_backward(x, w, dy)
+    assert rel_inf(dx, dy64 @ w64) < 1e-5
+    assert rel_inf(dw, dy64.T @ x64) < 1e-5
+    assert rel_inf(db, dy64.sum(axis=0)) < 1e-5
+    # sensitivity: the forward's own contraction (x W^T) and a dw without the
+    # transpose of dy have different values
+    assert rel_inf(dw, (dy64.T @ x64)[::-1]) > 1e-2
+    assert rel_inf(db, dy64.sum(axis=1)[:23]) > 1e-2
+    # the gradient of the forward: <dy, linear(x + e dx_dir)> is linear in e
+    e = RNG.normal(0, 1, x.shape)
+    lhs = np.sum(dy64 * (e @ w64.T))
+    assert abs(lhs - np.sum(dx * e)) <= 1e-4 * abs(lhs) + 1e-6
