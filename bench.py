@@ -45,6 +45,7 @@ run can be split per op.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -550,11 +551,15 @@ def bench_w8a16(ctx):
     tg, stream = ctx.tg, ctx.stream
     m = 4096
     rng = np.random.default_rng(0x7EE70005)
-    problems, host = [], []
+    problems, host, wdev = [], [], None
     for k, n in ((4096, 11008), (11008, 4096)):
         x = round_bf16(rng.standard_normal((m, k), dtype=np.float32))
         wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
-        q, s, _, _ = K.quantize_affine(ctx.dev.upload(wf), [n, k], "channel", 0)
+        wd = ctx.dev.upload(wf)
+        q, s, _, _ = K.quantize_affine(wd, [n, k], "channel", 0)
+        if wdev is None:
+            wdev = (wd, n, k)
+        del wd
         y = tg.Buffer(tg.bf16, (m, n))
         name = f"w8a16 {m}x{k}->{n}"
         problems.append((name, ctx.copies(upload_bf16(ctx, x), 2), ctx.copies(q, 2), s, [y, tg.Buffer(tg.bf16, (m, n))],
@@ -573,6 +578,24 @@ def bench_w8a16(ctx):
                   "traffic": load_traffic("w8a16_gemm", p[0]), "algorithmic_bytes": p[-2]} for p in problems}
     dom = max(per, key=per.get)
     fdom, bdom = [(p[-1], p[-2]) for p in problems if p[0] == dom][0]
+    # the quantizer that makes these weights (quantize_affine per output
+    # channel, fp32 [11008, 4096] -> int8 + scales), timed on its own
+    wq, qn, qk = wdev
+    wqs = ctx.copies(wq, 2)
+    qq = [tg.Buffer(tg.i8, (qn, qk)) for _ in range(2)]
+    qsc, qzp = tg.Buffer(tg.f32, (qn,)), tg.Buffer("i32", (qn,))
+    shape = (ctypes.c_int64 * 2)(qn, qk)
+    lib = tg._lib.lib
+    qfns = [lambda r=r: tg.check(lib.teeny_quantize_affine(wqs[r].ptr, shape, 2, 1, 0, 1, 1, 8, qq[r].ptr, qsc.ptr,
+                                                           qzp.ptr, None, stream.handle)) for r in range(2)]
+    qname = f"quantize_affine [{qn},{qk}]"
+    _, qper = ctx.measure([(qname, qfns)])
+    qbytes = 4 * qn * qk + qn * qk + 8 * qn
+    ops[qname] = {"us": round(qper[qname] * 1e3, 1), "GB/s": round(qbytes / (qper[qname] * 1e-3) / 1e9, 1),
+                  "frac": round(qbytes / (qper[qname] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": qbytes,
+                  "traffic": load_traffic("w8a16_gemm", qname),
+                  "note": "offline weight preparation, not part of the step: fp32 read + int8 written + scales"}
+    del wqs, qq
     cpu = None
     if not ctx.args.no_cpu:
         import oracle

@@ -231,7 +231,12 @@ def test_quant_known_answers(dev, case):
 RANDOM = [((64, 96), "channel", 0, 1, True, 8), ((64, 96), "channel", 1, 1, True, 8),
           ((64, 96), "tensor", 0, 1, False, 8), ((8, 5, 33), "group", 2, 8, True, 8),
           ((8, 5, 33), "group", 1, 2, False, 4), ((8, 5, 33), "group", 0, 3, True, 4),
-          ((256, 3, 3, 256), "channel", 0, 1, True, 8), ((3000, 17), "channel", 0, 1, False, 8)]
+          ((256, 3, 3, 256), "channel", 0, 1, True, 8), ((3000, 17), "channel", 0, 1, False, 8),
+          # contiguous groups split over several workgroups (rows of 40000 and a
+          # 100003-element tensor), groups of 7 and 5 (quads straddling two
+          # groups), and groups of 3 (the per-element kernel)
+          ((5, 40000), "channel", 0, 1, True, 8), ((100003,), "tensor", 0, 1, False, 8),
+          ((33, 7), "channel", 0, 1, True, 8), ((9, 5), "channel", 0, 1, False, 4), ((6, 3), "channel", 0, 1, True, 8)]
 
 
 @pytest.mark.parametrize("shape,gran,axis,gs,sym,bits", RANDOM)
