@@ -63,11 +63,16 @@ constexpr int dma_lds_bytes() {
 
 // BM x BN tile, NST LDS stages, MINW workgroups per CU; SPLIT: split-K
 // partial output when p.ws is set (a separate instantiation: the partial
-// store path alone costs the 256 x 256 tile spills).
-template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT>
+// store path alone costs the 256 x 256 tile spills).  WAVES_N: the four
+// waves as 2 x 2 blocks of the tile, or 1 x 4 (each wave all BM rows and a
+// quarter of the columns: with int8 weights every weight fragment is then
+// converted by one wave only, half the VALU work of the 2 x 2 layout, whose
+// two waves of a column block both convert it).
+template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT, int WAVES_N = 2>
 __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   constexpr int BK = kDmaBK;
-  constexpr int WM = BM / 2, WN = BN / 2;              // wave block (2 x 2 waves)
+  constexpr int WAVES_M = 4 / WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave block
   constexpr int MB = WM / 32, NB = WN / 32;            // 32 x 32 MFMA blocks per wave
   constexpr int H = MB * NB;                           // MFMA bundles per k-step
   constexpr int A_BYTES = BM * BK * 2;
@@ -86,7 +91,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
-  const int wm = w >> 1, wn = w & 1;  // wave block: rows wm*WM.. of m, wn*WN.. of n
+  const int wm = w / WAVES_N, wn = w % WAVES_N;  // wave block: rows wm*WM.. of m, wn*WN.. of n
 
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
@@ -320,7 +325,11 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
   // The bundle -> block maps are plain index arithmetic on the (unrolled)
   // bundle number, so every fragment index is a compile-time constant
   // (a run-time index would put the fragment set in scratch memory).
-  static_assert(H == 16 || (H == 8 && MB == 4 && NB == 2) || (H == 4 && MB == 2 && NB == 2),
+  //   H = 16, MB = 8, NB = 2 (256 x 256, waves 1 x 4): c1 quarter r of block
+  //            i at 8 i + 2 r + 1, qr = 8 + 8 i, xr = 16 + j, c0 quarters at
+  //            10 + 2 r (block 0) and 24 + 2 r (block 1)
+  static_assert((H == 16 && ((MB == 4 && NB == 4) || (MB == 8 && NB == 2))) || (H == 8 && MB == 4 && NB == 2) ||
+                    (H == 4 && MB == 2 && NB == 2),
                 "int8 schedule covers H = 4, 8, 16");
   constexpr int kC1 = H == 16 ? 4 : H == 8 ? 4 : 0, kC1Step = H == 16 ? 2 : 1;
   constexpr int kQr = H == 16 ? 16 : H == 8 ? 8 : 2;
@@ -344,7 +353,21 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
         dma_one(kt + NST - 1, b);
         if (b == A_LD - 1) advance_k();
       }
-      if constexpr (INT8B && H == 16) {
+      if constexpr (INT8B && H == 16 && MB == 8) {
+        if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
+        // k-step-1 conversions: block 0 at b = 1, 3, 5, 7, block 1 at 9 .. 15
+        // (first k-step-1 MFMAs of the blocks at b = 16 and 24)
+        if (b < 16 && (b & 1)) convert_q2(q[b >> 3], 1, b >> 3, (b >> 1) & 3, f);
+        // next k-tile's chunks, each after its block's k-step-1 conversion
+        if (more && b == 8) q[0] = read_q(nx, 0);
+        if (more && b == 16) q[1] = read_q(nx, 1);
+        // next k-tile's k-step-0 activations: slot j was last read at b = 8 + j
+        if (more && b >= 16 && b < 24) read_x(nx, 0, b - 16, f);
+        // next k-tile's k-step-0 conversions, after the last k-step-0 MFMA of
+        // the block (b = 7, 15) and its chunk read
+        if (more && b >= 10 && b <= 16 && !(b & 1)) convert_q2(q[0], 0, 0, (b - 10) >> 1, f);
+        if (more && b >= 24 && !(b & 1)) convert_q2(q[1], 0, 1, (b - 24) >> 1, f);
+      } else if constexpr (INT8B && H == 16) {
         if (b < MB) read_x(cu, 1, b, f);  // this k-tile's k-step 1
         if (b < 16) convert_q2(q[b >> 2], 1, b >> 2, b & 3, f);
         if (more && b >= 4 && b <= 16 && (b & 3) == 0) q[(b >> 2) - 1] = read_q(nx, (b >> 2) - 1);
@@ -516,28 +539,32 @@ inline bool big_gemm_fits(const GemmParams &p) {
          tiles_of(p, 256, 256) >= device_cu_count();
 }
 
-template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT>
+template <int BM, int BN, int NST, int MINW, bool INT8B, int AMODE, bool SPLIT, int WAVES_N = 2>
 inline void launch_dma_gemm(const GemmParams &p, hipStream_t s, int splits = 1) {
   constexpr int bytes = dma_lds_bytes<BM, BN, NST, INT8B>();
   static const bool attr_set = [] {
     return hipFuncSetAttribute(
-               reinterpret_cast<const void *>(&gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT>),
+               reinterpret_cast<const void *>(&gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT, WAVES_N>),
                hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
   }();
   (void)attr_set;
   const int grid = static_cast<int>(tiles_of(p, BM, BN)) * (SPLIT ? splits : 1);
-  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT>), dim3(grid), dim3(256), bytes, s,
-                     p);
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, NST, MINW, INT8B, AMODE, SPLIT, WAVES_N>), dim3(grid), dim3(256),
+                     bytes, s, p);
 }
 
 // The 256 x 256 kernel walks its tiles in groups of 8 along the slow
 // dimension: the 32 tiles an XCD runs at a time form an 8 x 4 block, whose
 // operand k-slices its L2 then serves several times (measured on the W8A16
 // shapes: 4096 -> 11008 425 -> 350 us, 11008 -> 4096 323 -> 317 us).
+// int8 weights take the 1 x 4 wave layout (each weight converted once per
+// workgroup): 4096 -> 11008 355 -> 345 us, 11008 -> 4096 327 -> 316 us,
+// interleaved on one box; bf16 weights keep 2 x 2 (fewer LDS bytes per MFMA).
 template <bool INT8B, int AMODE>
 inline void launch_big_gemm(GemmParams p, hipStream_t s) {
   p.group = 8;
-  launch_dma_gemm<256, 256, 4, 1, INT8B, AMODE, false>(p, s);
+  if constexpr (INT8B) launch_dma_gemm<256, 256, 4, 1, INT8B, AMODE, false, 4>(p, s);
+  else launch_dma_gemm<256, 256, 4, 1, INT8B, AMODE, false>(p, s);
 }
 
 }  // namespace teeny
