@@ -487,6 +487,10 @@ static S2DPlan s2d_plan(const ConvGeo &q) {
   return sp;
 }
 
+static bool stem_raw_ok(const ConvGeo &q, const void *x, const void *w, const void *y) {
+  return stem_raw_fits(q.B, q.Cin, q.Cout, q.H, q.W, q.OH, q.OW, q.KH, q.KW, q.SH, q.SW, q.PH, q.PW, q.G, x, w, y);
+}
+
 // How a groups == 1 bf16 NHWC conv maps onto the MFMA GEMM.
 enum ConvPath { kConvNoMfma, kConvPlain, kConvVec, kConvS2D, kConvScalarGemm };
 
@@ -517,6 +521,10 @@ static size_t conv_scratch_bytes(const ConvGeo &q) {
     case kConvVec: return gemm_scratch_bytes<INT8B, kAConvVec>(p);
     case kConvScalarGemm: return gemm_scratch_bytes<INT8B, kAConvScalar>(p);
     case kConvS2D: {
+      // (aligned operands assumed, as for every plan this reports)
+      if (stem_raw_ok(q, reinterpret_cast<const void *>(16), reinterpret_cast<const void *>(16),
+                      reinterpret_cast<const void *>(16)))
+        return 0;
       const S2DPlan sp = s2d_plan(q);
       const GemmParams p2 = conv_gemm_params(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, sp.g2);
       return sp.gemm_off + gemm_scratch_bytes<false, kAConvVec>(p2);
@@ -530,6 +538,12 @@ static size_t conv_scratch_bytes(const ConvGeo &q) {
 // is too small for the rewritten input and weights.
 static bool conv_s2d_mfma(const void *x, const void *w, const float *scale, const float *bias,
                           const bf16 *bias_bf16, void *y, const ConvGeo &q, int act, hipStream_t s, Scratch scr) {
+  // the RGB stem: the band kernel forms the space-to-depth input in LDS itself
+  if (stem_raw_ok(q, x, w, y)) {
+    launch_stem_raw(static_cast<const bf16 *>(x), static_cast<const bf16 *>(w), scale, bias, bias_bf16,
+                    static_cast<bf16 *>(y), q.B, q.H, q.OH, act, s);
+    return true;
+  }
   const S2DPlan sp = s2d_plan(q);
   if (scr.ptr == nullptr || scr.bytes < sp.gemm_off) return false;
   const ConvGeo &g2 = sp.g2;

@@ -48,8 +48,8 @@
 namespace teeny {
 
 struct BandParams {
-  const bf16 *x;  // [B, H, W, CIN]
-  const bf16 *w;  // [64, KH, KW, CIN]
+  const bf16 *x;  // [B, H, W, CIN]; raw-stem mode: the raw image [B, H, W, 3]
+  const bf16 *w;  // [64, KH, KW, CIN]; raw-stem mode: the raw 7x7 weights [64, 7, 7, 3]
   const float *scale, *bias;
   const bf16 *bias_bf16;
   bf16 *y;        // [B, OH, OW, 64]
@@ -80,22 +80,53 @@ struct BandShape {
   static_assert((WP / 16) % 2 == 1, "odd number of 16-byte units per weight row");
 };
 
-template <int CIN, int KH, int KW, int OWT, int RB, int NHB>
+// Raw-stem mode (RAWW > 0, the 7x7/2 stem over RAWW-pixel RGB rows): the
+// kernel reads the raw image itself and forms the space-to-depth halo in
+// LDS (see conv_band_kernel).  A band's halo rows hr = 0 .. HR-1 are s2d rows
+// oh0 + hr, i.e. raw rows 2 (oh0 + hr) + dy - 3, dy = 0, 1: 2 HR raw rows of
+// RAWW * 6 bytes, each staged as one zero 16-byte slot, the row, and two
+// zero slots (so the 12-byte window of any s2d column, read as four aligned
+// dwords, stays inside zeros where it leaves the image), after one zero
+// guard slot.
+template <int RAWW, int HR>
+struct RawShape {
+  static constexpr int DATA = RAWW * 6 / 16;                // 16-byte chunks of a raw row
+  static constexpr int ROW = DATA + 3;                      // slots per staged row
+  static constexpr int SLOTS = 1 + 2 * HR * ROW;            // guard + rows
+  static constexpr int INSTR = (SLOTS + 63) / 64;
+  static constexpr int BUF = INSTR * 1024;
+  static_assert(RAWW == 0 || RAWW * 6 % 16 == 0, "raw rows of whole 16-byte chunks");
+};
+
+template <int CIN, int KH, int KW, int OWT, int RB, int NHB, int RAWW = 0>
 constexpr int band_lds_bytes() {
   using S = BandShape<CIN, KH, KW, OWT, RB>;
+  if constexpr (RAWW > 0) {
+    // raw buffers, then one s2d halo buffer
+    return S::WBYTES + NHB * RawShape<RAWW, S::HR>::BUF + (S::HR * S::HC * S::CPP * 16 + 1023) / 1024 * 1024 + 1024 +
+           S::NW * S::STG;
+  }
   return S::WBYTES + NHB * S::HBUF + 1024 + S::NW * S::STG;
 }
 
-template <int CIN, int KH, int KW, int OWT, int RB, int NHB>
+template <int CIN, int KH, int KW, int OWT, int RB, int NHB, int RAWW = 0>
 __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv_band_kernel(BandParams p) {
   using S = BandShape<CIN, KH, KW, OWT, RB>;
-  constexpr int NW = S::NW, CC = S::CC, NCH = S::NCH, CPP = S::CPP, HC = S::HC, DI = S::DI;
+  using R = RawShape<RAWW, S::HR>;
+  constexpr bool RAW = RAWW > 0;
+  constexpr int NW = S::NW, CC = S::CC, NCH = S::NCH, CPP = S::CPP, HC = S::HC;
+  // DMA instructions per wave per stage: halo slots, or raw-row slots
+  constexpr int DI = RAW ? (R::INSTR + NW - 1) / NW : S::DI;
   constexpr int INFLIGHT = (NHB - 2) * DI;
   static_assert(NHB >= 2 && NHB <= 4 && INFLIGHT < 16, "halo stages / vmcnt field");
+  static_assert(!RAW || (CIN == 16 && KH == 4 && KW == 4 && NCH == 1), "raw mode: the 7x7/2 stem's s2d form");
+  constexpr int DBUF = RAW ? R::BUF : S::HBUF;  // bytes of one DMA stage buffer
+  constexpr int S2D_BYTES = (S::HR * HC * CPP * 16 + 1023) / 1024 * 1024;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *const wlds = smem;
-  char *const halo = smem + S::WBYTES;
-  char *const dummy = halo + NHB * S::HBUF;
+  char *const dbuf = smem + S::WBYTES;                       // DMA stage buffers
+  char *const s2d = dbuf + NHB * DBUF;                       // raw mode: the one s2d halo
+  char *const dummy = s2d + (RAW ? S2D_BYTES : 0);
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,7 +140,24 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   const int n_stages = my_units * NCH;
 
   // ── weights into LDS once (16-byte loads; before any DMA is in flight)
-  {
+  if constexpr (RAW) {
+    // the s2d form of the 7x7 weights, built here: tap (kh2, kw2) channel
+    // (2 dy + dx) 3 + c holds w[co][2 kh2 + dy][2 kw2 + dx][c] (zero past the
+    // 7x7 kernel, and for channels 12 .. 15)
+    for (int i = tid; i < S::COUT * 16; i += S::NT) {
+      const int co = i >> 4, tap = i & 15, kh2 = tap >> 2, kw2 = tap & 3;
+      bf16 e[16];
+#pragma unroll
+      for (int ch = 0; ch < 16; ++ch) {
+        const int q = ch / 3, cc = ch % 3, kh = 2 * kh2 + (q >> 1), kw = 2 * kw2 + (q & 1);
+        e[ch] = (ch < 12 && kh < 7 && kw < 7) ? p.w[((co * 7 + kh) * 7 + kw) * 3 + cc] : static_cast<bf16>(0.0f);
+      }
+      u32x4 v[2];
+      __builtin_memcpy(v, e, 32);
+      *reinterpret_cast<u32x4 *>(wlds + co * S::WP + 32 * tap) = v[0];
+      *reinterpret_cast<u32x4 *>(wlds + co * S::WP + 32 * tap + 16) = v[1];
+    }
+  } else {
     constexpr int CPR = S::K / 8;  // 16-byte chunks per weight row
     for (int i = tid; i < S::COUT * CPR; i += S::NT) {
       const int co = i / CPR, j = i % CPR;
@@ -151,14 +199,31 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   // holding data chunk (s % CPP) ^ swz(hc).  A wave's round r covers slots
   // [(r NW + w) 64, + 64); rounds past the halo write the dummy area.
   const __amdgpu_buffer_rsrc_t x_rsrc = buffer_rsrc(p.x, p.x_bytes);
-  const uint32_t halo0 = lds_address(halo), dummy0 = lds_address(dummy);
+  const uint32_t halo0 = lds_address(dbuf), dummy0 = lds_address(dummy);
   auto swz = [](int hc) { return CPP == 4 ? (hc >> 2) & 3 : 0; };
   auto dma_stage = [&](int st) __attribute__((always_inline)) {
     const bool live = st < n_stages;
     const int unit = wg + (st / NCH) * G, ch = st % NCH;
     const int b = unit / bands_per_img;
     const int oh0 = (unit % bands_per_img) * RB;
-    const uint32_t buf = halo0 + (st % NHB) * S::HBUF;
+    const uint32_t buf = halo0 + (st % NHB) * DBUF;
+    if constexpr (RAW) {
+      // raw rows 2 oh0 - 3 + row, row = 0 .. 2 HR - 1; slot 0 and each row's
+      // first and last two slots are zeros (out-of-extent offsets)
+#pragma unroll
+      for (int r = 0; r < DI; ++r) {
+        const int base = (r * NW + w) * 64;
+        const int s = base + lane - 1;
+        const int row = s / R::ROW, j = s % R::ROW - 1;
+        const int ih = 2 * oh0 - 3 + row;
+        const bool ok = live & (s >= 0) & (base + lane < R::SLOTS) & (j >= 0) & (j < R::DATA) &
+                        (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H));
+        const int off = ok ? static_cast<int>((static_cast<int64_t>(b) * p.H + ih) * (RAWW * 6) + 16 * j) : kOffNone;
+        const uint32_t dst = base < R::SLOTS ? buf + base * 16 : dummy0;
+        buffer_lds_dma16(x_rsrc, off, __builtin_amdgcn_readfirstlane(dst));
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < DI; ++r) {
       const int base = (r * NW + w) * 64;  // wave-uniform
@@ -180,8 +245,32 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   const int px = 32 * w + c;
   const int pr = px / OWT, pc = px % OWT;
   f32x16 acc[2] = {zero16(), zero16()};
+  // raw mode: s2d halo pixel (hr, hc) from its two raw rows 2 hr + dy: the
+  // 12 bytes (two pixels of three channels) of raw columns 2 hc - 3, 2 hc - 2
+  // of each row, read as four aligned dwords and shifted by a half-word,
+  // then four zero words: channels (2 dy + dx) 3 + c, 12 .. 15 zero
+  auto repack = [&](int st) __attribute__((always_inline)) {
+    const char *rb = dbuf + (st % NHB) * DBUF + 16;  // row 0 slot 0 (past the guard)
+    for (int px = tid; px < S::HR * HC; px += S::NT) {
+      const int hr = px / HC, hc = px % HC;
+      uint32_t o[6];
+#pragma unroll
+      for (int dy = 0; dy < 2; ++dy) {
+        // window start: row slot 1 (the data) + 6 (2 hc - 3) bytes = 12 hc + 16 - 18
+        const uint32_t *d = reinterpret_cast<const uint32_t *>(rb + (2 * hr + dy) * (R::ROW * 16) + 12 * hc - 4);
+        const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3];
+        o[3 * dy] = __builtin_amdgcn_alignbit(d1, d0, 16);
+        o[3 * dy + 1] = __builtin_amdgcn_alignbit(d2, d1, 16);
+        o[3 * dy + 2] = __builtin_amdgcn_alignbit(d3, d2, 16);
+      }
+      char *dst = s2d + px * 32;
+      *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4 *>(dst + 16) = u32x4{o[4], o[5], 0u, 0u};
+    }
+  };
+
   auto compute_stage = [&](int st) __attribute__((always_inline)) {
-    const char *hb = halo + (st % NHB) * S::HBUF;
+    const char *hb = RAW ? s2d : dbuf + (st % NHB) * S::HBUF;
     const int ch = st % NCH;
     constexpr int HS = CC / 16;  // k-steps per tap in a chunk
     constexpr int NKS = KH * KW * HS;
@@ -283,6 +372,11 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
     __syncthreads();
     // every wave is past stage st-1, whose buffer the DMA of st+NHB-1 reuses
     dma_stage(st + NHB - 1);
+    if constexpr (RAW) {
+      // every wave is past stage st-1's MFMAs too: the s2d halo is free
+      repack(st);
+      __syncthreads();
+    }
     compute_stage(st);
     if (st % NCH == NCH - 1) {
       const int unit = wg + (st / NCH) * G;
@@ -337,6 +431,51 @@ inline void launch_band(const GemmParams &p, int act, hipStream_t s) {
   const int units = b.B * (p.OH / RB);
   const int grid = std::min(units, device_cu_count());
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(BandShape<CIN, KH, KW, OWT, RB>::NT), bytes, s,
+                     b);
+}
+
+// The 7x7 stride-2 pad-3 RGB stem (3 -> 64 channels, 224-pixel rows, 112
+// output columns) straight from the raw image and raw weights: the band
+// kernel's raw-stem mode, no space-to-depth pass and no scratch.  x [B, H,
+// 224, 3], w [64, 7, 7, 3], y [B, OH, 112, 64], OH even.
+constexpr int kStemW = 224, kStemRB = 2, kStemNHB = 3;
+inline bool stem_raw_fits(int B, int Cin, int Cout, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW,
+                          int PH, int PW, int G, const void *x, const void *w, const void *y) {
+  return Cin == 3 && Cout == 64 && W == kStemW && OW == 112 && KH == 7 && KW == 7 && SH == 2 && SW == 2 && PH == 3 &&
+         PW == 3 && G == 1 && OH % kStemRB == 0 && OH == (H + 2 * PH - KH) / SH + 1 && B > 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 1) == 0 &&
+         (reinterpret_cast<uintptr_t>(y) & 15) == 0 && static_cast<int64_t>(B) * H * W * 3 * 2 < 0x7fffffff &&
+         static_cast<int64_t>(B) * OH * OW * 64 * 2 < 0x7fffffff;
+}
+
+inline void launch_stem_raw(const bf16 *x, const bf16 *w, const float *scale, const float *bias,
+                            const bf16 *bias_bf16, bf16 *y, int B, int H, int OH, int act, hipStream_t s) {
+  constexpr int bytes = band_lds_bytes<16, 4, 4, 112, kStemRB, kStemNHB, kStemW>();
+  static_assert(bytes <= 160 * 1024, "LDS");
+  auto kern = &conv_band_kernel<16, 4, 4, 112, kStemRB, kStemNHB, kStemW>;
+  static const bool attr_set = [kern] {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               bytes) == hipSuccess;
+  }();
+  (void)attr_set;
+  BandParams b{};
+  b.x = x;
+  b.w = w;
+  b.scale = scale;
+  b.bias = bias;
+  b.bias_bf16 = bias_bf16;
+  b.y = y;
+  b.B = B;
+  b.H = H;
+  b.W = kStemW;
+  b.OH = OH;
+  b.PH = 3;
+  b.PW = 3;
+  b.act = act;
+  b.x_bytes = static_cast<int>(static_cast<int64_t>(B) * H * kStemW * 3 * 2);
+  const int units = B * (OH / kStemRB);
+  const int grid = std::min(units, device_cu_count());
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(BandShape<16, 4, 4, 112, kStemRB>::NT), bytes, s,
                      b);
 }
 

@@ -223,8 +223,11 @@ BAND_CASES = [
     (2, 58, 58, 64, 64, 3, 1, 0, "gelu", "bias"),    # no padding: a 58-wide input for 56 outputs
     (2, 56, 56, 64, 64, 3, 1, 1, "silu", "bn"),      # folded BatchNorm scale / shift
     (1, 56, 56, 64, 64, 3, 1, 1, None, None),        # no bias
-    (2, 224, 224, 3, 64, 7, 2, 3, "relu", "bias"),   # the stem through its space-to-depth form
+    (2, 224, 224, 3, 64, 7, 2, 3, "relu", "bias"),   # the stem: raw rows, space-to-depth formed in LDS
     (1, 224, 224, 3, 64, 7, 2, 3, "gelu", "bn"),
+    (3, 100, 224, 3, 64, 7, 2, 3, "silu", "bias"),   # the raw stem on a short image (OH 50)
+    (2, 101, 224, 3, 64, 7, 2, 3, "relu", "bias"),   # odd OH: the space-to-depth pass + band kernel
+    (1, 64, 96, 3, 64, 7, 2, 3, None, "bias"),       # another width: the space-to-depth pass
 ]
 
 
@@ -259,13 +262,9 @@ def test_bf16_nhwc_band(dev, orc, case):
         return ref if act is None else {"relu": orc.relu, "silu": orc.silu, "gelu": orc.gelu}[act](ref)
 
     assert got.shape == (B, oh, ow, Cout)
-    assert np.all(np.isfinite(from_bf16(got)))
-    m = B * oh * ow
-    starts = np.arange(0, m, 64)
-    pix = starts + (rng.random(starts.size) * np.minimum(64, m - starts)).astype(np.int64)
-    check_bf16(got.reshape(m, Cout)[pix], finish(orc.conv2d_nhwc_pixels(x, w, pix, bias, stride=s, padding=p)),
-               f"{pix.size} sampled pixels")
-    check_bf16(got[B - 1:B], finish(orc.conv2d_nhwc(x[B - 1:B], w, bias, stride=s, padding=p)), f"image {B - 1}")
+    check_bf16(got, finish(orc.conv2d_nhwc(x, w, bias, stride=s, padding=p)), "all images")
+    if Cin == 3 and W == 224 and oh % 2 == 0:
+        assert need == 0, need  # the raw stem needs no space-to-depth scratch
 
 
 TILE_CASES = [

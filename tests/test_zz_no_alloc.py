@@ -5,7 +5,8 @@ Called through the C ABI and compared with teeny_conv2d_bias_forward given a
 stream workspace (the same plan and kernels, so the outputs are bit-identical)
 and with the oracle on sampled output pixels, for the two scratch users: the
 split-K partial sums of a deep 3x3 conv on a small grid, and the
-space-to-depth copy of the 3-channel stride-2 stem.  Each runs twice in a
+space-to-depth copy of a 3-channel stride-2 7x7 conv (the 224-wide RGB stem
+itself forms that copy in LDS and needs no scratch).  Each runs twice in a
 row, the second call on a smaller input, so the second reads none of the
 first call's leftovers."""
 import ctypes
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
 
 # (B, C_IN, C_OUT, H, K, stride, pad): first the larger input, then the smaller
 SPLIT_K = [(64, 512, 512, 7, 3, 1, 1), (2, 512, 512, 7, 3, 1, 1)]
-S2D = [(64, 3, 64, 224, 7, 2, 3), (3, 3, 64, 61, 7, 2, 3)]
+S2D = [(16, 3, 64, 160, 7, 2, 3), (3, 3, 64, 61, 7, 2, 3)]
 
 
 def make(shape, seed):
@@ -67,3 +68,9 @@ def test_noalloc_matches_workspace_entry(dev, orc, pair):
         pix = np.arange(0, m, 128) + (np.arange(-(-m // 128)) * 37) % np.minimum(128, m - np.arange(0, m, 128))
         ref = orc.relu(orc.conv2d_nhwc_pixels(from_bf16(x), from_bf16(w), pix, from_bf16(b), stride=s, padding=p))
         check_bf16(got.reshape(m, cout)[pix], ref, f"call {i + 1} {shape}")
+
+
+def test_raw_stem_needs_no_scratch():
+    # the 224-wide stem reads the raw image and forms the space-to-depth
+    # input in LDS: no workspace, so the no-allocation entry takes it too
+    assert K.conv2d_workspace_size((64, 224, 224, 3), (64, 7, 7, 3), 2, 3, 1, tg.bf16, "nhwc") == 0
