@@ -1,7 +1,7 @@
 // Row-band convolution for stride-1 bf16 NHWC convs with 64 output channels
 // whose whole weight tensor fits in LDS (the 56x56 3x3 64 -> 64 ResNet
 // layers; the space-to-depth form of the 7x7/2 stem, 4x4 taps over 16
-// channels):
+// channels, which the raw-stem mode below forms in LDS from the RGB image):
 //
 //   y[b, oh, ow, co] = act( scale[co] * sum_{kh, kw, ci} x[b, oh - PH + kh, ow - PW + kw, ci]
 //                                        * w[co, kh, kw, ci] + bias[co] )
@@ -27,6 +27,15 @@
 // chunk q of halo column hc at position q ^ ((hc >> 2) & 3) when CC = 32 (a
 // fragment read touches 8 consecutive columns per quarter-wave; unswizzled,
 // columns hc and hc + 4 share banks).
+//
+// Raw-stem mode (RAWW > 0): the DMA stages the band's raw RGB rows (2 of
+// them per space-to-depth row) instead of a precomputed space-to-depth
+// tensor; once a stage has landed, every thread rebuilds the s2d halo pixels
+// from them (two 12-byte raw windows per pixel, shifted into place with
+// alignbit), a second barrier publishes the halo, and the MFMA side is the
+// same.  The weights' s2d form is also built at start-up from the raw 7x7
+// weights.  This replaces a separate repack pass that wrote and re-read a
+// 27 MB space-to-depth copy of the batch-64 input (stem 50 -> 41 us).
 //
 // Pipeline: NHB halo buffers, the DMA NHB - 1 chunk stages ahead of the
 // MFMAs, one barrier per stage (a stage's DMA is issued after the barrier
