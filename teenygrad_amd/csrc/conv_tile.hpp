@@ -15,8 +15,11 @@
 // channels; per 32-channel chunk of C_IN, one LDS-DMA pass brings the rows'
 // input with its halo, (RB + KH - 1) x (OW + KW - 1) pixels (padding read as
 // zeros through out-of-extent buffer offsets), and the chunk's BN x KH x KW
-// x 32 weights; all taps are then read from LDS.  Two stages: the next
-// chunk's DMA runs under the current chunk's MFMAs.
+// x 32 weights; all taps are then read from LDS.  Three stages: the DMA of
+// the chunk after next is issued before the current chunk's MFMAs, so two
+// passes are in flight (with one, each chunk waited out a whole L2 round
+// trip: the 14x14 layers' DMA skeleton alone, without MFMAs or fragment
+// reads, took 22 of their 25.7 us).
 //
 // Seven waves; wave w owns pixels 32 w .. 32 w + 31 of the band (the last
 // wave's pixels past 196 read the last pixel's window and are not stored)
@@ -27,7 +30,8 @@
 // slot (an odd number of 16-byte units per row: conflict-free fragment
 // reads of consecutive rows); halo pixels of 4 x 16 bytes with chunk q of
 // halo column hc at position q ^ ((hc >> 2) & 3).  Epilogue through a
-// per-wave 4 KiB LDS slice, 64 channels at a time, written back as whole
+// per-wave 4 KiB LDS slice of the stage buffer the unit's last chunk used
+// (after a barrier), 64 channels at a time, written back as whole
 // 128-byte segments of the pixels' rows; the vmcnt waits count the
 // epilogue's stores (operations retire in issue order), so they stay in
 // flight.
@@ -61,11 +65,14 @@ struct TileShape {
   static constexpr int WSLOTS = BN * RS;
   static constexpr int HINSTR = (HSLOTS + 63) / 64, WINSTR = (WSLOTS + 63) / 64;
   static constexpr int INSTR = HINSTR + WINSTR;  // DMA instructions per stage (workgroup)
-  static constexpr int DI = (INSTR + NW - 1) / NW;  // per wave (the excess write a dummy area)
+  static constexpr int DI = (INSTR + NW - 1) / NW;  // per wave (the excess repeat the first ones)
   static constexpr int HBYTES = HINSTR * 1024, WBYTES = WINSTR * 1024;
   static constexpr int STAGE = HBYTES + WBYTES;
   static constexpr int STG = 4096;               // epilogue slice per wave
-  static constexpr int LDS = 2 * STAGE + 1024 + NW * STG + 2 * BN * 4;
+  static constexpr int NSTG = 3;                 // LDS stages: two DMA passes in flight
+  static constexpr int LDS = NSTG * STAGE + 2 * BN * 4;
+  static_assert(NW * STG <= STAGE, "epilogue slices fit one stage buffer");
+  static_assert(DI * NW - INSTR <= INSTR, "excess DMA instructions repeat real ones");
   static_assert(RS % 2 == 1, "odd number of 16-byte units per weight row");
   static_assert(BN % 64 == 0 && NW <= 16, "tile");
   static_assert(LDS <= 160 * 1024, "LDS");
@@ -76,14 +83,12 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
   constexpr int EPI_STORES = 4 * (BN / 64);
-  static_assert(EPI_STORES < 16, "vmcnt field");
+  static_assert(DI + 2 * EPI_STORES < 64, "vmcnt field");
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  char *const dummy = smem + 2 * S::STAGE;
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  char *const stg = dummy + 1024 + w * S::STG;
-  float *const cmul = reinterpret_cast<float *>(dummy + 1024 + NW * S::STG);
+  float *const cmul = reinterpret_cast<float *>(smem + S::NSTG * S::STAGE);
   float *const cadd = cmul + BN;
 
   const int bands_per_img = p.OH / RB;
@@ -105,23 +110,26 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
 
   const __amdgpu_buffer_rsrc_t x_rsrc = buffer_rsrc(p.x, p.x_bytes);
   const __amdgpu_buffer_rsrc_t w_rsrc = buffer_rsrc(p.w, p.w_bytes);
-  const uint32_t smem0 = lds_address(smem), dummy0 = lds_address(dummy);
+  const uint32_t smem0 = lds_address(smem);
   const int K = KH * KW * p.Cin;
   constexpr int ES = INT8B ? 1 : 2;  // bytes per weight element
-  // DMA of stage st (chunk st % nch of its unit) into stage buffer st % 2:
+  // DMA of stage st (chunk st % nch of its unit) into stage buffer st % 3:
   // instructions r NW + w; the first HINSTR fill the halo, the next WINSTR
-  // the weights, the rest go to the dummy area.
-  auto dma_stage = [&](int st) __attribute__((always_inline)) {
+  // the weights, and the excess ones (so that every wave issues DI) repeat
+  // the first ones: the same bytes to the same place.  Each lane's source
+  // offsets for the DMA cursor's unit are computed once, at its first chunk
+  // (kOffNone for padding, pad slots and past the last unit); a chunk adds
+  // its channel offset, which keeps kOffNone beyond every extent.
+  int dma_off[DI];
+  auto dma_unit = [&](int st) __attribute__((always_inline)) {
     const bool live = st < n_stages;
     int b, oh0, n0;
     unit_of(st, b, oh0, n0);
-    const int c0 = (st % nch) * 32;
-    const uint32_t buf = smem0 + (st & 1) * S::STAGE;
 #pragma unroll
     for (int r = 0; r < DI; ++r) {
-      const int ins = r * NW + w;  // wave-uniform
+      const int ins0 = r * NW + w;  // wave-uniform
+      const int ins = ins0 < S::INSTR ? ins0 : ins0 - S::INSTR;
       int off = kOffNone;
-      uint32_t dst = dummy0;
       if (ins < S::HINSTR) {
         const int s = ins * 64 + lane;
         const int pix = s >> 2, pos = s & 3;
@@ -131,17 +139,28 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
                         (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
         if (ok)
           off = static_cast<int>(((static_cast<int64_t>(b) * p.H + ih) * p.W + iw) * p.Cin * 2 +
-                                 (c0 + 8 * (pos ^ ((hc >> 2) & 3))) * 2);
-        dst = buf + ins * 1024;
-      } else if (ins < S::INSTR) {
+                                 16 * (pos ^ ((hc >> 2) & 3)));
+      } else {
         const int s = (ins - S::HINSTR) * 64 + lane;
         const int n = s / S::RS, j = s % S::RS;
         const int tap = j / S::QT, q = j % S::QT;
         const bool ok = live & (s < S::WSLOTS) & (j < S::RS - 1);
-        if (ok) off = static_cast<int>((static_cast<int64_t>(n0 + n) * K + tap * p.Cin + c0) * ES + 16 * q);
-        dst = buf + S::HBYTES + (ins - S::HINSTR) * 1024;
+        if (ok) off = static_cast<int>((static_cast<int64_t>(n0 + n) * K + tap * p.Cin) * ES + 16 * q);
       }
-      buffer_lds_dma16(ins < S::HINSTR ? x_rsrc : w_rsrc, off, __builtin_amdgcn_readfirstlane(dst));
+      dma_off[r] = off;
+    }
+  };
+  auto dma_stage = [&](int st) __attribute__((always_inline)) {
+    if (st % nch == 0) dma_unit(st);
+    const int c0 = (st % nch) * 32;
+    const uint32_t buf = smem0 + (st % S::NSTG) * S::STAGE;
+#pragma unroll
+    for (int r = 0; r < DI; ++r) {
+      const int ins0 = r * NW + w;  // wave-uniform
+      const int ins = ins0 < S::INSTR ? ins0 : ins0 - S::INSTR;
+      const bool halo = ins < S::HINSTR;
+      const uint32_t dst = halo ? buf + ins * 1024 : buf + S::HBYTES + (ins - S::HINSTR) * 1024;
+      buffer_lds_dma16(halo ? x_rsrc : w_rsrc, dma_off[r] + c0 * (halo ? 2 : ES), __builtin_amdgcn_readfirstlane(dst));
     }
   };
 
@@ -175,12 +194,15 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
       return q;
     }
   };
-  // One chunk: KH*KW taps x 2 k-steps.  The fragments of k-step ks + 1 are
-  // read while k-step ks multiplies; a scheduling fence per k-step keeps the
-  // compiler from hoisting every read of the unrolled loop (the int8 kernel
-  // then held ~480 registers).
+  // One chunk: KH*KW taps x 2 k-steps.  The fragments of k-step ks + kLA
+  // are read while k-step ks multiplies (a window of kLA + 1 fragment sets):
+  // with one k-step of lookahead every k-step waited for its reads behind a
+  // single MFMA.  A scheduling fence per k-step keeps the compiler from
+  // hoisting every read of the unrolled loop (the int8 kernel then held ~480
+  // registers).
+  constexpr int kLA = 2, kWin = kLA + 1;
   auto compute_stage = [&](int st) __attribute__((always_inline)) {
-    const char *hb = smem + (st & 1) * S::STAGE;
+    const char *hb = smem + (st % S::NSTG) * S::STAGE;
     const char *wb = hb + S::HBYTES;
     constexpr int NKS = KH * KW * 2;
     auto xread = [&](int ks) __attribute__((always_inline)) {
@@ -189,23 +211,21 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
       const int hc = pc + kw;
       return *reinterpret_cast<const bf16x8 *>(hb + ((pr + kh) * HC + hc) * 64 + 16 * ((2 * h + g) ^ ((hc >> 2) & 3)));
     };
-    bf16x8 xa = xread(0), xb;
-    wraw_t wa[NB], wn[NB];
+    bf16x8 xw[kWin];
+    wraw_t ww[kWin][NB];
+    auto fetch = [&](int ks) __attribute__((always_inline)) {
+      xw[ks % kWin] = xread(ks);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) wa[i] = wread(wb, i, 0, 0);
+      for (int i = 0; i < NB; ++i) ww[ks % kWin][i] = wread(wb, i, ks >> 1, ks & 1);
+    };
+#pragma unroll
+    for (int ks = 0; ks < kLA; ++ks) fetch(ks);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      if (ks + 1 < NKS) {
-        xb = xread(ks + 1);
+      if (ks + kLA < NKS) fetch(ks + kLA);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) wn[i] = wread(wb, i, (ks + 1) >> 1, (ks + 1) & 1);
-      }
-#pragma unroll
-      for (int i = 0; i < NB; ++i) acc[i] = mfma32x32x16(wconv(wa[i]), xa, acc[i]);
+      for (int i = 0; i < NB; ++i) acc[i] = mfma32x32x16(wconv(ww[ks % kWin][i]), xw[ks % kWin], acc[i]);
       __builtin_amdgcn_sched_barrier(0);
-      xa = xb;
-#pragma unroll
-      for (int i = 0; i < NB; ++i) wa[i] = wn[i];
     }
   };
 
@@ -221,6 +241,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   auto epilogue = [&](int st, auto sig) __attribute__((always_inline)) {
     int b, oh0, n0;
     unit_of(st, b, oh0, n0);
+    char *const stg = smem + (st % S::NSTG) * S::STAGE + w * S::STG;
     const int64_t pix0 = (static_cast<int64_t>(b) * p.OH + oh0) * OWT;  // the band's first pixel
 #pragma unroll
     for (int hp = 0; hp < NB / 2; ++hp) {
@@ -294,22 +315,29 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   __syncthreads();
 
   dma_stage(0);
-  unsigned epi_prev = 0;  // whether the previous iteration ended an epilogue
+  dma_stage(1);
+  // whether iterations st-1 and st-2 ended a unit (issued epilogue stores)
+  int epi1 = 0, epi2 = 0;
   for (int st = 0; st < n_stages; ++st) {
-    // stage st landed: allow the epilogue stores issued after its DMA
-    if (epi_prev) __builtin_amdgcn_s_waitcnt(0xF70 | EPI_STORES);
-    else __builtin_amdgcn_s_waitcnt(0xF70);
+    // stage st landed; issued after its DMA and left in flight: stage st+1's
+    // DMA and the epilogue stores of the last two iterations
+    const int epis = epi1 + epi2;
+    if (epis == 0) __builtin_amdgcn_s_waitcnt(vm_wait(DI));
+    else if (epis == 1) __builtin_amdgcn_s_waitcnt(vm_wait(DI + EPI_STORES));
+    else __builtin_amdgcn_s_waitcnt(vm_wait(DI + 2 * EPI_STORES));
     __syncthreads();
-    // every wave is past stage st-1, whose buffer stage st+1 reuses
-    dma_stage(st + 1);
+    // every wave is past stage st-1, whose buffer stage st+2 reuses
+    dma_stage(st + 2);
     compute_stage(st);
-    epi_prev = 0;
+    epi2 = epi1;
+    epi1 = 0;
     if (st % nch == nch - 1) {
+      __syncthreads();  // every wave has read stage st's buffer: the epilogue slices reuse it
       if (ea.sig) epilogue(st, std::true_type{});
       else epilogue(st, std::false_type{});
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[i] = zero16();
-      epi_prev = 1;
+      epi1 = 1;
       if (st + 1 < n_stages) {
         int b2, oh2, n2, b1, oh1, n1;
         unit_of(st, b1, oh1, n1);

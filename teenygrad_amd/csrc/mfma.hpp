@@ -35,6 +35,11 @@ __device__ __forceinline__ uint32_t lds_address(const void *p) {
 // the wave's LDS base and is restored afterwards.  Issued from inline
 // assembly, so the compiler neither tracks it (the caller waits on vmcnt
 // itself) nor lets it degrade its own LDS-read waits to lgkmcnt(0).
+// s_waitcnt immediate that waits until at most n vector memory operations
+// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and
+// lgkmcnt left at their maxima, i.e. not waited for).
+constexpr int vm_wait(int n) { return 0xF70 | (n & 15) | ((n >> 4) << 14); }
+
 __device__ __forceinline__ void buffer_lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, uint32_t lds) {
   uint32_t saved;
   asm volatile(

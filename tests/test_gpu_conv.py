@@ -277,6 +277,11 @@ TILE_CASES = [
     (5, 14, 14, 256, 256, 1, "relu", "bias", False),   # the 14x14 ResNet 3x3 at a ragged batch
     (2, 14, 14, 64, 128, 1, "gelu", "bn", False),      # two channel tiles, folded BatchNorm
     (2, 16, 16, 96, 64, 0, None, None, False),         # no padding: 16 -> 14, three chunks
+    # more units than workgroups (one per CU): workgroups walk several bands,
+    # with one chunk per band (every stage ends a band, and the channel tile
+    # changes between a workgroup's bands) or two
+    (90, 14, 14, 32, 192, 1, "silu", None, False),
+    (140, 14, 14, 64, 128, 1, "relu", "bias", False),
     (3, 28, 28, 128, 128, 1, "relu", "bias", False),   # the 28x28 ResNet 3x3
     (1, 28, 28, 32, 192, 1, "silu", None, False),      # one chunk, three channel tiles
     (3, 28, 28, 256, 256, 1, None, "bias", True),      # the W8A16 conv at a ragged batch
