@@ -15,11 +15,9 @@
 // channels; per 32-channel chunk of C_IN, one LDS-DMA pass brings the rows'
 // input with its halo, (RB + KH - 1) x (OW + KW - 1) pixels (padding read as
 // zeros through out-of-extent buffer offsets), and the chunk's BN x KH x KW
-// x 32 weights; all taps are then read from LDS.  Three stages: the DMA of
-// the chunk after next is issued before the current chunk's MFMAs, so two
-// passes are in flight (with one, each chunk waited out a whole L2 round
-// trip: the 14x14 layers' DMA skeleton alone, without MFMAs or fragment
-// reads, took 22 of their 25.7 us).
+// x 32 weights; all taps are then read from LDS.  Three LDS stages where
+// they fit (the DMA of the chunk after next is issued before the current
+// chunk's MFMAs), else two.
 //
 // Seven waves; wave w owns pixels 32 w .. 32 w + 31 of the band (the last
 // wave's pixels past 196 read the last pixel's window and are not stored)
@@ -69,7 +67,8 @@ struct TileShape {
   static constexpr int HBYTES = HINSTR * 1024, WBYTES = WINSTR * 1024;
   static constexpr int STAGE = HBYTES + WBYTES;
   static constexpr int STG = 4096;               // epilogue slice per wave
-  static constexpr int NSTG = 3;                 // LDS stages: two DMA passes in flight
+  // LDS stages: three (two DMA passes in flight) where they fit, else two
+  static constexpr int NSTG = 3 * STAGE + 2 * BN * 4 <= 160 * 1024 ? 3 : 2;
   static constexpr int LDS = NSTG * STAGE + 2 * BN * 4;
   static_assert(NW * STG <= STAGE, "epilogue slices fit one stage buffer");
   static_assert(DI * NW - INSTR <= INSTR, "excess DMA instructions repeat real ones");
@@ -83,7 +82,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
   constexpr int EPI_STORES = 4 * (BN / 64);
-  static_assert(DI + 2 * EPI_STORES < 64, "vmcnt field");
+  static_assert((S::NSTG - 2) * DI + 2 * EPI_STORES < 64 && S::NSTG <= 3, "vmcnt field / wait cases");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, c = lane & 31;
@@ -314,30 +313,32 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   }
   __syncthreads();
 
-  dma_stage(0);
-  dma_stage(1);
-  // whether iterations st-1 and st-2 ended a unit (issued epilogue stores)
-  int epi1 = 0, epi2 = 0;
+  constexpr int AHEAD = S::NSTG - 1;  // DMA passes issued ahead of the stage computed
+#pragma unroll
+  for (int j = 0; j < AHEAD; ++j) dma_stage(j);
+  // bit k: iteration st-1-k ended a unit (issued epilogue stores)
+  unsigned epi_hist = 0;
   for (int st = 0; st < n_stages; ++st) {
-    // stage st landed; issued after its DMA and left in flight: stage st+1's
-    // DMA and the epilogue stores of the last two iterations
-    const int epis = epi1 + epi2;
-    if (epis == 0) __builtin_amdgcn_s_waitcnt(vm_wait(DI));
-    else if (epis == 1) __builtin_amdgcn_s_waitcnt(vm_wait(DI + EPI_STORES));
-    else __builtin_amdgcn_s_waitcnt(vm_wait(DI + 2 * EPI_STORES));
+    // stage st landed; issued after its DMA and left in flight: the DMA of
+    // the next AHEAD-1 stages and the epilogue stores of the last AHEAD
+    // iterations
+    const int epis = __builtin_popcount(epi_hist & ((1u << AHEAD) - 1));
+    constexpr int base = (AHEAD - 1) * DI;
+    if (epis == 0) __builtin_amdgcn_s_waitcnt(vm_wait(base));
+    else if (epis == 1) __builtin_amdgcn_s_waitcnt(vm_wait(base + EPI_STORES));
+    else __builtin_amdgcn_s_waitcnt(vm_wait(base + 2 * EPI_STORES));
     __syncthreads();
-    // every wave is past stage st-1, whose buffer stage st+2 reuses
-    dma_stage(st + 2);
+    // every wave is past stage st-1, whose buffer stage st+AHEAD reuses
+    dma_stage(st + AHEAD);
     compute_stage(st);
-    epi2 = epi1;
-    epi1 = 0;
+    epi_hist <<= 1;
     if (st % nch == nch - 1) {
       __syncthreads();  // every wave has read stage st's buffer: the epilogue slices reuse it
       if (ea.sig) epilogue(st, std::true_type{});
       else epilogue(st, std::false_type{});
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[i] = zero16();
-      epi1 = 1;
+      epi_hist |= 1u;
       if (st + 1 < n_stages) {
         int b2, oh2, n2, b1, oh1, n1;
         unit_of(st, b1, oh1, n1);
@@ -407,6 +408,10 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
   if constexpr (!INT8B) {
     if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) {
       launch_tile_conv<3, 3, 14, 14, 64, false>(p, act, s);
+      return true;
+    }
+    if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) {
+      launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s);
       return true;
     }
   }

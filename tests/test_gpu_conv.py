@@ -269,11 +269,10 @@ def test_bf16_nhwc_band(dev, orc, case):
 
 TILE_CASES = [
     # B, H, W, Cin, Cout, pad, act, post, int8: stride-1 bf16 3x3 convs with
-    # 14-wide outputs take the band-tiled kernel (a band of 196 output pixels x
-    # 64 channels per workgroup, input rows with their halo and the chunk's
-    # weights staged per 32 input channels); the 28-wide and int8 cases run
-    # the implicit GEMM, at the same shapes as the band-tiled kernel's other
-    # instantiations would
+    # 14- and 28-wide outputs take the band-tiled kernel (a band of 196 output
+    # pixels x 64 channels per workgroup, input rows with their halo and the
+    # chunk's weights staged per 32 input channels); the int8 cases run the
+    # implicit GEMM
     (5, 14, 14, 256, 256, 1, "relu", "bias", False),   # the 14x14 ResNet 3x3 at a ragged batch
     (2, 14, 14, 64, 128, 1, "gelu", "bn", False),      # two channel tiles, folded BatchNorm
     (2, 16, 16, 96, 64, 0, None, None, False),         # no padding: 16 -> 14, three chunks
@@ -284,6 +283,7 @@ TILE_CASES = [
     (140, 14, 14, 64, 128, 1, "relu", "bias", False),
     (3, 28, 28, 128, 128, 1, "relu", "bias", False),   # the 28x28 ResNet 3x3
     (1, 28, 28, 32, 192, 1, "silu", None, False),      # one chunk, three channel tiles
+    (30, 28, 28, 64, 192, 1, "relu", None, False),     # 360 bands x tiles: two per workgroup
     (3, 28, 28, 256, 256, 1, None, "bias", True),      # the W8A16 conv at a ragged batch
     (2, 28, 28, 64, 128, 1, "relu", None, True),
 ]
