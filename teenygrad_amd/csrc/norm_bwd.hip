@@ -19,9 +19,9 @@
 // non-temporal loads: LayerNorm backward 88.7 -> 86.3 us, RMSNorm 84.5 ->
 // 80.1 us at [16384, 4096] bf16) before the current row's reductions, which are DPP wave sums plus one LDS exchange (one
 // barrier per row: each register set has its own LDS slot).  At the end each
-// workgroup writes its column partials to the stream workspace and two
-// small passes add them per column in a fixed order (slices of workgroups,
-// then the slices) to dweight (and dbias).  Without a large enough workspace
+// workgroup writes its column partials to the stream workspace and one
+// small pass adds them per column in a fixed order to dweight (and dbias).
+// Without a large enough workspace
 // the parameter gradients come from a column kernel that re-reads x and dy
 // instead (no scratch, two more tensor reads).  Rows that do not fit the
 // register plan (N > 8192 bf16 / 4096 fp32, N % 8 != 0, unaligned) take a
@@ -198,62 +198,53 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
   }
 }
 
-// Column sums of the per-workgroup partials, in two deterministic passes that
-// fill the chip.  Pass 1: workgroup (column block c, slice q) adds rows
-// [q G / S, (q+1) G / S) of part for 64 columns; its four waves take
-// interleaved rows with eight independent accumulators per lane (eight loads
-// in flight), combined in a fixed order, into out[q, n].  Pass 2 adds the S
-// slices in order to dweight (and dbias).
-__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum1(const float *__restrict__ part_g,
-                                                               const float *__restrict__ part_b, int G, int N, int S,
-                                                               float *__restrict__ out_g, float *__restrict__ out_b) {
-  __shared__ float red[kNbWaves][64][2];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n = blockIdx.x * 64 + lane;
-  const int q = blockIdx.y;
-  const int g0 = static_cast<int>(static_cast<int64_t>(q) * G / S);
-  const int g1 = static_cast<int>(static_cast<int64_t>(q + 1) * G / S);
-  float ag[8], ab[8];
+// Column sums of the per-workgroup partials in one deterministic pass.
+// Workgroup (column block c, array a: 0 the dweight partials, 1 the dbias
+// ones) is 64 row groups x 16 columns: thread (r, j) adds rows r, r + 64, ...
+// of column 16 c + j, eight loads in flight (every load of G = 512 rows
+// issued before the adds), the 16 columns of one row being one 64-byte
+// segment; the 64 row-group sums of a column are then added by a fixed
+// two-level tree in LDS and accumulated into dweight or dbias.  (Two
+// passes, slices of workgroups then the slices, ran the LayerNorm backward
+// at [16384, 4096] bf16 in 86.2 us against 81.4 us with this one, RMSNorm
+// 79.9 against 76.6 us.)
+constexpr int kCsCols = 16, kCsGroups = 64, kCsThreads = kCsCols * kCsGroups;
+__global__ __launch_bounds__(kCsThreads) void norm_bwd_colsum(const float *__restrict__ part_g,
+                                                              const float *__restrict__ part_b, int G, int N,
+                                                              float *__restrict__ dweight,
+                                                              float *__restrict__ dbias) {
+  __shared__ float red[kCsGroups][kCsCols + 1];
+  __shared__ float red2[kCsGroups / 4][kCsCols + 1];
+  const int t = threadIdx.x;
+  const int j = t % kCsCols, r = t / kCsCols;
+  const int n = blockIdx.x * kCsCols + j;
+  const bool bias = blockIdx.y == 1;
+  const float *part = bias ? part_b : part_g;
+  float acc[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) ag[k] = ab[k] = 0.0f;
+  for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
   if (n < N) {
-    int g = g0 + w;
-    for (; g + 7 * kNbWaves < g1; g += 8 * kNbWaves) {
+    int g = r;
+    for (; g + 7 * kCsGroups < G; g += 8 * kCsGroups) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int64_t o = static_cast<int64_t>(g + k * kNbWaves) * N + n;
-        ag[k] += part_g[o];
-        if (part_b != nullptr) ab[k] += part_b[o];
-      }
+      for (int k = 0; k < 8; ++k) acc[k] += part[static_cast<int64_t>(g + k * kCsGroups) * N + n];
     }
-    for (; g < g1; g += kNbWaves) {
-      const int64_t o = static_cast<int64_t>(g) * N + n;
-      ag[0] += part_g[o];
-      if (part_b != nullptr) ab[0] += part_b[o];
-    }
+    for (; g < G; g += kCsGroups) acc[0] += part[static_cast<int64_t>(g) * N + n];
   }
-  red[w][lane][0] = ((ag[0] + ag[1]) + (ag[2] + ag[3])) + ((ag[4] + ag[5]) + (ag[6] + ag[7]));
-  red[w][lane][1] = ((ab[0] + ab[1]) + (ab[2] + ab[3])) + ((ab[4] + ab[5]) + (ab[6] + ab[7]));
+  red[r][j] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (w == 0 && n < N) {
-    out_g[static_cast<int64_t>(q) * N + n] = ((red[0][lane][0] + red[1][lane][0]) + red[2][lane][0]) + red[3][lane][0];
-    if (out_b != nullptr)
-      out_b[static_cast<int64_t>(q) * N + n] = ((red[0][lane][1] + red[1][lane][1]) + red[2][lane][1]) + red[3][lane][1];
+  if (t < kCsGroups / 4 * kCsCols) {
+    const int q = t / kCsCols;
+    red2[q][j] = (red[4 * q][j] + red[4 * q + 1][j]) + (red[4 * q + 2][j] + red[4 * q + 3][j]);
   }
-}
-
-__global__ __launch_bounds__(kNbThreads) void norm_bwd_colsum2(const float *__restrict__ out_g,
-                                                               const float *__restrict__ out_b, int S, int N,
-                                                               float *__restrict__ dweight, float *__restrict__ dbias) {
-  const int n = blockIdx.x * kNbThreads + threadIdx.x;
-  if (n >= N) return;
-  float sg = 0.0f, sb = 0.0f;
-  for (int q = 0; q < S; ++q) {
-    sg += out_g[static_cast<int64_t>(q) * N + n];
-    if (out_b != nullptr) sb += out_b[static_cast<int64_t>(q) * N + n];
+  __syncthreads();
+  if (t < kCsCols && n < N) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kCsGroups / 4; ++q) sum += red2[q][j];
+    float *out = bias ? dbias : dweight;
+    out[n] = out[n] + sum;
   }
-  if (dweight != nullptr) dweight[n] = dweight[n] + sg;
-  if (dbias != nullptr) dbias[n] = dbias[n] + sb;
 }
 
 // Parameter gradients without scratch: thread = column, all rows in order.
@@ -328,17 +319,9 @@ static int bwd_vpt(int64_t N, bool vec_ok) {
   return 0;
 }
 
-// Slices of the first column-sum pass: about two workgroups per CU.
-static int colsum_slices(int64_t M, int64_t N) {
-  const int64_t blocks = cdiv(N, 64);
-  const int64_t s = std::max<int64_t>(1, 2 * static_cast<int64_t>(device_cu_count()) / blocks);
-  return static_cast<int>(std::min<int64_t>({s, 64, static_cast<int64_t>(bwd_groups(M))}));
-}
-
-// [part_g G x N][part_b G x N][out_g S x N][out_b S x N], fp32
+// [part_g G x N][part_b G x N], fp32
 static size_t bwd_scratch_bytes(int64_t M, int64_t N, bool rms) {
-  const size_t rows = static_cast<size_t>(bwd_groups(M)) + static_cast<size_t>(colsum_slices(M, N));
-  return rows * static_cast<size_t>(N) * 4 * (rms ? 1 : 2);
+  return static_cast<size_t>(bwd_groups(M)) * static_cast<size_t>(N) * 4 * (rms ? 1 : 2);
 }
 
 template <typename T, int VPT, bool RMS, bool PART>
@@ -384,13 +367,12 @@ static teeny_status norm_bwd(const void *dy, const void *x, void *dx, const void
   teeny_status st = after_launch(name, s);
   if (st != TEENY_OK || !grads) return st;
   if (part) {
-    const int S = colsum_slices(M, N);
-    float *og = pg + static_cast<int64_t>(G) * N * (RMS ? 1 : 2);
-    float *ob = RMS ? nullptr : og + static_cast<int64_t>(S) * N;
-    hipLaunchKernelGGL(norm_bwd_colsum1, dim3(static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(S)),
-                       dim3(kNbThreads), 0, s, pg, pb, G, static_cast<int>(N), S, og, ob);
-    hipLaunchKernelGGL(norm_bwd_colsum2, dim3(static_cast<unsigned>(cdiv(N, kNbThreads))), dim3(kNbThreads), 0, s,
-                       og, ob, S, static_cast<int>(N), dweight, RMS ? nullptr : dbias);
+    // one column-sum grid row per requested gradient (dweight, dbias)
+    const bool want_g = dweight != nullptr, want_b = !RMS && dbias != nullptr;
+    const float *src0 = want_g ? pg : pb;
+    float *dst0 = want_g ? dweight : dbias;
+    hipLaunchKernelGGL(norm_bwd_colsum, dim3(static_cast<unsigned>(cdiv(N, kCsCols)), want_g && want_b ? 2u : 1u),
+                       dim3(kCsThreads), 0, s, src0, pb, G, static_cast<int>(N), dst0, dbias);
   } else {
     hipLaunchKernelGGL((norm_bwd_cols_kernel<T, RMS>), dim3(static_cast<unsigned>(cdiv(N, kNbThreads))),
                        dim3(kNbThreads), 0, s, static_cast<const T *>(dy), static_cast<const T *>(x), st0, st1, M,

@@ -114,6 +114,29 @@ def test_norm_backward_skips_param_grads(dev, orc):
     check_f32(dx.to_host(), orc.layer_norm_backward(dy, x, w, mean, rstd)[0], "dx only")
 
 
+@pytest.mark.parametrize("which", ["dweight", "dbias"])
+def test_layer_norm_backward_one_param_grad(dev, orc, which):
+    # with the workspace, only one of dweight / dbias requested: the column
+    # sums run for that one alone
+    rng = np.random.default_rng(23 if which == "dweight" else 29)
+    m, n = 300, 1024
+    x, dy = rng.normal(0, 1, (m, n)).astype(np.float32), rng.normal(0, 1, (m, n)).astype(np.float32)
+    w = rng.normal(1, 0.2, n).astype(np.float32)
+    _, mean, rstd = orc.layer_norm_train(x, w, np.zeros(n, np.float32))
+    g0 = rng.normal(0, 1, n).astype(np.float32)
+    gb = dev.upload(g0)
+    need = K.norm_backward_workspace_size(m, n, False, tg.f32)
+    print(f"[ln bwd one grad] {which} workspace {need} B", flush=True)
+    kw = {which: gb}
+    with stream_workspace(dev, need):
+        dx = K.layer_norm_backward(dev.upload(dy), dev.upload(x), dev.upload(w), dev.upload(mean), dev.upload(rstd),
+                                   **kw)
+        dev.synchronize()
+    rdx, rdw, rdb = orc.layer_norm_backward(dy, x, w, mean, rstd, g0, g0)
+    check_f32(dx.to_host(), rdx, "dx")
+    check_f32(gb.to_host(), rdw if which == "dweight" else rdb, which)
+
+
 def test_layer_norm_backward_config(dev, orc):
     # the norm workload's shape: X[16384, 4096] bf16, with the stream workspace
     m, n = 16384, 4096
