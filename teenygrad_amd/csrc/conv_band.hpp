@@ -278,6 +278,7 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
     }
   };
 
+  constexpr int kLA = 2, kWin = kLA + 1;
   auto compute_stage = [&](int st) __attribute__((always_inline)) {
     const char *hb = RAW ? s2d : dbuf + (st % NHB) * S::HBUF;
     const int ch = st % NCH;
@@ -293,18 +294,18 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
       w0 = *reinterpret_cast<const bf16x8 *>(wlds + c * S::WP + kb);
       w1 = *reinterpret_cast<const bf16x8 *>(wlds + (32 + c) * S::WP + kb);
     };
-    bf16x8 xa, wa0, wa1, xb, wb0, wb1;
-    frags(0, xa, wa0, wa1);
+    // the fragments of k-step ks + kLA are read while k-step ks multiplies
+    // (a window of kLA + 1 sets; a scheduling fence per k-step keeps that
+    // order)
+    bf16x8 xw[kWin], ww0[kWin], ww1[kWin];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks += 2) {
-      if (ks + 1 < NKS) frags(ks + 1, xb, wb0, wb1);
-      acc[0] = mfma32x32x16(wa0, xa, acc[0]);
-      acc[1] = mfma32x32x16(wa1, xa, acc[1]);
-      if (ks + 2 < NKS) frags(ks + 2, xa, wa0, wa1);
-      if (ks + 1 < NKS) {
-        acc[0] = mfma32x32x16(wb0, xb, acc[0]);
-        acc[1] = mfma32x32x16(wb1, xb, acc[1]);
-      }
+    for (int ks = 0; ks < kLA && ks < NKS; ++ks) frags(ks, xw[ks % kWin], ww0[ks % kWin], ww1[ks % kWin]);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (ks + kLA < NKS) frags(ks + kLA, xw[(ks + kLA) % kWin], ww0[(ks + kLA) % kWin], ww1[(ks + kLA) % kWin]);
+      acc[0] = mfma32x32x16(ww0[ks % kWin], xw[ks % kWin], acc[0]);
+      acc[1] = mfma32x32x16(ww1[ks % kWin], xw[ks % kWin], acc[1]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
