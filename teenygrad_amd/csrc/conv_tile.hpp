@@ -49,17 +49,23 @@ struct TileConvParams {
   bf16 *y;           // [B, OH, OW, C_OUT]
   int B, H, W, Cin, Cout, OH, PH, PW, act;
   int x_bytes, w_bytes;  // byte extents (below 2^31)
+  // stride-2 3x3 dx mode: element offset of each sub-pixel phase's weights
+  int phase_off[4];
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false>
 struct TileShape {
   static constexpr int NPX = RB * OWT;           // pixels per band
   static constexpr int NW = (NPX + 31) / 32;     // waves
   static constexpr int NT = 64 * NW;
-  static constexpr int HR = RB + KH - 1, HC = OWT + KW - 1;
+  // dx mode: a phase reads dy rows u, u + 1 and columns v, v + 1 (no padding)
+  static constexpr int HR = DX2 ? RB + 1 : RB + KH - 1, HC = DX2 ? OWT + 1 : OWT + KW - 1;
   static constexpr int HSLOTS = HR * HC * 4;     // 16-byte halo slots (32 channels per pixel)
   static constexpr int QT = INT8B ? 2 : 4;       // 16-byte slots per tap segment
-  static constexpr int RS = KH * KW * QT + 1;    // slots per weight row (+ 1 pad slot)
+  // taps of a unit, at most (dx mode: row phase a = 1 with both column
+  // phases, 2 + 4 taps)
+  static constexpr int TAPS = DX2 ? 6 : KH * KW;
+  static constexpr int RS = TAPS * QT + 1;       // slots per weight row (+ 1 pad slot)
   static constexpr int WSLOTS = BN * RS;
   static constexpr int HINSTR = (HSLOTS + 63) / 64, WINSTR = (WSLOTS + 63) / 64;
   static constexpr int INSTR = HINSTR + WINSTR;  // DMA instructions per stage (workgroup)
@@ -77,11 +83,13 @@ struct TileShape {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
-__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) void conv_tile_kernel(TileConvParams p) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false>
+__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1) void conv_tile_kernel(
+    TileConvParams p) {
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>;
+  static_assert(!DX2 || (KH == 3 && KW == 3 && !INT8B), "dx mode: bf16 3x3 stride 2 pad 1");
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
-  constexpr int EPI_STORES = 4 * (BN / 64);
+  constexpr int EPI_STORES = 4 * (BN / 64) * (DX2 ? 2 : 1);  // per unit (dx mode: two phases)
   static_assert((S::NSTG - 2) * DI + 2 * EPI_STORES < 64 && S::NSTG <= 3, "vmcnt field / wait cases");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x;
@@ -92,15 +100,20 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
 
   const int bands_per_img = p.OH / RB;
   const int n_tiles = p.Cout / BN;
-  const int n_units = p.B * bands_per_img * n_tiles;
+  const int per_phase = p.B * bands_per_img * n_tiles;
+  const int n_units = (DX2 ? 2 : 1) * per_phase;
   const int nch = p.Cin / 32;
   const int G = static_cast<int>(gridDim.x);
   const int wg = static_cast<int>(blockIdx.x);
   const int my_units = wg < n_units ? (n_units - 1 - wg) / G + 1 : 0;
   const int n_stages = my_units * nch;
-  // unit u: co tile fastest (the tiles of one band share its input in L2)
-  auto unit_of = [&](int st, int &b, int &oh0, int &n0) __attribute__((always_inline)) {
-    const int u = wg + (st / nch) * G;
+  // unit u: co tile fastest (the tiles of one band share its input in L2);
+  // dx mode: the row phase ph slowest, so a workgroup's units cover both
+  // alike
+  auto unit_of = [&](int st, int &b, int &oh0, int &n0, int &ph) __attribute__((always_inline)) {
+    int u = wg + (st / nch) * G;
+    ph = DX2 ? u / per_phase : 0;
+    if constexpr (DX2) u %= per_phase;
     n0 = (u % n_tiles) * BN;
     const int band = u / n_tiles;
     b = band / bands_per_img;
@@ -122,8 +135,13 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   int dma_off[DI];
   auto dma_unit = [&](int st) __attribute__((always_inline)) {
     const bool live = st < n_stages;
-    int b, oh0, n0;
-    unit_of(st, b, oh0, n0);
+    int b, oh0, n0, ph;
+    unit_of(st, b, oh0, n0, ph);
+    // weight rows: forward [C_OUT][KH][KW][C_IN] (taps kh KW + kw); dx
+    // mode, row phase a = ph: the T = a + 1 taps of phase (a, 0), then the 2 T
+    // of phase (a, 1), each phase's block [C_IN][taps][C_OUT] at its offset
+    const int T = ph + 1;
+    const int taps = DX2 ? 3 * T : KH * KW;
 #pragma unroll
     for (int r = 0; r < DI; ++r) {
       const int ins0 = r * NW + w;  // wave-uniform
@@ -143,8 +161,14 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
         const int s = (ins - S::HINSTR) * 64 + lane;
         const int n = s / S::RS, j = s % S::RS;
         const int tap = j / S::QT, q = j % S::QT;
-        const bool ok = live & (s < S::WSLOTS) & (j < S::RS - 1);
-        if (ok) off = static_cast<int>((static_cast<int64_t>(n0 + n) * K + tap * p.Cin) * ES + 16 * q);
+        const bool ok = live & (s < S::WSLOTS) & (j < S::RS - 1) & (tap < taps);
+        int64_t e = static_cast<int64_t>(n0 + n) * K + tap * p.Cin;
+        if constexpr (DX2) {
+          const bool c1 = tap >= T;  // phase (a, 1)
+          e = p.phase_off[2 * ph + c1] + static_cast<int64_t>(n0 + n) * (c1 ? 2 * T : T) * p.Cin +
+              (c1 ? tap - T : tap) * p.Cin;
+        }
+        if (ok) off = static_cast<int>(e * ES + 16 * q);
       }
       dma_off[r] = off;
     }
@@ -166,9 +190,11 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   // ── MFMA side
   const int px = min(32 * w + c, S::NPX - 1);  // pixels past the band repeat the last one
   const int pr = px / OWT, pc = px % OWT;
-  f32x16 acc[NB];
+  // dx mode: one accumulator set per column phase
+  constexpr int NSET = DX2 ? 2 : 1;
+  f32x16 acc[NSET * NB];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) acc[i] = zero16();
+  for (int i = 0; i < NSET * NB; ++i) acc[i] = zero16();
   // Weight fragment of channel block i for k-step (tap, h): bf16 straight
   // from LDS, or int8 read raw (8 bytes) and converted in registers
   typedef typename std::conditional<INT8B, u32x2, bf16x8>::type wraw_t;
@@ -199,14 +225,23 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
   // single MFMA.  A scheduling fence per k-step keeps the compiler from
   // hoisting every read of the unrolled loop (the int8 kernel then held ~480
   // registers).
-  constexpr int kLA = 2, kWin = kLA + 1;
-  auto compute_stage = [&](int st) __attribute__((always_inline)) {
+  constexpr int kLA = DX2 ? 1 : 2, kWin = kLA + 1;
+  // The unit's taps: forward, tap j = (kh, kw) = (j / KW, j % KW); dx mode,
+  // row phase with TT taps: j < TT is tap (j, 0) of phase (a, 0)
+  // (accumulator set 0), then j - TT = 2 t + s is tap (t, s) of phase (a, 1)
+  // (set 1).  Tap (t, s) reads halo pixel (pr + t, pc + s).
+  auto compute_taps = [&](int st, auto tsel) __attribute__((always_inline)) {
+    constexpr int TT = decltype(tsel)::value;
+    constexpr int NTAP = DX2 ? 3 * TT : KH * KW;
+    auto tap_set = [](int j) { return DX2 && j >= TT ? 1 : 0; };
+    auto tap_dh = [](int j) { return DX2 ? (j < TT ? j : (j - TT) / 2) : j / KW; };
+    auto tap_dw = [](int j) { return DX2 ? (j < TT ? 0 : (j - TT) % 2) : j % KW; };
     const char *hb = smem + (st % S::NSTG) * S::STAGE;
     const char *wb = hb + S::HBYTES;
-    constexpr int NKS = KH * KW * 2;
+    constexpr int NKS = NTAP * 2;
     auto xread = [&](int ks) __attribute__((always_inline)) {
       const int tap = ks >> 1, h = ks & 1;
-      const int kh = tap / KW, kw = tap % KW;
+      const int kh = tap_dh(tap), kw = tap_dw(tap);
       const int hc = pc + kw;
       return *reinterpret_cast<const bf16x8 *>(hb + ((pr + kh) * HC + hc) * 64 + 16 * ((2 * h + g) ^ ((hc >> 2) & 3)));
     };
@@ -223,23 +258,38 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
     for (int ks = 0; ks < NKS; ++ks) {
       if (ks + kLA < NKS) fetch(ks + kLA);
 #pragma unroll
-      for (int i = 0; i < NB; ++i) acc[i] = mfma32x32x16(wconv(ww[ks % kWin][i]), xw[ks % kWin], acc[i]);
+      for (int i = 0; i < NB; ++i) {
+        const int a = tap_set(ks >> 1) * NB + i;
+        acc[a] = mfma32x32x16(wconv(ww[ks % kWin][i]), xw[ks % kWin], acc[a]);
+      }
       __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto compute_stage = [&](int st) __attribute__((always_inline)) {
+    if constexpr (DX2) {
+      int b, oh0, n0, ph;
+      unit_of(st, b, oh0, n0, ph);
+      if (ph == 0) compute_taps(st, std::integral_constant<int, 1>{});
+      else compute_taps(st, std::integral_constant<int, 2>{});
+    } else {
+      compute_taps(st, std::integral_constant<int, 0>{});
     }
   };
 
   const EpiAct ea = epi_act(p.act);
   const float lo = ea.relu ? 0.0f : -INFINITY;
+  // dx mode: y is dx, [B, 2 OH, 2 OWT, C]
   const __amdgpu_buffer_rsrc_t y_rsrc =
-      buffer_rsrc(p.y, static_cast<int>(static_cast<int64_t>(p.B) * p.OH * OWT * p.Cout * 2));
+      buffer_rsrc(p.y, static_cast<int>(static_cast<int64_t>(p.B) * p.OH * OWT * p.Cout * 2 * (DX2 ? 4 : 1)));
+  // dx mode: accumulator set `set` of row phase ph is phase (ph, set)
   // Epilogue of stage st's unit: 64 channels (blocks 2 hp, 2 hp + 1) at a
   // time; lane (c, g) holds channels 32 i + 8 q + 4 g + (0..3) of pixel c,
   // permlane32 swaps make 16-byte chunks 4 (i % 2) + 2 pr + g of the 128-byte
   // segment, staged at chunk position ^ (c & 7) and stored as 8 whole rows
   // per instruction.
-  auto epilogue = [&](int st, auto sig) __attribute__((always_inline)) {
-    int b, oh0, n0;
-    unit_of(st, b, oh0, n0);
+  auto epilogue = [&](int st, auto sig, int set) __attribute__((always_inline)) {
+    int b, oh0, n0, ph;
+    unit_of(st, b, oh0, n0, ph);
     char *const stg = smem + (st % S::NSTG) * S::STAGE + w * S::STG;
     const int64_t pix0 = (static_cast<int64_t>(b) * p.OH + oh0) * OWT;  // the band's first pixel
 #pragma unroll
@@ -247,11 +297,17 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int i = 2 * hp + ii;
+        // (dx mode: no scale, bias or activation)
         f32x4 em[4], ead[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          em[q] = *reinterpret_cast<const f32x4 *>(cmul + 32 * i + 8 * q + 4 * g);
-          ead[q] = *reinterpret_cast<const f32x4 *>(cadd + 32 * i + 8 * q + 4 * g);
+          if constexpr (DX2) {
+            em[q] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+            ead[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          } else {
+            em[q] = *reinterpret_cast<const f32x4 *>(cmul + 32 * i + 8 * q + 4 * g);
+            ead[q] = *reinterpret_cast<const f32x4 *>(cadd + 32 * i + 8 * q + 4 * g);
+          }
         }
 #pragma unroll
         for (int prr = 0; prr < 2; ++prr) {
@@ -262,7 +318,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
             bf16x4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float r = __builtin_fmaf(acc[i][4 * q + e], em[q][e], ead[q][e]);
+              float r = __builtin_fmaf(acc[set * NB + i][4 * q + e], em[q][e], ead[q][e]);
               if constexpr (decltype(sig)::value) r = epi_sig(r, ea);
               o[e] = static_cast<bf16>(r < lo ? lo : r);
             }
@@ -284,9 +340,13 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
         const int pl = 8 * r8 + (lane >> 3), k = lane & 7;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 128 + 16 * (k ^ (pl & 7)));
         const int pxl = 32 * w + pl;
-        const int off = pxl < S::NPX
-                            ? static_cast<int>(((pix0 + pxl) * p.Cout + n0 + 64 * hp) * 2 + 16 * k)
-                            : kOffNone;
+        int64_t opix = pix0 + pxl;
+        if constexpr (DX2) {
+          // phase pixel (u, v) of phase (a, c) is dx pixel (2 u + a, 2 v + c)
+          const int u = oh0 + pxl / OWT, v = pxl % OWT;
+          opix = (static_cast<int64_t>(b) * 2 * p.OH + 2 * u + ph) * (2 * OWT) + 2 * v + set;
+        }
+        const int off = pxl < S::NPX ? static_cast<int>((opix * p.Cout + n0 + 64 * hp) * 2 + 16 * k) : kOffNone;
         __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 0);
       }
     }
@@ -307,8 +367,8 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
     }
   };
   if (my_units > 0) {
-    int b, oh0, n0;
-    unit_of(0, b, oh0, n0);
+    int b, oh0, n0, ph;
+    unit_of(0, b, oh0, n0, ph);
     fill_coeffs(n0);
   }
   __syncthreads();
@@ -334,15 +394,18 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B>::NT), 1) voi
     epi_hist <<= 1;
     if (st % nch == nch - 1) {
       __syncthreads();  // every wave has read stage st's buffer: the epilogue slices reuse it
-      if (ea.sig) epilogue(st, std::true_type{});
-      else epilogue(st, std::false_type{});
 #pragma unroll
-      for (int i = 0; i < NB; ++i) acc[i] = zero16();
+      for (int set = 0; set < NSET; ++set) {
+        if (!DX2 && ea.sig) epilogue(st, std::true_type{}, set);
+        else epilogue(st, std::false_type{}, set);
+      }
+#pragma unroll
+      for (int i = 0; i < NSET * NB; ++i) acc[i] = zero16();
       epi_hist |= 1u;
       if (st + 1 < n_stages) {
-        int b2, oh2, n2, b1, oh1, n1;
-        unit_of(st, b1, oh1, n1);
-        unit_of(st + 1, b2, oh2, n2);
+        int b2, oh2, n2, b1, oh1, n1, ph1, ph2;
+        unit_of(st, b1, oh1, n1, ph1);
+        unit_of(st + 1, b2, oh2, n2, ph2);
         if (n2 != n1) {
           // every wave is done with this unit's coefficients (all passed its epilogue)
           __syncthreads();
@@ -398,11 +461,12 @@ inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
 }
 
 // The band-tiled kernel for this conv, if one is built for its shape: the
-// 14x14 bf16 3x3 convs (ResNet stage 3, 256 -> 256 at batch 64: 33.4 -> 26.1
-// us).  Measured and not taken: the 28x28 bf16 3x3 (128 -> 128: 28.5 us,
-// as the implicit GEMM) and the int8 28x28 conv (62 us against 54 us: each
-// converted weight fragment feeds one MFMA here, so the int8 -> bf16
-// conversion outweighs the matrix work; the GEMM reuses it across row blocks).
+// 14x14 and 28x28 bf16 3x3 convs (ResNet stages 2 and 3: 14x14 256 -> 256
+// at batch 64 33.4 -> 22.3 us, 28x28 128 -> 128 27.9 -> 23.6 us against the
+// implicit GEMM).  Measured and not taken: the int8 28x28 conv (62 us
+// against 54 us: each converted weight fragment feeds one MFMA here, so the
+// int8 -> bf16 conversion outweighs the matrix work; the GEMM reuses it
+// across row blocks).
 template <bool INT8B>
 inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
   if constexpr (!INT8B) {
@@ -416,6 +480,53 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
     }
   }
   return false;
+}
+
+// dx of a stride-2 3x3 pad-1 conv (dx = 2 OH x 2 OW) as the band-tiled
+// kernel over dy with all four sub-pixel phases in one launch: units are
+// (row phase a, image band, 64 input channels), each holding phases (a, 0)
+// and (a, 1) in two accumulator sets (3 or 6 taps per 32 channels of dy:
+// one unit per sub-pixel phase, 1 to 4 taps, took 45.8 us at 64 x 28 x 28,
+// 256 -> 256), and each phase pixel (u, v) stored to dx pixel (2 u + a,
+// 2 v + c).  wp holds the phases' flipped, transposed
+// weights ([C_IN][taps][C_OUT] each, at phase_off, in phase order (0, 0),
+// (0, 1), (1, 0), (1, 1)).
+template <int OWT, int RB>
+inline bool tile_dx2_fits(int B, int OH, int OW, int Kc, int N, const void *dy, const void *wp, const void *dx) {
+  return OW == OWT && OH % RB == 0 && Kc % 32 == 0 && N % 64 == 0 && aligned(dy, 16) && aligned(wp, 16) &&
+         aligned(dx, 16) && static_cast<int64_t>(B) * OH * OW * Kc * 2 < 0x7fffffff &&
+         static_cast<int64_t>(B) * 4 * OH * OW * N * 2 < 0x7fffffff && static_cast<int64_t>(9) * N * Kc * 2 < 0x7fffffff;
+}
+
+template <int OWT, int RB>
+inline void launch_tile_dx2(const bf16 *dy, const bf16 *wp, bf16 *dx, int B, int OH, int Kc, int N,
+                            const int64_t *phase_off, hipStream_t s) {
+  using S = TileShape<3, 3, OWT, RB, 64, false, true>;
+  auto kern = &conv_tile_kernel<3, 3, OWT, RB, 64, false, true>;
+  static const bool attr_set = [kern] {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               S::LDS) == hipSuccess;
+  }();
+  (void)attr_set;
+  TileConvParams t{};
+  t.x = dy;
+  t.w = wp;
+  t.y = dx;
+  t.B = B;
+  t.H = OH;
+  t.W = OWT;
+  t.Cin = Kc;
+  t.Cout = N;
+  t.OH = OH;
+  t.PH = 0;
+  t.PW = 0;
+  t.act = TEENY_ACT_NONE;
+  t.x_bytes = static_cast<int>(static_cast<int64_t>(B) * OH * OWT * Kc * 2);
+  t.w_bytes = static_cast<int>(static_cast<int64_t>(9) * N * Kc * 2);
+  for (int i = 0; i < 4; ++i) t.phase_off[i] = static_cast<int>(phase_off[i]);
+  const int units = 2 * B * (OH / RB) * (N / 64);
+  const int grid = std::min(units, device_cu_count());
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(S::NT), S::LDS, s, t);
 }
 
 }  // namespace teeny

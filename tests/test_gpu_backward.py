@@ -233,6 +233,11 @@ MFMA_DX_CASES = [  # bf16 NHWC, groups 1: B, H, Cin, Cout, K, stride, pad (ResNe
     # strided convs run as their sub-pixel phases (one stride-1 GEMM per
     # (ih % S, iw % S) class, remapped output rows; phases without taps zeroed)
     (4, 28, 256, 256, 3, 2, 1),   # the ResNet-50 stage-3 downsampling 3x3
+    # 3x3/2 pad 1 with 14- or 28-wide dy: the four phases in one band-tiled
+    # launch (units of phase, image band and 64 input channels)
+    (3, 56, 128, 128, 3, 2, 1),   # the stage-2 downsampling 3x3 (28-wide dy)
+    (2, 56, 64, 64, 3, 2, 1),
+    (40, 28, 192, 64, 3, 2, 1),   # 480 units: several per workgroup, channel tiles changing
     (2, 15, 64, 64, 3, 2, 1),     # odd H: phases of 8 and 7 rows
     (2, 13, 32, 48, 5, 3, 2),     # stride 3, 5x5
     (2, 12, 16, 32, 4, 2, 1),     # even kernel
