@@ -562,11 +562,46 @@ static bool conv_s2d_mfma(const void *x, const void *w, const float *scale, cons
   return true;
 }
 
+// Grouped bf16 NHWC conv (groups > 1) on the register-staged implicit GEMM,
+// one launch for all groups: group g reads input channels [g C_IN/G, (g+1)
+// C_IN/G) of each pixel (the gather's pixel stride stays C_IN), weight rows
+// [g C_OUT/G, (g+1) C_OUT/G) and writes those output channels.  Taken for
+// at least 16 output channels per group (fewer leave the 64-wide MFMA
+// tiles mostly empty: conv_direct instead); C_IN/G % 8 == 0 gathers 16-byte
+// chunks, other widths element by element.
+static bool try_conv_grouped(const void *x, const void *w, const float *scale, const float *bias,
+                             const bf16 *bias_bf16, void *y, const ConvGeo &q, int act, hipStream_t s) {
+  const int cin_g = q.Cin / q.G, cout_g = q.Cout / q.G;
+  if (q.G < 2 || q.B == 0 || cout_g < 16 || !aligned(x, 16) || !aligned(w, 16) ||
+      static_cast<int64_t>(q.H) * q.W * q.Cin >= (int64_t{1} << 30))
+    return false;
+  GemmParams p = conv_gemm_params(x, w, scale, bias, bias_bf16, y, q);
+  p.Cin = cin_g;
+  p.cst = q.Cin;
+  p.N = cout_g;
+  p.K = q.KH * q.KW * cin_g;
+  p.ldb = p.K;
+  p.ldc = q.Cout;
+  p.groups = q.G;
+  p.g_a = cin_g;
+  p.g_b = static_cast<int64_t>(cout_g) * p.K;
+  p.g_c = cout_g;
+  const bool one_by_one = q.KH == 1 && q.KW == 1 && q.SH == 1 && q.SW == 1 && q.PH == 0 && q.PW == 0;
+  if (cin_g % 8 == 0) {
+    return one_by_one ? launch_grouped_gemm<false, kAPlain>(p, act, s)
+                      : launch_grouped_gemm<false, kAConvVec>(p, act, s);
+  }
+  return launch_grouped_gemm<false, kAConvScalar>(p, act, s);
+}
+
 // bf16 NHWC, groups == 1 -> MFMA implicit GEMM.  Returns false if not taken.
 template <bool INT8B>
 static bool try_conv_mfma(const void *x, const void *w, const float *scale, const float *bias,
                           const bf16 *bias_bf16, void *y, const ConvGeo &q, int act,
                           hipStream_t s, const Scratch scr) {
+  if constexpr (!INT8B) {
+    if (q.G > 1) return try_conv_grouped(x, w, scale, bias, bias_bf16, y, q, act, s);
+  }
   if (!aligned(x, 16) || !aligned(w, 16)) return false;
   const ConvPath path = conv_path<INT8B>(q);
   if (path == kConvNoMfma) return false;

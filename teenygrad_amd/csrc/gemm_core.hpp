@@ -82,6 +82,12 @@ struct GemmParams {
   // register-staged kernels and the split-K finalize take it.
   int c_ow, c_oh;
   int64_t c_sb, c_su, c_sv;
+  // Grouped conv (groups > 1; register-staged kernels only): workgroup row
+  // blockIdx.y is group g, whose A, B and C start g g_a, g g_b and g g_c
+  // elements in and whose scale / bias start g N in; cst is the pixel
+  // stride of the NHWC gather (all the image's channels; 0: Cin).
+  int groups, cst;
+  int64_t g_a, g_b, g_c;
 };
 
 // Element offset of output row m in C (see GemmParams::c_ow).
@@ -175,7 +181,21 @@ constexpr int gemm_min_waves() {
 
 // BK: k-tile depth (32 or 64).  PF: global->register prefetch depth in k-tiles (1 or 2).
 template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE, bool KVEC = true>
-__global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_kernel(GemmParams p) {
+__global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_kernel(GemmParams p0) {
+  GemmParams p = p0;
+  if (p0.groups > 1) {
+    const int grp = static_cast<int>(blockIdx.y);
+    constexpr int ES = INT8B ? 1 : 2;
+    p.A += grp * p0.g_a;
+    p.a_bytes -= static_cast<int>(grp * p0.g_a * 2);
+    p.B = static_cast<const char *>(p0.B) + grp * p0.g_b * ES;
+    p.b_bytes -= static_cast<int>(grp * p0.g_b * ES);
+    p.C += grp * p0.g_c;
+    if (p.scale != nullptr) p.scale += static_cast<int64_t>(grp) * p0.N;
+    if (p.bias != nullptr) p.bias += static_cast<int64_t>(grp) * p0.N;
+    if (p.bias_bf16 != nullptr) p.bias_bf16 += static_cast<int64_t>(grp) * p0.N;
+  }
+  const int cst = p.cst > 0 ? p.cst : p.Cin;  // NHWC pixel stride (elements)
   // LDS rows.  k-depth 64: padded to 72 elements.  k-depth 32: dense
   // 32-element (64-byte) rows whose 16-byte chunk c sits at position
   // c ^ ((row >> 2) & 3), so that both the row-chunk stores (16 lanes: 4
@@ -255,9 +275,9 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
       const int b = t / p.OH;
       a_ih0[i] = oh * p.SH - p.PH;
       a_iw0[i] = ow * p.SW - p.PW;
-      const int64_t img = static_cast<int64_t>(b) * p.H * p.W * p.Cin;
+      const int64_t img = static_cast<int64_t>(b) * p.H * p.W * cst;
       a_base[i] = p.A + img;
-      a_off[i] = static_cast<int>(2 * (img + static_cast<int64_t>(a_ih0[i] * p.W + a_iw0[i]) * p.Cin));
+      a_off[i] = static_cast<int>(2 * (img + static_cast<int64_t>(a_ih0[i] * p.W + a_iw0[i]) * cst));
     }
   }
   // Implicit-GEMM k decomposition (vector mode), stepped per k-tile: tap
@@ -276,7 +296,7 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     const int r = k / p.Cin;
     t.kw = r % p.KW;
     t.kh = r / p.KW;
-    t.off = 2 * ((t.kh * p.W + t.kw) * p.Cin + t.ci);
+    t.off = 2 * ((t.kh * p.W + t.kw) * cst + t.ci);
     return t;
   };
   // u: the k-tile's first column (uniform); v: this thread's column
@@ -286,16 +306,17 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
     else v_tap = tap_at(k_first + a_col);
   }
   // advance by one k-tile: the offset moves by BK elements, plus
-  // (W - KW) C_IN each time kh steps
+  // cst - C_IN each time kw steps and (W - KW) cst each time kh steps
   auto tap_step = [&](TapState &t, bool once) __attribute__((always_inline)) {
     t.ci += BK;
     t.off += 2 * BK;
     while (t.ci >= p.Cin) {
       t.ci -= p.Cin;
+      t.off += 2 * (cst - p.Cin);
       if (++t.kw == p.KW) {
         t.kw = 0;
         ++t.kh;
-        t.off += 2 * (p.W - p.KW) * p.Cin;
+        t.off += 2 * (p.W - p.KW) * cst;
       }
       if (once) break;  // uniform case: C_IN % BK == 0, at most one step
     }
@@ -340,7 +361,7 @@ __global__ __launch_bounds__(256, (gemm_min_waves<BM, BN>())) void gemm_mfma_ker
           e[j] = static_cast<bf16>(0.0f);
           const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
           if (a_ok[i] && k + j < p.K && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-            e[j] = a_base[i][(static_cast<int64_t>(ih) * p.W + iw) * p.Cin + ci];
+            e[j] = a_base[i][(static_cast<int64_t>(ih) * p.W + iw) * cst + ci];
           if (++ci == p.Cin) {
             ci = 0;
             if (++kw == p.KW) {
@@ -683,11 +704,12 @@ static __global__ __launch_bounds__(256) void gemm_splitk_finalize(GemmParams p,
 template <int BM, int BN, int BK, int WAVES_M, int PF, bool INT8B, int AMODE>
 inline void launch_tile(const GemmParams &p, hipStream_t s, int splits = 1) {
   const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * splits;
+  const unsigned groups = p.groups > 1 ? static_cast<unsigned>(p.groups) : 1u;
   if (p.K % 8 == 0 && AMODE != kAConvScalar) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, true>), dim3(grid),
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, true>), dim3(grid, groups),
                        dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, false>), dim3(grid),
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WAVES_M, PF, INT8B, AMODE, false>), dim3(grid, groups),
                        dim3(256), 0, s, p);
   }
 }
@@ -831,6 +853,30 @@ inline int64_t gemm_a_extent(const GemmParams &p) {
 template <bool INT8B>
 inline int64_t gemm_b_extent(const GemmParams &p) {
   return (static_cast<int64_t>(p.N - 1) * p.ldb + p.K) * (INT8B ? 1 : 2);
+}
+
+// Grouped conv on the register-staged kernels, all groups in one launch
+// (workgroup row blockIdx.y = group; GemmParams::groups): no split along K.
+// False (nothing launched) when an operand's extent reaches 2^31 bytes.
+template <bool INT8B, int AMODE>
+inline bool launch_grouped_gemm(GemmParams p, int act, hipStream_t s) {
+  if (act < TEENY_ACT_NONE || act > TEENY_ACT_SILU || p.groups < 2) return false;
+  constexpr int64_t kMaxExtent = 0x7fffffff;
+  const int64_t a_ext = AMODE == kAPlain
+                            ? (static_cast<int64_t>(p.M - 1) * p.lda + p.cst) * 2
+                            : static_cast<int64_t>(p.M / (p.OH * p.OW)) * p.H * p.W * p.cst * 2;
+  const int64_t b_ext = static_cast<int64_t>(p.groups) * p.g_b * (INT8B ? 1 : 2);
+  if (a_ext > kMaxExtent || b_ext > kMaxExtent || static_cast<int64_t>(p.M) * p.ldc * 2 > kMaxExtent) return false;
+  p.a_bytes = static_cast<int>(a_ext);
+  p.b_bytes = static_cast<int>(b_ext);
+  p.n_fast = static_cast<int64_t>(p.M) * p.K * 2 > static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2);
+  p.act = act;
+  p.ws = nullptr;
+  p.c_ow = 0;
+  if (p.N <= 64) launch_tile<128, 64, 32, 2, 2, INT8B, AMODE>(p, s);
+  else if (p.K <= 256) launch_tile<128, 128, 32, 2, 2, INT8B, AMODE>(p, s);
+  else launch_tile<128, 128, 64, 2, 1, INT8B, AMODE>(p, s);
+  return true;
 }
 
 template <bool INT8B, int AMODE>

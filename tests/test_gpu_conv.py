@@ -452,3 +452,46 @@ def test_w8a16_conv_large_tile(dev, orc, scratch):
     for b in (0, 77, B - 1):
         ref = orc.relu(orc.conv2d_nhwc(x[b:b + 1], wdeq, bias, stride=1, padding=1))
         check_bf16(got[b:b + 1], ref, f"image {b}")
+
+
+GROUPED_CASES = [
+    # B, H, W, Cin, Cout, K, stride, pad, groups, act, post: bf16 NHWC grouped
+    # convs with >= 16 output channels per group run all groups in one
+    # implicit-GEMM launch (input channels of group g at a pixel stride of
+    # C_IN); fewer per group stay on the direct kernel
+    (2, 14, 14, 64, 128, 3, 1, 1, 4, "relu", "bias"),   # 16 -> 32 per group
+    (3, 9, 11, 128, 128, 3, 2, 1, 8, None, None),       # strided, 16 -> 16
+    (2, 10, 10, 32, 64, 1, 1, 0, 2, "silu", "bias"),    # 1x1: plain rows at a C_IN row stride
+    (2, 12, 12, 24, 48, 3, 1, 1, 2, None, "bn"),        # 12 channels per group: element gather
+    (4, 7, 7, 256, 512, 3, 1, 1, 2, "gelu", "bias"),    # deep K per group (1152)
+    (1, 8, 8, 64, 64, 3, 1, 1, 8, None, None),          # 8 -> 8 per group: the direct kernel
+]
+
+
+@pytest.mark.parametrize("case", GROUPED_CASES)
+def test_bf16_nhwc_grouped(dev, orc, case):
+    B, H, W, cin, cout, k, s, p, G, act, post = case
+    print(f"[conv grouped] {case}", flush=True)
+    rng = np.random.default_rng(cin * 7 + cout + G)
+    xb = to_bf16(rng.standard_normal((B, H, W, cin), dtype=np.float32))
+    wb = to_bf16((rng.standard_normal((cout, k, k, cin // G), dtype=np.float32) *
+                  np.float32(np.sqrt(2.0 / (k * k * cin // G)))))
+    x, w = from_bf16(xb), from_bf16(wb)
+    bias = scale = shift = None
+    if post == "bn":
+        scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+        shift = rng.normal(0, 0.1, cout).astype(np.float32)
+        got = K.conv2d_bn_act(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(scale),
+                              dev.upload(shift), s, p, G, act, layout="nhwc").to_host()
+    else:
+        if post == "bias":
+            bias = from_bf16(to_bf16(rng.normal(0, 0.1, cout).astype(np.float32)))
+        got = K.conv2d(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16),
+                       dev.upload(to_bf16(bias), tg.bf16) if bias is not None else None, s, p, G, act,
+                       layout="nhwc").to_host()
+    ref = orc.conv2d_nhwc(x, w, bias, stride=s, padding=p, groups=G)
+    if post == "bn":
+        ref = ref * scale + shift
+    if act is not None:
+        ref = {"relu": orc.relu, "silu": orc.silu, "gelu": orc.gelu}[act](ref)
+    check_bf16(got, ref, str(case))
