@@ -334,7 +334,9 @@ teeny_status teeny_norm_act_forward(const void *x, void *y, const void *weight, 
  * BLOCK_OW is a reference tiling choice and has no counterpart here.
  * `act` fuses an activation after the bias (TEENY_ACT_NONE = reference).
  * Layout NCHW: any dtype (F32, BF16).  Layout NHWC: BF16 runs the MFMA
- * implicit-GEMM kernels (weights [C_OUT,KH,KW,C_IN/G]); F32 also accepted. */
+ * implicit-GEMM kernels (weights [C_OUT,KH,KW,C_IN/G]; grouped convs with
+ * at least 16 output channels per group too, all groups in one launch);
+ * F32 also accepted. */
 typedef struct teeny_conv2d_params {
   int32_t KH, KW;
   int32_t stride_h, stride_w;
@@ -382,9 +384,9 @@ teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, con
  * conv2d_bn_silu_gemm.rs:61-260, conv2d_bn_silu_tiled.rs:49-293, whose
  * padded output rows are expressed here by `y_strides` (NCHW only: element
  * strides between consecutive b, c, oh, ow; NULL = tight).  Any dtype,
- * layout and groups, as teeny_conv2d_forward; the bf16 NHWC groups == 1 case
- * runs on the MFMA implicit GEMM with the affine and activation applied to
- * the fp32 accumulator. */
+ * layout and groups, as teeny_conv2d_forward; bf16 NHWC (groups == 1, or
+ * at least 16 output channels per group) runs on the MFMA implicit GEMM
+ * with the affine and activation applied to the fp32 accumulator. */
 teeny_status teeny_conv2d_bn_act_forward(const void *x, const void *w, const float *bn_scale, const float *bn_shift,
                                         void *y, int64_t B, int64_t C_IN, int64_t C_OUT, int64_t H, int64_t W,
                                         int64_t OH, int64_t OW, const int64_t *y_strides,
