@@ -53,13 +53,17 @@ struct TileConvParams {
   int phase_off[4];
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false>
+// IPB > 1: a band is IPB whole images of RB = OH rows (the 7x7 layers),
+// their halos stacked (image i's halo rows at i (RB + KH - 1)).
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1>
 struct TileShape {
-  static constexpr int NPX = RB * OWT;           // pixels per band
+  static constexpr int NPX = RB * OWT * IPB;     // pixels per band
   static constexpr int NW = (NPX + 31) / 32;     // waves
   static constexpr int NT = 64 * NW;
   // dx mode: a phase reads dy rows u, u + 1 and columns v, v + 1 (no padding)
-  static constexpr int HR = DX2 ? RB + 1 : RB + KH - 1, HC = DX2 ? OWT + 1 : OWT + KW - 1;
+  static constexpr int HRI = DX2 ? RB + 1 : RB + KH - 1;  // halo rows per image of the band
+  static constexpr int HR = HRI * IPB, HC = DX2 ? OWT + 1 : OWT + KW - 1;
+  static_assert(IPB == 1 || !DX2, "multi-image bands: forward only");
   static constexpr int HSLOTS = HR * HC * 4;     // 16-byte halo slots (32 channels per pixel)
   static constexpr int QT = INT8B ? 2 : 4;       // 16-byte slots per tap segment
   // taps of a unit, at most (dx mode: row phase a = 1 with both column
@@ -83,10 +87,10 @@ struct TileShape {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false>
-__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1) void conv_tile_kernel(
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1>
+__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::NT), 1) void conv_tile_kernel(
     TileConvParams p) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>;
   static_assert(!DX2 || (KH == 3 && KW == 3 && !INT8B), "dx mode: bf16 3x3 stride 2 pad 1");
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
   constexpr int EPI_STORES = 4 * (BN / 64) * (DX2 ? 2 : 1);  // per unit (dx mode: two phases)
@@ -100,7 +104,8 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1
 
   const int bands_per_img = p.OH / RB;
   const int n_tiles = p.Cout / BN;
-  const int per_phase = p.B * bands_per_img * n_tiles;
+  const int n_bands = IPB > 1 ? (p.B + IPB - 1) / IPB : p.B * bands_per_img;
+  const int per_phase = n_bands * n_tiles;
   const int n_units = (DX2 ? 2 : 1) * per_phase;
   const int nch = p.Cin / 32;
   const int G = static_cast<int>(gridDim.x);
@@ -116,8 +121,13 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1
     if constexpr (DX2) u %= per_phase;
     n0 = (u % n_tiles) * BN;
     const int band = u / n_tiles;
-    b = band / bands_per_img;
-    oh0 = (band % bands_per_img) * RB;
+    if constexpr (IPB > 1) {
+      b = band * IPB;  // the band's first image (the last band may be partial)
+      oh0 = 0;
+    } else {
+      b = band / bands_per_img;
+      oh0 = (band % bands_per_img) * RB;
+    }
   };
 
   const __amdgpu_buffer_rsrc_t x_rsrc = buffer_rsrc(p.x, p.x_bytes);
@@ -151,11 +161,13 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1
         const int s = ins * 64 + lane;
         const int pix = s >> 2, pos = s & 3;
         const int hr = pix / HC, hc = pix % HC;
-        const int ih = oh0 - p.PH + hr, iw = hc - p.PW;
+        // multi-image band: halo row hr is row hr % HRI of image b + hr / HRI
+        const int bi = b + (IPB > 1 ? hr / S::HRI : 0);
+        const int ih = oh0 - p.PH + (IPB > 1 ? hr % S::HRI : hr), iw = hc - p.PW;
         const bool ok = live & (s < S::HSLOTS) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
-                        (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W));
+                        (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W)) & (bi < p.B);
         if (ok)
-          off = static_cast<int>(((static_cast<int64_t>(b) * p.H + ih) * p.W + iw) * p.Cin * 2 +
+          off = static_cast<int>(((static_cast<int64_t>(bi) * p.H + ih) * p.W + iw) * p.Cin * 2 +
                                  16 * (pos ^ ((hc >> 2) & 3)));
       } else {
         const int s = (ins - S::HINSTR) * 64 + lane;
@@ -189,7 +201,9 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1
 
   // ── MFMA side
   const int px = min(32 * w + c, S::NPX - 1);  // pixels past the band repeat the last one
-  const int pr = px / OWT, pc = px % OWT;
+  // halo row of the pixel's output row (multi-image band: its image's halo)
+  const int pr = IPB > 1 ? (px / (RB * OWT)) * S::HRI + (px % (RB * OWT)) / OWT : px / OWT;
+  const int pc = px % OWT;
   // dx mode: one accumulator set per column phase
   constexpr int NSET = DX2 ? 2 : 1;
   f32x16 acc[NSET * NB];
@@ -417,9 +431,10 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2>::NT), 1
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
 }
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1>
 inline bool tile_conv_fits(const GemmParams &p) {
-  return p.KH == KH && p.KW == KW && p.SH == 1 && p.SW == 1 && p.OW == OWT && p.OH % RB == 0 && p.PH >= 0 &&
+  return p.KH == KH && p.KW == KW && p.SH == 1 && p.SW == 1 && p.OW == OWT && p.OH % RB == 0 &&
+         (IPB == 1 || p.OH == RB) && p.PH >= 0 &&
          p.PW >= 0 && p.Cin % 32 == 0 && p.N % BN == 0 && p.ldc == p.N && p.c_ow <= 0 &&
          (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(p.C) & 15) == 0 &&
@@ -428,10 +443,10 @@ inline bool tile_conv_fits(const GemmParams &p) {
          static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2) < 0x7fffffff;
 }
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1>
 inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B>;
-  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, false, IPB>;
+  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B, false, IPB>;
   static const bool attr_set = [kern] {
     return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                S::LDS) == hipSuccess;
@@ -455,15 +470,17 @@ inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
   t.act = act;
   t.x_bytes = static_cast<int>(static_cast<int64_t>(t.B) * p.H * p.W * p.Cin * 2);
   t.w_bytes = static_cast<int>(static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2));
-  const int units = t.B * (p.OH / RB) * (p.N / BN);
+  const int bands = IPB > 1 ? (t.B + IPB - 1) / IPB : t.B * (p.OH / RB);
+  const int units = bands * (p.N / BN);
   const int grid = std::min(units, device_cu_count());
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(S::NT), S::LDS, s, t);
 }
 
 // The band-tiled kernel for this conv, if one is built for its shape: the
-// 14x14 and 28x28 bf16 3x3 convs (ResNet stages 2 and 3: 14x14 256 -> 256
-// at batch 64 33.4 -> 22.3 us, 28x28 128 -> 128 27.9 -> 23.6 us against the
-// implicit GEMM).  Measured and not taken: the int8 28x28 conv (62 us
+// 14x14, 28x28 and 7x7 bf16 3x3 convs (ResNet stages 2-4: 14x14 256 -> 256
+// at batch 64 33.4 -> 22.3 us, 28x28 128 -> 128 27.9 -> 23.6 us, 7x7 512 ->
+// 512 36.6 -> 31.1 us against the implicit GEMM, split four ways along K
+// there).  Measured and not taken: the int8 28x28 conv (62 us
 // against 54 us: each converted weight fragment feeds one MFMA here, so the
 // int8 -> bf16 conversion outweighs the matrix work; the GEMM reuses it
 // across row blocks).
@@ -476,6 +493,11 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
     }
     if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) {
       launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s);
+      return true;
+    }
+    // 7x7 images, two per band (98 pixels, four waves)
+    if (tile_conv_fits<3, 3, 7, 7, 64, false, 2>(p)) {
+      launch_tile_conv<3, 3, 7, 7, 64, false, 2>(p, act, s);
       return true;
     }
   }

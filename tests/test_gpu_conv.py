@@ -271,8 +271,8 @@ TILE_CASES = [
     # B, H, W, Cin, Cout, pad, act, post, int8: stride-1 bf16 3x3 convs with
     # 14- and 28-wide outputs take the band-tiled kernel (a band of 196 output
     # pixels x 64 channels per workgroup, input rows with their halo and the
-    # chunk's weights staged per 32 input channels); the int8 cases run the
-    # implicit GEMM
+    # chunk's weights staged per 32 input channels), 7x7 outputs a band of
+    # two images; the int8 cases run the implicit GEMM
     (5, 14, 14, 256, 256, 1, "relu", "bias", False),   # the 14x14 ResNet 3x3 at a ragged batch
     (2, 14, 14, 64, 128, 1, "gelu", "bn", False),      # two channel tiles, folded BatchNorm
     (2, 16, 16, 96, 64, 0, None, None, False),         # no padding: 16 -> 14, three chunks
@@ -284,6 +284,12 @@ TILE_CASES = [
     (3, 28, 28, 128, 128, 1, "relu", "bias", False),   # the 28x28 ResNet 3x3
     (1, 28, 28, 32, 192, 1, "silu", None, False),      # one chunk, three channel tiles
     (30, 28, 28, 64, 192, 1, "relu", None, False),     # 360 bands x tiles: two per workgroup
+    # 7x7 outputs: two whole images per band (the last band of an odd batch
+    # half empty)
+    (5, 7, 7, 64, 128, 1, "relu", "bias", False),
+    (4, 7, 7, 96, 64, 1, None, "bn", False),           # three chunks
+    (600, 7, 7, 32, 64, 1, "silu", None, False),       # 300 bands: several per workgroup
+    (3, 9, 9, 64, 64, 0, "gelu", "bias", False),       # no padding: 9 -> 7
     (3, 28, 28, 256, 256, 1, None, "bias", True),      # the W8A16 conv at a ragged batch
     (2, 28, 28, 64, 128, 1, "relu", None, True),
 ]
