@@ -130,16 +130,20 @@ class Ctx:
         self.stream.synchronize()
         return out
 
-    def measure(self, ops):
+    def measure(self, ops, step_ops=None, extra_steps=None):
         """ops: [(name, [launch_0, launch_1, ...])], launch_r running the op on
-        rotation r.  Returns (step ms, {name: ms per launch of the op alone})."""
+        rotation r.  Returns (step ms, {name: ms per launch of the op alone}).
+        `step_ops` (same form, default `ops`) are what one step runs;
+        `extra_steps` ({label: ops}) are timed the same way after it, into
+        self.extra_step_ms."""
         tg, dev, stream = self.tg, self.dev, self.stream
         steps, warmup = self.args.steps, self.args.warmup
+        step_ops = ops if step_ops is None else step_ops
         if self.marker is not None:
             log(f"[bench] ops per step: {json.dumps([n for n, _ in ops])} steps={steps}")
 
         def step(i):
-            for _, fns in ops:
+            for _, fns in step_ops:
                 fns[i % len(fns)]()
 
         def replay_ms(enqueue, count):
@@ -175,6 +179,15 @@ class Ctx:
             step(i)
         warm(step, self.args.warm_ms)
         ms = replay_ms(step, steps)
+        self.extra_step_ms = {}
+        for label, xops in (extra_steps or {}).items():
+            def xstep(i, xops=xops):
+                for _, fns in xops:
+                    fns[i % len(fns)]()
+            for i in range(warmup):
+                xstep(i)
+            warm(xstep, self.args.warm_ms)
+            self.extra_step_ms[label] = replay_ms(xstep, steps)
         per = {}
         for name, fns in ops:
             if self.marker is not None:
@@ -491,7 +504,38 @@ def bench_resnet(ctx):
                    K.conv2d(x[r], w[r], b, s, p, 1, "relu" if relu else None, "nhwc", y=y[r], stream=stream)
                    for r in range(2)])
            for name, x, w, b, y, s, p, relu, _, _ in bufs]
-    ms, per = ctx.measure(ops)
+    # The step is the stack: each conv reads the activation the previous one
+    # wrote (c1 -> c2 -> c3 -> the next block's c1; a downsample reads its
+    # block's input, as c1 does; stage 1's first block reads its own buffer,
+    # the stem's pooled output, which no conv writes).  Each op's own timing,
+    # and the `independent_inputs` step, give every conv a separate input.
+    byname = {bb[0]: bb for bb in bufs}
+    chain_in, prev, block_in = {}, None, None
+    for name, cin, cout, h, k, s, p, relu in layers:
+        if name == "stem":
+            src = None
+        elif name.endswith("c1"):
+            block_in = None if name == "l1b0c1" else prev
+            src = block_in
+        elif name.endswith("ds"):
+            src = block_in
+        else:
+            src = prev
+        chain_in[name] = src
+        if not name.endswith("ds"):
+            prev = name
+    step_ops = []
+    for name, x, w, b, y, s, p, relu, _, _ in bufs:
+        src = chain_in[name]
+        xin = x if src is None else byname[src][4]  # the producing conv's outputs, one per rotation
+        if name == "l1b0ds":
+            xin = byname["l1b0c1"][1]  # stage 1's first block: c1's own input
+        step_ops.append((name, [lambda r=r, xin=xin, w=w, b=b, y=y, s=s, p=p, relu=relu:
+                                K.conv2d(xin[r], w[r], b, s, p, 1, "relu" if relu else None, "nhwc", y=y[r],
+                                         stream=stream)
+                                for r in range(2)]))
+    ms, per = ctx.measure(ops, step_ops, {"independent_inputs": ops})
+    independent_ms = ctx.extra_step_ms["independent_inputs"]
     value = flops / (ms * 1e-3) / 1e12
     # each layer's own floor: the longer of its MFMA time at the bf16 peak and
     # its algorithmic bytes at the HBM peak; the stack's floor is their sum
@@ -509,10 +553,15 @@ def bench_resnet(ctx):
     stack = {"floor_us": round(floor_sum, 1), "step_us": round(ms * 1e3, 1),
              "frac_of_floor": round(floor_sum / (ms * 1e3), 4), "alone_sum_us": round(kernel_sum_us, 1),
              "step_minus_alone_us": round(ms * 1e3 - kernel_sum_us, 1),
+             "independent_inputs_step_us": round(independent_ms * 1e3, 1),
+             "step": "chained: each conv reads the activation the previous conv wrote (downsamples their block's "
+                     "input); independent_inputs_step_us runs the same 53 convs with every conv reading its own "
+                     "buffer (the step as timed before the chaining)",
              "how": "floor = sum over layers of max(FLOP / 2.5 PFLOP/s, algorithmic bytes / 8 TB/s); alone_sum = "
-                    "the layers timed alone (own replay, operands warm in the Infinity Cache); a kernel trace of "
-                    "the step graph shows no idle time between its kernels: the difference is the kernels "
-                    "running longer inside the step (cold operands, the previous layer's output written back)"}
+                    "the layers timed alone (own replay over two operand copies); a kernel trace of the step "
+                    "graph shows no idle time between its kernels: the difference is the kernels running longer "
+                    "inside the step (the previous layer's output written back meanwhile, weights and inputs "
+                    "that are not in the Infinity Cache)"}
     dom = max(per, key=per.get)
     fdom, bdom = [(bb[8], bb[9]) for bb in bufs if bb[0] == dom][0]
     cpu = None
