@@ -180,7 +180,7 @@ class Ctx:
         warm(step, self.args.warm_ms)
         ms = replay_ms(step, steps)
         self.extra_step_ms = {}
-        for label, xops in (extra_steps or {}).items():
+        for label, xops in ({} if self.args.no_extra_steps else (extra_steps or {})).items():
             def xstep(i, xops=xops):
                 for _, fns in xops:
                     fns[i % len(fns)]()
@@ -535,7 +535,7 @@ def bench_resnet(ctx):
                                          stream=stream)
                                 for r in range(2)]))
     ms, per = ctx.measure(ops, step_ops, {"independent_inputs": ops})
-    independent_ms = ctx.extra_step_ms["independent_inputs"]
+    independent_ms = ctx.extra_step_ms.get("independent_inputs", float("nan"))
     value = flops / (ms * 1e-3) / 1e12
     # each layer's own floor: the longer of its MFMA time at the bf16 peak and
     # its algorithmic bytes at the HBM peak; the stack's floor is their sum
@@ -553,7 +553,7 @@ def bench_resnet(ctx):
     stack = {"floor_us": round(floor_sum, 1), "step_us": round(ms * 1e3, 1),
              "frac_of_floor": round(floor_sum / (ms * 1e3), 4), "alone_sum_us": round(kernel_sum_us, 1),
              "step_minus_alone_us": round(ms * 1e3 - kernel_sum_us, 1),
-             "independent_inputs_step_us": round(independent_ms * 1e3, 1),
+             "independent_inputs_step_us": None if math.isnan(independent_ms) else round(independent_ms * 1e3, 1),
              "step": "chained: each conv reads the activation the previous conv wrote (downsamples their block's "
                      "input); independent_inputs_step_us runs the same 53 convs with every conv reading its own "
                      "buffer (the step as timed before the chaining)",
@@ -944,6 +944,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--op-markers", action="store_true",
                     help="an empty marker launch after every op (splits a rocprofv3 run per op)")
+    ap.add_argument("--no-extra-steps", action="store_true",
+                    help="skip the second step timing of a workload (the ResNet stack with independent "
+                         "inputs), as the profiler runs do: one step graph per workload under the tracer")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="first run one device-to-device copy of BYTES (a reference kernel of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
