@@ -32,10 +32,13 @@
 // them per space-to-depth row) instead of a precomputed space-to-depth
 // tensor; once a stage has landed, every thread rebuilds the s2d halo pixels
 // from them (two 12-byte raw windows per pixel, shifted into place with
-// alignbit), a second barrier publishes the halo, and the MFMA side is the
-// same.  The weights' s2d form is also built at start-up from the raw 7x7
-// weights.  This replaces a separate repack pass that wrote and re-read a
-// 27 MB space-to-depth copy of the batch-64 input (stem 50 -> 41 us).
+// alignbit), a second barrier publishes the halo, and the MFMAs read it.
+// The weights' s2d form is also built at start-up from the raw 7x7 weights.
+// This replaces a separate repack pass that wrote and re-read a 27 MB
+// space-to-depth copy of the batch-64 input (stem 50 -> 41 us).  The s2d
+// pixels hold their 12 channels with no padding (24 bytes), so a kernel
+// row's 4 taps are 48 consecutive k and the MFMAs run 12 k-steps per
+// output, not the 16 of 16-channel pixels (stem 38.6 -> 35.2 us).
 //
 // Pipeline: NHB halo buffers, the DMA NHB - 1 chunk stages ahead of the
 // MFMAs, one barrier per stage (a stage's DMA is issued after the barrier
@@ -130,7 +133,13 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   static_assert(NHB >= 2 && NHB <= 4 && INFLIGHT < 16, "halo stages / vmcnt field");
   static_assert(!RAW || (CIN == 16 && KH == 4 && KW == 4 && NCH == 1), "raw mode: the 7x7/2 stem's s2d form");
   constexpr int DBUF = RAW ? R::BUF : S::HBUF;  // bytes of one DMA stage buffer
-  constexpr int S2D_BYTES = (S::HR * HC * CPP * 16 + 1023) / 1024 * 1024;
+  // raw mode: s2d halo pixels of 12 channels (24 bytes, no padding), so a
+  // kernel row's 4 taps are 48 consecutive k; weight rows of 4 x 48 k plus
+  // one 16-byte pad (an odd number of 16-byte units)
+  constexpr int kRawPix = 24, kRawWP = 4 * 48 * 2 + 16;
+  static_assert(!RAW || kRawWP <= S::WP, "packed weight rows fit the weight area");
+  constexpr int S2D_BYTES = RAW ? (S::HR * HC * kRawPix + 1023) / 1024 * 1024
+                                : (S::HR * HC * CPP * 16 + 1023) / 1024 * 1024;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *const wlds = smem;
   char *const dbuf = smem + S::WBYTES;                       // DMA stage buffers
@@ -150,21 +159,23 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
 
   // ── weights into LDS once (16-byte loads; before any DMA is in flight)
   if constexpr (RAW) {
-    // the s2d form of the 7x7 weights, built here: tap (kh2, kw2) channel
-    // (2 dy + dx) 3 + c holds w[co][2 kh2 + dy][2 kw2 + dx][c] (zero past the
-    // 7x7 kernel, and for channels 12 .. 15)
+    // the s2d form of the 7x7 weights, built here, packed: row co holds, per
+    // kernel row kh2, the 4 taps kw2 x 12 channels (2 dy + dx) 3 + c, i.e.
+    // k = 48 kh2 + 12 kw2 + (2 dy + dx) 3 + c holds w[co][2 kh2 + dy][2 kw2 +
+    // dx][c] (zero past the 7x7 kernel)
     for (int i = tid; i < S::COUT * 16; i += S::NT) {
       const int co = i >> 4, tap = i & 15, kh2 = tap >> 2, kw2 = tap & 3;
-      bf16 e[16];
+      bf16 e[12];
 #pragma unroll
-      for (int ch = 0; ch < 16; ++ch) {
+      for (int ch = 0; ch < 12; ++ch) {
         const int q = ch / 3, cc = ch % 3, kh = 2 * kh2 + (q >> 1), kw = 2 * kw2 + (q & 1);
-        e[ch] = (ch < 12 && kh < 7 && kw < 7) ? p.w[((co * 7 + kh) * 7 + kw) * 3 + cc] : static_cast<bf16>(0.0f);
+        e[ch] = (kh < 7 && kw < 7) ? p.w[((co * 7 + kh) * 7 + kw) * 3 + cc] : static_cast<bf16>(0.0f);
       }
-      u32x4 v[2];
-      __builtin_memcpy(v, e, 32);
-      *reinterpret_cast<u32x4 *>(wlds + co * S::WP + 32 * tap) = v[0];
-      *reinterpret_cast<u32x4 *>(wlds + co * S::WP + 32 * tap + 16) = v[1];
+      u32x2 v[3];
+      __builtin_memcpy(v, e, 24);
+      char *dst = wlds + co * kRawWP + 2 * (48 * kh2 + 12 * kw2);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) *reinterpret_cast<u32x2 *>(dst + 8 * j) = v[j];
     }
   } else {
     constexpr int CPR = S::K / 8;  // 16-byte chunks per weight row
@@ -256,8 +267,8 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   f32x16 acc[2] = {zero16(), zero16()};
   // raw mode: s2d halo pixel (hr, hc) from its two raw rows 2 hr + dy: the
   // 12 bytes (two pixels of three channels) of raw columns 2 hc - 3, 2 hc - 2
-  // of each row, read as four aligned dwords and shifted by a half-word,
-  // then four zero words: channels (2 dy + dx) 3 + c, 12 .. 15 zero
+  // of each row, read as four aligned dwords and shifted by a half-word:
+  // channels (2 dy + dx) 3 + c, 24 bytes
   auto repack = [&](int st) __attribute__((always_inline)) {
     const char *rb = dbuf + (st % NHB) * DBUF + 16;  // row 0 slot 0 (past the guard)
     for (int px = tid; px < S::HR * HC; px += S::NT) {
@@ -272,9 +283,9 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
         o[3 * dy + 1] = __builtin_amdgcn_alignbit(d2, d1, 16);
         o[3 * dy + 2] = __builtin_amdgcn_alignbit(d3, d2, 16);
       }
-      char *dst = s2d + px * 32;
-      *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<u32x4 *>(dst + 16) = u32x4{o[4], o[5], 0u, 0u};
+      char *dst = s2d + px * kRawPix;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) *reinterpret_cast<u32x2 *>(dst + 8 * j) = u32x2{o[2 * j], o[2 * j + 1]};
     }
   };
 
@@ -283,16 +294,33 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
     const char *hb = RAW ? s2d : dbuf + (st % NHB) * S::HBUF;
     const int ch = st % NCH;
     constexpr int HS = CC / 16;  // k-steps per tap in a chunk
-    constexpr int NKS = KH * KW * HS;
+    // raw mode: 3 k-steps per kernel row (48 packed k), 12 in all, against
+    // the 16 of the padded 16-channel s2d form
+    constexpr int NKS = RAW ? KH * 3 : KH * KW * HS;
     auto frags = [&](int ks, bf16x8 &xf, bf16x8 &w0, bf16x8 &w1) __attribute__((always_inline)) {
-      const int tap = ks / HS, h = ks % HS;
-      const int kh = tap / KW, kw = tap % KW;
-      const int hc = pc + kw;
-      const int hp = (pr + kh) * HC + hc;
-      xf = *reinterpret_cast<const bf16x8 *>(hb + hp * (CC * 2) + 16 * ((2 * h + g) ^ swz(hc)));
-      const int kb = 2 * (tap * CIN + ch * CC + 16 * h + 8 * g);
-      w0 = *reinterpret_cast<const bf16x8 *>(wlds + c * S::WP + kb);
-      w1 = *reinterpret_cast<const bf16x8 *>(wlds + (32 + c) * S::WP + kb);
+      if constexpr (RAW) {
+        // k-step ks: kernel row kh2 = ks / 3, k 16 j .. 16 j + 15 of its 48
+        // (j = ks % 3): s2d pixels pc .. pc + 3 of halo row pr + kh2 are 96
+        // consecutive bytes, of which lane half g reads 16 at 32 j + 16 g
+        // (8-byte aligned: two 8-byte reads)
+        const int kh2 = ks / 3, j = ks % 3;
+        const char *xp = hb + ((pr + kh2) * HC + pc) * kRawPix + 32 * j + 16 * g;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(xp), hi = *reinterpret_cast<const u32x2 *>(xp + 8);
+        const u32x4 v = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        __builtin_memcpy(&xf, &v, 16);
+        const int kb = 2 * (48 * kh2 + 16 * j + 8 * g);
+        w0 = *reinterpret_cast<const bf16x8 *>(wlds + c * kRawWP + kb);
+        w1 = *reinterpret_cast<const bf16x8 *>(wlds + (32 + c) * kRawWP + kb);
+      } else {
+        const int tap = ks / HS, h = ks % HS;
+        const int kh = tap / KW, kw = tap % KW;
+        const int hc = pc + kw;
+        const int hp = (pr + kh) * HC + hc;
+        xf = *reinterpret_cast<const bf16x8 *>(hb + hp * (CC * 2) + 16 * ((2 * h + g) ^ swz(hc)));
+        const int kb = 2 * (tap * CIN + ch * CC + 16 * h + 8 * g);
+        w0 = *reinterpret_cast<const bf16x8 *>(wlds + c * S::WP + kb);
+        w1 = *reinterpret_cast<const bf16x8 *>(wlds + (32 + c) * S::WP + kb);
+      }
     };
     // the fragments of k-step ks + kLA are read while k-step ks multiplies
     // (a window of kLA + 1 sets; a scheduling fence per k-step keeps that
