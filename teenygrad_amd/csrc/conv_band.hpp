@@ -153,7 +153,9 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
   const int bands_per_img = p.OH / RB;
   const int n_units = p.B * bands_per_img;
   const int G = static_cast<int>(gridDim.x);
-  const int wg = static_cast<int>(blockIdx.x);
+  // consecutive units on one XCD: the channel tiles of a band (and
+  // neighbouring bands) read the same input rows from that XCD's L2
+  const int wg = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int my_units = wg < n_units ? (n_units - 1 - wg) / G + 1 : 0;
   const int n_stages = my_units * NCH;
 

@@ -109,7 +109,9 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::N
   const int n_units = (DX2 ? 2 : 1) * per_phase;
   const int nch = p.Cin / 32;
   const int G = static_cast<int>(gridDim.x);
-  const int wg = static_cast<int>(blockIdx.x);
+  // consecutive units on one XCD: the channel tiles of a band (and
+  // neighbouring bands) read the same input rows from that XCD's L2
+  const int wg = xcd_remap(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int my_units = wg < n_units ? (n_units - 1 - wg) / G + 1 : 0;
   const int n_stages = my_units * nch;
   // unit u: co tile fastest (the tiles of one band share its input in L2);
