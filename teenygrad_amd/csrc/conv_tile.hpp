@@ -482,25 +482,28 @@ inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
 // 14x14, 28x28 and 7x7 bf16 3x3 convs (ResNet stages 2-4: 14x14 256 -> 256
 // at batch 64 33.4 -> 22.3 us, 28x28 128 -> 128 27.9 -> 23.6 us, 7x7 512 ->
 // 512 36.6 -> 31.1 us against the implicit GEMM, split four ways along K
-// there).  Measured and not taken: the int8 28x28 conv (62 us
-// against 54 us: each converted weight fragment feeds one MFMA here, so the
-// int8 -> bf16 conversion outweighs the matrix work; the GEMM reuses it
-// across row blocks).
+// there).  int8 weights do not run here as int8 (the 28x28 conv: 62 us
+// against 54 us for the GEMM: each converted weight fragment feeds one MFMA
+// here, so the int8 -> bf16 conversion outweighs the matrix work); the int8
+// conv converts its weights to a bf16 copy first and runs the bf16 kernel.
+// Which band-tiled shape takes this bf16 conv: 1 (14x14), 2 (28-wide), 3
+// (7x7, two images per band), 0 none.
+inline int tile_conv_shape(const GemmParams &p) {
+  if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) return 1;
+  if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) return 2;
+  if (tile_conv_fits<3, 3, 7, 7, 64, false, 2>(p)) return 3;
+  return 0;
+}
+
 template <bool INT8B>
 inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
   if constexpr (!INT8B) {
-    if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) {
-      launch_tile_conv<3, 3, 14, 14, 64, false>(p, act, s);
-      return true;
-    }
-    if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) {
-      launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s);
-      return true;
-    }
-    // 7x7 images, two per band (98 pixels, four waves)
-    if (tile_conv_fits<3, 3, 7, 7, 64, false, 2>(p)) {
-      launch_tile_conv<3, 3, 7, 7, 64, false, 2>(p, act, s);
-      return true;
+    switch (tile_conv_shape(p)) {
+      case 1: launch_tile_conv<3, 3, 14, 14, 64, false>(p, act, s); return true;
+      case 2: launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s); return true;
+      // 7x7 images, two per band (98 pixels, four waves)
+      case 3: launch_tile_conv<3, 3, 7, 7, 64, false, 2>(p, act, s); return true;
+      default: break;
     }
   }
   return false;

@@ -415,45 +415,59 @@ def test_w8a16_conv(dev, orc, B, Cin, Cout, H, act, scratch):
     check_bf16(got, ref, "w8a16 conv")
 
 
-def test_w8a16_conv_config_batch32(dev, orc):
-    # 32 x 256 x 28 x 28, 3x3 p1: the whole output against the oracle
+@pytest.mark.parametrize("scratch", ["none", "workspace"])
+def test_w8a16_conv_config_batch32(dev, orc, scratch):
+    # 32 x 256 x 28 x 28, 3x3 p1: the whole output against the oracle; without
+    # scratch the int8 implicit GEMM, with it the band-tiled kernel on a bf16
+    # copy of the weights
     B, C, H = 32, 256, 28
     rng = np.random.default_rng(0x7EE70004)
     x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
     q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
-    print("[w8a16 conv config] 32x256x28x28", flush=True)
-    got = K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), None, 1, 1).to_host()
+    need = K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)
+    assert need == C * 9 * C * 2, need
+    print(f"[w8a16 conv config] 32x256x28x28 scratch={scratch}", flush=True)
+
+    def run():
+        return K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), None, 1, 1).to_host()
+
+    if scratch == "workspace":
+        with stream_workspace(dev, need):
+            got = run()
+    else:
+        got = run()
     assert np.all(np.isfinite(from_bf16(got)))
     wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
     ref = orc.conv2d_nhwc(x, wdeq, None, stride=1, padding=1)
     check_bf16(got, ref, "all 32 images")
 
 
-@pytest.mark.parametrize("scratch", ["none", "workspace"])
+@pytest.mark.parametrize("scratch", ["none", "short", "workspace"])
 def test_w8a16_conv_large_tile(dev, orc, scratch):
     # 128 x 256 x 28 x 28, 3x3 p1, with bias and ReLU: M = 100352 gives 392
-    # 256 x 256 tiles, so the implicit GEMM takes the large-tile LDS-DMA
-    # kernel on int8 weights (converted in registers; no scratch needed);
-    # images 0, 77 and 127 against the oracle
+    # 256 x 256 tiles, so without scratch (or with less than the bf16 weight
+    # copy needs) the implicit GEMM takes the large-tile LDS-DMA kernel on int8
+    # weights converted in registers; with the reported workspace the
+    # band-tiled kernel runs on the bf16 copy; images 0, 77 and 127 against
+    # the oracle
     B, C, H = 128, 256, 28
     rng = np.random.default_rng(0x7EE70128)
     x = rb(rng.standard_normal((B, H, H, C), dtype=np.float32))
     q, s = quantized_conv_weight(orc, rng, C, 3, 3, C)
     bias = rng.normal(0, 0.1, C).astype(np.float32)
     need = K.conv2d_workspace_size((B, H, H, C), (C, 3, 3, C), 1, 1, 1, tg.i8)
-    assert need == 0, need
+    assert need == C * 9 * C * 2, need
     print(f"[w8a16 conv large tile] 128x256x28x28 scratch={scratch}", flush=True)
 
     def run():
         return K.w8a16_conv2d(dev.upload(to_bf16(x), tg.bf16), dev.upload(q), dev.upload(s), dev.upload(bias), 1, 1,
                               act="relu").to_host()
 
-    if scratch == "workspace":
-        # a caller's workspace attached anyway must not change the plan
-        with stream_workspace(dev, 1 << 20):
-            got = run()
-    else:
+    if scratch == "none":
         got = run()
+    else:
+        with stream_workspace(dev, need if scratch == "workspace" else need - 16):
+            got = run()
     wdeq = orc.dequantize_affine(q.reshape(-1), s, None, q.shape, "channel", 0)
     for b in (0, 77, B - 1):
         ref = orc.relu(orc.conv2d_nhwc(x[b:b + 1], wdeq, bias, stride=1, padding=1))
