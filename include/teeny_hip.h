@@ -585,7 +585,11 @@ teeny_status teeny_w8a16_linear_forward(const void *x, const int8_t *qweight, co
 
 /* W8A16 conv2d, NHWC bf16 activations, int8 weights [C_OUT,KH,KW,C_IN/G]
  * with per-output-channel fp32 scale, fp32 bias or NULL, bf16 output:
- * conv2d_bias_forward (conv2d.rs:642-764) on dequantize_affine's weights. */
+ * conv2d_bias_forward (conv2d.rs:642-764) on dequantize_affine's weights.
+ * With the workspace teeny_conv2d_workspace_size reports (dtype I8), the
+ * 3x3 shapes of the band-tiled kernel run on a bf16 copy of the int8 values
+ * made there (exact; the scale multiplies the accumulator either way);
+ * without it they take the int8 implicit GEMM. */
 teeny_status teeny_w8a16_conv2d_forward(const void *x, const int8_t *qweight, const float *scale,
                                         const float *bias, void *y, int64_t B, int64_t C_IN,
                                         int64_t C_OUT, int64_t H, int64_t W, int64_t OH,
