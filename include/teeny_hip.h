@@ -152,9 +152,9 @@ teeny_status teeny_hip_stream_sync(teeny_stream stream);
  * operator scratch; ptr NULL or bytes 0 detaches.  Operators never allocate:
  * the paths that need scratch -- split-K partial sums for GEMM and conv grids
  * too small to fill the device, the space-to-depth copy of stride-2 NHWC
- * convs whose C_IN is not a multiple of 8, and the one-pass bf16 copy of
- * W8A16 weights for the large compute-bound shapes (M >= 512 and at least
- * one 256 x 256 output tile per CU) -- run only when the stream's
+ * convs whose C_IN is not a multiple of 8, and the bf16 copy of the int8
+ * weights of W8A16 3x3 convs that run on the band-tiled kernel -- run only
+ * when the stream's
  * workspace is large enough (sizes from teeny_linear_workspace_size and
  * teeny_conv2d_workspace_size), and otherwise the operator takes a path that
  * needs none.  Work on one stream runs in order, so every operator on it may

@@ -252,8 +252,10 @@ def test_workspace_registry_and_sizes():
         assert tg.kernels.linear_workspace_size(4096, 4096, 11008, tg.i8) == 0
         assert tg.kernels.linear_workspace_size(4096, 11008, 4096, tg.bf16) == 0
         assert tg.kernels.linear_workspace_size(600, 96, 128, tg.i8) == 0
-        assert tg.kernels.conv2d_workspace_size((32, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 0
-        assert tg.kernels.conv2d_workspace_size((128, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 0
+        # the W8A16 3x3 convs whose shape the band-tiled kernel takes: a bf16
+        # copy of the int8 weights (256 x 9 x 256 x 2 B)
+        assert tg.kernels.conv2d_workspace_size((32, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 256 * 9 * 256 * 2
+        assert tg.kernels.conv2d_workspace_size((128, 28, 28, 256), (256, 3, 3, 256), 1, 1, 1, tg.i8) == 256 * 9 * 256 * 2
         # stride-2 3x3 conv, 3 channels, 20 x 20 -> 10 x 10: space-to-depth input
         # [1, 11, 11, 16] bf16 (3872 B -> 4096) then weights [16, 2, 2, 16] bf16 (2048 B)
         assert tg.kernels.conv2d_workspace_size((1, 20, 20, 3), (16, 3, 3, 3), 2, 1, 1, tg.bf16) == 4096 + 2048
