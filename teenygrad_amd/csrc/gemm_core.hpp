@@ -795,8 +795,9 @@ inline void launch_persist_default(const GemmParams &p, hipStream_t s);
 
 // Tile choice (measured on MI355X over the ResNet-50 and W8A16 shapes):
 //  * the persistent LDS-DMA kernel (gemm_persist.hpp) for bf16 problems of
-//    many 128 x 128 tiles (>= 4 per CU) and K of 128 .. 512 (the 1x1 and
-//    strided 1x1 convs of a ResNet's second stage);
+//    many 128 x 128 tiles (>= 1.5 per CU) and K of 128 .. 512, or up to 1024
+//    for N <= 1024 (the 1x1 and strided 1x1 convs of a ResNet's second and
+//    third stages);
 //  * the streaming kernel (gemm_stream.hpp) for long, HBM-bound problems
 //    with K, N <= 256 and bf16 weights (the full-resolution 1x1 convs);
 //  * the 256 x 256 LDS-DMA kernel (gemm_dma.hpp) when its tiles fill the chip;

@@ -403,18 +403,23 @@ inline void launch_persist_gemm(const GemmParams &p, hipStream_t s, int max_grid
 // kPersistMaxN (narrower outputs waste tile columns: the 64-channel stem GEMM
 // ran 74 -> 124 us), C rows 16-byte aligned with
 // 32-bit byte offsets, and a problem of many tiles with a short k-loop:
-// >= 4 tiles of 128 x 128 per CU and K of 128 .. 512.  Measured on MI355X
-// (batch-64 ResNet-50 convs): 200704 x 128 x 256 43.6 -> 37.4 us (against the
-// streaming kernel), 50176 x 512 x 128 23.5 -> 20.5 us, 50176 x 512 x 256
-// (stride-2 1x1) 34.0 -> 30.6 us; at 784 tiles or K >= 1024 the
-// non-persistent kernels are as fast or faster (deep K: 40 vs 65 us).
+// >= 1.5 tiles of 128 x 128 per CU and K of 128 .. 512 (.. 1024 for N <=
+// 1024).  Measured on MI355X (batch-64 ResNet-50 convs): 200704 x 128 x 256
+// 43.6 -> 37.4 us (against the streaming kernel), 50176 x 512 x 128 23.5 ->
+// 20.5 us, 50176 x 512 x 256 (stride-2 1x1) 34.0 -> 30.6 us; with each conv
+// reading the previous one's output, the stage-3 1x1 convs (784 tiles)
+// 20.9 -> 18.6 us, 50176 x 256 x 512 29.3 -> 26.5 us, 12544 x 512 x 1024
+// 24.6 -> 23.0 us (the ResNet step 1.332 -> 1.312 ms); 3136 x 2048 x 1024
+// (strided 1x1) 25.7 -> 27.5 us and deep K (40 vs 65 us) stay on the
+// non-persistent kernels.
 template <bool INT8B, int AMODE>
 inline bool persist_gemm_fits(const GemmParams &p) {
   if constexpr (INT8B || (AMODE != kAPlain && AMODE != kAConvVec)) {
     return false;
   } else {
-    return dma_gemm_ok<false, AMODE>(p) && p.N % 128 == 0 && p.N <= kPersistMaxN && p.K >= 128 && p.K <= 512 &&
-           tiles_of(p, 128, 128) >= 4 * static_cast<int64_t>(device_cu_count()) && p.ldc % 8 == 0 &&
+    return dma_gemm_ok<false, AMODE>(p) && p.N % 128 == 0 && p.N <= kPersistMaxN && p.K >= 128 &&
+           (p.K <= 512 || (p.K <= 1024 && p.N <= 1024)) &&
+           2 * tiles_of(p, 128, 128) >= 3 * static_cast<int64_t>(device_cu_count()) && p.ldc % 8 == 0 &&
            (reinterpret_cast<uintptr_t>(p.C) & 15) == 0 && static_cast<int64_t>(p.M) * p.ldc * 2 < 0x7fffffff;
   }
 }

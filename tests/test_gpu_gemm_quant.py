@@ -104,11 +104,14 @@ def tile_rows(m, tile, rng):
 
 
 @pytest.mark.parametrize("m,n,k,pad", [(50000, 512, 128, 0), (50000, 512, 256, 8), (131072, 128, 384, 0),
-                                       (40000, 1024, 512, 16)])
+                                       (40000, 1024, 512, 16), (12544, 1024, 256, 0), (12544, 512, 1024, 0),
+                                       (20000, 384, 768, 8)])
 def test_linear_bf16_persistent(dev, orc, m, n, k, pad):
-    # >= 4 tiles of 128 x 128 per CU and 128 <= K <= 512: the persistent
-    # LDS-DMA kernel (one DMA ring per workgroup across its tiles; 50000 and
-    # 40000 end in a partial row tile, K = 128 is shorter than the ring).
+    # >= 1.5 tiles of 128 x 128 per CU and 128 <= K <= 512 (<= 1024 for
+    # N <= 1024): the persistent LDS-DMA kernel (one DMA ring per workgroup
+    # across its tiles; 50000, 40000 and 20000 end in a partial row tile,
+    # K = 128 is shorter than the ring; 12544 x 512 x 1024 and 20000 x 384
+    # x 768 run 1.5-1.8 tiles per CU, some workgroups one tile).
     # Output rows padded to N + pad: the padding columns stay untouched.
     # One row of every 128-row tile (each workgroup's every tile) vs the oracle.
     print(f"[linear persistent] m={m} n={n} k={k} ldy={n + pad}", flush=True)
