@@ -304,7 +304,10 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
         }
       }
       // rows back as 128-byte segments: instruction r8, lane L holds row
-      // 8 r8 + L / 8, position L % 8 = column chunk (L % 8) ^ (row % 8)
+      // 8 r8 + L / 8, position L % 8 = column chunk (L % 8) ^ (row % 8), by
+      // non-temporal stores (cache policy nt), which leave the caches to the
+      // DMA ring's operands: 200704 x 128 x 256 35.7 -> 28.0 us, the stage-3
+      // 1x1 convs 17.9 -> 15.2 us, the ResNet step 1.278 -> 1.257 ms
 #pragma clang loop unroll(full)
       for (int r8 = 0; r8 < 4; ++r8) {
         const int r = 8 * r8 + (lane >> 3), pos = lane & 7;
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(256, MINW) void gemm_persist_kernel(GemmParams p) {
                             ? static_cast<int>((static_cast<uint32_t>(m) * static_cast<uint32_t>(p.ldc) +
                                                 static_cast<uint32_t>(nw)) * 2u) + 16 * (pos ^ (r & 7))
                             : kOffNone;
-        __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, off, 0, 2);
       }
     }
   };
