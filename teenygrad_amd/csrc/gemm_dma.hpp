@@ -508,7 +508,9 @@ __global__ __launch_bounds__(256, MINW) void gemm_dma_kernel(GemmParams p) {
       const u32x4 v = *reinterpret_cast<const u32x4 *>(cs + ml * CP + (((nl >> 3) ^ ((ml >> 4) & 1)) << 3));
       bf16 *dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
       if (vec16 && n + 8 <= p.N) {
-        *reinterpret_cast<u32x4 *>(dst) = v;
+        // non-temporal: the output does not displace the operand k-slices
+        // the XCD's other tiles still read (11008 -> 4096 316 -> 311 us)
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(dst));
       } else {
         bf16 e[8];
         __builtin_memcpy(e, &v, 16);
