@@ -1329,7 +1329,9 @@ __global__ __launch_bounds__(256, 2) void conv_dw_mfma(const bf16 *__restrict__ 
       for (int v = 0; v < 16; ++v) {
         const int m = co0 + 64 * wm + 32 * i + mfma32_row(v, g);
         if (m >= M) continue;
-        if constexpr (PART) part[(static_cast<int64_t>(split) * M + m) * N + n] = acc[i][j][v];
+        // partials by non-temporal stores (1x1 512 -> 2048 dw 27.2 -> 24.7 us,
+        // 3x3 128 -> 128 40.1 -> 39.3 us)
+        if constexpr (PART) __builtin_nontemporal_store(acc[i][j][v], part + (static_cast<int64_t>(split) * M + m) * N + n);
         else dw[static_cast<int64_t>(m) * N + n] = static_cast<bf16>(acc[i][j][v]);
       }
     }
