@@ -527,6 +527,8 @@ static size_t conv_scratch_bytes(const ConvGeo &q) {
     case kConvPlain: return gemm_scratch_bytes<INT8B, kAPlain>(p);
     case kConvVec:
       if (INT8B && tile_w8_scratch_bytes(p) > 0) return tile_w8_scratch_bytes(p);
+      // the row-band and band-tiled kernels need none
+      if (!INT8B && (band_fits<64, 3, 3, 56, 4>(p) || tile_conv_shape(p) != 0)) return 0;
       return gemm_scratch_bytes<INT8B, kAConvVec>(p);
     case kConvScalarGemm: return gemm_scratch_bytes<INT8B, kAConvScalar>(p);
     case kConvS2D: {

@@ -1,6 +1,7 @@
 // Band-tiled convolution with streamed weights, for stride-1 NHWC convs whose
 // input rows are short (built for the 14x14 3x3 ResNet layers; the template
-// also takes 28-wide outputs and int8 weights):
+// also takes 28-wide outputs, 7x7 outputs two images at a time, stride-2 3x3
+// convs to 7x7 outputs, and int8 weights):
 //
 //   y[b, oh, ow, n] = act( scale[n] * sum_{kh, kw, ci} x[b, oh - PH + kh, ow - PW + kw, ci]
 //                                      * w[n, kh, kw, ci] + bias[n] )
@@ -55,15 +56,21 @@ struct TileConvParams {
 
 // IPB > 1: a band is IPB whole images of RB = OH rows (the 7x7 layers),
 // their halos stacked (image i's halo rows at i (RB + KH - 1)).
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1>
+// S2: stride 2 (3x3): the halo holds input rows 2 oh0 - PH .. 2 (oh0 + RB -
+// 1) - PH + 2 and, per row, its columns as two phase planes, the even halo
+// columns hc = 2 j at slots j = 0 .. OWT, then the odd ones at OWT + 1 + j,
+// so the 32 consecutive output pixels of a fragment read consecutive slots.
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false>
 struct TileShape {
   static constexpr int NPX = RB * OWT * IPB;     // pixels per band
   static constexpr int NW = (NPX + 31) / 32;     // waves
   static constexpr int NT = 64 * NW;
+  static constexpr int PLANE = OWT + 1;          // stride 2: slots per column phase plane
   // dx mode: a phase reads dy rows u, u + 1 and columns v, v + 1 (no padding)
-  static constexpr int HRI = DX2 ? RB + 1 : RB + KH - 1;  // halo rows per image of the band
-  static constexpr int HR = HRI * IPB, HC = DX2 ? OWT + 1 : OWT + KW - 1;
+  static constexpr int HRI = DX2 ? RB + 1 : (S2 ? 2 * RB + 1 : RB + KH - 1);  // halo rows per image of the band
+  static constexpr int HR = HRI * IPB, HC = DX2 ? OWT + 1 : (S2 ? 2 * PLANE : OWT + KW - 1);
   static_assert(IPB == 1 || !DX2, "multi-image bands: forward only");
+  static_assert(!S2 || (KH == 3 && KW == 3 && !DX2), "stride-2 mode: 3x3 forward");
   static constexpr int HSLOTS = HR * HC * 4;     // 16-byte halo slots (32 channels per pixel)
   static constexpr int QT = INT8B ? 2 : 4;       // 16-byte slots per tap segment
   // taps of a unit, at most (dx mode: row phase a = 1 with both column
@@ -87,10 +94,10 @@ struct TileShape {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1>
-__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::NT), 1) void conv_tile_kernel(
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false>
+__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2>::NT), 1) void conv_tile_kernel(
     TileConvParams p) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2>;
   static_assert(!DX2 || (KH == 3 && KW == 3 && !INT8B), "dx mode: bf16 3x3 stride 2 pad 1");
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
   constexpr int EPI_STORES = 4 * (BN / 64) * (DX2 ? 2 : 1);  // per unit (dx mode: two phases)
@@ -162,15 +169,17 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::N
       if (ins < S::HINSTR) {
         const int s = ins * 64 + lane;
         const int pix = s >> 2, pos = s & 3;
-        const int hr = pix / HC, hc = pix % HC;
+        // halo slot cs of row hr holds halo column hc (stride 2: its phase plane)
+        const int hr = pix / HC, cs = pix % HC;
+        const int hc = S2 ? 2 * (cs % S::PLANE) + cs / S::PLANE : cs;
         // multi-image band: halo row hr is row hr % HRI of image b + hr / HRI
         const int bi = b + (IPB > 1 ? hr / S::HRI : 0);
-        const int ih = oh0 - p.PH + (IPB > 1 ? hr % S::HRI : hr), iw = hc - p.PW;
+        const int ih = (S2 ? 2 * oh0 : oh0) - p.PH + (IPB > 1 ? hr % S::HRI : hr), iw = hc - p.PW;
         const bool ok = live & (s < S::HSLOTS) & (static_cast<unsigned>(ih) < static_cast<unsigned>(p.H)) &
                         (static_cast<unsigned>(iw) < static_cast<unsigned>(p.W)) & (bi < p.B);
         if (ok)
           off = static_cast<int>(((static_cast<int64_t>(bi) * p.H + ih) * p.W + iw) * p.Cin * 2 +
-                                 16 * (pos ^ ((hc >> 2) & 3)));
+                                 16 * (pos ^ ((cs >> 2) & 3)));
       } else {
         const int s = (ins - S::HINSTR) * 64 + lane;
         const int n = s / S::RS, j = s % S::RS;
@@ -203,8 +212,9 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::N
 
   // ── MFMA side
   const int px = min(32 * w + c, S::NPX - 1);  // pixels past the band repeat the last one
-  // halo row of the pixel's output row (multi-image band: its image's halo)
-  const int pr = IPB > 1 ? (px / (RB * OWT)) * S::HRI + (px % (RB * OWT)) / OWT : px / OWT;
+  // halo row of the pixel's first tap (multi-image band: in its image's halo)
+  constexpr int SR = S2 ? 2 : 1;
+  const int pr = IPB > 1 ? (px / (RB * OWT)) * S::HRI + SR * ((px % (RB * OWT)) / OWT) : SR * (px / OWT);
   const int pc = px % OWT;
   // dx mode: one accumulator set per column phase
   constexpr int NSET = DX2 ? 2 : 1;
@@ -258,8 +268,9 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::N
     auto xread = [&](int ks) __attribute__((always_inline)) {
       const int tap = ks >> 1, h = ks & 1;
       const int kh = tap_dh(tap), kw = tap_dw(tap);
-      const int hc = pc + kw;
-      return *reinterpret_cast<const bf16x8 *>(hb + ((pr + kh) * HC + hc) * 64 + 16 * ((2 * h + g) ^ ((hc >> 2) & 3)));
+      // halo column pc + kw, or (stride 2) 2 pc + kw in its phase plane
+      const int cs = S2 ? (kw & 1) * S::PLANE + pc + (kw >> 1) : pc + kw;
+      return *reinterpret_cast<const bf16x8 *>(hb + ((pr + kh) * HC + cs) * 64 + 16 * ((2 * h + g) ^ ((cs >> 2) & 3)));
     };
     bf16x8 xw[kWin];
     wraw_t ww[kWin][NB];
@@ -433,9 +444,10 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB>::N
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-source DMA
 }
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1, bool S2 = false>
 inline bool tile_conv_fits(const GemmParams &p) {
-  return p.KH == KH && p.KW == KW && p.SH == 1 && p.SW == 1 && p.OW == OWT && p.OH % RB == 0 &&
+  const int st = S2 ? 2 : 1;
+  return p.KH == KH && p.KW == KW && p.SH == st && p.SW == st && p.OW == OWT && p.OH % RB == 0 &&
          (IPB == 1 || p.OH == RB) && p.PH >= 0 &&
          p.PW >= 0 && p.Cin % 32 == 0 && p.N % BN == 0 && p.ldc == p.N && p.c_ow <= 0 &&
          (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 &&
@@ -445,10 +457,10 @@ inline bool tile_conv_fits(const GemmParams &p) {
          static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2) < 0x7fffffff;
 }
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1, bool S2 = false>
 inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, false, IPB>;
-  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B, false, IPB>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2>;
+  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2>;
   static const bool attr_set = [kern] {
     return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                S::LDS) == hipSuccess;
@@ -487,11 +499,16 @@ inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
 // here, so the int8 -> bf16 conversion outweighs the matrix work); the int8
 // conv converts its weights to a bf16 copy first and runs the bf16 kernel.
 // Which band-tiled shape takes this bf16 conv: 1 (14x14), 2 (28-wide), 3
-// (7x7, two images per band), 0 none.
+// (7x7, two images per band), 4 (stride 2 to 7x7 outputs, two images per
+// band: 14x14 512 -> 512 at batch 64 35.9 -> 34.6 us against the split-K
+// implicit GEMM; the stride-2 mode measured slower at 14x14 outputs with
+// half-image bands, 33.5 -> 38.8 us, and at 28-wide ones with four-row
+// bands, 28.0 -> 49.5 us, so those stay on the GEMM); 0 none.
 inline int tile_conv_shape(const GemmParams &p) {
   if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) return 1;
   if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) return 2;
   if (tile_conv_fits<3, 3, 7, 7, 64, false, 2>(p)) return 3;
+  if (tile_conv_fits<3, 3, 7, 7, 64, false, 2, true>(p)) return 4;
   return 0;
 }
 
@@ -503,6 +520,7 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
       case 2: launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s); return true;
       // 7x7 images, two per band (98 pixels, four waves)
       case 3: launch_tile_conv<3, 3, 7, 7, 64, false, 2>(p, act, s); return true;
+      case 4: launch_tile_conv<3, 3, 7, 7, 64, false, 2, true>(p, act, s); return true;
       default: break;
     }
   }

@@ -112,8 +112,8 @@ BF16_CASES = [
     (1, 12, 20, 7, 7, 3, 3, 1, 1, "relu"),     # C_IN % 8 != 0
     (1, 512, 2048, 7, 7, 1, 1, 1, 0, None),    # deep 1x1 (M = 49)
     (2, 64, 96, 10, 10, 3, 3, 1, 0, None),     # N = 96: BN=128 tile, half-empty
-    (2, 512, 512, 7, 7, 3, 3, 1, 1, "relu"),   # deep 3x3 (ResNet stage 4 shape): split-K
-    (2, 256, 256, 14, 14, 3, 3, 1, 1, "relu"), # ResNet stage 3 shape: split-K
+    (2, 512, 512, 6, 6, 3, 3, 1, 1, "relu"),   # deep 3x3 on a small grid: split-K
+    (2, 256, 256, 14, 14, 3, 3, 1, 1, "relu"), # ResNet stage 3 shape: the band-tiled kernel
     (1, 20, 48, 8, 8, 5, 5, 1, 2, None),       # element-wise gather, 5x5
     (2, 3, 32, 29, 31, 7, 7, 2, 3, None),      # stride-2 space-to-depth, odd sizes
     (1, 3, 16, 20, 20, 3, 3, 2, 1, "relu"),    # space-to-depth, 3x3 -> 2x2
@@ -124,7 +124,7 @@ BF16_CASES = [
 
 # cases whose fastest plan needs stream scratch (split-K partials or the
 # space-to-depth copy) on a 256-CU device
-SCRATCH_CASES = {BF16_CASES[i] for i in (4, 9, 10, 12, 13, 14, 15)}
+SCRATCH_CASES = {BF16_CASES[i] for i in (4, 9, 12, 13, 14, 15)}
 
 
 @pytest.mark.parametrize("case", BF16_CASES)
@@ -295,14 +295,41 @@ TILE_CASES = [
 ]
 
 
+S2_TILE_CASES = [
+    # B, H, W, Cin, Cout, pad, act, post, int8: stride-2 bf16 3x3 convs with
+    # 7x7 outputs take the band-tiled kernel in its stride-2 mode (two images
+    # per band, the halo's columns as even and odd phase planes); 14- and
+    # 28-wide outputs run the implicit GEMM
+    (5, 14, 14, 512, 512, 1, "relu", "bias", False),   # the 7x7 ResNet stride-2 3x3, ragged batch
+    (3, 13, 13, 64, 128, 1, None, "bn", False),        # odd input: the last column and row are padding
+    (2, 15, 15, 32, 64, 0, "silu", None, False),       # no padding: 15 -> 7
+    (600, 14, 14, 32, 64, 1, "silu", None, False),     # 300 bands: several per workgroup
+    (3, 28, 28, 256, 256, 1, "relu", "bias", False),   # the 14x14 ResNet stride-2 3x3
+    (2, 27, 27, 64, 64, 1, "gelu", None, False),
+    (40, 28, 28, 64, 192, 1, "relu", None, False),     # 240 units, three channel tiles
+    (2, 56, 56, 128, 128, 1, "relu", "bias", False),   # the 28x28 ResNet stride-2 3x3
+    (20, 56, 56, 64, 128, 1, None, "bn", False),       # 280 units
+    (2, 28, 28, 256, 256, 1, None, "bias", True),      # int8 weights: the implicit GEMM (no workspace)
+]
+
+
 @pytest.mark.parametrize("case", TILE_CASES)
 def test_nhwc_band_tiles(dev, orc, case):
+    run_band_tile_case(dev, orc, case, 1)
+
+
+@pytest.mark.parametrize("case", S2_TILE_CASES)
+def test_nhwc_band_tiles_stride2(dev, orc, case):
+    run_band_tile_case(dev, orc, case, 2)
+
+
+def run_band_tile_case(dev, orc, case, st):
     B, H, W, Cin, Cout, p, act, post, int8 = case
-    print(f"[conv band tiles] {case}", flush=True)
+    print(f"[conv band tiles] stride {st} {case}", flush=True)
     rng = np.random.default_rng(H * W + Cin + Cout + p)
     xb = to_bf16(rng.standard_normal((B, H, W, Cin), dtype=np.float32))
     x = from_bf16(xb)
-    oh, ow = H + 2 * p - 2, W + 2 * p - 2
+    oh, ow = (H + 2 * p - 3) // st + 1, (W + 2 * p - 3) // st + 1
     bias = scale = shift = None
     if int8:
         q, qs = quantized_conv_weight(orc, rng, Cout, 3, 3, Cin)
@@ -310,7 +337,7 @@ def test_nhwc_band_tiles(dev, orc, case):
         if post == "bias":
             bias = rng.normal(0, 0.1, Cout).astype(np.float32)
         got = K.w8a16_conv2d(dev.upload(xb, tg.bf16), dev.upload(q), dev.upload(qs),
-                             dev.upload(bias) if bias is not None else None, 1, p, act=act).to_host()
+                             dev.upload(bias) if bias is not None else None, st, p, act=act).to_host()
     else:
         wb = to_bf16((rng.standard_normal((Cout, 3, 3, Cin), dtype=np.float32) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32))
         w = from_bf16(wb)
@@ -318,12 +345,12 @@ def test_nhwc_band_tiles(dev, orc, case):
             scale = rng.uniform(0.5, 1.5, Cout).astype(np.float32)
             shift = rng.normal(0, 0.1, Cout).astype(np.float32)
             got = K.conv2d_bn_act(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16), dev.upload(scale),
-                                  dev.upload(shift), 1, p, 1, act, layout="nhwc").to_host()
+                                  dev.upload(shift), st, p, 1, act, layout="nhwc").to_host()
         else:
             if post == "bias":
                 bias = rb(rng.normal(0, 0.1, Cout).astype(np.float32))
             got = K.conv2d(dev.upload(xb, tg.bf16), dev.upload(wb, tg.bf16),
-                           dev.upload(to_bf16(bias), tg.bf16) if bias is not None else None, 1, p, 1, act,
+                           dev.upload(to_bf16(bias), tg.bf16) if bias is not None else None, st, p, 1, act,
                            layout="nhwc").to_host()
 
     def finish(ref):
@@ -333,7 +360,7 @@ def test_nhwc_band_tiles(dev, orc, case):
 
     assert got.shape == (B, oh, ow, Cout)
     assert np.all(np.isfinite(from_bf16(got)))
-    check_bf16(got, finish(orc.conv2d_nhwc(x, w, bias, stride=1, padding=p)), str(case))
+    check_bf16(got, finish(orc.conv2d_nhwc(x, w, bias, stride=st, padding=p)), f"stride {st} {case}")
 
 
 STREAM_CASES = [

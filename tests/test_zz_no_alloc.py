@@ -24,7 +24,7 @@ from teenygrad_amd.dtypes import from_bf16, to_bf16
 pytestmark = pytest.mark.gpu
 
 # (B, C_IN, C_OUT, H, K, stride, pad): first the larger input, then the smaller
-SPLIT_K = [(64, 512, 512, 7, 3, 1, 1), (2, 512, 512, 7, 3, 1, 1)]
+SPLIT_K = [(64, 512, 512, 6, 3, 1, 1), (2, 512, 512, 6, 3, 1, 1)]
 S2D = [(16, 3, 64, 160, 7, 2, 3), (3, 3, 64, 61, 7, 2, 3)]
 
 
