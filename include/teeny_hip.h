@@ -364,8 +364,8 @@ teeny_status teeny_conv2d_bias_forward(const void *x, const void *w, const void 
  * copy of stride-2 convs over few channels) is a fixed 32 MiB device array
  * inside the library, one per GPU, held until the process ends.  A shape
  * whose plan needs more than 32 MiB of scratch is rejected with
- * TEENY_ERR_UNSUPPORTED before anything is enqueued (every ResNet-50 layer at
- * batch 64 needs at most 26 MiB).  Every call on one GPU shares that GPU's
+ * TEENY_ERR_UNSUPPORTED before anything is enqueued (no ResNet-50 layer at
+ * batch 64 needs scratch at all).  Every call on one GPU shares that GPU's
  * array: calls that overlap in time on one GPU (different streams, or other
  * host threads) race on it, so serialize them.  Calls no hipMalloc/hipFree. */
 teeny_status teeny_conv2d_bias_forward_noalloc(const void *x, const void *w, const void *bias, void *y,
