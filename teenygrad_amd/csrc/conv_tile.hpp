@@ -1,7 +1,8 @@
-// Band-tiled convolution with streamed weights, for stride-1 NHWC convs whose
-// input rows are short (built for the 14x14 3x3 ResNet layers; the template
-// also takes 28-wide outputs, 7x7 outputs two images at a time, stride-2 3x3
-// convs to 7x7 outputs, and int8 weights):
+// Band-tiled convolution with streamed weights, for NHWC convs whose input
+// rows are short (built for the 14x14 3x3 ResNet layers; the template also
+// takes 28-wide outputs, 7x7 outputs two images at a time, stride-2 3x3 convs
+// to 7x7 outputs, the stride-2 dx mode below, and int8 weights), here for
+// stride 1:
 //
 //   y[b, oh, ow, n] = act( scale[n] * sum_{kh, kw, ci} x[b, oh - PH + kh, ow - PW + kw, ci]
 //                                      * w[n, kh, kw, ci] + bias[n] )
@@ -20,15 +21,19 @@
 // they fit (the DMA of the chunk after next is issued before the current
 // chunk's MFMAs), else two.
 //
-// Seven waves; wave w owns pixels 32 w .. 32 w + 31 of the band (the last
-// wave's pixels past 196 read the last pixel's window and are not stored)
-// and all BN channels: per k-step (16 channels of one tap) one pixel
+// One wave per 32 pixels of the band (seven for 196 pixels, four for the
+// 98 of two 7x7 images); wave w owns pixels 32 w .. 32 w + 31 (the last
+// wave's pixels past the band read the last pixel's window and are not
+// stored) and all BN channels: per k-step (16 channels of one tap) one pixel
 // fragment and BN / 32 weight fragments feed BN / 32
 // v_mfma_f32_32x32x16_bf16 computing D[n][px].  LDS rows: weight rows of
 // KH*KW 64-byte (bf16) or 32-byte (int8) tap segments plus one 16-byte pad
 // slot (an odd number of 16-byte units per row: conflict-free fragment
 // reads of consecutive rows); halo pixels of 4 x 16 bytes with chunk q of
-// halo column hc at position q ^ ((hc >> 2) & 3).  Epilogue through a
+// halo slot cs (the halo column, or its phase-plane slot at stride 2) at
+// position q ^ ((cs >> 2) & 3).  Units (band, channel tile) are dealt to
+// workgroups XCD by XCD, so the channel tiles of a band read its input rows
+// from one L2.  Epilogue through a
 // per-wave 4 KiB LDS slice of the stage buffer the unit's last chunk used
 // (after a barrier), 64 channels at a time, written back as whole
 // 128-byte segments of the pixels' rows; the vmcnt waits count the
