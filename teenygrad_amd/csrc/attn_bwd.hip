@@ -264,9 +264,11 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_bf16(const bf16 *__restrict_
   if (row < rows && t % CPR == 0) delta[row] = s;
 }
 
-// dK, dV for the 32 * WAVES keys of one workgroup (wave w: keys k0 + 0..31).
-// (head_dim 128: the K^T / V^T operands and both accumulators take 192 of a
-// lane's registers, so one workgroup per CU, with the accumulators in AGPRs.)
+// dK, dV for the 32 * WAVES keys of one workgroup (wave w: keys k0 + 0..31),
+// head_dim 64.  (At head_dim 128 the K^T / V^T operands and both
+// accumulators take 192 of a lane's registers: one workgroup per CU; that
+// size runs fa_bwd_dkv_vl_bf16 below, 923 -> 820 us at B*H = 256, S = 2048
+// causal.)
 template <int D, bool CAUSAL, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, (D == 128 ? 4 : 8) / WAVES) void fa_bwd_dkv_bf16(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
@@ -354,6 +356,107 @@ __global__ __launch_bounds__(64 * WAVES, (D == 128 ? 4 : 8) / WAVES) void fa_bwd
         for (int d = 0; d < ND; ++d) {
           dv[d] = mfma32x32x16(frag_tr<D>(dos, 32 * sb + 16 * t, d, lane), pb, dv[d]);
           dk[d] = mfma32x32x16(frag_tr<D>(qs, 32 * sb + 16 * t, d, lane), db8, dk[d]);
+        }
+      }
+    }
+    if (idx + 1 < total && tid < BM) {
+      lbuf[b ^ 1][tid] = l_next;
+      dbuf[b ^ 1][tid] = d_next;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  if (key < nk) {
+    const int64_t row = static_cast<int64_t>(bhk) * nk + key;
+    store_rows<ND>(dK + row * D, dk, scale, g);
+    store_rows<ND>(dV + row * D, dv, 1.0f, g);
+  }
+}
+
+// dK, dV at head_dim 128 in two workgroups per CU: the same products as
+// fa_bwd_dkv_bf16 for the 128 keys of a workgroup, with V^T read from an LDS
+// copy of the workgroup's V rows instead of registers and query tiles of 32
+// rows, so that a wave fits 256 registers (K^T 32, the dK / dV accumulators
+// 128, S and dP 32) and each SIMD runs two waves, whose exponentials and
+// MFMAs overlap.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dkv_vl_bf16(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ L, const float *__restrict__ Delta,
+    bf16 *__restrict__ dK, bf16 *__restrict__ dV, int nq, int nk, float scale, float sc, int nkb, int kv_group) {
+  constexpr int D = 128, NT = 256, BN = 128, BM = 32, NS = D / 16, ND = D / 32, TILE = BM * D;
+  __shared__ __attribute__((aligned(16))) bf16 qbuf[2][TILE], dobuf[2][TILE], vl[BN * D];
+  __shared__ __attribute__((aligned(16))) float lbuf[2][BM], dbuf[2][BM];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
+  const int tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bhk = tile_id / nkb, kblk = tile_id % nkb;
+  const int kb0 = kblk * BN, k0 = kb0 + 32 * w, key = k0 + c;
+  const bf16 *Kr = K + (static_cast<int64_t>(bhk) * nk + key) * D;
+  // the workgroup's V rows (rows past nk read as zeros), one DMA pass
+  dma_tile<D, BN, NT>(buffer_rsrc(V + static_cast<int64_t>(bhk) * nk * D, nk * D * 2), vl, kb0, tid);
+  bf16x8 kT[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) kT[st] = key < nk ? load8(Kr + 16 * st + 8 * g) : zero8();
+  f32x16 dk[ND], dv[ND];
+#pragma unroll
+  for (int d = 0; d < ND; ++d) dk[d] = dv[d] = zero16();
+
+  const int qt0 = CAUSAL ? kb0 / BM : 0;
+  const int per_head = (nq + BM - 1) / BM - qt0;
+  const int total = per_head > 0 ? per_head * kv_group : 0;
+  float l_next = 0.0f, d_next = 0.0f;
+  auto issue = [&](int idx, int b) __attribute__((always_inline)) {
+    const int hq = idx / per_head, qt = qt0 + idx % per_head;
+    const int64_t bh = static_cast<int64_t>(bhk) * kv_group + hq;
+    dma_tile<D, BM, NT>(buffer_rsrc(Q + bh * nq * D, nq * D * 2), qbuf[b], qt * BM, tid);
+    dma_tile<D, BM, NT>(buffer_rsrc(dO + bh * nq * D, nq * D * 2), dobuf[b], qt * BM, tid);
+    if (tid < BM) {
+      const int row = qt * BM + tid;
+      l_next = row < nq ? L[bh * nq + row] * kBwdLog2e : INFINITY;
+      d_next = row < nq ? Delta[bh * nq + row] : 0.0f;
+    }
+  };
+  if (total > 0) issue(0, 0);
+  if (tid < BM) {
+    lbuf[0][tid] = l_next;
+    dbuf[0][tid] = d_next;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int idx = 0; idx < total; ++idx) {
+    const int b = idx & 1;
+    if (idx + 1 < total) issue(idx + 1, b ^ 1);
+    const int q0 = (qt0 + idx % per_head) * BM;
+    const bf16 *qs = qbuf[b], *dos = dobuf[b];
+    // wave-uniform: skip when no query of the tile sees these keys
+    if (q0 < nq && !(CAUSAL && q0 + BM - 1 < k0)) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        s = mfma32x32x16(frag_row<D>(qs, 0, st, lane), kT[st], s);
+        dp = mfma32x32x16(frag_row<D>(dos, 0, st, lane), frag_row<D>(vl, 32 * w, st, lane), dp);
+      }
+      float p[16], ds[16];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lbuf[b][8 * a + 4 * g]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&dbuf[b][8 * a + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * a + e;
+          float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[v], sc, -l4[e]));
+          if (CAUSAL && key > q0 + 8 * a + 4 * g + e) pv = 0.0f;
+          p[v] = pv;
+          ds[v] = pv * (dp[v] - d4[e]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 pb = pack_b(p, t), db8 = pack_b(ds, t);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+          dv[d] = mfma32x32x16(frag_tr<D>(dos, 16 * t, d, lane), pb, dv[d]);
+          dk[d] = mfma32x32x16(frag_tr<D>(qs, 16 * t, d, lane), db8, dk[d]);
         }
       }
     }
@@ -524,6 +627,14 @@ template <int D, bool CAUSAL>
 static void mfma_dkv(const BwdArgs &a, const float *delta) {
   constexpr int BN = 32 * kBwdWaves;
   const int nkb = (a.nk + BN - 1) / BN;
+  if constexpr (D == 128 && kBwdWaves == 4) {
+    hipLaunchKernelGGL((fa_bwd_dkv_vl_bf16<CAUSAL>), dim3((a.BH / a.group) * nkb), dim3(256), 0, a.s,
+                       static_cast<const bf16 *>(a.q), static_cast<const bf16 *>(a.k),
+                       static_cast<const bf16 *>(a.v), static_cast<const bf16 *>(a.dout), a.l, delta,
+                       static_cast<bf16 *>(a.dk), static_cast<bf16 *>(a.dv), a.nq, a.nk, a.scale,
+                       a.scale * kBwdLog2e, nkb, a.group);
+    return;
+  }
   hipLaunchKernelGGL((fa_bwd_dkv_bf16<D, CAUSAL, kBwdWaves>), dim3((a.BH / a.group) * nkb), dim3(64 * kBwdWaves), 0,
                      a.s, static_cast<const bf16 *>(a.q), static_cast<const bf16 *>(a.k),
                      static_cast<const bf16 *>(a.v), static_cast<const bf16 *>(a.dout), a.l, delta,
