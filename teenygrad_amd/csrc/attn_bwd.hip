@@ -431,11 +431,17 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkv_vl_bf16(
     // wave-uniform: skip when no query of the tile sees these keys
     if (q0 < nq && !(CAUSAL && q0 + BM - 1 < k0)) {
       f32x16 s = zero16(), dp = zero16();
+      // wave priority 1 over S and dP, 0 over the exponentials and the dV /
+      // dK products: of the two waves on a SIMD, the one starting a tile's
+      // products issues first (1.350 -> 1.319 ms for the causal S = 2048
+      // backward)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         s = mfma32x32x16(frag_row<D>(qs, 0, st, lane), kT[st], s);
         dp = mfma32x32x16(frag_row<D>(dos, 0, st, lane), frag_row<D>(vl, 32 * w, st, lane), dp);
       }
+      __builtin_amdgcn_s_setprio(0);
       float p[16], ds[16];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
