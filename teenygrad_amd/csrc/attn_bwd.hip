@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_bf16(const bf16 *__restrict_
 // dK, dV for the 32 * WAVES keys of one workgroup (wave w: keys k0 + 0..31),
 // head_dim 64.  (At head_dim 128 the K^T / V^T operands and both
 // accumulators take 192 of a lane's registers: one workgroup per CU; that
-// size runs fa_bwd_dkv_vl_bf16 below, 923 -> 820 us at B*H = 256, S = 2048
+// size runs fa_bwd_dkv_vl_bf16 below, 923 -> 790 us at B*H = 256, S = 2048
 // causal.)
 template <int D, bool CAUSAL, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, (D == 128 ? 4 : 8) / WAVES) void fa_bwd_dkv_bf16(
