@@ -98,6 +98,10 @@ BF16_CASES = [  # bh, nq, nk, d, causal, group
     (2, 96, 160, 128, False, 1),
     (4, 130, 130, 64, True, 2),
     (8, 64, 200, 128, False, 4),
+    # head_dim 128 on the two-workgroup dK/dV kernel (32-row query tiles):
+    # causal with fewer queries than keys, and grouped causal at a ragged size
+    (2, 77, 300, 128, True, 1),
+    (4, 130, 130, 128, True, 2),
 ]
 
 
