@@ -21,10 +21,12 @@
 // they fit (the DMA of the chunk after next is issued before the current
 // chunk's MFMAs), else two.
 //
-// One wave per 32 pixels of the band (seven for 196 pixels, four for the
-// 98 of two 7x7 images); wave w owns pixels 32 w .. 32 w + 31 (the last
-// wave's pixels past the band read the last pixel's window and are not
-// stored) and all BN channels: per k-step (16 channels of one tap) one pixel
+// One wave per 32 pixels of the band (seven for 196 pixels), or two (eight
+// for the 98 of two 7x7 images, each taking one of the two k-steps of every
+// tap, their sums added through LDS at the unit's end); wave w owns pixels
+// 32 w .. 32 w + 31 (the last wave's pixels past the band read the last
+// pixel's window and are not stored) and all BN channels: per k-step (16
+// channels of one tap) one pixel
 // fragment and BN / 32 weight fragments feed BN / 32
 // v_mfma_f32_32x32x16_bf16 computing D[n][px].  LDS rows: weight rows of
 // KH*KW 64-byte (bf16) or 32-byte (int8) tap segments plus one 16-byte pad
@@ -65,10 +67,16 @@ struct TileConvParams {
 // 1) - PH + 2 and, per row, its columns as two phase planes, the even halo
 // columns hc = 2 j at slots j = 0 .. OWT, then the odd ones at OWT + 1 + j,
 // so the 32 consecutive output pixels of a fragment read consecutive slots.
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false>
+// KS = 2: two waves per 32-pixel block, each taking one of the two k-steps
+// of every tap (16 of a chunk's 32 channels); their sums meet in LDS at the
+// unit's end.  For bands of few pixels (four blocks), so that each SIMD runs
+// two waves.
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false,
+          int KS = 1>
 struct TileShape {
   static constexpr int NPX = RB * OWT * IPB;     // pixels per band
-  static constexpr int NW = (NPX + 31) / 32;     // waves
+  static constexpr int NPB = (NPX + 31) / 32;    // 32-pixel blocks
+  static constexpr int NW = NPB * KS;            // waves
   static constexpr int NT = 64 * NW;
   static constexpr int PLANE = OWT + 1;          // stride 2: slots per column phase plane
   // dx mode: a phase reads dy rows u, u + 1 and columns v, v + 1 (no padding)
@@ -92,17 +100,19 @@ struct TileShape {
   // LDS stages: three (two DMA passes in flight) where they fit, else two
   static constexpr int NSTG = 3 * STAGE + 2 * BN * 4 <= 160 * 1024 ? 3 : 2;
   static constexpr int LDS = NSTG * STAGE + 2 * BN * 4;
-  static_assert(NW * STG <= STAGE, "epilogue slices fit one stage buffer");
+  static_assert(NPB * STG + (KS - 1) * NPB * 8192 <= STAGE, "epilogue slices (and k-split sums) fit one stage buffer");
+  static_assert(KS == 1 || (KS == 2 && !DX2 && !INT8B), "k-split waves: bf16 forward");
   static_assert(DI * NW - INSTR <= INSTR, "excess DMA instructions repeat real ones");
   static_assert(RS % 2 == 1, "odd number of 16-byte units per weight row");
   static_assert(BN % 64 == 0 && NW <= 16, "tile");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false>
-__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2>::NT), 1) void conv_tile_kernel(
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, bool DX2 = false, int IPB = 1, bool S2 = false,
+          int KS = 1>
+__global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2, KS>::NT), 1) void conv_tile_kernel(
     TileConvParams p) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2, KS>;
   static_assert(!DX2 || (KH == 3 && KW == 3 && !INT8B), "dx mode: bf16 3x3 stride 2 pad 1");
   constexpr int NW = S::NW, HC = S::HC, DI = S::DI, NB = BN / 32;
   constexpr int EPI_STORES = 4 * (BN / 64) * (DX2 ? 2 : 1);  // per unit (dx mode: two phases)
@@ -216,7 +226,9 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
   };
 
   // ── MFMA side
-  const int px = min(32 * w + c, S::NPX - 1);  // pixels past the band repeat the last one
+  // the wave's pixel block and (KS = 2) its k-step of every tap
+  const int pbk = KS > 1 ? w % S::NPB : w, hk = KS > 1 ? w / S::NPB : 0;
+  const int px = min(32 * pbk + c, S::NPX - 1);  // pixels past the band repeat the last one
   // halo row of the pixel's first tap (multi-image band: in its image's halo)
   constexpr int SR = S2 ? 2 : 1;
   const int pr = IPB > 1 ? (px / (RB * OWT)) * S::HRI + SR * ((px % (RB * OWT)) / OWT) : SR * (px / OWT);
@@ -269,9 +281,12 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
     auto tap_dw = [](int j) { return DX2 ? (j < TT ? 0 : (j - TT) % 2) : j % KW; };
     const char *hb = smem + (st % S::NSTG) * S::STAGE;
     const char *wb = hb + S::HBYTES;
-    constexpr int NKS = NTAP * 2;
+    // the wave's k-steps i = 0 .. NKS-1: tap tap_of(i), channel half h_of(i)
+    constexpr int NKS = NTAP * 2 / KS;
+    auto tap_of = [](int i) { return KS > 1 ? i : i >> 1; };
+    auto h_of = [&](int i) { return KS > 1 ? hk : i & 1; };
     auto xread = [&](int ks) __attribute__((always_inline)) {
-      const int tap = ks >> 1, h = ks & 1;
+      const int tap = tap_of(ks), h = h_of(ks);
       const int kh = tap_dh(tap), kw = tap_dw(tap);
       // halo column pc + kw, or (stride 2) 2 pc + kw in its phase plane
       const int cs = S2 ? (kw & 1) * S::PLANE + pc + (kw >> 1) : pc + kw;
@@ -282,7 +297,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
     auto fetch = [&](int ks) __attribute__((always_inline)) {
       xw[ks % kWin] = xread(ks);
 #pragma unroll
-      for (int i = 0; i < NB; ++i) ww[ks % kWin][i] = wread(wb, i, ks >> 1, ks & 1);
+      for (int i = 0; i < NB; ++i) ww[ks % kWin][i] = wread(wb, i, tap_of(ks), h_of(ks));
     };
 #pragma unroll
     for (int ks = 0; ks < kLA; ++ks) fetch(ks);
@@ -291,7 +306,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
       if (ks + kLA < NKS) fetch(ks + kLA);
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
-        const int a = tap_set(ks >> 1) * NB + i;
+        const int a = tap_set(tap_of(ks)) * NB + i;
         acc[a] = mfma32x32x16(wconv(ww[ks % kWin][i]), xw[ks % kWin], acc[a]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -322,7 +337,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
   auto epilogue = [&](int st, auto sig, int set) __attribute__((always_inline)) {
     int b, oh0, n0, ph;
     unit_of(st, b, oh0, n0, ph);
-    char *const stg = smem + (st % S::NSTG) * S::STAGE + w * S::STG;
+    char *const stg = smem + (st % S::NSTG) * S::STAGE + pbk * S::STG;
     const int64_t pix0 = (static_cast<int64_t>(b) * p.OH + oh0) * OWT;  // the band's first pixel
 #pragma unroll
     for (int hp = 0; hp < NB / 2; ++hp) {
@@ -371,7 +386,7 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
       for (int r8 = 0; r8 < 4; ++r8) {
         const int pl = 8 * r8 + (lane >> 3), k = lane & 7;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 128 + 16 * (k ^ (pl & 7)));
-        const int pxl = 32 * w + pl;
+        const int pxl = 32 * pbk + pl;
         int64_t opix = pix0 + pxl;
         if constexpr (DX2) {
           // phase pixel (u, v) of phase (a, c) is dx pixel (2 u + a, 2 v + c)
@@ -426,14 +441,40 @@ __global__ __launch_bounds__((TileShape<KH, KW, OWT, RB, BN, INT8B, DX2, IPB, S2
     epi_hist <<= 1;
     if (st % nch == nch - 1) {
       __syncthreads();  // every wave has read stage st's buffer: the epilogue slices reuse it
+      if constexpr (KS == 2) {
+        // the second k-half's sums, after the epilogue slices, added into the first's
+        f32x4 *const part = reinterpret_cast<f32x4 *>(smem + (st % S::NSTG) * S::STAGE + S::NPB * S::STG);
+        if (hk == 1) {
 #pragma unroll
-      for (int set = 0; set < NSET; ++set) {
-        if (!DX2 && ea.sig) epilogue(st, std::true_type{}, set);
-        else epilogue(st, std::false_type{}, set);
+          for (int i = 0; i < NB; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              part[((pbk * NB + i) * 4 + q) * 64 + lane] =
+                  f32x4{acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]};
+        }
+        __syncthreads();
+        if (hk == 0) {
+#pragma unroll
+          for (int i = 0; i < NB; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 v = part[((pbk * NB + i) * 4 + q) * 64 + lane];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[i][4 * q + e] += v[e];
+            }
+        }
+      }
+      if (hk == 0) {
+#pragma unroll
+        for (int set = 0; set < NSET; ++set) {
+          if (!DX2 && ea.sig) epilogue(st, std::true_type{}, set);
+          else epilogue(st, std::false_type{}, set);
+        }
       }
 #pragma unroll
       for (int i = 0; i < NSET * NB; ++i) acc[i] = zero16();
-      epi_hist |= 1u;
+      // (the epilogue's stores, which the waits count: first k-half only)
+      epi_hist |= hk == 0 ? 1u : 0u;
       if (st + 1 < n_stages) {
         int b2, oh2, n2, b1, oh1, n1, ph1, ph2;
         unit_of(st, b1, oh1, n1, ph1);
@@ -462,10 +503,10 @@ inline bool tile_conv_fits(const GemmParams &p) {
          static_cast<int64_t>(p.N) * p.K * (INT8B ? 1 : 2) < 0x7fffffff;
 }
 
-template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1, bool S2 = false>
+template <int KH, int KW, int OWT, int RB, int BN, bool INT8B, int IPB = 1, bool S2 = false, int KS = 1>
 inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
-  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2>;
-  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2>;
+  using S = TileShape<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2, KS>;
+  auto kern = &conv_tile_kernel<KH, KW, OWT, RB, BN, INT8B, false, IPB, S2, KS>;
   static const bool attr_set = [kern] {
     return hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                S::LDS) == hipSuccess;
@@ -524,8 +565,11 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
       case 1: launch_tile_conv<3, 3, 14, 14, 64, false>(p, act, s); return true;
       case 2: launch_tile_conv<3, 3, 28, 7, 64, false>(p, act, s); return true;
       // 7x7 images, two per band (98 pixels, four waves)
-      case 3: launch_tile_conv<3, 3, 7, 7, 64, false, 2>(p, act, s); return true;
-      case 4: launch_tile_conv<3, 3, 7, 7, 64, false, 2, true>(p, act, s); return true;
+      // (with two waves per pixel block, each on half of every chunk's
+      // channels: 512 -> 512 at batch 64 30.2 -> 26.1 us, stride 2 34.5 ->
+      // 30.0 us, against one wave per block and SIMD)
+      case 3: launch_tile_conv<3, 3, 7, 7, 64, false, 2, false, 2>(p, act, s); return true;
+      case 4: launch_tile_conv<3, 3, 7, 7, 64, false, 2, true, 2>(p, act, s); return true;
       default: break;
     }
   }
