@@ -546,15 +546,17 @@ inline void launch_tile_conv(const GemmParams &p, int act, hipStream_t s) {
 // conv converts its weights to a bf16 copy first and runs the bf16 kernel.
 // Which band-tiled shape takes this bf16 conv: 1 (14x14), 2 (28-wide), 3
 // (7x7, two images per band), 4 (stride 2 to 7x7 outputs, two images per
-// band: 14x14 512 -> 512 at batch 64 35.9 -> 34.6 us against the split-K
-// implicit GEMM; the stride-2 mode measured slower at 14x14 outputs with
-// half-image bands, 33.5 -> 38.8 us, and at 28-wide ones with four-row
-// bands, 28.0 -> 49.5 us, so those stay on the GEMM); 0 none.
+// band: 14x14 512 -> 512 at batch 64 35.9 -> 30.0 us against the split-K
+// implicit GEMM), 5 (stride 2 to 14x14 outputs, half-image bands: 28x28
+// 256 -> 256 33.5 -> 31.0 us against the implicit GEMM; 38.8 us with one
+// wave per pixel block); stride 2 to 28-wide outputs (four-row bands, 28.0
+// -> 49.5 us) stays on the GEMM; 0 none.
 inline int tile_conv_shape(const GemmParams &p) {
   if (tile_conv_fits<3, 3, 14, 14, 64, false>(p)) return 1;
   if (tile_conv_fits<3, 3, 28, 7, 64, false>(p)) return 2;
   if (tile_conv_fits<3, 3, 7, 7, 64, false, 2>(p)) return 3;
   if (tile_conv_fits<3, 3, 7, 7, 64, false, 2, true>(p)) return 4;
+  if (tile_conv_fits<3, 3, 14, 7, 64, false, 1, true>(p)) return 5;
   return 0;
 }
 
@@ -570,6 +572,7 @@ inline bool try_conv_tile(const GemmParams &p, int act, hipStream_t s) {
       // 30.0 us, against one wave per block and SIMD)
       case 3: launch_tile_conv<3, 3, 7, 7, 64, false, 2, false, 2>(p, act, s); return true;
       case 4: launch_tile_conv<3, 3, 7, 7, 64, false, 2, true, 2>(p, act, s); return true;
+      case 5: launch_tile_conv<3, 3, 14, 7, 64, false, 1, true, 2>(p, act, s); return true;
       default: break;
     }
   }

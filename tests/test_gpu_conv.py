@@ -297,9 +297,10 @@ TILE_CASES = [
 
 S2_TILE_CASES = [
     # B, H, W, Cin, Cout, pad, act, post, int8: stride-2 bf16 3x3 convs with
-    # 7x7 outputs take the band-tiled kernel in its stride-2 mode (two images
-    # per band, the halo's columns as even and odd phase planes); 14- and
-    # 28-wide outputs run the implicit GEMM
+    # 7x7 and 14x14 outputs take the band-tiled kernel in its stride-2 mode
+    # (two images or half an image per band, the halo's columns as even and
+    # odd phase planes, two waves per pixel block); 28-wide outputs run the
+    # implicit GEMM
     (5, 14, 14, 512, 512, 1, "relu", "bias", False),   # the 7x7 ResNet stride-2 3x3, ragged batch
     (3, 13, 13, 64, 128, 1, None, "bn", False),        # odd input: the last column and row are padding
     (2, 15, 15, 32, 64, 0, "silu", None, False),       # no padding: 15 -> 7
