@@ -86,7 +86,10 @@ struct BandShape {
   static constexpr int K = KH * KW * CIN;
   static constexpr int WP = K * 2 + 16;             // weight row pitch (bytes)
   static constexpr int WBYTES = COUT * WP;
-  static constexpr int STG = 2048;                  // epilogue slice per wave
+  // epilogue slice per wave: both 32-channel blocks at once for the stem
+  // (one LDS write-then-read round trip per band instead of two: 35.5 ->
+  // 33.6 us), one at a time where the LDS is full (the 56x56 3x3 layers)
+  static constexpr int STG = CIN == 16 ? 4096 : 2048;
   static_assert(NPX % 32 == 0 && NW <= 16, "a band is whole 32-pixel blocks");
   static_assert(CIN % 16 == 0 && CC % 16 == 0 && (CPP == 2 || CPP == 4), "16-channel k-steps");
   static_assert((WP / 16) % 2 == 1, "odd number of 16-byte units per weight row");
@@ -377,17 +380,31 @@ __global__ __launch_bounds__((BandShape<CIN, KH, KW, OWT, RB>::NT), 1) void conv
           v[2 + d] = sw[1];
         }
         const int k = 2 * prr + g;
-        *reinterpret_cast<u32x4 *>(stg + c * 64 + 16 * (k ^ ((c >> 1) & 3))) = v;
+        *reinterpret_cast<u32x4 *>(stg + (S::STG >= 4096 ? 2048 * i : 0) + c * 64 + 16 * (k ^ ((c >> 1) & 3))) = v;
       }
-      // 32 pixels x 64 bytes back out: round r2, lane L holds pixel 16 r2 + L / 4,
-      // chunk L % 4, by non-temporal stores (cache policy nt: in the ResNet
-      // step the stem 35.4 -> 33.5 us and the 56x56 3x3 24.0 -> 22.7 us)
+      if constexpr (S::STG < 4096) {
 #pragma unroll
-      for (int r2 = 0; r2 < 2; ++r2) {
-        const int pl = 16 * r2 + (lane >> 2), k = lane & 3;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 64 + 16 * (k ^ ((pl >> 1) & 3)));
-        const int off = static_cast<int>(((pix0 + pl) * S::COUT + 32 * i) * 2 + 16 * k);
-        __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 2);
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const int pl = 16 * r2 + (lane >> 2), k = lane & 3;
+          const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + pl * 64 + 16 * (k ^ ((pl >> 1) & 3)));
+          const int off = static_cast<int>(((pix0 + pl) * S::COUT + 32 * i) * 2 + 16 * k);
+          __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 2);
+        }
+      }
+    }
+    // 32 pixels x 64 bytes back out: round r2, lane L holds pixel 16 r2 + L / 4,
+    // chunk L % 4, by non-temporal stores (cache policy nt: in the ResNet
+    // step the stem 35.4 -> 33.5 us and the 56x56 3x3 24.0 -> 22.7 us)
+    if constexpr (S::STG >= 4096) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const int pl = 16 * r2 + (lane >> 2), k = lane & 3;
+          const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + 2048 * i + pl * 64 + 16 * (k ^ ((pl >> 1) & 3)));
+          const int off = static_cast<int>(((pix0 + pl) * S::COUT + 32 * i) * 2 + 16 * k);
+          __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, off, 0, 2);
+        }
       }
     }
   };
