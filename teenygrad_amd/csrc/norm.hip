@@ -197,12 +197,17 @@ __global__ __launch_bounds__(kNormThreads) void norm_multipass_kernel(
   }
 }
 
+// Dynamic LDS that no kernel touches, sized so that at most `wgs` workgroups
+// fit in one CU's 160 KiB (0: no cap).  Used as an occupancy cap where fewer
+// resident rows stream faster.
+static unsigned occupancy_cap_lds(int wgs) { return wgs > 0 ? 160u * 1024u / (wgs + 1) + 1024u : 0u; }
+
 template <typename T, int WPR, int VPL, bool RMS, int ACT>
 static void launch_rows(const void *x, void *y, const void *g, const void *b, float *st0, float *st1,
-                        int64_t M, int64_t N, float eps, float inv_n, hipStream_t s) {
+                        int64_t M, int64_t N, float eps, float inv_n, hipStream_t s, int wgs_per_cu = 0) {
   constexpr int RPB = kNormWaves / WPR;
   hipLaunchKernelGGL((norm_rows_kernel<T, WPR, VPL, RMS, ACT>), dim3(cdiv(M, RPB)),
-                     dim3(kNormThreads), 0, s, static_cast<const T *>(x), static_cast<T *>(y),
+                     dim3(kNormThreads), occupancy_cap_lds(wgs_per_cu), s, static_cast<const T *>(x), static_cast<T *>(y),
                      static_cast<const T *>(g), static_cast<const T *>(b), st0, st1, M,
                      static_cast<int32_t>(N), eps, inv_n);
 }
@@ -224,8 +229,11 @@ static teeny_status launch_norm(const void *x, void *y, const void *g, const voi
     launch_rows<T, 4, 1, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 512) {
     // two waves per row, two rows per workgroup: measured against four waves
-    // per row at [16384, 4096] bf16, LayerNorm 47.3 vs 50.1 us, RMSNorm equal
-    launch_rows<T, 2, 4, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
+    // per row at [16384, 4096] bf16, LayerNorm 47.3 vs 50.1 us, RMSNorm equal.
+    // At most four workgroups per CU (registers alone allow five): LayerNorm
+    // 47.7 -> 46.4 us, RMSNorm 45.9 -> 45.0 us; three per CU 47.8 / 45.9 us,
+    // two 52 / 48 us.
+    launch_rows<T, 2, 4, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s, 4);
   } else if (vec_ok && nv <= 1024) {
     launch_rows<T, 4, 4, RMS, ACT>(x, y, g, b, st0, st1, M, N, eps, inv_n, s);
   } else if (vec_ok && nv <= 2048) {
