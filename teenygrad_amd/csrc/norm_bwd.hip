@@ -15,10 +15,14 @@
 // workgroups walks the rows (row r on workgroup r mod G); each thread owns
 // VPT fixed 16-byte column vectors of every row, so gamma is loaded once and
 // the per-column gradient partials stay in fp32 registers across rows.  The
-// rows two ahead are loaded (raw, with their statistics; x and dy by
-// non-temporal loads: LayerNorm backward 88.7 -> 86.3 us, RMSNorm 84.5 ->
-// 80.1 us at [16384, 4096] bf16) before the current row's reductions, which are DPP wave sums plus one LDS exchange (one
-// barrier per row: each register set has its own LDS slot).  At the end each
+// next row is loaded (raw, with its statistics; x and dy by non-temporal
+// loads: LayerNorm backward 88.7 -> 86.3 us, RMSNorm 84.5 -> 80.1 us at
+// [16384, 4096] bf16) before the current row's reductions, which are DPP
+// wave sums plus one LDS exchange (one barrier per row: each register set
+// has its own LDS slot).  One row ahead rather than two: 81.5 -> 78.8 us and
+// 76.9 -> 75.7 us (fewer bytes in flight stream faster here, as in the
+// forward); three workgroups per CU ran 85.5 / 78.8 us, and no prefetch at
+// three, four or five per CU 81.3 / 74.7, 87 / 79 and 94 / 86 us.  At the end each
 // workgroup writes its column partials to the stream workspace and one
 // small pass adds them per column in a fixed order to dweight (and dbias).
 // Without a large enough workspace
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
     float *__restrict__ part_b, int64_t M, int32_t N, float inv_n) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NS = RMS ? 1 : 2;  // row sums
-  __shared__ float red[3][kNbWaves][NS];
+  __shared__ float red[2][kNbWaves][NS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nv = N / VEC;
   const int64_t G = gridDim.x;
@@ -160,27 +164,24 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
       if (v < nv) store_vec(dxr + static_cast<int64_t>(v) * VEC, o);
     }
   };
-  // three register sets, two rows ahead, unrolled by three so the sets
-  // rotate without copies; each set has its own LDS slot (one barrier per
-  // row).  Past the last row a prefetch re-reads the current row (cached, and
-  // never used), so the loads need no branch.  The grid has at most M
-  // workgroups.
-  u32x4 xa[VPT], da[VPT], xb[VPT], db[VPT], xc[VPT], dc[VPT];
-  float sa0, sa1, sb0, sb1, sc0, sc1;
+  // two register sets, one row ahead, unrolled by two so the sets alternate
+  // without copies; each set has its own LDS slot (one barrier per row: a
+  // slot is written again only after the barrier of the row in between,
+  // which every wave reaches after reading it).  Past the last row a
+  // prefetch re-reads the current row (cached, and never used), so the loads
+  // need no branch.  The grid has at most M workgroups.
+  u32x4 xa[VPT], da[VPT], xb[VPT], db[VPT];
+  float sa0, sa1, sb0, sb1;
   auto clamp = [&](int64_t r, int64_t cur) { return r < M ? r : cur; };
   int64_t row = blockIdx.x;
   load_raw(row, xa, da, sa0, sa1);
-  load_raw(clamp(row + G, row), xb, db, sb0, sb1);
-  for (; row < M; row += 3 * G) {
-    const int64_t r1 = row + G, r2 = row + 2 * G;
-    load_raw(clamp(r2, row), xc, dc, sc0, sc1);
+  for (; row < M; row += 2 * G) {
+    const int64_t r1 = row + G;
+    load_raw(clamp(r1, row), xb, db, sb0, sb1);
     process(row, xa, da, sa0, sa1, 0);
     if (r1 >= M) break;
-    load_raw(clamp(r2 + G, r1), xa, da, sa0, sa1);
+    load_raw(clamp(r1 + G, r1), xa, da, sa0, sa1);
     process(r1, xb, db, sb0, sb1, 1);
-    if (r2 >= M) break;
-    load_raw(clamp(r2 + 2 * G, r2), xb, db, sb0, sb1);
-    process(r2, xc, dc, sc0, sc1, 2);
   }
   if constexpr (PART) {
     float *pg = part_g + static_cast<int64_t>(blockIdx.x) * N;
