@@ -201,50 +201,53 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
 
 // Column sums of the per-workgroup partials in one deterministic pass.
 // Workgroup (column block c, array a: 0 the dweight partials, 1 the dbias
-// ones) is 64 row groups x 16 columns: thread (r, j) adds rows r, r + 64, ...
-// of column 16 c + j, eight loads in flight (every load of G = 512 rows
-// issued before the adds), the 16 columns of one row being one 64-byte
-// segment; the 64 row-group sums of a column are then added by a fixed
-// two-level tree in LDS and accumulated into dweight or dbias.  (Two
-// passes, slices of workgroups then the slices, ran the LayerNorm backward
-// at [16384, 4096] bf16 in 86.2 us against 81.4 us with this one, RMSNorm
-// 79.9 against 76.6 us.)
-constexpr int kCsCols = 16, kCsGroups = 64, kCsThreads = kCsCols * kCsGroups;
+// ones) is 64 row groups x 16 column quads: thread (r, j) adds rows r, r +
+// 64, ... of columns 64 c + 4 j .. + 3 (one 16-byte load per row), eight
+// loads in flight (every load of G = 512 rows issued before the adds), the
+// 64 columns of one row being one 256-byte segment; the 64 row-group sums of
+// a column are then added by a fixed two-level tree in LDS and accumulated
+// into dweight or dbias.  (Single columns, 64-byte row segments: LayerNorm
+// backward 79.1 against 76.8 us at [16384, 4096] bf16.  Two passes, slices
+// of workgroups then the slices, ran it in 86.2 us against 81.4 us with one
+// pass of single columns, RMSNorm 79.9 against 76.6 us.)
+constexpr int kCsQuads = 16, kCsCols = 4 * kCsQuads, kCsGroups = 64, kCsThreads = kCsQuads * kCsGroups;
 __global__ __launch_bounds__(kCsThreads) void norm_bwd_colsum(const float *__restrict__ part_g,
                                                               const float *__restrict__ part_b, int G, int N,
                                                               float *__restrict__ dweight,
                                                               float *__restrict__ dbias) {
-  __shared__ float red[kCsGroups][kCsCols + 1];
-  __shared__ float red2[kCsGroups / 4][kCsCols + 1];
+  __shared__ f32x4 red[kCsGroups][kCsQuads];
+  __shared__ f32x4 red2[kCsGroups / 4][kCsQuads];
   const int t = threadIdx.x;
-  const int j = t % kCsCols, r = t / kCsCols;
-  const int n = blockIdx.x * kCsCols + j;
+  const int j = t % kCsQuads, r = t / kCsQuads;
+  const int n = blockIdx.x * kCsCols + 4 * j;  // the thread's four columns n .. n + 3 (N % 4 == 0)
   const bool bias = blockIdx.y == 1;
   const float *part = bias ? part_b : part_g;
-  float acc[8];
+  f32x4 acc[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
+  for (int k = 0; k < 8; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto ld = [&](int g) { return *reinterpret_cast<const f32x4 *>(part + static_cast<int64_t>(g) * N + n); };
   if (n < N) {
     int g = r;
     for (; g + 7 * kCsGroups < G; g += 8 * kCsGroups) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] += part[static_cast<int64_t>(g + k * kCsGroups) * N + n];
+      for (int k = 0; k < 8; ++k) acc[k] += ld(g + k * kCsGroups);
     }
-    for (; g < G; g += kCsGroups) acc[0] += part[static_cast<int64_t>(g) * N + n];
+    for (; g < G; g += kCsGroups) acc[0] += ld(g);
   }
   red[r][j] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (t < kCsGroups / 4 * kCsCols) {
-    const int q = t / kCsCols;
+  if (t < kCsGroups / 4 * kCsQuads) {
+    const int q = t / kCsQuads;
     red2[q][j] = (red[4 * q][j] + red[4 * q + 1][j]) + (red[4 * q + 2][j] + red[4 * q + 3][j]);
   }
   __syncthreads();
-  if (t < kCsCols && n < N) {
-    float sum = 0.0f;
+  if (t < kCsQuads && n < N) {
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < kCsGroups / 4; ++q) sum += red2[q][j];
-    float *out = bias ? dbias : dweight;
-    out[n] = out[n] + sum;
+    float *out = (bias ? dbias : dweight) + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = out[e] + sum[e];
   }
 }
 
@@ -343,7 +346,8 @@ static teeny_status norm_bwd(const void *dy, const void *x, void *dx, const void
   const bool grads = dweight != nullptr || (!RMS && dbias != nullptr);
   const int G = bwd_groups(M);
   const Scratch scr = stream_scratch(s);
-  const bool part = grads && vpt > 0 && scr.ptr != nullptr && scr.bytes >= bwd_scratch_bytes(M, N, RMS);
+  const bool part = grads && vpt > 0 && scr.ptr != nullptr && aligned(scr.ptr, 16) &&
+                    scr.bytes >= bwd_scratch_bytes(M, N, RMS);
   float *pg = part ? static_cast<float *>(scr.ptr) : nullptr;
   float *pb = part && !RMS ? pg + static_cast<int64_t>(G) * N : nullptr;
   if (vpt > 0) {
