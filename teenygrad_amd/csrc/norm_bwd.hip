@@ -15,14 +15,16 @@
 // workgroups walks the rows (row r on workgroup r mod G); each thread owns
 // VPT fixed 16-byte column vectors of every row, so gamma is loaded once and
 // the per-column gradient partials stay in fp32 registers across rows.  The
-// next row is loaded (raw, with its statistics; x and dy by non-temporal
-// loads: LayerNorm backward 88.7 -> 86.3 us, RMSNorm 84.5 -> 80.1 us at
-// [16384, 4096] bf16) before the current row's reductions, which are DPP
-// wave sums plus one LDS exchange (one barrier per row: each register set
-// has its own LDS slot).  One row ahead rather than two: 81.5 -> 78.8 us and
-// 76.9 -> 75.7 us (fewer bytes in flight stream faster here, as in the
-// forward); three workgroups per CU ran 85.5 / 78.8 us, and no prefetch at
-// three, four or five per CU 81.3 / 74.7, 87 / 79 and 94 / 86 us.  At the end each
+// rows two ahead are loaded (raw, with their statistics; x and dy by
+// non-temporal loads: LayerNorm backward 88.7 -> 86.3 us, RMSNorm 84.5 ->
+// 80.1 us at [16384, 4096] bf16) before the current row's reductions, which
+// are DPP wave sums plus one LDS exchange (one barrier per row: each
+// register set has its own LDS slot).  One workgroup per CU: with the
+// column sums below, LayerNorm backward 76.7 -> 72.0 us and RMSNorm 75.8 ->
+// 70.4 us against two per CU (half the partials, and fewer bytes in flight,
+// which stream faster here as in the forward); one per CU with one row
+// ahead 76.0 / 70.8 us, three ahead 72.7 / 71.2 us; two per CU with one row
+// ahead 76.8 / 75.7 us, three per CU 85.5 / 78.8 us.  At the end each
 // workgroup writes its column partials to the stream workspace and one
 // small pass adds them per column in a fixed order to dweight (and dbias).
 // Without a large enough workspace
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
     float *__restrict__ part_b, int64_t M, int32_t N, float inv_n) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NS = RMS ? 1 : 2;  // row sums
-  __shared__ float red[2][kNbWaves][NS];
+  __shared__ float red[3][kNbWaves][NS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nv = N / VEC;
   const int64_t G = gridDim.x;
@@ -164,24 +166,27 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
       if (v < nv) store_vec(dxr + static_cast<int64_t>(v) * VEC, o);
     }
   };
-  // two register sets, one row ahead, unrolled by two so the sets alternate
-  // without copies; each set has its own LDS slot (one barrier per row: a
-  // slot is written again only after the barrier of the row in between,
-  // which every wave reaches after reading it).  Past the last row a
-  // prefetch re-reads the current row (cached, and never used), so the loads
-  // need no branch.  The grid has at most M workgroups.
-  u32x4 xa[VPT], da[VPT], xb[VPT], db[VPT];
-  float sa0, sa1, sb0, sb1;
+  // three register sets, two rows ahead, unrolled by three so the sets
+  // rotate without copies; each set has its own LDS slot (one barrier per
+  // row).  Past the last row a prefetch re-reads the current row (cached, and
+  // never used), so the loads need no branch.  The grid has at most M
+  // workgroups.
+  u32x4 xa[VPT], da[VPT], xb[VPT], db[VPT], xc[VPT], dc[VPT];
+  float sa0, sa1, sb0, sb1, sc0, sc1;
   auto clamp = [&](int64_t r, int64_t cur) { return r < M ? r : cur; };
   int64_t row = blockIdx.x;
   load_raw(row, xa, da, sa0, sa1);
-  for (; row < M; row += 2 * G) {
-    const int64_t r1 = row + G;
-    load_raw(clamp(r1, row), xb, db, sb0, sb1);
+  load_raw(clamp(row + G, row), xb, db, sb0, sb1);
+  for (; row < M; row += 3 * G) {
+    const int64_t r1 = row + G, r2 = row + 2 * G;
+    load_raw(clamp(r2, row), xc, dc, sc0, sc1);
     process(row, xa, da, sa0, sa1, 0);
     if (r1 >= M) break;
-    load_raw(clamp(r1 + G, r1), xa, da, sa0, sa1);
+    load_raw(clamp(r2 + G, r1), xa, da, sa0, sa1);
     process(r1, xb, db, sb0, sb1, 1);
+    if (r2 >= M) break;
+    load_raw(clamp(r2 + 2 * G, r2), xb, db, sb0, sb1);
+    process(r2, xc, dc, sc0, sc1, 2);
   }
   if constexpr (PART) {
     float *pg = part_g + static_cast<int64_t>(blockIdx.x) * N;
@@ -202,8 +207,8 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_rows_kernel(
 // Column sums of the per-workgroup partials in one deterministic pass.
 // Workgroup (column block c, array a: 0 the dweight partials, 1 the dbias
 // ones) is 64 row groups x 16 column quads: thread (r, j) adds rows r, r +
-// 64, ... of columns 64 c + 4 j .. + 3 (one 16-byte load per row), eight
-// loads in flight (every load of G = 512 rows issued before the adds), the
+// 64, ... of columns 64 c + 4 j .. + 3 (one 16-byte load per row; eight
+// loads in flight per batch of 512 rows, the rest one at a time), the
 // 64 columns of one row being one 256-byte segment; the 64 row-group sums of
 // a column are then added by a fixed two-level tree in LDS and accumulated
 // into dweight or dbias.  (Single columns, 64-byte row segments: LayerNorm
@@ -308,9 +313,9 @@ __global__ __launch_bounds__(kNbThreads) void norm_bwd_multipass_kernel(
   }
 }
 
-// Workgroups of the row kernel: two per CU, at most one per row.
+// Workgroups of the row kernel: one per CU, at most one per row.
 static int bwd_groups(int64_t M) {
-  return static_cast<int>(std::min<int64_t>(M, 2 * static_cast<int64_t>(device_cu_count())));
+  return static_cast<int>(std::min<int64_t>(M, static_cast<int64_t>(device_cu_count())));
 }
 
 template <typename T>
