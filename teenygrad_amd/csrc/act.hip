@@ -14,8 +14,10 @@
 // vector; lanes of a wave touch consecutive 16-byte chunks so every load
 // instruction is one fully coalesced 1 KiB request; both the loads and the
 // stores are non-temporal (the data streams through once).  With ~16 VGPRs
-// the kernel runs at 8 waves per SIMD; a [16384, 4096] bf16 tensor is 32768
-// workgroups.  Measured on MI355X at the settled clock over rotating 128 MiB
+// the kernel runs at 8 waves per SIMD; a [16384, 4096] bf16 tensor is 16384
+// workgroups of 512 threads (256-thread workgroups: the forward the same,
+// the three gradients 64.0-65.8 against 63.2-64.4 us; 1024 threads: the
+// forward 42.5 -> 44.5 us).  Measured on MI355X at the settled clock over rotating 128 MiB
 // buffers (GELU, [16384, 4096] bf16): one vector per thread with
 // non-temporal loads 42.3 us (0.79 of 8 TB/s), against 45.1 us for two
 // vectors with temporal loads, 43.4-43.5 us for either change alone, 46.5 us
@@ -28,7 +30,7 @@
 
 namespace teeny {
 
-constexpr int kActThreads = 256;
+constexpr int kActThreads = 512;
 constexpr int kActUnroll = 1;
 
 template <typename T, int ACT>
